@@ -1,0 +1,295 @@
+"""Benchmark of the per-stage update path on one MI355X (config C1 of
+one of the 2 pipeline stages of the 2.8B model).
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1]
+
+A step is one optimizer step of the stage's shard with every input resident
+in HBM: 16 GPT blocks at d = 2560 (192 tensors, 1,258,823,680 fp32 params),
+bf16 grads N(0, 1e-4), fp32 m and v, a bf16 working copy out, AdamW lr 3e-4,
+betas 0.9/0.95, eps 1e-8, weight decay 0.1, global-norm clip 1.0 -- i.e.
+the deterministic grad-norm launch plus the fused clip + AdamW launch.
+`value` is params/s of the whole timed step.  The fp8 boundary codec is
+timed beside it on C1's activation [8, 2048, 2560] (e4m3) and gradient
+(e5m2), per-row scaling, rotating through enough copies that no launch
+reads from the 256 MB MALL.
+
+Prints one JSON line (rank 0):
+  roofline      -- the fused AdamW kernel: algorithmic bytes per launch
+                   (28 B/elem: read p, g(bf16), m, v; write p, m, v, copy)
+                   over its average duration from HIP events on its stream;
+  cpu_baseline  -- the oracle's HostAdamW arithmetic (oracle/ely_oracle.c,
+                   one thread) timed on this host on a bounded prefix of the
+                   same shard.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, HERE)
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+D_MODEL, N_BLOCKS = 2560, 16
+LR, BETAS, EPS, WD, MAX_NORM = 3e-4, (0.9, 0.95), 1e-8, 0.1, 1.0
+ADAM_BYTES_PER_ELEM = 28  # bf16 grads, bf16 copy out
+NORM_BYTES_PER_ELEM = 2
+CODEC_BYTES_PER_ELEM = 3  # bf16 in / fp8 out (quantize); fp8 in / bf16 out (dequantize)
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def block_shapes(d: int):
+    return [(d,), (d,), (3 * d, d), (3 * d,), (d, d), (d,), (d,), (d,), (4 * d, d), (4 * d,), (d, 4 * d), (d,)]
+
+
+def make_shard(device):
+    """C1's shard: params N(0, 0.02) fp32, grads N(0, 1e-4) bf16, generated on
+    the device (seeded)."""
+    gen = torch.Generator(device=device).manual_seed(1234)
+    shapes = block_shapes(D_MODEL) * N_BLOCKS
+    params, grads = [], []
+    for s in shapes:
+        p = torch.empty(s, dtype=torch.float32, device=device)
+        p.normal_(0.0, 0.02, generator=gen)
+        g = torch.empty(s, dtype=torch.float32, device=device)
+        g.normal_(0.0, 1e-4, generator=gen)
+        params.append(p.requires_grad_(True))
+        grads.append(g.to(torch.bfloat16))
+        del g
+    return params, grads
+
+
+def time_events(fn, iters, stream):
+    """Average duration (ms) of fn() over iters launches, HIP events on `stream`."""
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
+    for i in range(iters):
+        starts[i].record(stream)
+        fn(i)
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    return sum(s.elapsed_time(e) for s, e in zip(starts, ends)) / iters
+
+
+def bench_optimizer(args, device, stream):
+    from elysium_wan_amd import _lib, optim
+
+    params, grads = make_shard(device)
+    n_elem = sum(p.numel() for p in params)
+    log(f"C1 shard: {len(params)} tensors, {n_elem} elements")
+    opt = optim.FusedAdamW(params, lr=LR, betas=BETAS, eps=EPS, weight_decay=WD, order="host", max_norm=MAX_NORM, working_copy=True)
+    for _ in range(args.warmup):
+        opt.step(grads=grads)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        opt.step(grads=grads)
+    torch.cuda.synchronize()
+    step_s = (time.perf_counter() - t0) / args.steps
+
+    # Per-kernel durations: the same two launches through the C ABI, with HIP
+    # events on the launch stream between them.
+    L = _lib.load()
+    sptr = _lib.stream_ptr(device)
+    garr = _lib.tensor_array(grads)
+    nws = _lib.workspace(device, L.ely_grad_norm_workspace_bytes(garr, len(grads)))
+    res = torch.zeros(16, dtype=torch.uint8, device=device)
+    n = len(params)
+    parr = _lib.tensor_array(params)
+    marr = _lib.tensor_array([opt.state[i]["exp_avg"] for i in range(n)])
+    varr = _lib.tensor_array([opt.state[i]["exp_avg_sq"] for i in range(n)])
+    carr = _lib.tensor_array(opt.working_copies)
+    consts = (_lib.ElyConsts * n)()
+    base_step = float(opt.state[0]["step"])
+    aws = torch.empty(L.ely_adamw_workspace_bytes(n), dtype=torch.uint8, device=device)
+
+    def norm(_):
+        _lib.check(L.ely_grad_norm(garr, n, MAX_NORM, res.data_ptr(), nws.data_ptr(), nws.numel(), sptr), "norm")
+
+    iters = max(args.steps, 5)
+    per_step = [optim.host_consts(LR, BETAS, EPS, WD, base_step + 1 + i) for i in range(iters)]
+
+    def adam(i):
+        for j in range(n):
+            consts[j].c[:] = per_step[i]
+        _lib.check(L.ely_adamw_step(parr, garr, marr, varr, carr, n, consts, _lib.ORDER_HOST, 1, res.data_ptr() + 12, aws.data_ptr(), aws.numel(), sptr), "adamw")
+
+    norm_ms = time_events(norm, iters, stream)
+    adam_ms = time_events(adam, iters, stream)
+    return {
+        "n_elem": n_elem,
+        "step_s": step_s,
+        "norm_ms": norm_ms,
+        "adam_ms": adam_ms,
+        "grad_norm": float(opt.grad_norm()),
+    }
+
+
+def bench_codec(device, stream, iters=20):
+    from elysium_wan_amd import _lib
+
+    L = _lib.load()
+    sptr = _lib.stream_ptr(device)
+    rows, cols = 8 * 2048, D_MODEL
+    n = rows * cols
+    copies = 8  # 8 x 84 MB inputs + outputs: every launch reads HBM, not the MALL
+    gen = torch.Generator(device=device).manual_seed(7)
+    xs, qs, ks, outs = [], [], [], []
+    for i in range(copies):
+        x = torch.empty(rows, cols, device=device)
+        x.normal_(generator=gen)
+        mask = torch.rand(rows, cols, device=device, generator=gen) < 1e-3
+        x = torch.where(mask, x * 50.0, x).to(torch.bfloat16)
+        xs.append(x)
+        qs.append(torch.empty(rows, cols, dtype=torch.uint8, device=device))
+        ks.append(torch.empty(rows, dtype=torch.int32, device=device))
+        outs.append(torch.empty(rows, cols, dtype=torch.bfloat16, device=device))
+    ws = _lib.workspace(device, L.ely_fp8_workspace_bytes(rows, cols, _lib.BF16))
+    out = {}
+    for fmt in ("e4m3", "e5m2"):
+        f = _lib.FMT[fmt]
+
+        def quant(i, f=f):
+            j = i % copies
+            _lib.check(L.ely_fp8_quantize(xs[j].data_ptr(), _lib.BF16, rows, cols, f, qs[j].data_ptr(), ks[j].data_ptr(), ws.data_ptr(), ws.numel(), sptr), "q")
+
+        def deq(i, f=f):
+            j = i % copies
+            _lib.check(L.ely_fp8_dequantize(qs[j].data_ptr(), ks[j].data_ptr(), rows, cols, f, outs[j].data_ptr(), _lib.BF16, sptr), "dq")
+
+        for i in range(copies):
+            quant(i)
+        q_ms = time_events(quant, iters, stream)
+        d_ms = time_events(deq, iters, stream)
+        out[fmt] = {
+            "quantize_ms": q_ms,
+            "quantize_GBs": n * CODEC_BYTES_PER_ELEM / q_ms / 1e6,
+            "dequantize_ms": d_ms,
+            "dequantize_GBs": n * CODEC_BYTES_PER_ELEM / d_ms / 1e6,
+        }
+    return out
+
+
+def cpu_baseline(sample_elems: int, steps: int = 2):
+    """The oracle's HostAdamW (one thread of C) over a prefix of C1's shard."""
+    from oracle import oracle as O
+
+    rng = np.random.default_rng(0)
+    block = 1 << 22
+    reps = -(-sample_elems // block)
+    p = np.tile((rng.standard_normal(block) * 0.02).astype(np.float32), reps)[:sample_elems]
+    g = np.tile(O.f32_to_bf16_bits((rng.standard_normal(block) * 1e-4).astype(np.float32)), reps)[:sample_elems]
+    m = np.zeros(sample_elems, np.float32)
+    v = np.zeros(sample_elems, np.float32)
+    cp = np.zeros(sample_elems, np.uint16)
+    t0 = time.perf_counter()
+    for s in range(steps):
+        O.adamw_host(p, g, m, v, O.host_adamw_consts(LR, BETAS, EPS, WD, s + 1), True, 1.0, cp)
+    dt = time.perf_counter() - t0
+    return sample_elems * steps / dt, dt
+
+
+def read_traffic():
+    """HBM bytes per AdamW launch measured by rocprofv3 --pmc (FETCH_SIZE +
+    WRITE_SIZE, scaled by a plain copy's reading), if that profile is
+    committed; otherwise None."""
+    path = os.path.join(HERE, "profiles", "adamw_c1_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("traffic_bytes_per_launch")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-codec", action="store_true", help="skip the fp8 codec leg")
+    ap.add_argument("--cpu-sample", type=int, default=256 * 1024 * 1024)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    stream = torch.cuda.Stream(device)
+    with torch.cuda.stream(stream):
+        log("optimizer leg")
+        o = bench_optimizer(args, device, stream)
+        codec = None
+        if not args.no_codec:
+            log("codec leg")
+            codec = bench_codec(device, stream)
+    n = o["n_elem"]
+    adam_bytes = n * ADAM_BYTES_PER_ELEM
+    achieved = adam_bytes / (o["adam_ms"] * 1e-3) / 1e9
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline leg")
+        rate, secs = cpu_baseline(args.cpu_sample)
+        cpu = {
+            "value": rate,
+            "unit": "params/s",
+            "cores": 1,
+            "kind": "port",
+            "sample": f"oracle HostAdamW (C, 1 thread) over a {args.cpu_sample}-element prefix of the C1 shard, 2 steps, bf16 grads + bf16 copy ({secs:.1f} s)",
+        }
+    result = {
+        "metric": "fused AdamW params/s & GB/s (% HBM peak); fp8 codec GB/s; 2.8B stage",
+        "value": n / o["step_s"],
+        "unit": "params/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": o["step_s"] * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic",
+        "config": {
+            "workload": "C1: 2.8B model, stage 1 of 2 -- 16 GPT blocks d=2560, 192 tensors, 1,258,823,680 fp32 params, bf16 grads, bf16 working copy, AdamW + global-norm clip 1.0",
+            "n_params": n,
+            "tensors": 192,
+            "optimizer": "adamw-host op order (bit-exact), fused clip",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS,
+            "traffic": read_traffic(),
+        },
+        "cpu_baseline": cpu,
+        "kernels": {
+            "adamw_ms": o["adam_ms"],
+            "adamw_GBs": achieved,
+            "adamw_params_per_s": n / (o["adam_ms"] * 1e-3),
+            "grad_norm_ms": o["norm_ms"],
+            "grad_norm_GBs": n * NORM_BYTES_PER_ELEM / (o["norm_ms"] * 1e-3) / 1e9,
+            "step_GBs": n * (ADAM_BYTES_PER_ELEM + NORM_BYTES_PER_ELEM) / o["step_s"] / 1e9,
+        },
+        "fp8_codec": codec,
+        "grad_norm": o["grad_norm"],
+    }
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

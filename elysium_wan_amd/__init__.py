@@ -1,0 +1,16 @@
+"""elysium_wan_amd -- the per-stage mixed-precision update path of
+elysium-wan (wantrain) as MI355X-native HIP kernels behind wantrain's own
+Python signatures.
+
+Modules mirror the reference's:
+  optim   -- runtime/optim.py   (build, hparams, state_bytes_per_param, the
+             fused clip + AdamW + bf16 working copy, clip_grad_norm_)
+  fp8     -- model/fp8.py       (scale_exp, quantize, dequantize, roundtrip)
+  pieces  -- runtime/pieces.py  (cast_piece, fold_start, fold_add, fold)
+The kernels live in libelyhip.so (C ABI: include/ely.h), built by
+elysium_wan_amd.build for gfx950.
+"""
+
+from . import fp8, optim, pieces  # noqa: F401
+
+__all__ = ["fp8", "optim", "pieces"]

@@ -1,0 +1,618 @@
+// fp8.hip -- the fp8 boundary codec of model/fp8.py on gfx950.
+//
+// quantize (fp8.py:28-49): per row, k = frexp(amax|x|).exponent - ebias and
+// q = fp8(x * 2^-k).  Three launch shapes:
+//   * rows that fit a wavefront's registers (<= 64 lanes x 16 vectors of
+//     16 bytes: 8192 bf16 / 4096 fp32 columns, 16-byte aligned): one wave per
+//     row, the row is read once into VGPRs, |x|max is a butterfly over the
+//     wave, and codes are written from the same registers: one HBM read and
+//     one write per element (3 B/elem for bf16 -> fp8).
+//   * longer rows (per-tensor scaling is rows = 1): the row is cut into
+//     2048-element segments, one wave each; a first launch folds each
+//     segment's |x|max into the row's slot with an integer atomicMax (order
+//     free, so deterministic), a second converts.  Two reads of x.
+//   * any other shape (unaligned, columns not a multiple of the vector):
+//     the same two launches with element-wise loads.
+// Every row whose exponent keeps 2^-k, 2^k and every product exact
+// (|k| <= 110, finite |x|max) converts with v_cvt_pk_fp8_f32 /
+// v_cvt_pk_bf8_f32 (proved equal to torch's rounding on that domain by
+// ely_selftest_fp8_cvt); the other rows follow the bit-level restatement of
+// torch's arithmetic (pow2 rounded to the dtype, product rounded to the
+// dtype, software conversion), uniformly per row.
+//
+// dequantize (fp8.py:52-53): out = float(q) * 2^k in the output dtype,
+// 16 codes per lane per step; roundtrip (fp8.py:56-63) fuses both.
+#include <algorithm>
+
+#include "ely_device.hpp"
+#include "ely_host.hpp"
+
+#pragma clang fp contract(off)
+
+namespace ely {
+
+constexpr int kQBlock = 256;                   // 4 waves, one row (or segment) each
+constexpr int kWavesPerBlock = kQBlock / kWave;
+constexpr int64_t kSegElems = 2048;            // split-path segment, elements
+constexpr int64_t kDeqSegCodes = 4096;         // dequantize segment, codes
+constexpr int kFastK = 110;                    // |k| bound of the instruction path
+
+// ----------------------------------------------------------- element helpers
+
+template <bool BF16>
+__device__ __forceinline__ float load_x(const void* x, int64_t i) {
+    if (BF16) return bf16_to_f32(static_cast<const uint16_t*>(x)[i]);
+    return static_cast<const float*>(x)[i];
+}
+
+__device__ __forceinline__ float round_to(float v, bool bf16) { return bf16 ? bf16_to_f32(f32_to_bf16(v)) : v; }
+
+// Exact-arithmetic (slow-path) quantize of one element: fp8.py:49.
+template <int FMT, bool BF16>
+__device__ __forceinline__ uint32_t quant_sw(float xv, float s_down) {
+    return fp8_from_f32_sw<FMT>(round_to(xv * s_down, BF16));
+}
+
+// Exact-arithmetic (slow-path) dequantize of one code: fp8.py:53.
+template <int FMT, bool BF16OUT>
+__device__ __forceinline__ float dequant_sw(uint32_t c, float s_up) {
+    float v = round_to(fp8_to_f32_sw<FMT>(c), BF16OUT);
+    return round_to(v * s_up, BF16OUT);
+}
+
+// A dequantized value from the instruction path as its output dtype's bits.
+// In that path the value is exact in bf16, so truncation is the rounding.
+__device__ __forceinline__ uint32_t fast_bf16_bits(float v) { return __float_as_uint(v) >> 16; }
+
+struct RowScale {
+    int k;
+    bool fast;
+    float s_down;   // 2^-k in the input dtype
+    float s_up;     // 2^k in the output dtype
+};
+
+template <int FMT>
+__device__ __forceinline__ RowScale row_scale(uint32_t abits, bool bf16_in, bool bf16_out) {
+    RowScale r;
+    r.k = scale_exp_from_amax<FMT>(abits);
+    r.fast = abits < 0x7F800000u && r.k >= -kFastK && r.k <= kFastK;
+    if (r.fast) {
+        r.s_down = __uint_as_float((uint32_t)(127 - r.k) << 23);
+        r.s_up = __uint_as_float((uint32_t)(127 + r.k) << 23);
+    } else {
+        r.s_down = pow2_dtype(-r.k, bf16_in);
+        r.s_up = pow2_dtype(r.k, bf16_out);
+    }
+    return r;
+}
+
+// |x| bits of 8 bf16 packed in a uint4 / 4 fp32 in a uint4, maxed into m.
+template <bool BF16>
+__device__ __forceinline__ uint32_t vec_absmax(const uint4& w, uint32_t m) {
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        if (BF16) {
+            const uint32_t lo = ws[j] & 0x7FFFu, hi = (ws[j] >> 16) & 0x7FFFu;
+            m = max(m, max(lo, hi));
+        } else {
+            m = max(m, ws[j] & 0x7FFFFFFFu);
+        }
+    }
+    return m;
+}
+
+template <bool BF16>
+__device__ __forceinline__ uint32_t to_f32_bits(uint32_t amax) {
+    return BF16 ? amax << 16 : amax;
+}
+
+// Unpack a uint4 into 8 (bf16) or 4 (fp32) floats.
+template <bool BF16>
+__device__ __forceinline__ void unpack(const uint4& w, float* f) {
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        if (BF16) {
+            f[2 * j] = bf16_to_f32(ws[j] & 0xFFFFu);
+            f[2 * j + 1] = bf16_to_f32(ws[j] >> 16);
+        } else {
+            f[j] = __uint_as_float(ws[j]);
+        }
+    }
+}
+
+// Quantize one 16-byte input vector (8 bf16 or 4 fp32) into codes packed in
+// words[0..1] (bf16: 8 codes) or words[0] (fp32: 4 codes); with `out`,
+// also write the dequantized values in the input dtype at out_vec.
+template <int FMT, bool BF16>
+__device__ __forceinline__ void quant_vec(const uint4& w, const RowScale& rs, uint32_t* words, void* out_vec) {
+    constexpr int EPV = BF16 ? 8 : 4;
+    float f[EPV];
+    unpack<BF16>(w, f);
+    uint32_t codes[EPV];
+    if (rs.fast) {
+#pragma unroll
+        for (int j = 0; j < EPV; j += 4) {
+            uint32_t pk = cvt_pk_fp8<FMT, false>(f[j] * rs.s_down, f[j + 1] * rs.s_down, 0u);
+            pk = cvt_pk_fp8<FMT, true>(f[j + 2] * rs.s_down, f[j + 3] * rs.s_down, pk);
+            words[j / 4] = pk;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < EPV; ++j) codes[j] = quant_sw<FMT, BF16>(f[j], rs.s_down);
+#pragma unroll
+        for (int j = 0; j < EPV; j += 4)
+            words[j / 4] = codes[j] | (codes[j + 1] << 8) | (codes[j + 2] << 16) | (codes[j + 3] << 24);
+    }
+    if (out_vec) {
+        float o[EPV];
+        if (rs.fast) {
+#pragma unroll
+            for (int j = 0; j < EPV; j += 4) {
+                float a, b, c, d;
+                cvt_pk_f32<FMT, false>(words[j / 4], a, b);
+                cvt_pk_f32<FMT, true>(words[j / 4], c, d);
+                o[j] = a * rs.s_up;
+                o[j + 1] = b * rs.s_up;
+                o[j + 2] = c * rs.s_up;
+                o[j + 3] = d * rs.s_up;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < EPV; ++j) o[j] = dequant_sw<FMT, BF16>((words[j / 4] >> (8 * (j % 4))) & 0xFFu, rs.s_up);
+        }
+        uint4 r;
+        if (BF16) {
+            uint32_t b[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) b[j] = rs.fast ? fast_bf16_bits(o[j]) : f32_to_bf16(o[j]);
+            r = make_uint4(b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16), b[6] | (b[7] << 16));
+        } else {
+            r = make_uint4(__float_as_uint(o[0]), __float_as_uint(o[1]), __float_as_uint(o[2]),
+                           __float_as_uint(o[3]));
+        }
+        *static_cast<uint4*>(out_vec) = r;
+    }
+}
+
+// ------------------------------------------------- wave-per-row (registers)
+
+template <int FMT, bool BF16, int VPL>
+__global__ __launch_bounds__(kQBlock) void quant_rows_kernel(const void* __restrict__ x, int64_t rows, int64_t cols,
+                                                             uint8_t* __restrict__ q, int32_t* __restrict__ k,
+                                                             void* __restrict__ out) {
+    constexpr int EPV = BF16 ? 8 : 4;
+    constexpr int ESZ = BF16 ? 2 : 4;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + wave_uniform(threadIdx.x / kWave);
+    if (row >= rows) return;  // whole waves leave; the kernel has no block barrier
+    const int64_t nvec = cols / EPV;
+    const uint4* xr = reinterpret_cast<const uint4*>(static_cast<const char*>(x) + row * cols * ESZ);
+    uint4 buf[VPL];
+    uint32_t amax = 0;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+        const int64_t vi = lane + (int64_t)kWave * j;
+        buf[j] = vi < nvec ? xr[vi] : make_uint4(0u, 0u, 0u, 0u);
+        amax = vec_absmax<BF16>(buf[j], amax);
+    }
+    amax = wave_max_u32(amax);
+    const RowScale rs = row_scale<FMT>(to_f32_bits<BF16>(amax), BF16, BF16);
+    if (lane == 0 && k) k[row] = rs.k;
+    uint8_t* qr = q ? q + row * cols : nullptr;
+    char* orow = out ? static_cast<char*>(out) + row * cols * ESZ : nullptr;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+        const int64_t vi = lane + (int64_t)kWave * j;
+        if (vi < nvec) {
+            uint32_t words[2];
+            quant_vec<FMT, BF16>(buf[j], rs, words, orow ? orow + vi * 16 : nullptr);
+            if (qr) {
+                if (BF16) *reinterpret_cast<uint2*>(qr + vi * 8) = make_uint2(words[0], words[1]);
+                else *reinterpret_cast<uint32_t*>(qr + vi * 4) = words[0];
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------- split long rows
+
+__global__ void fill_u32_kernel(uint32_t* p, int64_t n, uint32_t value) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = value;
+}
+
+// |x|max of each 2048-element segment, folded into rowmax[row] (fp32 bits of
+// |x|max for fp32 input, bf16 bits for bf16 input).
+template <bool BF16>
+__global__ __launch_bounds__(kQBlock) void rowmax_split_kernel(const void* __restrict__ x, int64_t rows, int64_t cols,
+                                                               int64_t segs, int vec, uint32_t* __restrict__ rowmax) {
+    constexpr int EPV = BF16 ? 8 : 4;
+    constexpr int ESZ = BF16 ? 2 : 4;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t gw = (int64_t)blockIdx.x * kWavesPerBlock + wave_uniform(threadIdx.x / kWave);
+    const int64_t row = gw / segs, seg = gw % segs;
+    if (row >= rows) return;
+    const int64_t e0 = seg * kSegElems, e1 = min(e0 + kSegElems, cols);
+    uint32_t amax = 0;
+    if (vec) {
+        const uint4* xr = reinterpret_cast<const uint4*>(static_cast<const char*>(x) + (row * cols + e0) * ESZ);
+        const int64_t nv = (e1 - e0) / EPV;
+        for (int64_t vi = lane; vi < nv; vi += kWave) amax = vec_absmax<BF16>(xr[vi], amax);
+    } else {
+        for (int64_t e = e0 + lane; e < e1; e += kWave) {
+            uint32_t b = BF16 ? (uint32_t)static_cast<const uint16_t*>(x)[row * cols + e] & 0x7FFFu
+                              : __float_as_uint(static_cast<const float*>(x)[row * cols + e]) & 0x7FFFFFFFu;
+            amax = max(amax, b);
+        }
+    }
+    amax = wave_max_u32(amax);
+    if (lane == 0) atomicMax(rowmax + row, amax);
+}
+
+template <int FMT, bool BF16>
+__global__ __launch_bounds__(kQBlock) void quant_split_kernel(const void* __restrict__ x, int64_t rows, int64_t cols,
+                                                              int64_t segs, int vec,
+                                                              const uint32_t* __restrict__ rowmax,
+                                                              uint8_t* __restrict__ q, int32_t* __restrict__ k,
+                                                              void* __restrict__ out) {
+    constexpr int EPV = BF16 ? 8 : 4;
+    constexpr int ESZ = BF16 ? 2 : 4;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t gw = (int64_t)blockIdx.x * kWavesPerBlock + wave_uniform(threadIdx.x / kWave);
+    const int64_t row = gw / segs, seg = gw % segs;
+    if (row >= rows) return;
+    const RowScale rs = row_scale<FMT>(to_f32_bits<BF16>(rowmax[row]), BF16, BF16);
+    if (seg == 0 && lane == 0 && k) k[row] = rs.k;
+    const int64_t e0 = seg * kSegElems, e1 = min(e0 + kSegElems, cols);
+    const int64_t base = row * cols;
+    if (vec) {
+        const uint4* xr = reinterpret_cast<const uint4*>(static_cast<const char*>(x) + (base + e0) * ESZ);
+        const int64_t nv = (e1 - e0) / EPV;
+        for (int64_t vi = lane; vi < nv; vi += kWave) {
+            uint32_t words[2];
+            const int64_t e = e0 + vi * EPV;
+            quant_vec<FMT, BF16>(xr[vi], rs, words, out ? static_cast<char*>(out) + (base + e) * ESZ : nullptr);
+            if (q) {
+                if (BF16) *reinterpret_cast<uint2*>(q + base + e) = make_uint2(words[0], words[1]);
+                else *reinterpret_cast<uint32_t*>(q + base + e) = words[0];
+            }
+        }
+    } else {
+        for (int64_t e = e0 + lane; e < e1; e += kWave) {
+            const float xv = load_x<BF16>(x, base + e);
+            const uint32_t c = quant_sw<FMT, BF16>(xv, rs.s_down);
+            if (q) q[base + e] = (uint8_t)c;
+            if (out) {
+                const float o = dequant_sw<FMT, BF16>(c, rs.s_up);
+                if (BF16) static_cast<uint16_t*>(out)[base + e] = (uint16_t)f32_to_bf16(o);
+                else static_cast<float*>(out)[base + e] = o;
+            }
+        }
+    }
+}
+
+// -------------------------------------------------------------- dequantize
+
+template <int FMT, bool BF16OUT>
+__global__ __launch_bounds__(kQBlock) void dequant_kernel(const uint8_t* __restrict__ q, const int32_t* __restrict__ k,
+                                                          int64_t rows, int64_t cols, int64_t segs, int vec,
+                                                          void* __restrict__ out) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t gw = (int64_t)blockIdx.x * kWavesPerBlock + wave_uniform(threadIdx.x / kWave);
+    const int64_t row = gw / segs, seg = gw % segs;
+    if (row >= rows) return;
+    const int kk = k[row];
+    const bool fast = kk >= -kFastK && kk <= kFastK;
+    const float s_up = fast ? __uint_as_float((uint32_t)(127 + kk) << 23) : pow2_dtype(kk, BF16OUT);
+    const int64_t e0 = seg * kDeqSegCodes, e1 = min(e0 + kDeqSegCodes, cols);
+    const int64_t base = row * cols;
+    if (vec) {
+        const uint4* qr = reinterpret_cast<const uint4*>(q + base + e0);
+        const int64_t nv = (e1 - e0) / 16;
+        for (int64_t vi = lane; vi < nv; vi += kWave) {
+            const uint4 w = qr[vi];
+            const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+            float o[16];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if (fast) {
+                    float a, b, c, d;
+                    cvt_pk_f32<FMT, false>(ws[j], a, b);
+                    cvt_pk_f32<FMT, true>(ws[j], c, d);
+                    o[4 * j] = a * s_up;
+                    o[4 * j + 1] = b * s_up;
+                    o[4 * j + 2] = c * s_up;
+                    o[4 * j + 3] = d * s_up;
+                } else {
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) o[4 * j + t] = dequant_sw<FMT, BF16OUT>((ws[j] >> (8 * t)) & 0xFFu, s_up);
+                }
+            }
+            const int64_t e = e0 + vi * 16;
+            if (BF16OUT) {
+                uint32_t b[16];
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    // an fp8 NaN is the only non-exact value the instruction path sees
+                    const float v = o[j];
+                    b[j] = fast ? (v != v ? 0x7FC0u : fast_bf16_bits(v)) : f32_to_bf16(v);
+                }
+                uint4* op = reinterpret_cast<uint4*>(static_cast<uint16_t*>(out) + base + e);
+                op[0] = make_uint4(b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16), b[6] | (b[7] << 16));
+                op[1] = make_uint4(b[8] | (b[9] << 16), b[10] | (b[11] << 16), b[12] | (b[13] << 16),
+                                   b[14] | (b[15] << 16));
+            } else {
+                float4* op = reinterpret_cast<float4*>(static_cast<float*>(out) + base + e);
+                op[0] = make_float4(o[0], o[1], o[2], o[3]);
+                op[1] = make_float4(o[4], o[5], o[6], o[7]);
+                op[2] = make_float4(o[8], o[9], o[10], o[11]);
+                op[3] = make_float4(o[12], o[13], o[14], o[15]);
+            }
+        }
+    } else {
+        for (int64_t e = e0 + lane; e < e1; e += kWave) {
+            const float o = dequant_sw<FMT, BF16OUT>(q[base + e], s_up);
+            if (BF16OUT) static_cast<uint16_t*>(out)[base + e] = (uint16_t)f32_to_bf16(o);
+            else static_cast<float*>(out)[base + e] = o;
+        }
+    }
+}
+
+// --------------------------------------------------------------- self-test
+
+template <int FMT>
+__global__ void selftest_cvt_kernel(uint32_t start, uint64_t count, unsigned long long* mism) {
+    using F = Fp8Fmt<FMT>;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        const uint32_t u = (uint32_t)(start + i);
+        const float x = __uint_as_float(u);
+        const uint32_t sw = fp8_from_f32_sw<FMT>(x);
+        const uint32_t lo = cvt_pk_fp8<FMT, false>(x, 0.0f, 0u);
+        const uint32_t hi = cvt_pk_fp8<FMT, true>(0.0f, x, 0u);
+        const uint32_t hw0 = lo & 0xFFu, hw1 = (hi >> 24) & 0xFFu;
+        const bool domain = (u & 0x7FFFFFFFu) <= F::kMaxFiniteBits;
+        if (hw0 != sw || hw1 != sw) atomicAdd(mism + (domain ? 0 : 1), 1ull);
+        if (u - start < 256u && start == 0u) {
+            // decode: every code, instruction vs restatement, both halves of the word
+            const uint32_t c = u;
+            float a, b, c2, d;
+            cvt_pk_f32<FMT, false>(c | (c << 8), a, b);
+            cvt_pk_f32<FMT, true>((c << 16) | (c << 24), c2, d);
+            const float ref = fp8_to_f32_sw<FMT>(c);
+            const float got[4] = {a, b, c2, d};
+            bool bad = false;
+            for (int j = 0; j < 4; ++j) {
+                if (ref != ref) bad |= got[j] == got[j];
+                else bad |= __float_as_uint(got[j]) != __float_as_uint(ref);
+            }
+            if (bad) atomicAdd(mism + 2, 1ull);
+        }
+    }
+}
+
+__global__ void selftest_sqrt_kernel(uint32_t start, uint64_t count, unsigned long long* mism) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        const uint32_t u = (uint32_t)(start + i) & 0x7FFFFFFFu;  // non-negative patterns
+        const float x = __uint_as_float(u);
+        const float a = __builtin_sqrtf(x);
+        const float b = (float)__builtin_sqrt((double)x);
+        if (__float_as_uint(a) != __float_as_uint(b) && !(a != a && b != b)) atomicAdd(mism, 1ull);
+    }
+}
+
+// ------------------------------------------------------------------ launch
+
+static void check_fmt(int32_t fmt) {
+    if (fmt != ELY_E4M3 && fmt != ELY_E5M2) fail(ELY_EINVAL, "fp8 format must be ELY_E4M3 or ELY_E5M2");
+}
+
+static void check_dtype(int32_t dt, const char* what) {
+    if (dt != ELY_F32 && dt != ELY_BF16) fail(ELY_EINVAL, std::string(what) + " must be ELY_F32 or ELY_BF16");
+}
+
+static void check_shape(int64_t rows, int64_t cols) {
+    if (rows < 0 || cols < 0) fail(ELY_EINVAL, "negative rows or cols");
+    if (cols > 0 && rows > INT64_MAX / cols) fail(ELY_EINVAL, "rows * cols overflows");
+}
+
+static unsigned blocks_for_waves(int64_t waves) {
+    const int64_t b = (waves + kWavesPerBlock - 1) / kWavesPerBlock;
+    if (b > 0x7FFFFFFF) fail(ELY_EINVAL, "grid too large");
+    return (unsigned)b;
+}
+
+constexpr int kVplChoices[] = {1, 2, 3, 4, 5, 6, 8, 10, 12, 16};
+
+template <int FMT, bool BF16, int VPL>
+static void launch_rows(const void* x, int64_t rows, int64_t cols, uint8_t* q, int32_t* k, void* out, hipStream_t s) {
+    hipLaunchKernelGGL((quant_rows_kernel<FMT, BF16, VPL>), dim3(blocks_for_waves(rows)), dim3(kQBlock), 0, s, x,
+                       rows, cols, q, k, out);
+    check_launch("quant_rows_kernel");
+}
+
+template <int FMT, bool BF16>
+static void dispatch_rows(int vpl, const void* x, int64_t rows, int64_t cols, uint8_t* q, int32_t* k, void* out,
+                          hipStream_t s) {
+    switch (vpl) {
+        case 1: return launch_rows<FMT, BF16, 1>(x, rows, cols, q, k, out, s);
+        case 2: return launch_rows<FMT, BF16, 2>(x, rows, cols, q, k, out, s);
+        case 3: return launch_rows<FMT, BF16, 3>(x, rows, cols, q, k, out, s);
+        case 4: return launch_rows<FMT, BF16, 4>(x, rows, cols, q, k, out, s);
+        case 5: return launch_rows<FMT, BF16, 5>(x, rows, cols, q, k, out, s);
+        case 6: return launch_rows<FMT, BF16, 6>(x, rows, cols, q, k, out, s);
+        case 8: return launch_rows<FMT, BF16, 8>(x, rows, cols, q, k, out, s);
+        case 10: return launch_rows<FMT, BF16, 10>(x, rows, cols, q, k, out, s);
+        case 12: return launch_rows<FMT, BF16, 12>(x, rows, cols, q, k, out, s);
+        case 16: return launch_rows<FMT, BF16, 16>(x, rows, cols, q, k, out, s);
+        default: fail(ELY_EINVAL, "internal: no register path for this row length");
+    }
+}
+
+// Register path's vectors per lane for these columns, or 0 when the row does
+// not fit it.
+static int rows_vpl(int64_t cols, int32_t dtype, const void* x, const uint8_t* q, const void* out) {
+    const int64_t epv = dtype == ELY_BF16 ? 8 : 4;
+    if (cols == 0 || cols % epv != 0) return 0;
+    if (!aligned16(x) || (out && !aligned16(out))) return 0;
+    if (q && (reinterpret_cast<uintptr_t>(q) % (uintptr_t)epv) != 0) return 0;
+    const int64_t nvec = cols / epv;
+    for (int v : kVplChoices)
+        if (nvec <= (int64_t)kWave * v) return v;
+    return 0;
+}
+
+static size_t split_ws_bytes(int64_t rows) { return align_up((size_t)std::max<int64_t>(rows, 1) * 4, 256); }
+
+template <int FMT, bool BF16>
+static void quantize_impl(const void* x, int64_t rows, int64_t cols, uint8_t* q, int32_t* k, void* out,
+                          void* workspace, int64_t ws_bytes, hipStream_t s) {
+    if (rows == 0) return;
+    if (cols == 0) {
+        // an empty row has |x|max 0, so k = 0 (fp8.py:38)
+        if (k) {
+            hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)std::min<int64_t>((rows + 255) / 256, 4096)), dim3(256),
+                               0, s, reinterpret_cast<uint32_t*>(k), rows, 0u);
+            check_launch("fill_u32_kernel");
+        }
+        return;
+    }
+    const int32_t dt = BF16 ? ELY_BF16 : ELY_F32;
+    const int vpl = rows_vpl(cols, dt, x, q, out);
+    if (vpl) return dispatch_rows<FMT, BF16>(vpl, x, rows, cols, q, k, out, s);
+    const int64_t epv = BF16 ? 8 : 4;
+    const int vec = (cols % epv == 0) && aligned16(x) && (!out || aligned16(out)) &&
+                    (!q || reinterpret_cast<uintptr_t>(q) % (uintptr_t)epv == 0);
+    if (!workspace || ws_bytes < (int64_t)split_ws_bytes(rows))
+        fail(ELY_EWORKSPACE, "fp8 quantize: this shape needs " + std::to_string(split_ws_bytes(rows)) +
+                                 " workspace bytes (ely_fp8_workspace_bytes)");
+    uint32_t* rowmax = static_cast<uint32_t*>(workspace);
+    const int64_t segs = (cols + kSegElems - 1) / kSegElems;
+    if (rows > INT64_MAX / segs) fail(ELY_EINVAL, "too many segments");
+    hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)std::min<int64_t>((rows + 255) / 256, 4096)), dim3(256), 0,
+                       s, rowmax, rows, 0u);
+    check_launch("fill_u32_kernel");
+    const unsigned blocks = blocks_for_waves(rows * segs);
+    hipLaunchKernelGGL((rowmax_split_kernel<BF16>), dim3(blocks), dim3(kQBlock), 0, s, x, rows, cols, segs, vec,
+                       rowmax);
+    check_launch("rowmax_split_kernel");
+    hipLaunchKernelGGL((quant_split_kernel<FMT, BF16>), dim3(blocks), dim3(kQBlock), 0, s, x, rows, cols, segs, vec,
+                       (const uint32_t*)rowmax, q, k, out);
+    check_launch("quant_split_kernel");
+}
+
+template <int FMT, bool BF16OUT>
+static void dequantize_impl(const uint8_t* q, const int32_t* k, int64_t rows, int64_t cols, void* out,
+                            hipStream_t s) {
+    if (rows == 0 || cols == 0) return;
+    const int vec = (cols % 16 == 0) && aligned16(q) && aligned16(out);
+    const int64_t segs = (cols + kDeqSegCodes - 1) / kDeqSegCodes;
+    if (rows > INT64_MAX / segs) fail(ELY_EINVAL, "too many segments");
+    hipLaunchKernelGGL((dequant_kernel<FMT, BF16OUT>), dim3(blocks_for_waves(rows * segs)), dim3(kQBlock), 0, s, q, k,
+                       rows, cols, segs, vec, out);
+    check_launch("dequant_kernel");
+}
+
+}  // namespace ely
+
+using namespace ely;
+
+extern "C" {
+
+int64_t ely_fp8_workspace_bytes(int64_t rows, int64_t cols, int32_t x_dtype) {
+    (void)cols;
+    (void)x_dtype;
+    if (rows < 0) return -1;
+    return (int64_t)split_ws_bytes(rows);
+}
+
+int ely_fp8_quantize(const void* x, int32_t x_dtype, int64_t rows, int64_t cols, int32_t fmt, uint8_t* q, int32_t* k,
+                     void* workspace, int64_t ws_bytes, void* stream) {
+    return guarded([&] {
+        check_fmt(fmt);
+        check_dtype(x_dtype, "x_dtype");
+        check_shape(rows, cols);
+        if (rows * cols > 0 && !x) fail(ELY_EINVAL, "ely_fp8_quantize: null x");
+        if (rows > 0 && !k) fail(ELY_EINVAL, "ely_fp8_quantize: null k");
+        hipStream_t s = static_cast<hipStream_t>(stream);
+        if (fmt == ELY_E4M3) {
+            if (x_dtype == ELY_BF16) quantize_impl<kE4M3, true>(x, rows, cols, q, k, nullptr, workspace, ws_bytes, s);
+            else quantize_impl<kE4M3, false>(x, rows, cols, q, k, nullptr, workspace, ws_bytes, s);
+        } else {
+            if (x_dtype == ELY_BF16) quantize_impl<kE5M2, true>(x, rows, cols, q, k, nullptr, workspace, ws_bytes, s);
+            else quantize_impl<kE5M2, false>(x, rows, cols, q, k, nullptr, workspace, ws_bytes, s);
+        }
+    });
+}
+
+int ely_fp8_dequantize(const uint8_t* q, const int32_t* k, int64_t rows, int64_t cols, int32_t fmt, void* out,
+                       int32_t out_dtype, void* stream) {
+    return guarded([&] {
+        check_fmt(fmt);
+        check_dtype(out_dtype, "out_dtype");
+        check_shape(rows, cols);
+        if (rows * cols > 0 && (!q || !k || !out)) fail(ELY_EINVAL, "ely_fp8_dequantize: null pointer");
+        hipStream_t s = static_cast<hipStream_t>(stream);
+        if (fmt == ELY_E4M3) {
+            if (out_dtype == ELY_BF16) dequantize_impl<kE4M3, true>(q, k, rows, cols, out, s);
+            else dequantize_impl<kE4M3, false>(q, k, rows, cols, out, s);
+        } else {
+            if (out_dtype == ELY_BF16) dequantize_impl<kE5M2, true>(q, k, rows, cols, out, s);
+            else dequantize_impl<kE5M2, false>(q, k, rows, cols, out, s);
+        }
+    });
+}
+
+int ely_fp8_roundtrip(const void* x, int32_t x_dtype, int64_t rows, int64_t cols, int32_t fmt, void* out, uint8_t* q,
+                      int32_t* k, void* workspace, int64_t ws_bytes, void* stream) {
+    return guarded([&] {
+        check_fmt(fmt);
+        check_dtype(x_dtype, "x_dtype");
+        check_shape(rows, cols);
+        if (rows * cols > 0 && (!x || !out)) fail(ELY_EINVAL, "ely_fp8_roundtrip: null x or out");
+        hipStream_t s = static_cast<hipStream_t>(stream);
+        if (fmt == ELY_E4M3) {
+            if (x_dtype == ELY_BF16) quantize_impl<kE4M3, true>(x, rows, cols, q, k, out, workspace, ws_bytes, s);
+            else quantize_impl<kE4M3, false>(x, rows, cols, q, k, out, workspace, ws_bytes, s);
+        } else {
+            if (x_dtype == ELY_BF16) quantize_impl<kE5M2, true>(x, rows, cols, q, k, out, workspace, ws_bytes, s);
+            else quantize_impl<kE5M2, false>(x, rows, cols, q, k, out, workspace, ws_bytes, s);
+        }
+    });
+}
+
+int ely_selftest_fp8_cvt(uint32_t start, uint64_t count, int32_t fmt, unsigned long long* mismatches_dev,
+                         void* stream) {
+    return guarded([&] {
+        check_fmt(fmt);
+        if (!mismatches_dev) fail(ELY_EINVAL, "null counters");
+        if (count > (1ull << 32) || (uint64_t)start + count > (1ull << 32))
+            fail(ELY_EINVAL, "range beyond the 2^32 fp32 patterns");
+        if (count == 0) return;
+        hipStream_t s = static_cast<hipStream_t>(stream);
+        const unsigned blocks = (unsigned)std::min<uint64_t>((count + 255) / 256, 65536);
+        if (fmt == ELY_E4M3)
+            hipLaunchKernelGGL(selftest_cvt_kernel<kE4M3>, dim3(blocks), dim3(256), 0, s, start, count, mismatches_dev);
+        else
+            hipLaunchKernelGGL(selftest_cvt_kernel<kE5M2>, dim3(blocks), dim3(256), 0, s, start, count, mismatches_dev);
+        check_launch("selftest_cvt_kernel");
+    });
+}
+
+int ely_selftest_sqrt(uint32_t start, uint64_t count, unsigned long long* mismatches_dev, void* stream) {
+    return guarded([&] {
+        if (!mismatches_dev) fail(ELY_EINVAL, "null counter");
+        if (count > (1ull << 32) || (uint64_t)start + count > (1ull << 32))
+            fail(ELY_EINVAL, "range beyond the 2^32 fp32 patterns");
+        if (count == 0) return;
+        hipStream_t s = static_cast<hipStream_t>(stream);
+        const unsigned blocks = (unsigned)std::min<uint64_t>((count + 255) / 256, 65536);
+        hipLaunchKernelGGL(selftest_sqrt_kernel, dim3(blocks), dim3(256), 0, s, start, count, mismatches_dev);
+        check_launch("selftest_sqrt_kernel");
+    });
+}
+
+}  // extern "C"

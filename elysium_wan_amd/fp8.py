@@ -1,0 +1,139 @@
+"""Scaled fp8 boundary quantization on MI355X: the drop-in for wantrain's
+model/fp8.py (same names, arguments, return shapes and errors).
+
+One power-of-two scale per row (last dim): k = frexp(amax|x|).exponent -
+ebias, q = fp8(x * 2^-k), x_hat = float(q) * 2^k, bit for bit what the
+reference's torch ops give (model/fp8.py:28-63).  The work runs in the gfx950
+kernels of libelyhip.so; a row is read once, scaled and converted in
+registers.  Per-tensor scaling is a single row: quantize(x.reshape(1, -1)),
+or per_tensor=True.
+
+Inputs must be CUDA tensors of dtype bfloat16 or float32.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+# fmt -> (torch dtype, e with 2^e above the format's largest finite value);
+# model/fp8.py:17-20.
+FORMATS = {
+    "e4m3": (torch.float8_e4m3fn, 8),
+    "e5m2": (torch.float8_e5m2, 15),
+}
+
+# Candidate offsets of recover_exp, in the order they are tried
+# (model/fp8.py:25).
+_DELTAS = (0, -1, 1, -2, 2)
+
+
+def _fmt(fmt: str) -> int:
+    if fmt not in FORMATS:
+        raise ValueError(f"fp8 format {fmt!r} is not one of {tuple(FORMATS)}")
+    return _lib.FMT[fmt]
+
+
+def _rows(x: torch.Tensor, what: str):
+    _lib.require_gpu(x, what)
+    if x.dim() == 0:
+        raise ValueError(f"{what}: a 0-d tensor has no rows")
+    x = x.detach()
+    if not x.is_contiguous():
+        x = x.contiguous()
+    cols = x.shape[-1]
+    rows = x.numel() // cols if cols else 0
+    return x, rows, cols
+
+
+def _k_shape(x: torch.Tensor):
+    return tuple(x.shape[:-1]) + (1,)
+
+
+def scale_exp(x: torch.Tensor, fmt: str = "e4m3", per_tensor: bool = False) -> torch.Tensor:
+    """Per-row exponent k (int32, shaped like x with the last dim 1) such that
+    x * 2^-k fits the fp8 range; 0 for an all-zero row (model/fp8.py:28-38)."""
+    f = _fmt(fmt)
+    if per_tensor:
+        return scale_exp(x.reshape(1, -1), fmt).reshape((1,) * x.dim())
+    x, rows, cols = _rows(x, "scale_exp")
+    k = torch.empty(_k_shape(x), dtype=torch.int32, device=x.device)
+    L = _lib.load()
+    ws = _lib.workspace(x.device, L.ely_fp8_workspace_bytes(rows, cols, _lib.dtype_code(x)))
+    _lib.check(
+        L.ely_fp8_quantize(x.data_ptr(), _lib.dtype_code(x), rows, cols, f, None, k.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_ptr(x.device)),
+        "scale_exp",
+    )
+    return k
+
+
+def quantize(x: torch.Tensor, fmt: str = "e4m3", per_tensor: bool = False):
+    """x -> (fp8 tensor shaped like x, int32 k shaped like x with the last dim
+    1).  Exact given k (model/fp8.py:45-49)."""
+    f = _fmt(fmt)
+    if per_tensor:
+        q, k = quantize(x.reshape(1, -1), fmt)
+        return q.reshape(x.shape), k.reshape((1,) * x.dim())
+    dt, _ = FORMATS[fmt]
+    x, rows, cols = _rows(x, "quantize")
+    q = torch.empty(x.shape, dtype=dt, device=x.device)
+    k = torch.empty(_k_shape(x), dtype=torch.int32, device=x.device)
+    L = _lib.load()
+    ws = _lib.workspace(x.device, L.ely_fp8_workspace_bytes(rows, cols, _lib.dtype_code(x)))
+    _lib.check(
+        L.ely_fp8_quantize(x.data_ptr(), _lib.dtype_code(x), rows, cols, f, q.data_ptr(), k.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_ptr(x.device)),
+        "quantize",
+    )
+    return q, k
+
+
+def _fmt_of(q: torch.Tensor) -> str:
+    for name, (dt, _) in FORMATS.items():
+        if q.dtype == dt:
+            return name
+    raise ValueError(f"dequantize takes a float8_e4m3fn or float8_e5m2 tensor, got {q.dtype}")
+
+
+def dequantize(q: torch.Tensor, k: torch.Tensor, dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """q.to(dtype) * 2^k, exact (model/fp8.py:52-53).  k holds one exponent
+    per row of q (shape [..., 1], or one element for a per-tensor q)."""
+    fmt = _fmt_of(q)
+    _lib.require_gpu(q, "dequantize")
+    if dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError(f"dequantize writes float32 or bfloat16, got {dtype}")
+    q = q.contiguous()
+    if q.dim() == 0:
+        raise ValueError("dequantize: a 0-d tensor has no rows")
+    k = k.to(device=q.device, dtype=torch.int32).contiguous()
+    cols = q.shape[-1]
+    rows = q.numel() // cols if cols else 0
+    if k.numel() == 1 and rows != 1:
+        # per-tensor exponent: one row of every element
+        rows, cols = 1, q.numel()
+    if k.numel() != rows:
+        raise ValueError(f"dequantize: {k.numel()} exponents for {rows} rows")
+    out = torch.empty(q.shape, dtype=dtype, device=q.device)
+    L = _lib.load()
+    _lib.check(
+        L.ely_fp8_dequantize(q.data_ptr(), k.data_ptr(), rows, cols, _lib.FMT[fmt], out.data_ptr(), _lib.dtype_code(out), _lib.stream_ptr(q.device)),
+        "dequantize",
+    )
+    return out
+
+
+def roundtrip(x: torch.Tensor, fmt: str = "e4m3", per_tensor: bool = False) -> torch.Tensor:
+    """The declared recipe at a boundary: quantize then dequantize, in x's
+    dtype (model/fp8.py:56-63), fused into one pass."""
+    f = _fmt(fmt)
+    if per_tensor:
+        return roundtrip(x.reshape(1, -1), fmt).reshape(x.shape)
+    x, rows, cols = _rows(x, "roundtrip")
+    out = torch.empty_like(x)
+    L = _lib.load()
+    ws = _lib.workspace(x.device, L.ely_fp8_workspace_bytes(rows, cols, _lib.dtype_code(x)))
+    _lib.check(
+        L.ely_fp8_roundtrip(x.data_ptr(), _lib.dtype_code(x), rows, cols, f, out.data_ptr(), None, None, ws.data_ptr(), ws.numel(), _lib.stream_ptr(x.device)),
+        "roundtrip",
+    )
+    return out

@@ -1,0 +1,391 @@
+"""The stage optimizer on MI355X: the drop-in for wantrain's runtime/optim.py.
+
+`build(optimizer, params, lr)` keeps the reference's names and recipes
+(runtime/optim.py:32-69):
+
+* "adamw"      -> FusedAdamW(order="torch"): torch.optim.AdamW's arithmetic
+                  (TORCH/optim/adam.py:554-800), within 1 ulp of it.
+* "adamw-host" -> FusedAdamW(order="host"): HostAdamW's single-rounding op
+                  order (runtime/optim.py:277-298), bit for bit.  The moments
+                  stay in HBM (a 288 GB MI355X holds a stage's fp32
+                  p/m/v/g); checkpoints keep the reference's host layout.
+
+Either way one step is at most two launches over the whole parameter list:
+the deterministic grad-norm (when max_norm is set) and the fused
+clip + AdamW + bf16-working-copy kernel, one HBM pass per element.
+
+The torch.optim surface the runtime uses is kept: step(on_param=None),
+zero_grad, state_dict, load_state_dict (torch's AdamW layout: state[i] =
+{step, exp_avg, exp_avg_sq}, one param group; "moments": "host" for
+adamw-host), param_groups and state.
+"""
+
+from __future__ import annotations
+
+import math
+from collections.abc import Iterable
+
+import numpy as np
+import torch
+
+from . import _lib
+
+OPTIMIZERS = ("adamw", "adamw-host")
+CHUNK = 1 << 24  # the reference's streamed chunk (runtime/optim.py:33); kept for callers that read it
+STATE_BYTES = {"adamw": 16, "adamw-host": 8}
+# runtime/spec.py:27: the AdamW every stage and the reference run.
+ADAMW = {"betas": (0.9, 0.95), "eps": 1e-8, "weight_decay": 0.0}
+_ALIGN = 64  # moment views start on 256-byte boundaries of the flat buffers
+
+
+def state_bytes_per_param(optimizer: str = "adamw") -> int:
+    """runtime/optim.py:39-42: device bytes per trainable element the
+    reference's planner charges for each recipe."""
+    if optimizer not in STATE_BYTES:
+        raise ValueError(f"optimizer {optimizer!r} is not one of {OPTIMIZERS}")
+    return STATE_BYTES[optimizer]
+
+
+def build(optimizer: str, params: Iterable[torch.Tensor], lr: float, **kw):
+    """runtime/optim.py:45-54: the optimizer a stage and the reference
+    construct over their trainable parameters, in order."""
+    if optimizer == "adamw":
+        return FusedAdamW(params, lr=lr, order="torch", **{**ADAMW, **kw})
+    if optimizer == "adamw-host":
+        return FusedAdamW(params, lr=lr, order="host", **{**ADAMW, **kw})
+    raise ValueError(f"optimizer {optimizer!r} is not one of {OPTIMIZERS}")
+
+
+def hparams(lr: float, optimizer: str = "adamw") -> dict:
+    """runtime/optim.py:57-69: the param-group hyperparameters a checkpoint
+    records, read off torch's own AdamW defaults."""
+    probe = torch.optim.AdamW([torch.zeros(1, requires_grad=True)], lr=lr, **ADAMW)
+    group = {k: v for k, v in probe.state_dict()["param_groups"][0].items() if k != "params"}
+    if optimizer == "adamw-host":
+        group["moments"] = "host"
+    elif optimizer != "adamw":
+        raise ValueError(f"optimizer {optimizer!r} is not one of {OPTIMIZERS}")
+    return group
+
+
+def json_norm(group: dict) -> dict:
+    """runtime/optim.py:366-369: tuples as lists, so a group read back from
+    JSON or torch.load compares equal to a fresh one."""
+    return {k: (list(v) if isinstance(v, tuple) else v) for k, v in sorted(group.items())}
+
+
+def _f32(x: float) -> float:
+    """A double rounded once to fp32 (runtime/optim.py:72-74)."""
+    return float(np.float32(x))
+
+
+def host_consts(lr: float, betas, eps: float, weight_decay: float, t: float) -> list:
+    """HostAdamW.step's per-step constants (runtime/optim.py:158-167), each
+    computed in double and rounded once to fp32."""
+    b1, b2 = betas
+    return [
+        _f32(1.0 - lr * weight_decay),
+        _f32(b1),
+        _f32(1.0 - b1),
+        _f32(b2),
+        _f32(1.0 - b2),
+        _f32(1.0 / math.sqrt(1.0 - b2**t)),
+        _f32(eps),
+        _f32(lr / (1.0 - b1**t)),
+    ]
+
+
+def torch_consts(lr: float, betas, eps: float, weight_decay: float, t: float) -> list:
+    """The fp32 scalars torch's _multi_tensor_adam hands its kernels for step
+    t (TORCH/optim/adam.py:689-800): decay, 1-b1, b2, 1-b2, bc2**0.5, eps,
+    (lr/bc1)*-1."""
+    b1, b2 = betas
+    bc1 = 1 - b1**t
+    bc2 = 1 - b2**t
+    return [
+        _f32(1 - lr * weight_decay),
+        _f32(1 - b1),
+        _f32(b2),
+        _f32(1 - b2),
+        _f32(bc2**0.5),
+        _f32(eps),
+        _f32((lr / bc1) * -1),
+        0.0,
+    ]
+
+
+class FusedAdamW:
+    """AdamW (decoupled weight decay, no amsgrad) over a ragged list of fp32
+    CUDA parameters, one fused launch per step.
+
+    order: "host" (HostAdamW's bits) or "torch" (torch.optim.AdamW's op order).
+    max_norm: clip the global L2 norm of the gradients to this value before
+        the update (torch.nn.utils.clip_grad_norm_'s coefficient), fused into
+        the same launch; None disables clipping.
+    working_copy: None, True (allocate a bf16 copy of every parameter) or a
+        list of bf16 tensors shaped like the parameters; refreshed with the
+        RNE bf16 cast of the updated parameter (pieces.cast_piece) in the
+        update's own pass.
+    Gradients (p.grad) may be float32 or bfloat16 (the bf16 fold start of
+    runtime/pieces.py:198-203 happens in registers).
+    """
+
+    def __init__(
+        self,
+        params: Iterable[torch.Tensor],
+        lr: float,
+        betas: tuple = (0.9, 0.999),
+        eps: float = 1e-8,
+        weight_decay: float = 0.0,
+        *,
+        order: str = "host",
+        max_norm: float | None = None,
+        working_copy=None,
+    ):
+        self.params = list(params)
+        if order not in ("host", "torch"):
+            raise ValueError(f"order {order!r} is not 'host' or 'torch'")
+        self.order = order
+        self.recipe = "adamw-host" if order == "host" else "adamw"
+        devices = set()
+        for p in self.params:
+            if p.requires_grad and p.dtype != torch.float32:
+                raise ValueError(f"{self.recipe} trains fp32 parameters, got {p.dtype}")
+            if p.requires_grad:
+                _lib.require_gpu(p, self.recipe)
+                devices.add(p.device)
+        if len(devices) > 1:
+            raise ValueError(f"{self.recipe}: parameters span devices {sorted(map(str, devices))}; build one optimizer per device")
+        self.device = devices.pop() if devices else None
+        self.lr, self.betas, self.eps, self.weight_decay = lr, tuple(betas), eps, weight_decay
+        self.max_norm = None if max_norm is None else float(max_norm)
+        group = hparams(lr, self.recipe)
+        group.update(lr=lr, betas=self.betas, eps=eps, weight_decay=weight_decay)
+        self._group = group
+        self.param_groups = [{**group, "params": self.params}]
+        self.state: dict = {}
+        self._flat_m = self._flat_v = None
+        self._norm = None  # device ely_norm_result of the last clipped step
+        self.working_copies = self._init_copies(working_copy)
+
+    # ------------------------------------------------------------ storage
+
+    def _init_copies(self, working_copy):
+        if working_copy is None:
+            return None
+        if working_copy is True:
+            return [torch.empty(p.shape, dtype=torch.bfloat16, device=p.device) if p.requires_grad else None for p in self.params]
+        copies = list(working_copy)
+        if len(copies) != len(self.params):
+            raise ValueError(f"{len(copies)} working copies for {len(self.params)} parameters")
+        for c, p in zip(copies, self.params):
+            if c is None:
+                continue
+            if c.dtype != torch.bfloat16 or tuple(c.shape) != tuple(p.shape) or not c.is_contiguous() or c.device != p.device:
+                raise ValueError("a working copy is a contiguous bf16 tensor shaped like its parameter, on its device")
+        return copies
+
+    def _alloc_state(self) -> None:
+        """Moments live in two flat fp32 buffers in parameter order, each
+        tensor's slice starting on a 256-byte boundary; state[i] holds views."""
+        offs, total = [], 0
+        for p in self.params:
+            offs.append(total)
+            total += -(-p.numel() // _ALIGN) * _ALIGN
+        dev = self.device
+        self._flat_m = torch.zeros(max(total, 1), dtype=torch.float32, device=dev)
+        self._flat_v = torch.zeros(max(total, 1), dtype=torch.float32, device=dev)
+        self._offs = offs
+
+    def _slot(self, i: int, p: torch.Tensor) -> dict:
+        st = self.state.get(i)
+        if st is None:
+            if self._flat_m is None:
+                self._alloc_state()
+            o, n = self._offs[i], p.numel()
+            st = self.state[i] = {
+                "step": torch.tensor(0.0, dtype=torch.float32),
+                "exp_avg": self._flat_m[o : o + n].view(p.shape),
+                "exp_avg_sq": self._flat_v[o : o + n].view(p.shape),
+            }
+        return st
+
+    # --------------------------------------------------------------- step
+
+    def _consts(self, t: float) -> list:
+        if self.order == "host":
+            return host_consts(self.lr, self.betas, self.eps, self.weight_decay, t)
+        return torch_consts(self.lr, self.betas, self.eps, self.weight_decay, t)
+
+    @torch.no_grad()
+    def step(self, on_param=None, grads=None) -> None:
+        """One AdamW step over every parameter with a gradient, in order;
+        `on_param(i)` runs after parameter i's update is issued
+        (runtime/optim.py:145-170).  Nothing here waits for the GPU.
+
+        grads: optional list aligned with the parameters (None entries skip
+        a parameter) used instead of p.grad -- the way to hand in bf16
+        gradients, which torch does not let an fp32 parameter's .grad hold."""
+        if grads is not None and len(grads) != len(self.params):
+            raise ValueError(f"{len(grads)} gradients for {len(self.params)} parameters")
+        idx, ps, gs, ms, vs, cs, consts = [], [], [], [], [], [], []
+        cache: dict = {}
+        for i, p in enumerate(self.params):
+            g = p.grad if grads is None else grads[i]
+            if g is None:
+                continue  # as torch: a parameter without a gradient is not stepped
+            if not p.is_contiguous():
+                raise ValueError(f"{self.recipe} steps contiguous parameters only")
+            if g.shape != p.shape or not g.is_contiguous() or g.device != p.device:
+                raise ValueError(f"{self.recipe}: the gradient of parameter {i} must be contiguous, shaped like it, on its device")
+            if g.dtype not in (torch.float32, torch.bfloat16):
+                raise ValueError(f"{self.recipe}: gradients are float32 or bfloat16, got {g.dtype}")
+            st = self._slot(i, p)
+            st["step"] += 1
+            t = float(st["step"])
+            c = cache.get(t)
+            if c is None:
+                c = cache[t] = self._consts(t)
+            idx.append(i)
+            ps.append(p)
+            gs.append(g)
+            ms.append(st["exp_avg"])
+            vs.append(st["exp_avg_sq"])
+            cs.append(self.working_copies[i] if self.working_copies is not None else None)
+            consts.append(c)
+        if idx:
+            dev = ps[0].device
+            with torch.cuda.device(dev):
+                coef_ptr = self._clip_coef(gs) if self.max_norm is not None else None
+                # one launch per gradient dtype (torch groups by dtype the same way)
+                for gdt in (torch.bfloat16, torch.float32):
+                    sel = [j for j, g in enumerate(gs) if g.dtype == gdt]
+                    if sel:
+                        self._launch([ps[j] for j in sel], [gs[j] for j in sel], [ms[j] for j in sel],
+                                     [vs[j] for j in sel], [cs[j] for j in sel], [consts[j] for j in sel], coef_ptr)
+        if on_param is not None:
+            for i in idx:
+                on_param(i)
+
+    def _clip_coef(self, grads) -> int:
+        """Launch the deterministic norm of every gradient of the step (any
+        dtype); returns the device address of its fp32 clip coefficient."""
+        L = _lib.load()
+        dev = grads[0].device
+        if self._norm is None or self._norm.device != dev:
+            self._norm = torch.empty(16, dtype=torch.uint8, device=dev)
+        garr = _lib.tensor_array(grads)
+        ws = _lib.workspace(dev, L.ely_grad_norm_workspace_bytes(garr, len(grads)))
+        _lib.check(
+            L.ely_grad_norm(garr, len(grads), self.max_norm, self._norm.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_ptr(dev)),
+            "grad norm",
+        )
+        return self._norm.data_ptr() + 12
+
+    def _launch(self, ps, gs, ms, vs, cs, consts, coef_ptr) -> None:
+        L = _lib.load()
+        dev = ps[0].device
+        stream = _lib.stream_ptr(dev)
+        n = len(ps)
+        carr = (_lib.ElyConsts * n)()
+        for j, c in enumerate(consts):
+            carr[j].c[:] = c
+        copies = [(_lib.ely_tensor(c) if c is not None else _lib.ElyTensor(None, 0, _lib.BF16, 0)) for c in cs]
+        ws = _lib.workspace(dev, L.ely_adamw_workspace_bytes(n))
+        _lib.check(
+            L.ely_adamw_step(
+                _lib.tensor_array(ps), _lib.tensor_array(gs), _lib.tensor_array(ms), _lib.tensor_array(vs),
+                _lib.tensor_array(copies), n, carr, _lib.ORDER_HOST if self.order == "host" else _lib.ORDER_TORCH,
+                int(self.weight_decay != 0), coef_ptr, ws.data_ptr(), ws.numel(), stream,
+            ),
+            f"{self.recipe} step",
+        )
+
+    def grad_norm(self) -> torch.Tensor | None:
+        """The fp32 global gradient norm of the last clipped step (a device
+        tensor, no synchronization), or None."""
+        if self._norm is None:
+            return None
+        return self._norm[8:12].view(torch.float32).reshape(())
+
+    def zero_grad(self, set_to_none: bool = True) -> None:
+        for p in self.params:
+            if set_to_none:
+                p.grad = None
+            elif p.grad is not None:
+                p.grad.zero_()
+
+    # --------------------------------------------------------- checkpoint
+
+    def state_dict(self) -> dict:
+        """torch's AdamW layout; adamw-host returns host copies of the moments
+        as the reference does (runtime/optim.py:238-250)."""
+        host = self.order == "host"
+        return {
+            "state": {
+                i: {
+                    "step": st["step"].clone(),
+                    "exp_avg": st["exp_avg"].cpu() if host else st["exp_avg"],
+                    "exp_avg_sq": st["exp_avg_sq"].cpu() if host else st["exp_avg_sq"],
+                }
+                for i, st in sorted(self.state.items())
+            },
+            "param_groups": [{**self._group, "params": list(range(len(self.params)))}],
+        }
+
+    def load_state_dict(self, sd: dict) -> None:
+        """runtime/optim.py:252-274: refuses another recipe's state, other
+        parameters and wrong shapes."""
+        groups = sd.get("param_groups") or []
+        if len(groups) != 1:
+            raise ValueError(f"{self.recipe} state holds one param group")
+        theirs = {k: v for k, v in groups[0].items() if k != "params"}
+        mine = json_norm(self._group)
+        if json_norm(theirs) != mine:
+            raise ValueError(f"optimizer state of another recipe: {json_norm(theirs)} is not {mine}")
+        if list(groups[0]["params"]) != list(range(len(self.params))):
+            raise ValueError("optimizer state names other parameters")
+        for i, st in sd.get("state", {}).items():
+            i = int(i)
+            p = self.params[i]
+            for k in ("exp_avg", "exp_avg_sq"):
+                if tuple(st[k].shape) != tuple(p.shape):
+                    raise ValueError(f"optimizer state {i}.{k} has shape {tuple(st[k].shape)}")
+        self.state = {}
+        for i, st in sd.get("state", {}).items():
+            i = int(i)
+            slot = self._slot(i, self.params[i])
+            slot["step"] = torch.as_tensor(st["step"], dtype=torch.float32).clone().cpu()
+            slot["exp_avg"].copy_(st["exp_avg"])
+            slot["exp_avg_sq"].copy_(st["exp_avg_sq"])
+
+
+def clip_grad_norm_(parameters, max_norm: float, norm_type: float = 2.0, error_if_nonfinite: bool = False, foreach=None) -> torch.Tensor:
+    """torch.nn.utils.clip_grad_norm_ (TORCH/nn/utils/clip_grad.py:50-183)
+    for the 2-norm: the deterministic device norm of every gradient, then each
+    gradient scaled in place by min(max_norm / (norm + 1e-6), 1).  Returns the
+    fp32 total norm as a device tensor."""
+    if norm_type != 2.0:
+        raise ValueError("clip_grad_norm_ on MI355X computes the 2-norm only")
+    if isinstance(parameters, torch.Tensor):
+        parameters = [parameters]
+    grads = [p.grad for p in parameters if p.grad is not None]
+    if not grads:
+        return torch.tensor(0.0)
+    dev = grads[0].device
+    for g in grads:
+        _lib.require_gpu(g, "clip_grad_norm_")
+        if g.device != dev or not g.is_contiguous():
+            raise ValueError("clip_grad_norm_: gradients must be contiguous and on one device")
+    L = _lib.load()
+    with torch.cuda.device(dev):
+        res = torch.empty(16, dtype=torch.uint8, device=dev)
+        garr = _lib.tensor_array(grads)
+        ws = _lib.workspace(dev, L.ely_grad_norm_workspace_bytes(garr, len(grads)))
+        _lib.check(L.ely_grad_norm(garr, len(grads), float(max_norm), res.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_ptr(dev)), "clip_grad_norm_")
+        total = res[8:12].view(torch.float32).reshape(()).clone()
+        if error_if_nonfinite and bool(~torch.isfinite(total)):
+            raise RuntimeError(f"The total norm of order {norm_type} for gradients from `parameters` is non-finite, so it cannot be clipped.")
+        # g <- g * coef in g's dtype, torch's _foreach_mul_ by the clamped coefficient
+        _lib.check(L.ely_scale_inplace(garr, len(grads), res.data_ptr() + 12, _lib.stream_ptr(dev)), "clip_grad_norm_ scale")
+    return total

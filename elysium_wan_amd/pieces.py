@@ -1,0 +1,72 @@
+"""The elementwise kernels of the sharded "pieces" update on MI355X: the
+drop-in for wantrain's runtime/pieces.py:192-227 (same names and semantics).
+
+cast_piece: fp32 master -> working copy (bf16 RNE, or a plain copy for fp32).
+fold_start / fold_add / fold: the fixed-order fp32 gradient fold, widening
+bf16 parts exactly.  int64 count lanes stay on torch's exact integer add, as
+the reference does (runtime/pieces.py:198-214).
+"""
+
+from __future__ import annotations
+
+from collections.abc import Iterable
+
+import torch
+
+from . import _lib
+
+
+def cast_piece(p: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """runtime/pieces.py:192-195: a new tensor, never an alias of the master."""
+    if dtype == torch.bfloat16 and p.dtype == torch.float32:
+        _lib.require_gpu(p, "cast_piece")
+        src = p.detach().contiguous()
+        out = torch.empty(src.shape, dtype=torch.bfloat16, device=src.device)
+        L = _lib.load()
+        _lib.check(L.ely_cast_bf16(src.data_ptr(), out.data_ptr(), src.numel(), _lib.stream_ptr(src.device)), "cast_piece")
+        return out
+    if dtype == p.dtype:
+        return p.detach().clone()
+    raise TypeError(f"cast_piece on MI355X casts float32 to bfloat16 (or copies), not {p.dtype} -> {dtype}")
+
+
+def fold_start(g: torch.Tensor) -> torch.Tensor:
+    """runtime/pieces.py:198-203: the fp32 accumulator, a copy of microbatch
+    0's widened gradient (an int64 count lane stays int64)."""
+    if g.dtype == torch.int64:
+        return g.clone()
+    _lib.require_gpu(g, "fold_start")
+    if g.dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError(f"fold_start widens float32 or bfloat16 gradients, got {g.dtype}")
+    # widening is exact (the fp32 value of a bf16 is its bits shifted up): a copy
+    return g.detach().to(torch.float32, copy=True)
+
+
+def fold_add(acc: torch.Tensor, g: torch.Tensor) -> None:
+    """runtime/pieces.py:206-214: acc += widen(g), one fp32 rounding per element."""
+    if acc.dtype == torch.int64:
+        if g.dtype != torch.int64:
+            raise ValueError(f"a count lane folds int64 only, got {g.dtype}")
+        acc.add_(g)
+        return
+    _lib.require_gpu(acc, "fold_add")
+    if acc.dtype != torch.float32 or not acc.is_contiguous():
+        raise ValueError("fold_add accumulates into a contiguous float32 tensor")
+    g = g.detach().contiguous()
+    if g.numel() != acc.numel() or g.device != acc.device:
+        raise ValueError("fold_add: gradient and accumulator differ in size or device")
+    L = _lib.load()
+    _lib.check(L.ely_fold_add(acc.data_ptr(), g.data_ptr(), _lib.dtype_code(g), acc.numel(), _lib.stream_ptr(acc.device)), "fold_add")
+
+
+def fold(gs: Iterable[torch.Tensor]) -> torch.Tensor:
+    """runtime/pieces.py:217-227: left fold in microbatch-index order."""
+    acc = None
+    for g in gs:
+        if acc is None:
+            acc = fold_start(g)
+        else:
+            fold_add(acc, g)
+    if acc is None:
+        raise ValueError("a fold over zero microbatches")
+    return acc

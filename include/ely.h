@@ -1,0 +1,172 @@
+/*
+ * ely.h -- C ABI of libelyhip.so, the MI355X (gfx950) kernels of the
+ * per-stage mixed-precision update path.
+ *
+ * Every entry point is `extern "C"`, takes plain pointers and sizes, never
+ * throws, and returns an ely_status (0 = ok).  On failure ely_last_error()
+ * returns a thread-local message.  Device pointers are HIP device memory
+ * (e.g. torch's data_ptr()); `stream` is a hipStream_t passed as void*
+ * (torch.cuda.current_stream().cuda_stream).  Every launch goes to that
+ * stream; nothing synchronizes the device.  The library never allocates or
+ * frees caller memory; scratch comes from the caller's `workspace` (sized by
+ * the *_workspace_bytes queries) plus a small pinned host ring the library
+ * owns for uploading tensor tables.
+ *
+ * Citations name the reference function each entry point replaces (paths
+ * relative to the reference repository root; TORCH/ = the torch package).
+ */
+#ifndef ELY_H
+#define ELY_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum ely_status {
+    ELY_OK = 0,
+    ELY_EINVAL = 1,       /* bad argument: shape, dtype, alignment, size (-> ValueError) */
+    ELY_EHIP = 2,         /* a HIP runtime call or launch failed (-> RuntimeError) */
+    ELY_ENOTREPR = 3,     /* tensor is not scaled-fp8 representable (-> ValueError) */
+    ELY_EWORKSPACE = 4    /* workspace smaller than the *_workspace_bytes query */
+} ely_status;
+
+enum { ELY_F32 = 0, ELY_BF16 = 1 };          /* element types */
+enum { ELY_E4M3 = 0, ELY_E5M2 = 1 };         /* fp8 formats: float8_e4m3fn, float8_e5m2 */
+enum { ELY_ORDER_HOST = 0, ELY_ORDER_TORCH = 1 };
+
+/* One tensor of a multi-tensor call: a contiguous range of `numel` elements. */
+typedef struct ely_tensor {
+    void* ptr;
+    int64_t numel;
+    int32_t dtype;        /* ELY_F32 | ELY_BF16 */
+    int32_t reserved;     /* must be 0 */
+} ely_tensor;
+
+/* Result of the grad-norm reduction, written to device memory. */
+typedef struct ely_norm_result {
+    double sumsq;         /* sum of g^2 over every element, fp64 */
+    float norm;           /* (float)sqrt(sumsq) */
+    float coef;           /* clip coefficient, 1 when max_norm <= 0 */
+} ely_norm_result;
+
+/* AdamW per-step fp32 constants, one block per tensor.
+ * ELY_ORDER_HOST uses, in order, the eight scalars runtime/optim.py:158-167
+ * computes: decay, b1, one_b1, b2, one_b2, inv_bc2_sqrt, eps, step_size.
+ * ELY_ORDER_TORCH uses the first seven slots as the scalars of torch's
+ * _multi_tensor_adam (TORCH/optim/adam.py:689-800): decay, 1-b1, b2, 1-b2,
+ * bc2_sqrt, eps, -(lr/bc1); the eighth is ignored. */
+typedef struct ely_adamw_consts {
+    float c[8];
+} ely_adamw_consts;
+
+/* Library identity and errors. */
+int32_t ely_abi_version(void);
+const char* ely_last_error(void);
+
+/* ---------------------------------------------------------------- (a) */
+
+/* Workspace bytes ely_grad_norm needs for these tensors. */
+int64_t ely_grad_norm_workspace_bytes(const ely_tensor* grads, int32_t n);
+
+/* Deterministic global L2 norm of a ragged gradient list, and the clip
+ * coefficient clip_grad_norm_ derives from it.  Replaces the norm of
+ * TORCH/nn/utils/clip_grad.py:50-108 and the coefficient of :160-169 (the
+ * reference itself never clips; its optimizer is runtime/optim.py:45-54).
+ * Each fixed 16,384-element tile is reduced in a fixed lane order (fp32
+ * squares of at most 8 elements, fp64 above), tiles in index order: the
+ * result is bitwise identical across runs and grid sizes.  coef =
+ * min(max_norm * (1/(norm + 1e-6)), 1) in fp32 when max_norm > 0, else 1. */
+int ely_grad_norm(const ely_tensor* grads, int32_t n, float max_norm,
+                  ely_norm_result* out_dev, void* workspace, int64_t ws_bytes, void* stream);
+
+/* ---------------------------------------------------------------- (b) */
+
+int64_t ely_adamw_workspace_bytes(int32_t n);
+
+/* One fused AdamW step over a ragged tensor list, one HBM pass per element:
+ * read p, g, m, v; write p, m, v and (optionally) the bf16 working copy.
+ * Replaces HostAdamW.step/_update/_adamw_math (runtime/optim.py:145-204,
+ * 277-298) for ELY_ORDER_HOST, torch.optim.AdamW.step (runtime/optim.py:50-51,
+ * TORCH/optim/adam.py:554-800) for ELY_ORDER_TORCH, plus the fp32->bf16 cast
+ * of pieces.cast_piece (runtime/pieces.py:192-195) and the bf16 widening of
+ * pieces.fold_start (runtime/pieces.py:198-203) when grads are bf16.
+ * params/exp_avg/exp_avg_sq: fp32; grads: all ELY_F32 or all ELY_BF16;
+ * copies: NULL or n bf16 tensors (a NULL ptr skips that tensor's copy);
+ * coef_dev: NULL (no clip) or &ely_norm_result.coef from ely_grad_norm. */
+int ely_adamw_step(const ely_tensor* params, const ely_tensor* grads,
+                   const ely_tensor* exp_avg, const ely_tensor* exp_avg_sq,
+                   const ely_tensor* copies, int32_t n,
+                   const ely_adamw_consts* consts, int32_t order, int32_t weight_decay_nonzero,
+                   const float* coef_dev, void* workspace, int64_t ws_bytes, void* stream);
+
+/* ---------------------------------------------------------------- (c) */
+
+int64_t ely_fp8_workspace_bytes(int64_t rows, int64_t cols, int32_t x_dtype);
+
+/* fp8.quantize (model/fp8.py:28-49): per row of `cols` elements,
+ * k = frexp(amax(|x|)).exponent - ebias (0 for an all-zero row, ebias 8 for
+ * e4m3, 15 for e5m2) and q = fp8(x * 2^-k) with the multiply in x's dtype
+ * and torch's round-to-nearest-even conversion.  Per-tensor scaling is
+ * rows = 1.  x: [rows, cols] bf16 or fp32; q: [rows, cols] bytes, or NULL to
+ * compute k alone (fp8.scale_exp); k: [rows] int32. */
+int ely_fp8_quantize(const void* x, int32_t x_dtype, int64_t rows, int64_t cols, int32_t fmt,
+                     uint8_t* q, int32_t* k, void* workspace, int64_t ws_bytes, void* stream);
+
+/* fp8.dequantize (model/fp8.py:52-53): out = float(q) * 2^k in out_dtype
+ * (ELY_F32 is the reference's default; ELY_BF16 is roundtrip's dtype). */
+int ely_fp8_dequantize(const uint8_t* q, const int32_t* k, int64_t rows, int64_t cols, int32_t fmt,
+                       void* out, int32_t out_dtype, void* stream);
+
+/* fp8.roundtrip (model/fp8.py:56-63) fused: out = dequantize(quantize(x)) in
+ * x's dtype, q and k written too when non-NULL. */
+int ely_fp8_roundtrip(const void* x, int32_t x_dtype, int64_t rows, int64_t cols, int32_t fmt,
+                      void* out, uint8_t* q, int32_t* k, void* workspace, int64_t ws_bytes,
+                      void* stream);
+
+/* ------------------------------------------------------------ casts/fold */
+
+/* pieces.cast_piece (runtime/pieces.py:192-195): fp32 -> bf16, RNE,
+ * every NaN -> 0x7FC0. */
+int ely_cast_bf16(const float* x, uint16_t* out, int64_t n, void* stream);
+
+/* pieces.fold_add (runtime/pieces.py:206-214): acc += float(g), one fp32
+ * rounding; g_dtype ELY_F32 or ELY_BF16. */
+int ely_fold_add(float* acc, const void* g, int32_t g_dtype, int64_t n, void* stream);
+
+/* In-place g <- g * (*coef_dev) over a tensor list, the product rounded to
+ * each tensor's dtype: the scaling step of clip_grad_norm_
+ * (TORCH/nn/utils/clip_grad.py:170-183) with the coefficient ely_grad_norm
+ * left on the device. */
+int ely_scale_inplace(const ely_tensor* tensors, int32_t n, const float* coef_dev, void* stream);
+
+/* Cap on the blocks one multi-tensor launch (grad-norm, AdamW) may use; 0
+ * restores the default (8 per compute unit).  For tuning and for the tests
+ * that prove results do not depend on the grid.  Process-wide. */
+int ely_set_max_blocks(int32_t max_blocks);
+
+/* ------------------------------------------------------------ self-test */
+
+/* Device self-check of the gfx950 fp8 conversion instruction against the
+ * library's bit-level restatement of torch's conversion, over the fp32 bit
+ * patterns [start, start + count).  mismatches_dev: three uint64 counters
+ * the caller zeroes: [0] patterns the kernels' instruction path relies on
+ * (|x| at most the format's largest finite value) whose code differs,
+ * [1] differing patterns outside that domain (NaN, overflow; informational),
+ * [2] (only when start == 0) decoded codes that differ from the format's
+ * definition, over all 256 codes. */
+int ely_selftest_fp8_cvt(uint32_t start, uint64_t count, int32_t fmt,
+                         unsigned long long* mismatches_dev, void* stream);
+
+/* Device self-check that the kernels' fp32 sqrt (used by the AdamW update)
+ * equals the fp64 sqrt rounded once to fp32 (runtime/optim.py:288-291) on
+ * the non-negative fp32 patterns of [start, start + count) (sign bit
+ * cleared).  mismatches_dev: one uint64 counter the caller zeroes. */
+int ely_selftest_sqrt(uint32_t start, uint64_t count, unsigned long long* mismatches_dev, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ELY_H */

@@ -1,0 +1,136 @@
+"""The C ABI without a GPU: libelyhip.so loads, exports every function
+include/ely.h declares (and nothing the Python binding expects is missing),
+the header's constants match the binding's, and argument errors come back as
+status codes and messages, never crashes.  No call here launches a kernel:
+each one fails its argument check before touching the HIP runtime."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "ely.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ely_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from elysium_wan_amd import _lib
+
+    return _lib.load()
+
+
+def test_library_exports_every_declared_function(lib):
+    names = _declared()
+    assert len(names) >= 15
+    for n in names:
+        assert hasattr(lib, n), n
+
+
+def test_binding_covers_the_header():
+    from elysium_wan_amd import _lib
+
+    assert sorted(_lib.EXPORTS) == _declared()
+
+
+def test_header_constants_match_the_binding():
+    from elysium_wan_amd import _lib
+
+    text = open(HEADER).read()
+    consts = dict(re.findall(r"\b(ELY_\w+)\s*=\s*(\d+)", text))
+    assert int(consts["ELY_F32"]) == _lib.F32 and int(consts["ELY_BF16"]) == _lib.BF16
+    assert int(consts["ELY_E4M3"]) == _lib.E4M3 and int(consts["ELY_E5M2"]) == _lib.E5M2
+    assert int(consts["ELY_ORDER_HOST"]) == _lib.ORDER_HOST and int(consts["ELY_ORDER_TORCH"]) == _lib.ORDER_TORCH
+    assert int(consts["ELY_EINVAL"]) == _lib.EINVAL and int(consts["ELY_EWORKSPACE"]) == _lib.EWORKSPACE
+    assert ctypes.sizeof(_lib.ElyTensor) == 24 and ctypes.sizeof(_lib.ElyConsts) == 32
+    assert ctypes.sizeof(_lib.ElyNormResult) == 16
+
+
+def test_abi_version(lib):
+    assert lib.ely_abi_version() == 1
+
+
+def test_argument_errors_are_status_codes(lib):
+    from elysium_wan_amd import _lib
+
+    st = lib.ely_fp8_quantize(None, _lib.BF16, 4, 8, 7, None, None, None, 0, None)
+    assert st == _lib.EINVAL and b"fp8 format" in lib.ely_last_error()
+    st = lib.ely_fp8_dequantize(None, None, 4, 8, _lib.E4M3, None, 9, None)
+    assert st == _lib.EINVAL and b"out_dtype" in lib.ely_last_error()
+    st = lib.ely_fp8_quantize(None, _lib.BF16, -1, 8, _lib.E4M3, None, None, None, 0, None)
+    assert st == _lib.EINVAL
+    st = lib.ely_adamw_step(None, None, None, None, None, -1, None, 0, 0, None, None, 0, None)
+    assert st == _lib.EINVAL and b"negative tensor count" in lib.ely_last_error()
+    arr = _lib.tensor_array([_lib.ElyTensor(None, 5, _lib.F32, 0)])
+    st = lib.ely_grad_norm(arr, 1, 1.0, None, None, 0, None)
+    assert st == _lib.EINVAL and b"null pointer" in lib.ely_last_error()
+    assert lib.ely_set_max_blocks(-1) == _lib.EINVAL
+    assert lib.ely_cast_bf16(None, None, -3, None) == _lib.EINVAL
+    assert lib.ely_fold_add(None, None, 5, 4, None) == _lib.EINVAL
+    assert lib.ely_selftest_fp8_cvt(0, 1 << 33, 0, None, None) == _lib.EINVAL
+
+
+def test_workspace_queries_are_host_arithmetic(lib):
+    from elysium_wan_amd import _lib
+
+    arr = _lib.tensor_array([_lib.ElyTensor(None, 16384 * 3 + 1, _lib.BF16, 0), _lib.ElyTensor(None, 7, _lib.F32, 0)])
+    need = lib.ely_grad_norm_workspace_bytes(arr, 2)
+    assert need >= 5 * 8 and need % 256 == 0
+    assert lib.ely_grad_norm_workspace_bytes(arr, -1) == -1
+    assert lib.ely_adamw_workspace_bytes(192) >= 192 * (64 + 32)
+    assert lib.ely_fp8_workspace_bytes(16384, 2560, _lib.BF16) >= 16384 * 4
+
+
+def test_python_surface_fails_loudly_off_the_gpu():
+    from elysium_wan_amd import fp8, optim, pieces
+
+    x = torch.randn(4, 32)
+    with pytest.raises(ValueError, match="GPU"):
+        fp8.quantize(x)
+    with pytest.raises(ValueError, match="GPU"):
+        fp8.roundtrip(x.bfloat16(), "e5m2")
+    with pytest.raises(ValueError, match="GPU"):
+        optim.build("adamw-host", [torch.zeros(3, requires_grad=True)], 1e-3)
+    with pytest.raises(ValueError, match="fp32"):
+        optim.build("adamw-host", [torch.zeros(3, dtype=torch.bfloat16, requires_grad=True)], 1e-3)
+    with pytest.raises(ValueError, match="not one of"):
+        optim.build("sgd", [], 1e-3)
+    with pytest.raises(ValueError, match="GPU"):
+        pieces.cast_piece(x, torch.bfloat16)
+    with pytest.raises(ValueError, match="not one of"):
+        fp8.quantize(x, "e3m4")
+
+
+def test_optimizer_bookkeeping_matches_the_reference():
+    from elysium_wan_amd import optim
+
+    assert optim.OPTIMIZERS == ("adamw", "adamw-host")
+    assert optim.state_bytes_per_param("adamw-host") == 8 and optim.state_bytes_per_param() == 16
+    assert optim.hparams(1e-3, "adamw-host")["moments"] == "host"
+    assert "moments" not in optim.hparams(1e-3)
+    assert optim.ADAMW == {"betas": (0.9, 0.95), "eps": 1e-8, "weight_decay": 0.0}
+
+
+def test_host_constants_equal_the_reference_golden():
+    """The package's own constant code (not the oracle's) against the
+    constants HostAdamW.step computed in the reference."""
+    from conftest import golden
+    from elysium_wan_amd import optim
+
+    g = golden("host_adamw.npz")
+    for case in ("unit", "decay", "c0"):
+        lr, b1, b2, eps, wd, steps = g[f"{case}_hyper"]
+        for step in range(int(steps)):
+            c = optim.host_consts(lr, (b1, b2), eps, wd, float(step + 1))
+            assert [float(x) for x in g[f"{case}_consts"][step][0]] == c

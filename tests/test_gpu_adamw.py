@@ -1,0 +1,231 @@
+"""The fused clip + AdamW step on the GPU against the oracle, the reference's
+golden vectors and torch.optim.AdamW:
+
+* "adamw-host" order: p, m, v and the bf16 working copy bit for bit
+  (runtime/optim.py:277-298, pieces.py:192-195), with fp32 and bf16 grads,
+  weight decay on and off, clipping on and off, aligned and unaligned
+  tensors, any grid size;
+* "adamw" order: within 1 ulp of torch.optim.AdamW on the same GPU;
+* the torch.optim surface: state_dict layout, resume bit for bit, refusal of
+  another recipe, on_param order (the reference's test_host_adamw.py)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import golden
+from gpu_util import bits, gpt_block_shapes, say, ulp_distance
+
+pytestmark = pytest.mark.gpu
+
+ADAMW = {"betas": (0.9, 0.95), "eps": 1e-8, "weight_decay": 0.0}
+
+
+def _set_blocks(n: int) -> None:
+    from elysium_wan_amd import _lib
+
+    _lib.check(_lib.load().ely_set_max_blocks(n), "ely_set_max_blocks")
+
+
+@pytest.mark.parametrize("case", ["unit", "decay", "c0"])
+def test_reference_golden_steps_bit_for_bit(case):
+    """Replays the reference's HostAdamW runs (tests/golden/make_golden.py)
+    through optim.build("adamw-host") on the GPU."""
+    from elysium_wan_amd import optim
+
+    g = golden("host_adamw.npz")
+    lr, b1, b2, eps, wd, steps = g[f"{case}_hyper"]
+    numel = [int(n) for n in g[f"{case}_numel"]]
+    shapes = [tuple(int(s) for s in row if s) for row in g[f"{case}_shapes"]]
+    p0 = torch.from_numpy(g[f"{case}_p0"].copy())
+    params = [t.reshape(s).clone().cuda().requires_grad_(True) for t, s in zip(torch.split(p0, numel), shapes)]
+    say("golden adamw-host", case)
+    opt = optim.build("adamw-host", params, float(lr), betas=(float(b1), float(b2)), eps=float(eps), weight_decay=float(wd))
+    for step in range(int(steps)):
+        gs = torch.split(torch.from_numpy(g[f"{case}_grads"][step].copy()), numel)
+        for p, gr, s in zip(params, gs, shapes):
+            p.grad = gr.reshape(s).cuda()
+        opt.step()
+        opt.zero_grad()
+    cat = lambda ts: torch.cat([t.detach().reshape(-1).cpu() for t in ts]).numpy()  # noqa: E731
+    assert np.array_equal(cat(params).view(np.uint32), g[f"{case}_p"].view(np.uint32))
+    assert np.array_equal(cat([opt.state[i]["exp_avg"] for i in range(len(params))]).view(np.uint32), g[f"{case}_m"].view(np.uint32))
+    assert np.array_equal(cat([opt.state[i]["exp_avg_sq"] for i in range(len(params))]).view(np.uint32), g[f"{case}_v"].view(np.uint32))
+
+
+def _c0_shard(seed: int, gdtype, scale=1e-3, hot=()):
+    """Config C0: 3 GPT blocks at d = 768 plus two d-vectors (38 tensors,
+    21,265,152 elements); N(0, 0.02) params, N(0, scale) grads; tensors in
+    `hot` get grads x100 so the global-norm clip triggers."""
+    gen = torch.Generator().manual_seed(seed)
+    shapes = gpt_block_shapes(768) * 3 + [(768,), (768,)]
+    params = [(torch.randn(s, generator=gen) * 0.02) for s in shapes]
+    grads = [(torch.randn(s, generator=gen) * scale * (100.0 if i in hot else 1.0)).to(gdtype) for i, s in enumerate(shapes)]
+    return params, grads
+
+
+def _oracle_steps(oracle, params, grads_per_step, lr, wd, max_norm, copies=True):
+    """The oracle's HostAdamW over the flat concatenation, with the clip
+    coefficient from the oracle's fp64 norm when max_norm is set."""
+    p = np.concatenate([t.reshape(-1).numpy() for t in params]).astype(np.float32)
+    m, v = np.zeros_like(p), np.zeros_like(p)
+    cp = np.zeros(p.size, dtype=np.uint16) if copies else None
+    for step, grads in enumerate(grads_per_step):
+        gflat = np.concatenate([bits(t).reshape(-1) for t in grads])
+        coef = 1.0
+        if max_norm is not None:
+            norm = float(np.float32(np.sqrt(oracle.sumsq([gflat]))))
+            coef = oracle.clip_coef(norm, max_norm)
+        c = oracle.host_adamw_consts(lr, (0.9, 0.95), 1e-8, wd, step + 1)
+        oracle.adamw_host(p, gflat, m, v, c, wd != 0, coef, cp)
+    return p, m, v, cp
+
+
+@pytest.mark.parametrize("gdtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("clip", [None, 1.0])
+def test_c0_shard_equals_the_oracle(oracle, gdtype, clip):
+    from elysium_wan_amd import optim
+
+    hot = (2, 20) if clip else ()
+    params, g0 = _c0_shard(1, gdtype, hot=hot)
+    steps = [g0] + [_c0_shard(2 + s, gdtype, hot=hot)[1] for s in range(2)]
+    dev = [p.clone().cuda().requires_grad_(True) for p in params]
+    say("C0 shard", gdtype, "clip", clip)
+    opt = optim.FusedAdamW(dev, lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, order="host", max_norm=clip, working_copy=True)
+    for gs in steps:
+        opt.step(grads=[gr.cuda() for gr in gs])
+    if clip:
+        assert float(opt.grad_norm()) > clip  # the clip did trigger
+    p, m, v, cp = _oracle_steps(oracle, params, steps, 3e-4, 0.1, clip)
+    cat = lambda ts: torch.cat([t.detach().reshape(-1) for t in ts]).cpu()  # noqa: E731
+    assert np.array_equal(bits(cat(dev)).view(np.uint32), p.view(np.uint32))
+    assert np.array_equal(bits(cat([opt.state[i]["exp_avg"] for i in range(len(dev))])).view(np.uint32), m.view(np.uint32))
+    assert np.array_equal(bits(cat([opt.state[i]["exp_avg_sq"] for i in range(len(dev))])).view(np.uint32), v.view(np.uint32))
+    assert np.array_equal(bits(cat(opt.working_copies)), cp)
+
+
+def test_unaligned_views_and_grid_sizes_do_not_move_a_bit(oracle):
+    """Parameters that are views at odd offsets of one buffer take the element
+    path; capping the grid at 1, 7 or 300 blocks changes nothing."""
+    from elysium_wan_amd import optim
+
+    gen = torch.Generator().manual_seed(9)
+    sizes = [1, 7, 8, 4095, 4097, 100003, 3, 65536]
+    flat = torch.randn(sum(sizes) + 1, generator=gen)
+    grads = [torch.randn(n, generator=gen) * 1e-2 for n in sizes]
+    results = []
+    for cap in (0, 1, 7, 300):
+        _set_blocks(cap)
+        try:
+            buf = flat.clone().cuda()
+            ps, o = [], 1  # offset 1: every view is 4 bytes off a 16-byte boundary
+            for n in sizes:
+                ps.append(buf[o : o + n].requires_grad_(True))
+                o += n
+            say("unaligned views, block cap", cap)
+            opt = optim.FusedAdamW(ps, lr=1e-2, betas=(0.9, 0.95), eps=1e-8, order="host", weight_decay=0.1, max_norm=0.5)
+            for _ in range(3):
+                for p, gr in zip(ps, grads):
+                    p.grad = gr.cuda()
+                opt.step()
+            results.append(bits(buf).copy())
+        finally:
+            _set_blocks(0)
+    assert all(np.array_equal(results[0].view(np.uint32), r.view(np.uint32)) for r in results[1:])
+    pf, _, _, _ = _oracle_steps(oracle, [flat[1:]], [[torch.cat(grads)]] * 3, 1e-2, 0.1, 0.5, copies=False)
+    assert np.array_equal(results[0][1:].view(np.uint32), pf.view(np.uint32))
+
+
+def test_torch_order_is_within_one_ulp_of_torch_adamw():
+    """optim.build("adamw") against torch.optim.AdamW (foreach, the GPU
+    default) on the same GPU, 5 steps, weight decay on."""
+    from elysium_wan_amd import optim
+
+    gen = torch.Generator().manual_seed(4)
+    shapes = [(37, 19), (19,), (5, 3, 7), (1001,), (2560, 64)]
+    init = [torch.randn(s, generator=gen) for s in shapes]
+    mine = [t.clone().cuda().requires_grad_(True) for t in init]
+    ref = [t.clone().cuda().requires_grad_(True) for t in init]
+    a = optim.build("adamw", mine, 1e-2, weight_decay=0.1)
+    b = torch.optim.AdamW(ref, lr=1e-2, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
+    say("torch order vs torch.optim.AdamW")
+    for step in range(5):
+        g = torch.Generator().manual_seed(5 + step)
+        gs = [torch.randn(s, generator=g) * 10.0 ** (-step % 4) for s in shapes]
+        for p, q, gr in zip(mine, ref, gs):
+            p.grad = gr.cuda()
+            q.grad = gr.cuda()
+        a.step()
+        b.step()
+    d = [ulp_distance(bits(x.detach()), bits(y.detach())) for x, y in zip(mine, ref)]
+    dm = [ulp_distance(bits(a.state[i]["exp_avg"]), bits(b.state[q]["exp_avg"])) for i, q in enumerate(ref)]
+    worst = max(int(x.max()) for x in d + dm)
+    exact = sum(int((x == 0).sum()) for x in d) / sum(x.size for x in d)
+    say(f"  max ulp {worst}, bit-identical fraction {exact:.6f}")
+    assert worst <= 1
+
+
+def test_state_dict_layout_resume_and_refusals():
+    """The reference's test_host_adamw.py contracts on the GPU: torch's AdamW
+    layout with "moments": "host", a resume continuing bit for bit, another
+    recipe's state refused."""
+    from elysium_wan_amd import optim
+
+    def run(params, opt, lo, hi):
+        for step in range(lo, hi):
+            g = torch.Generator().manual_seed(5 + step)
+            for p in params:
+                p.grad = (torch.randn(p.shape, generator=g) * 10.0 ** (-step % 4)).cuda()
+            opt.step()
+            opt.zero_grad()
+
+    gen = torch.Generator().manual_seed(3)
+    init = [torch.randn(s, generator=gen) for s in [(37, 19), (19,), (5, 3, 7), (1001,)]]
+    full = [t.clone().cuda().requires_grad_(True) for t in init]
+    run(full, optim.build("adamw-host", full, 1e-3), 0, 6)
+    part = [t.clone().cuda().requires_grad_(True) for t in init]
+    opt = optim.build("adamw-host", part, 1e-3)
+    run(part, opt, 0, 3)
+    sd = opt.state_dict()
+    group = dict(sd["param_groups"][0])
+    assert group.pop("moments") == "host" and group["params"] == [0, 1, 2, 3]
+    for i, p in enumerate(part):
+        st = sd["state"][i]
+        assert set(st) == {"step", "exp_avg", "exp_avg_sq"} and float(st["step"]) == 3.0
+        assert st["exp_avg"].device.type == "cpu" and st["exp_avg"].shape == p.shape
+    resumed = [p.detach().clone().requires_grad_(True) for p in part]
+    opt2 = optim.build("adamw-host", resumed, 1e-3)
+    opt2.load_state_dict(sd)
+    run(resumed, opt2, 3, 6)
+    assert all(torch.equal(a.view(torch.int32), b.view(torch.int32)) for a, b in zip(full, resumed))
+    torch_opt = torch.optim.AdamW([torch.zeros(3, requires_grad=True)], lr=1e-3, **ADAMW)
+    with pytest.raises(ValueError, match="another recipe"):
+        optim.build("adamw-host", resumed, 1e-3).load_state_dict(torch_opt.state_dict())
+
+
+def test_on_param_runs_in_parameter_order_and_skips_gradless():
+    from elysium_wan_amd import optim
+
+    ps = [torch.zeros(5, device="cuda", requires_grad=True) for _ in range(4)]
+    for i in (0, 2, 3):
+        ps[i].grad = torch.ones(5, device="cuda")
+    seen = []
+    optim.build("adamw-host", ps, 1e-3).step(on_param=seen.append)
+    assert seen == [0, 2, 3]
+    assert torch.equal(ps[1], torch.zeros(5, device="cuda"))
+
+
+def test_mixed_grad_dtypes_take_one_launch_each(oracle):
+    from elysium_wan_amd import optim
+
+    gen = torch.Generator().manual_seed(8)
+    init = [torch.randn(1000, generator=gen), torch.randn(77, generator=gen)]
+    grads = [torch.randn(1000, generator=gen).bfloat16(), torch.randn(77, generator=gen)]
+    ps = [t.clone().cuda().requires_grad_(True) for t in init]
+    opt = optim.FusedAdamW(ps, lr=1e-3, betas=(0.9, 0.95), eps=1e-8, order="host", max_norm=1.0)
+    opt.step(grads=[g.cuda() for g in grads])
+    p, _, _, _ = _oracle_steps(oracle, init, [grads], 1e-3, 0.0, 1.0, copies=False)
+    got = torch.cat([x.detach().cpu() for x in ps]).numpy()
+    assert np.array_equal(got.view(np.uint32), p.view(np.uint32))

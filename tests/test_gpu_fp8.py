@@ -1,0 +1,176 @@
+"""fp8 boundary codec on the GPU (elysium_wan_amd.fp8 -> libelyhip.so) against
+the oracle, the reference's golden vectors and torch-on-GPU: fp8 bytes,
+exponents and dequantized values bit for bit (model/fp8.py:28-63)."""
+
+from __future__ import annotations
+
+import zlib
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import golden
+from gpu_util import activation, bits, f32_equal, from_bits_bf16, say
+
+pytestmark = pytest.mark.gpu
+
+DT = {"f32": torch.float32, "bf16": torch.bfloat16}
+
+
+def _oracle_in(x: torch.Tensor) -> np.ndarray:
+    return bits(x) if x.dtype == torch.bfloat16 else bits(x).astype(np.float32)
+
+
+def _check_against_oracle(oracle, x: torch.Tensor, fmt: str, per_tensor=False):
+    from elysium_wan_amd import fp8
+
+    xs = x.reshape(1, -1) if per_tensor else x
+    q, k = fp8.quantize(x, fmt, per_tensor=per_tensor)
+    oq, ok = oracle.quantize(_oracle_in(xs), fmt)
+    assert np.array_equal(bits(q).reshape(-1), oq.reshape(-1)), "fp8 bytes"
+    assert np.array_equal(bits(k).reshape(-1), ok.reshape(-1)), "exponents"
+    for out_dt, name in ((torch.float32, "f32"), (torch.bfloat16, "bf16")):
+        d = fp8.dequantize(q, k, out_dt)
+        od = oracle.dequantize(oq, ok, fmt, name)
+        if name == "f32":
+            assert f32_equal(bits(d).reshape(-1), od.reshape(-1)), "dequantize f32"
+        else:
+            assert np.array_equal(bits(d).reshape(-1), od.reshape(-1)), "dequantize bf16"
+    rt = fp8.roundtrip(x, fmt, per_tensor=per_tensor)
+    ort = oracle.roundtrip(_oracle_in(xs), fmt)
+    if x.dtype == torch.bfloat16:
+        assert np.array_equal(bits(rt).reshape(-1), ort.reshape(-1)), "roundtrip bf16"
+    else:
+        assert f32_equal(bits(rt).reshape(-1), ort.reshape(-1)), "roundtrip f32"
+    assert torch.equal(bits_t(rt), bits_t(fp8.dequantize(q, k, x.dtype))), "fused roundtrip == quantize+dequantize"
+
+
+def bits_t(t: torch.Tensor) -> torch.Tensor:
+    return t.view(torch.int16) if t.dtype == torch.bfloat16 else t.view(torch.int32)
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+@pytest.mark.parametrize("dname", ["bf16", "f32"])
+@pytest.mark.parametrize(
+    "shape",
+    [(4, 1024, 768), (16, 2560), (7, 8192), (3, 4096 + 8), (5, 1000), (3, 7), (2, 1), (9, 16384 + 24), (1, 3 * 65536 + 5)],
+)
+def test_quantize_dequantize_roundtrip_equal_the_oracle(oracle, fmt, dname, shape):
+    say("fp8 vs oracle", fmt, dname, shape)
+    x = activation(shape, seed=zlib.crc32(repr((fmt, dname, shape)).encode()) % 1000, dtype=DT[dname])
+    _check_against_oracle(oracle, x, fmt)
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+def test_per_tensor_scaling_equals_the_oracle(oracle, fmt):
+    say("fp8 per-tensor", fmt)
+    x = activation((4, 1024, 768), seed=3)  # config C0's activation, one exponent
+    _check_against_oracle(oracle, x, fmt, per_tensor=True)
+
+
+def test_unaligned_and_strided_inputs(oracle):
+    """A row view that starts off a 16-byte boundary takes the element path."""
+    base = activation((4 * 777 + 3,), seed=5)
+    x = base[3:].reshape(4, 777)
+    say("fp8 unaligned", x.data_ptr() % 16)
+    _check_against_oracle(oracle, x, "e4m3")
+    t = activation((64, 96), seed=6).t()  # non-contiguous: made contiguous first
+    _check_against_oracle(oracle, t, "e5m2")
+
+
+def test_extreme_rows_equal_torch_on_the_gpu(oracle):
+    """Rows whose scale 2^-k or 2^k leaves the dtype's range (subnormal rows,
+    huge rows), NaN and Inf rows: the kernels' exact-arithmetic path against
+    the reference's own torch expressions evaluated on this GPU, NaN signs
+    included (model/fp8.py:28-53)."""
+    from elysium_wan_amd import fp8
+
+    g = golden("fp8_rows.npz")
+    for fmt, tdt in (("e4m3", torch.float8_e4m3fn), ("e5m2", torch.float8_e5m2)):
+        for dname in ("bf16", "f32"):
+            pre = f"{fmt}_{dname}"
+            for key in ("x", "sx"):
+                raw = g[f"{pre}_{key}"]
+                x = from_bits_bf16(raw, "cuda") if dname == "bf16" else torch.from_numpy(raw.astype(np.float32)).cuda()
+                say("fp8 extreme rows", pre, key)
+                _, eb = fp8.FORMATS[fmt]
+                amax = x.abs().amax(dim=-1, keepdim=True)
+                _, e = torch.frexp(amax)
+                kref = torch.where(amax > 0, (e - eb).to(torch.int32), torch.zeros_like(e, dtype=torch.int32))
+                qref = (x * torch.exp2((-kref).to(x.dtype))).to(tdt)
+                dref = qref.to(x.dtype) * torch.exp2(kref.to(x.dtype))
+                q, k = fp8.quantize(x, fmt)
+                assert torch.equal(k, kref)
+                assert np.array_equal(bits(q), bits(qref))
+                d = fp8.dequantize(q, k, x.dtype)
+                if dname == "bf16":
+                    assert np.array_equal(bits(d), bits(dref))
+                else:
+                    assert f32_equal(bits(d), bits(dref))
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+@pytest.mark.parametrize("dname", ["f32", "bf16"])
+def test_reference_golden_rows_on_the_gpu(fmt, dname):
+    """The reference's own outputs (made on x86) through the GPU path; a NaN
+    made inside the arithmetic is compared as NaN (its sign is the device's)."""
+    from elysium_wan_amd import fp8
+
+    g = golden("fp8_rows.npz")
+    pre = f"{fmt}_{dname}"
+    raw = g[f"{pre}_x"]
+    x = from_bits_bf16(raw, "cuda") if dname == "bf16" else torch.from_numpy(raw.astype(np.float32)).cuda()
+    say("fp8 golden rows", pre)
+    q, k = fp8.quantize(x, fmt)
+    assert np.array_equal(bits(k).reshape(-1), g[f"{pre}_qk"])
+    qb, want = bits(q), g[f"{pre}_q"]
+    nan = ((qb & 0x7F) == 0x7F) if fmt == "e4m3" else ((qb & 0x7F) > 0x7C)
+    nanw = ((want & 0x7F) == 0x7F) if fmt == "e4m3" else ((want & 0x7F) > 0x7C)
+    assert np.array_equal(nan, nanw) and np.array_equal(qb[~nan], want[~nanw])
+    d = fp8.dequantize(q, k)
+    assert f32_equal(bits(d), g[f"{pre}_deq_f32"])
+
+
+def test_full_size_activation_c1_properties(oracle):
+    """Config C1's activation [8, 2048, 2560] (e4m3) and gradient (e5m2):
+    fused == unfused, every fp8-normal element within half an fp8 ulp of x,
+    and 512 seeded rows bit-identical to the oracle."""
+    from elysium_wan_amd import fp8
+
+    for fmt, seed, mant in (("e4m3", 11, 3), ("e5m2", 12, 2)):
+        say("fp8 C1 full size", fmt)
+        x = activation((8, 2048, 2560), seed=seed)
+        q, k = fp8.quantize(x, fmt)
+        rt = fp8.roundtrip(x, fmt)
+        assert torch.equal(bits_t(rt), bits_t(fp8.dequantize(q, k, torch.bfloat16)))
+        xf, rf = x.float(), rt.float()
+        scale = torch.exp2(k.float())
+        normal = xf.abs() >= scale * (2.0 ** (-6 if fmt == "e4m3" else -14))
+        err = ((rf - xf).abs() / xf.abs().clamp_min(1e-30))[normal]
+        assert float(err.max()) <= 2.0 ** -(mant + 1) * (1 + 1e-6)
+        rows = torch.randperm(16384, generator=torch.Generator().manual_seed(seed))[:512]
+        xr = x.reshape(16384, 2560)[rows.cuda()]
+        oq, ok = oracle.quantize(bits(xr), fmt)
+        assert np.array_equal(bits(q.reshape(16384, 2560)[rows.cuda()]), oq)
+        assert np.array_equal(bits(k.reshape(-1)[rows.cuda()]), ok)
+
+
+def test_scale_exp_is_the_quantize_exponent():
+    from elysium_wan_amd import fp8
+
+    x = activation((33, 2560), seed=13)
+    _, k = fp8.quantize(x, "e4m3")
+    assert torch.equal(fp8.scale_exp(x, "e4m3"), k)
+
+
+def test_empty_inputs():
+    from elysium_wan_amd import fp8
+
+    x = torch.empty(0, 64, dtype=torch.bfloat16, device="cuda")
+    q, k = fp8.quantize(x)
+    assert q.shape == (0, 64) and k.shape == (0, 1)
+    assert fp8.dequantize(q, k).shape == (0, 64)
+    z = torch.empty(3, 0, dtype=torch.bfloat16, device="cuda")
+    q, k = fp8.quantize(z)
+    assert k.shape == (3, 1) and int(k.abs().sum()) == 0

@@ -1,0 +1,121 @@
+"""The deterministic global grad-norm on the GPU: within 1e-6 relative of the
+oracle's brute-force sum, bitwise identical across runs and grid sizes, and
+the clip coefficient and in-place clip of torch's clip_grad_norm_
+(TORCH/nn/utils/clip_grad.py:50-183; the reference itself never clips)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import bits, say
+
+pytestmark = pytest.mark.gpu
+
+
+def _norm(grads, max_norm=1.0):
+    from elysium_wan_amd import _lib
+
+    L = _lib.load()
+    dev = grads[0].device
+    res = torch.zeros(16, dtype=torch.uint8, device=dev)
+    arr = _lib.tensor_array(grads)
+    ws = _lib.workspace(dev, L.ely_grad_norm_workspace_bytes(arr, len(grads)))
+    _lib.check(L.ely_grad_norm(arr, len(grads), float(max_norm), res.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_ptr(dev)), "norm")
+    r = res.cpu().numpy()
+    return float(r[:8].view(np.float64)[0]), float(r[8:12].view(np.float32)[0]), float(r[12:16].view(np.float32)[0]), r.copy()
+
+
+def _ragged(seed, n_vec=1000, n_mat=3, d=6144, cols=1024, dtype=torch.bfloat16):
+    """Config C3's layout at reduced matrix size: vectors of d interleaved
+    with d x cols matrices; Student-t (df 3) x 1e-4 values."""
+    gen = torch.Generator().manual_seed(seed)
+    torch.manual_seed(seed)  # StudentT samples from the global generator
+    t = torch.distributions.StudentT(3.0)
+    out = []
+    per = max(1, n_vec // max(1, n_mat))
+    for i in range(n_vec):
+        out.append((t.sample((d,)) * 1e-4).to(dtype))
+        if i % per == per - 1 and len(out) < n_vec + n_mat:
+            out.append((torch.randn(d, cols, generator=gen) * 1e-4).to(dtype))
+    return [g.cuda() for g in out]
+
+
+def test_norm_is_within_1e6_of_the_brute_force_sum(oracle):
+    gs = _ragged(1)
+    say("norm ragged C3-like", len(gs), sum(g.numel() for g in gs))
+    sumsq, norm, coef, _ = _norm(gs, 1.0)
+    ref = oracle.sumsq([bits(g) for g in gs])
+    assert abs(sumsq - ref) <= 1e-6 * ref
+    assert norm == float(np.float32(np.sqrt(sumsq)))
+    assert coef == oracle.clip_coef(norm, 1.0)
+
+
+def test_norm_is_bitwise_reproducible_across_runs_and_grids():
+    from elysium_wan_amd import _lib
+
+    gs = _ragged(2) + [torch.randn(1000003, device="cuda") * 1e-3]
+    gs.append(torch.randn(77, device="cuda")[1:])  # unaligned fp32 view
+    runs = []
+    for cap in (0, 0, 0, 0, 0, 1, 13, 999):
+        _lib.check(_lib.load().ely_set_max_blocks(cap), "cap")
+        try:
+            say("norm run, cap", cap)
+            runs.append(_norm(gs)[3])
+        finally:
+            _lib.load().ely_set_max_blocks(0)
+    assert all(np.array_equal(runs[0], r) for r in runs[1:])
+
+
+def test_alignment_does_not_move_a_bit():
+    base = torch.randn(200001, device="cuda")
+    a = base[:200000].clone()
+    b = base[1:].clone()
+    b.copy_(a)  # same values, now 16-byte aligned
+    buf = torch.empty(200001, device="cuda")
+    buf[1:].copy_(a)
+    say("norm alignment")
+    assert np.array_equal(_norm([a])[3], _norm([buf[1:]])[3])
+
+
+def test_non_finite_gradients_follow_torch():
+    g = torch.ones(100, device="cuda")
+    g[3] = float("inf")
+    _, norm, coef, _ = _norm([g])
+    assert np.isinf(norm) and coef == 0.0
+    g[3] = float("nan")
+    _, norm, coef, _ = _norm([g])
+    assert np.isnan(norm) and np.isnan(coef)
+
+
+def test_clip_grad_norm_matches_torch(oracle):
+    """elysium_wan_amd.optim.clip_grad_norm_ against torch's own on fp32
+    grads: the same total norm to 1e-6 and g * coef bit for bit given the
+    coefficient (torch sums in fp32, this build in fp64)."""
+    from elysium_wan_amd import optim
+
+    gen = torch.Generator().manual_seed(3)
+    shapes = [(300, 7), (5000,), (3,)]
+    base = [torch.randn(s, generator=gen) * 0.3 for s in shapes]
+    ps = [torch.zeros(s, device="cuda", requires_grad=True) for s in shapes]
+    qs = [torch.zeros(s, device="cuda", requires_grad=True) for s in shapes]
+    for p, q, g in zip(ps, qs, base):
+        p.grad = g.cuda()
+        q.grad = g.cuda()
+    say("clip_grad_norm_ drop-in")
+    mine = optim.clip_grad_norm_(ps, 1.0)
+    ref = torch.nn.utils.clip_grad_norm_(qs, 1.0)
+    assert abs(float(mine) - float(ref)) <= 1e-6 * float(ref)
+    coef = oracle.clip_coef(float(mine), 1.0)
+    for p, g in zip(ps, base):
+        want = (g.numpy() * np.float32(coef)).astype(np.float32)
+        assert np.array_equal(bits(p.grad).view(np.uint32), want.view(np.uint32))
+    # bf16 gradients are scaled in fp32 and rounded once to bf16
+    h = [torch.randn(4097, device="cuda").bfloat16() * 3]
+    hp = [torch.zeros(4097, device="cuda", dtype=torch.bfloat16, requires_grad=True)]
+    hp[0].grad = h[0].clone()
+    total = optim.clip_grad_norm_(hp, 1.0)
+    c = oracle.clip_coef(float(total), 1.0)
+    want = oracle.f32_to_bf16_bits(oracle.bf16_bits_to_f32(bits(h[0])) * np.float32(c))
+    assert np.array_equal(bits(hp[0].grad), want)

@@ -1,0 +1,48 @@
+"""The pieces kernels on the GPU: the fp32 -> bf16 working-copy cast bit for
+bit against torch-on-GPU's `.to(bfloat16)` (NaN, Inf, ties, subnormals
+included) and the oracle, and the ordered fp32 fold (runtime/pieces.py)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import bits, say
+
+pytestmark = pytest.mark.gpu
+
+
+def test_cast_piece_equals_torch_on_the_gpu(oracle):
+    from elysium_wan_amd import pieces
+
+    g = torch.Generator().manual_seed(0)
+    u = torch.randint(-(1 << 31), 1 << 31, (3_000_001,), generator=g, dtype=torch.int64).to(torch.int32)
+    ties = (torch.randint(0, 1 << 16, (10000,), generator=g, dtype=torch.int64) << 16 | 0x8000).to(torch.int32)
+    x = torch.cat([u, ties]).view(torch.float32).cuda()
+    for view in (x, x[1:]):  # aligned and 4 bytes off
+        say("cast_piece", view.data_ptr() % 16)
+        got = pieces.cast_piece(view, torch.bfloat16)
+        assert got.data_ptr() != view.data_ptr()
+        assert np.array_equal(bits(got), bits(view.to(torch.bfloat16)))
+        assert np.array_equal(bits(got), oracle.f32_to_bf16_bits(bits(view)))
+
+
+def test_fold_is_widen_then_add_in_order(oracle):
+    from elysium_wan_amd import pieces
+
+    gen = torch.Generator().manual_seed(1)
+    parts = [torch.randn(100003, generator=gen).bfloat16() for _ in range(3)] + [torch.randn(100003, generator=gen)]
+    say("fold")
+    acc = pieces.fold([p.cuda() for p in parts])
+    ref = parts[0].float().numpy().copy()
+    for p in parts[1:]:
+        oracle.fold_add(ref, bits(p) if p.dtype == torch.bfloat16 else p.numpy())
+    assert np.array_equal(bits(acc).view(np.uint32), ref.view(np.uint32))
+    # tests/unit/test_stream_fold.py:213-236: a bf16 part folded into an fp32
+    # sum equals widen-then-add
+    a = torch.randn(5000, device="cuda")
+    b = torch.randn(5000, device="cuda").bfloat16()
+    want = a + b.float()
+    pieces.fold_add(a, b)
+    assert torch.equal(a, want)
