@@ -5,12 +5,14 @@ Python signatures.
 Modules mirror the reference's:
   optim   -- runtime/optim.py   (build, hparams, state_bytes_per_param, the
              fused clip + AdamW + bf16 working copy, clip_grad_norm_)
-  fp8     -- model/fp8.py       (scale_exp, quantize, dequantize, roundtrip)
+  fp8     -- model/fp8.py       (scale_exp, quantize, dequantize, roundtrip,
+             recover_exp)
   pieces  -- runtime/pieces.py  (cast_piece, fold_start, fold_add, fold)
+  planes  -- codec/planes.py    (encode_scaled_fp8, decode: the scaled-fp8 wire)
 The kernels live in libelyhip.so (C ABI: include/ely.h), built by
 elysium_wan_amd.build for gfx950.
 """
 
-from . import fp8, optim, pieces  # noqa: F401
+from . import fp8, optim, pieces, planes  # noqa: F401
 
-__all__ = ["fp8", "optim", "pieces"]
+__all__ = ["fp8", "optim", "pieces", "planes"]

@@ -34,6 +34,9 @@ EXPORTS = (
     "ely_fp8_quantize",
     "ely_fp8_dequantize",
     "ely_fp8_roundtrip",
+    "ely_fp8_recover_workspace_bytes",
+    "ely_fp8_recover_exp",
+    "ely_fp8_quantize_k",
     "ely_cast_bf16",
     "ely_fold_add",
     "ely_scale_inplace",
@@ -88,6 +91,10 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
         L.ely_fp8_quantize.argtypes = [P, I32, I64, I64, I32, P, P, P, I64, P]
         L.ely_fp8_dequantize.argtypes = [P, P, I64, I64, I32, P, I32, P]
         L.ely_fp8_roundtrip.argtypes = [P, I32, I64, I64, I32, P, P, P, P, I64, P]
+        L.ely_fp8_recover_workspace_bytes.restype = I64
+        L.ely_fp8_recover_workspace_bytes.argtypes = [I64]
+        L.ely_fp8_recover_exp.argtypes = [P, I32, I64, I64, I32, P, P, P, I64, P]
+        L.ely_fp8_quantize_k.argtypes = [P, I32, I64, I64, I32, P, P, P]
         L.ely_cast_bf16.argtypes = [P, P, I64, P]
         L.ely_fold_add.argtypes = [P, P, I32, I64, P]
         L.ely_scale_inplace.argtypes = [TP, I32, P, P]

@@ -360,6 +360,104 @@ __global__ __launch_bounds__(kQBlock) void dequant_kernel(const uint8_t* __restr
     }
 }
 
+// ------------------------------------------------------- recover_exp / wire
+
+// Bit i of the candidate mask stands for offset kDeltas[i] (fp8.py:25).
+__constant__ int kDeltas[5] = {0, -1, 1, -2, 2};
+
+// Is v (a value of the tensor's dtype) exactly fp8(v * 2^-c) * 2^c in that
+// dtype's arithmetic (fp8.py:85-86)?  `fast` rows use the conversion
+// instructions: every candidate's 2^+-c is a normal power of two there and
+// every product exact, so the test is just whether v * 2^-c lies on the fp8
+// grid; non-finite elements always take the restatement.
+template <int FMT, bool BF16>
+__device__ __forceinline__ bool exact_at(float v, int c, bool fast) {
+    if (fast && __builtin_isfinite(v)) {
+        const float y = v * __uint_as_float((uint32_t)(127 - c) << 23);
+        const uint32_t code = cvt_pk_fp8<FMT, false>(y, 0.0f, 0u) & 0xFFu;
+        float back, unused;
+        cvt_pk_f32<FMT, false>(code, back, unused);
+        return back * __uint_as_float((uint32_t)(127 + c) << 23) == v;
+    }
+    const float y = round_to(v * pow2_dtype(-c, BF16), BF16);
+    const uint32_t code = fp8_from_f32_sw<FMT>(y);
+    const float back = round_to(round_to(fp8_to_f32_sw<FMT>(code), BF16) * pow2_dtype(c, BF16), BF16);
+    return back == v;
+}
+
+__device__ __forceinline__ uint32_t wave_and_u32(uint32_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v &= (uint32_t)__shfl_xor((int)v, o, kWave);
+    return v;
+}
+
+// Per (row, segment): AND of the exactness masks of the segment's elements,
+// folded into rowmask[row] (set to all candidates beforehand).
+template <int FMT, bool BF16>
+__global__ __launch_bounds__(kQBlock) void recover_mask_kernel(const void* __restrict__ t, int64_t rows, int64_t cols,
+                                                               int64_t segs, const uint32_t* __restrict__ rowmax,
+                                                               uint32_t* __restrict__ rowmask) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t gw = (int64_t)blockIdx.x * kWavesPerBlock + wave_uniform(threadIdx.x / kWave);
+    const int64_t row = gw / segs, seg = gw % segs;
+    if (row >= rows) return;
+    const int base = scale_exp_from_amax<FMT>(to_f32_bits<BF16>(rowmax[row]));
+    const bool fast = base - 2 >= -kFastK && base + 2 <= kFastK;
+    const int64_t e0 = seg * kSegElems, e1 = min(e0 + kSegElems, cols);
+    uint32_t mask = 0x1Fu;
+    for (int64_t e = e0 + lane; e < e1; e += kWave) {
+        const float v = load_x<BF16>(t, row * cols + e);
+#pragma unroll
+        for (int i = 0; i < 5; ++i)
+            if ((mask >> i) & 1u)
+                if (!exact_at<FMT, BF16>(v, base + kDeltas[i], fast)) mask &= ~(1u << i);
+    }
+    mask = wave_and_u32(mask);
+    if (lane == 0 && mask != 0x1Fu) atomicAnd(rowmask + row, mask);
+}
+
+// k = base + the first exact offset; a row with none counts as bad and keeps
+// the last candidate, as the reference's `best` does (fp8.py:82-93).
+template <int FMT, bool BF16>
+__global__ void recover_final_kernel(int64_t rows, const uint32_t* __restrict__ rowmax,
+                                     const uint32_t* __restrict__ rowmask, int32_t* __restrict__ k,
+                                     unsigned long long* __restrict__ bad) {
+    for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < rows; r += (int64_t)gridDim.x * blockDim.x) {
+        const int base = scale_exp_from_amax<FMT>(to_f32_bits<BF16>(rowmax[r]));
+        const uint32_t m = rowmask[r];
+        int kk = base + 2;
+        if (m == 0u) {
+            atomicAdd(bad, 1ull);
+        } else {
+            kk = base + kDeltas[__builtin_ctz(m)];
+        }
+        k[r] = kk;
+    }
+}
+
+// q = fp8(x * 2^-k) with the caller's k per row (planes.py:110-111): the
+// wire image of a tensor whose exponents recover_exp found.
+template <int FMT, bool BF16>
+__global__ __launch_bounds__(kQBlock) void quant_k_kernel(const void* __restrict__ x, int64_t rows, int64_t cols,
+                                                          int64_t segs, const int32_t* __restrict__ kin,
+                                                          uint8_t* __restrict__ q) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t gw = (int64_t)blockIdx.x * kWavesPerBlock + wave_uniform(threadIdx.x / kWave);
+    const int64_t row = gw / segs, seg = gw % segs;
+    if (row >= rows) return;
+    const int kk = kin[row];
+    const bool fast = kk >= -kFastK && kk <= kFastK;
+    const float s_down = fast ? __uint_as_float((uint32_t)(127 - kk) << 23) : pow2_dtype(-kk, BF16);
+    const int64_t e0 = seg * kSegElems, e1 = min(e0 + kSegElems, cols);
+    for (int64_t e = e0 + lane; e < e1; e += kWave) {
+        const float v = load_x<BF16>(x, row * cols + e);
+        uint32_t c;
+        if (fast && __builtin_isfinite(v)) c = cvt_pk_fp8<FMT, false>(v * s_down, 0.0f, 0u) & 0xFFu;
+        else c = quant_sw<FMT, BF16>(v, s_down);
+        q[row * cols + e] = (uint8_t)c;
+    }
+}
+
 // --------------------------------------------------------------- self-test
 
 template <int FMT>
@@ -612,6 +710,96 @@ int ely_selftest_sqrt(uint32_t start, uint64_t count, unsigned long long* mismat
         const unsigned blocks = (unsigned)std::min<uint64_t>((count + 255) / 256, 65536);
         hipLaunchKernelGGL(selftest_sqrt_kernel, dim3(blocks), dim3(256), 0, s, start, count, mismatches_dev);
         check_launch("selftest_sqrt_kernel");
+    });
+}
+
+int64_t ely_fp8_recover_workspace_bytes(int64_t rows) {
+    if (rows < 0) return -1;
+    return (int64_t)(2 * split_ws_bytes(rows));
+}
+
+int ely_fp8_recover_exp(const void* t, int32_t t_dtype, int64_t rows, int64_t cols, int32_t fmt, int32_t* k,
+                        unsigned long long* bad_rows_dev, void* workspace, int64_t ws_bytes, void* stream) {
+    return guarded([&] {
+        check_fmt(fmt);
+        check_dtype(t_dtype, "t_dtype");
+        check_shape(rows, cols);
+        if (rows == 0) return;
+        if (!k || !bad_rows_dev || (cols > 0 && !t)) fail(ELY_EINVAL, "ely_fp8_recover_exp: null pointer");
+        if (!workspace || ws_bytes < ely_fp8_recover_workspace_bytes(rows))
+            fail(ELY_EWORKSPACE, "ely_fp8_recover_exp: workspace smaller than ely_fp8_recover_workspace_bytes");
+        hipStream_t s = static_cast<hipStream_t>(stream);
+        uint32_t* rowmax = static_cast<uint32_t*>(workspace);
+        uint32_t* rowmask = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + split_ws_bytes(rows));
+        const unsigned fb = (unsigned)std::min<int64_t>((rows + 255) / 256, 4096);
+        hipLaunchKernelGGL(fill_u32_kernel, dim3(fb), dim3(256), 0, s, rowmax, rows, 0u);
+        check_launch("fill_u32_kernel");
+        hipLaunchKernelGGL(fill_u32_kernel, dim3(fb), dim3(256), 0, s, rowmask, rows, 0x1Fu);
+        check_launch("fill_u32_kernel");
+        const bool bf16 = t_dtype == ELY_BF16;
+        if (cols > 0) {
+            const int64_t segs = (cols + kSegElems - 1) / kSegElems;
+            if (rows > INT64_MAX / segs) fail(ELY_EINVAL, "too many segments");
+            const unsigned blocks = blocks_for_waves(rows * segs);
+            if (bf16)
+                hipLaunchKernelGGL(rowmax_split_kernel<true>, dim3(blocks), dim3(kQBlock), 0, s, t, rows, cols, segs, 0,
+                                   rowmax);
+            else
+                hipLaunchKernelGGL(rowmax_split_kernel<false>, dim3(blocks), dim3(kQBlock), 0, s, t, rows, cols, segs,
+                                   0, rowmax);
+            check_launch("rowmax_split_kernel");
+#define ELY_RECOVER_MASK(F, B)                                                                                    \
+    hipLaunchKernelGGL((recover_mask_kernel<F, B>), dim3(blocks), dim3(kQBlock), 0, s, t, rows, cols, segs,        \
+                       (const uint32_t*)rowmax, rowmask)
+            if (fmt == ELY_E4M3) {
+                if (bf16) ELY_RECOVER_MASK(kE4M3, true);
+                else ELY_RECOVER_MASK(kE4M3, false);
+            } else {
+                if (bf16) ELY_RECOVER_MASK(kE5M2, true);
+                else ELY_RECOVER_MASK(kE5M2, false);
+            }
+#undef ELY_RECOVER_MASK
+            check_launch("recover_mask_kernel");
+        }
+#define ELY_RECOVER_FINAL(F, B)                                                                                   \
+    hipLaunchKernelGGL((recover_final_kernel<F, B>), dim3(fb), dim3(256), 0, s, rows, (const uint32_t*)rowmax,      \
+                       (const uint32_t*)rowmask, k, bad_rows_dev)
+        if (fmt == ELY_E4M3) {
+            if (bf16) ELY_RECOVER_FINAL(kE4M3, true);
+            else ELY_RECOVER_FINAL(kE4M3, false);
+        } else {
+            if (bf16) ELY_RECOVER_FINAL(kE5M2, true);
+            else ELY_RECOVER_FINAL(kE5M2, false);
+        }
+#undef ELY_RECOVER_FINAL
+        check_launch("recover_final_kernel");
+    });
+}
+
+int ely_fp8_quantize_k(const void* x, int32_t x_dtype, int64_t rows, int64_t cols, int32_t fmt, const int32_t* k,
+                       uint8_t* q, void* stream) {
+    return guarded([&] {
+        check_fmt(fmt);
+        check_dtype(x_dtype, "x_dtype");
+        check_shape(rows, cols);
+        if (rows * cols == 0) return;
+        if (!x || !k || !q) fail(ELY_EINVAL, "ely_fp8_quantize_k: null pointer");
+        hipStream_t s = static_cast<hipStream_t>(stream);
+        const int64_t segs = (cols + kSegElems - 1) / kSegElems;
+        if (rows > INT64_MAX / segs) fail(ELY_EINVAL, "too many segments");
+        const unsigned blocks = blocks_for_waves(rows * segs);
+        const bool bf16 = x_dtype == ELY_BF16;
+#define ELY_QK(F, B) \
+    hipLaunchKernelGGL((quant_k_kernel<F, B>), dim3(blocks), dim3(kQBlock), 0, s, x, rows, cols, segs, k, q)
+        if (fmt == ELY_E4M3) {
+            if (bf16) ELY_QK(kE4M3, true);
+            else ELY_QK(kE4M3, false);
+        } else {
+            if (bf16) ELY_QK(kE5M2, true);
+            else ELY_QK(kE5M2, false);
+        }
+#undef ELY_QK
+        check_launch("quant_k_kernel");
     });
 }
 

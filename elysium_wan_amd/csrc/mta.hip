@@ -28,12 +28,54 @@
 
 namespace ely {
 
-constexpr int64_t kAdamTile = 4096;     // elements per AdamW tile
-constexpr int64_t kNormTile = 16384;    // elements per grad-norm tile (one wave)
+// Compile-time tunables (chosen by measurement on MI355X; see the defaults).
+#ifndef ELY_ADAM_TILE
+#define ELY_ADAM_TILE 16384      // elements per AdamW tile
+#endif
+#ifndef ELY_ADAM_SCHED
+#define ELY_ADAM_SCHED 1         // 0: contiguous tile range per block, 1: interleaved rounds
+#endif
+#ifndef ELY_NORM_SCHED
+#define ELY_NORM_SCHED 0         // same choice for the grad-norm waves
+#endif
+#ifndef ELY_NORM_NT
+#define ELY_NORM_NT 0            // nontemporal grad-norm loads
+#endif
+#ifndef ELY_NORM_UNROLL
+#define ELY_NORM_UNROLL 4        // 16-byte loads a grad-norm lane keeps in flight
+#endif
+#ifndef ELY_NT
+#define ELY_NT 0                 // bit 0: nontemporal AdamW loads, bit 1: nontemporal stores
+#endif
+#ifndef ELY_ADAM_UNROLL
+#define ELY_ADAM_UNROLL 1        // 8-element groups a thread keeps in flight (1 or 2)
+#endif
+#ifndef ELY_ADAM_BPC
+#define ELY_ADAM_BPC 8           // AdamW blocks per compute unit
+#endif
+#ifndef ELY_NORM_BPC
+#define ELY_NORM_BPC 8           // grad-norm blocks (of 4 waves) per compute unit
+#endif
+
+constexpr int64_t kAdamTile = ELY_ADAM_TILE;
+constexpr int64_t kNormTile = 16384;    // elements per grad-norm tile (one wave): fixes the summation order
 constexpr int kBlock = 256;
 constexpr int kFinalThreads = 1024;
 
 // --------------------------------------------------------------- (a) norm
+
+// Last tensor whose first tile is <= tile (binary search over the table).
+template <class Desc>
+__device__ __forceinline__ int find_tensor(const Desc* desc, int n, int64_t tile) {
+    int lo = 0, hi = n - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (desc[mid].tile_begin <= tile) lo = mid;
+        else hi = mid - 1;
+    }
+    return lo;
+}
+
 
 struct NormDesc {          // 32 bytes
     const void* g;
@@ -50,33 +92,62 @@ __device__ __forceinline__ float sq8(const float (&x)[8]) {
     return ((s0 + s1) + (s2 + s3)) + ((s4 + s5) + (s6 + s7));
 }
 
-__device__ __forceinline__ void load8(const NormDesc& d, int64_t i, int64_t end, float (&x)[8]) {
-    if (d.aligned && i + 8 <= end) {
-        if (d.dtype == ELY_BF16) {
-            uint4 w = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(d.g) + i);
-            uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+// Pointers read from the descriptor table are generic to the compiler; cast
+// them to the global address space so accesses are global_load/global_store
+// (flat accesses also count against the LDS/scalar counter and serialize).
+#define ELY_GLOBAL __attribute__((address_space(1)))
+template <typename T>
+__device__ __forceinline__ ELY_GLOBAL T* gp(T* p) {
+    return (ELY_GLOBAL T*)p;
+}
+template <typename T>
+__device__ __forceinline__ const ELY_GLOBAL T* gp(const T* p) {
+    return (const ELY_GLOBAL T*)p;
+}
+
+typedef float nf32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t nu32x4 __attribute__((ext_vector_type(4)));
+
+template <typename T>
+__device__ __forceinline__ T ld_norm(const ELY_GLOBAL T* p) {
+#if ELY_NORM_NT
+    return __builtin_nontemporal_load(p);
+#else
+    return *p;
+#endif
+}
+
+// 8 consecutive gradient values from a 16-byte aligned address.
+__device__ __forceinline__ void load8_vec(const NormDesc& d, int64_t i, float (&x)[8]) {
+    if (d.dtype == ELY_BF16) {
+        const nu32x4 w = ld_norm(gp(reinterpret_cast<const nu32x4*>(static_cast<const uint16_t*>(d.g) + i)));
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                x[2 * j] = bf16_to_f32(ws[j] & 0xFFFFu);
-                x[2 * j + 1] = bf16_to_f32(ws[j] >> 16);
-            }
-        } else {
-            const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(d.g) + i);
-            float4 a = p[0], b = p[1];
-            x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
-            x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+        for (int j = 0; j < 4; ++j) {
+            x[2 * j] = bf16_to_f32(w[j] & 0xFFFFu);
+            x[2 * j + 1] = bf16_to_f32(w[j] >> 16);
         }
     } else {
+        const ELY_GLOBAL nf32x4* p = gp(reinterpret_cast<const nf32x4*>(static_cast<const float*>(d.g) + i));
+        const nf32x4 a = ld_norm(p), b = ld_norm(p + 1);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            int64_t e = i + j;
-            float v = 0.0f;
-            if (e < end) {
-                v = d.dtype == ELY_BF16 ? bf16_to_f32(static_cast<const uint16_t*>(d.g)[e])
-                                        : static_cast<const float*>(d.g)[e];
-            }
-            x[j] = v;
+        for (int j = 0; j < 4; ++j) {
+            x[j] = a[j];
+            x[4 + j] = b[j];
         }
+    }
+}
+
+// The same 8 values element by element (0 past `end`): any alignment.
+__device__ __forceinline__ void load8_any(const NormDesc& d, int64_t i, int64_t end, float (&x)[8]) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int64_t e = i + j;
+        float v = 0.0f;
+        if (e < end) {
+            v = d.dtype == ELY_BF16 ? bf16_to_f32(*gp(static_cast<const uint16_t*>(d.g) + e))
+                                    : *gp(static_cast<const float*>(d.g) + e);
+        }
+        x[j] = v;
     }
 }
 
@@ -85,27 +156,33 @@ __global__ __launch_bounds__(kBlock) void norm_partials_kernel(const NormDesc* _
     const int lane = threadIdx.x & (kWave - 1);
     const int64_t waves = (int64_t)gridDim.x * (kBlock / kWave);
     const int64_t w = (int64_t)blockIdx.x * (kBlock / kWave) + wave_uniform(threadIdx.x / kWave);
-    const int64_t t0 = w * total_tiles / waves, t1 = (w + 1) * total_tiles / waves;
+#if ELY_NORM_SCHED == 0
+    const int64_t t0 = w * total_tiles / waves, t1 = (w + 1) * total_tiles / waves, tstep = 1;
+#else
+    const int64_t t0 = w, t1 = total_tiles, tstep = waves;
+#endif
     if (t0 >= t1) return;
-    int lo = 0, hi = n - 1;  // last tensor whose first tile is <= t0
-    while (lo < hi) {
-        int mid = (lo + hi + 1) >> 1;
-        if (desc[mid].tile_begin <= t0) lo = mid;
-        else hi = mid - 1;
-    }
-    int ti = lo;
-    for (int64_t tile = t0; tile < t1; ++tile) {
+    int ti = find_tensor(desc, n, t0);
+    for (int64_t tile = t0; tile < t1; tile += tstep) {
         while (ti + 1 < n && desc[ti + 1].tile_begin <= tile) ++ti;
         const NormDesc d = desc[ti];
         const int64_t e0 = (tile - d.tile_begin) * kNormTile;
         const int64_t e1 = min(e0 + kNormTile, d.numel);
         double acc = 0.0;
-#pragma unroll 4
-        for (int j = 0; j < (int)(kNormTile / (kWave * 8)); ++j) {
-            const int64_t i = e0 + ((int64_t)j * kWave + lane) * 8;
-            float x[8];
-            load8(d, i, e1, x);
-            acc += (double)sq8(x);
+        // lane l owns groups j*64 + l of 8 elements, in the same order on both paths
+        if (d.aligned && e1 - e0 == kNormTile) {
+#pragma unroll ELY_NORM_UNROLL
+            for (int j = 0; j < (int)(kNormTile / (kWave * 8)); ++j) {
+                float x[8];
+                load8_vec(d, e0 + ((int64_t)j * kWave + lane) * 8, x);
+                acc += (double)sq8(x);
+            }
+        } else {
+            for (int j = 0; j < (int)(kNormTile / (kWave * 8)); ++j) {
+                float x[8];
+                load8_any(d, e0 + ((int64_t)j * kWave + lane) * 8, e1, x);
+                acc += (double)sq8(x);
+            }
         }
         acc = wave_sum_f64(acc);
         if (lane == 0) partials[tile] = acc;
@@ -174,60 +251,124 @@ struct AdamOp {
     }
 };
 
+// Native vector types, so the nontemporal builtins apply to 16-byte accesses.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <typename T>
+__device__ __forceinline__ T ld_stream(const ELY_GLOBAL T* p) {
+#if ELY_NT & 1
+    return __builtin_nontemporal_load(p);
+#else
+    return *p;
+#endif
+}
+
+template <typename T>
+__device__ __forceinline__ void st_stream(ELY_GLOBAL T* p, T v) {
+#if ELY_NT & 2
+    __builtin_nontemporal_store(v, p);
+#else
+    *p = v;
+#endif
+}
+
+// One 8-element group of AdamW at element i (all pointers 16-byte aligned).
+template <bool BF16G>
+struct Group {
+    f32x4 p0, p1, m0, m1, v0, v1;
+    float g[8];
+};
+
+template <bool BF16G>
+__device__ __forceinline__ void group_load(const AdamDesc& d, int64_t i, Group<BF16G>& G) {
+    const ELY_GLOBAL f32x4* pp = gp(reinterpret_cast<const f32x4*>(d.p + i));
+    const ELY_GLOBAL f32x4* mp = gp(reinterpret_cast<const f32x4*>(d.m + i));
+    const ELY_GLOBAL f32x4* vp = gp(reinterpret_cast<const f32x4*>(d.v + i));
+    G.p0 = ld_stream(pp); G.p1 = ld_stream(pp + 1);
+    G.m0 = ld_stream(mp); G.m1 = ld_stream(mp + 1);
+    G.v0 = ld_stream(vp); G.v1 = ld_stream(vp + 1);
+    if (BF16G) {
+        const u32x4 w = ld_stream(gp(reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(d.g) + i)));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            G.g[2 * j] = bf16_to_f32(w[j] & 0xFFFFu);
+            G.g[2 * j + 1] = bf16_to_f32(w[j] >> 16);
+        }
+    } else {
+        const ELY_GLOBAL f32x4* q = gp(reinterpret_cast<const f32x4*>(static_cast<const float*>(d.g) + i));
+        const f32x4 a = ld_stream(q), b = ld_stream(q + 1);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            G.g[j] = a[j];
+            G.g[4 + j] = b[j];
+        }
+    }
+}
+
+template <bool BF16G, int ORDER, bool WD, bool CLIP>
+__device__ __forceinline__ void group_update_store(const AdamDesc& d, int64_t i, Group<BF16G>& G,
+                                                   const ely_adamw_consts& c, float coef) {
+    using Op = AdamOp<BF16G, ORDER, WD, CLIP>;
+    float p[8], m[8], v[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        p[j] = G.p0[j]; p[4 + j] = G.p1[j];
+        m[j] = G.m0[j]; m[4 + j] = G.m1[j];
+        v[j] = G.v0[j]; v[4 + j] = G.v1[j];
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) Op::elem(p[j], G.g[j], m[j], v[j], c, coef);
+    ELY_GLOBAL f32x4* pp = gp(reinterpret_cast<f32x4*>(d.p + i));
+    ELY_GLOBAL f32x4* mp = gp(reinterpret_cast<f32x4*>(d.m + i));
+    ELY_GLOBAL f32x4* vp = gp(reinterpret_cast<f32x4*>(d.v + i));
+    st_stream(pp, f32x4{p[0], p[1], p[2], p[3]});
+    st_stream(pp + 1, f32x4{p[4], p[5], p[6], p[7]});
+    st_stream(mp, f32x4{m[0], m[1], m[2], m[3]});
+    st_stream(mp + 1, f32x4{m[4], m[5], m[6], m[7]});
+    st_stream(vp, f32x4{v[0], v[1], v[2], v[3]});
+    st_stream(vp + 1, f32x4{v[4], v[5], v[6], v[7]});
+    if (d.copy) {
+        u32x4 o;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = f32_to_bf16(p[2 * j]) | (f32_to_bf16(p[2 * j + 1]) << 16);
+        st_stream(gp(reinterpret_cast<u32x4*>(d.copy + i)), o);
+    }
+}
+
 template <bool BF16G, int ORDER, bool WD, bool CLIP>
 __device__ __forceinline__ void adam_range(const AdamDesc& d, const ely_adamw_consts& c, float coef, int64_t e0,
                                            int64_t e1) {
     using Op = AdamOp<BF16G, ORDER, WD, CLIP>;
     const int64_t vend = e0 + ((e1 - e0) & ~(int64_t)7);
     if (d.aligned) {
-        for (int64_t i = e0 + (int64_t)threadIdx.x * 8; i < vend; i += (int64_t)kBlock * 8) {
-            float4* pp = reinterpret_cast<float4*>(d.p + i);
-            float4* mp = reinterpret_cast<float4*>(d.m + i);
-            float4* vp = reinterpret_cast<float4*>(d.v + i);
-            float4 p0 = pp[0], p1 = pp[1], m0 = mp[0], m1 = mp[1], v0 = vp[0], v1 = vp[1];
-            float g[8];
-            if (BF16G) {
-                uint4 w = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(d.g) + i);
-                g[0] = bf16_to_f32(w.x & 0xFFFFu); g[1] = bf16_to_f32(w.x >> 16);
-                g[2] = bf16_to_f32(w.y & 0xFFFFu); g[3] = bf16_to_f32(w.y >> 16);
-                g[4] = bf16_to_f32(w.z & 0xFFFFu); g[5] = bf16_to_f32(w.z >> 16);
-                g[6] = bf16_to_f32(w.w & 0xFFFFu); g[7] = bf16_to_f32(w.w >> 16);
-            } else {
-                const float4* gp = reinterpret_cast<const float4*>(static_cast<const float*>(d.g) + i);
-                float4 a = gp[0], b = gp[1];
-                g[0] = a.x; g[1] = a.y; g[2] = a.z; g[3] = a.w;
-                g[4] = b.x; g[5] = b.y; g[6] = b.z; g[7] = b.w;
-            }
-            float p[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
-            float m[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
-            float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-#pragma unroll
-            for (int j = 0; j < 8; ++j) Op::elem(p[j], g[j], m[j], v[j], c, coef);
-            pp[0] = make_float4(p[0], p[1], p[2], p[3]);
-            pp[1] = make_float4(p[4], p[5], p[6], p[7]);
-            mp[0] = make_float4(m[0], m[1], m[2], m[3]);
-            mp[1] = make_float4(m[4], m[5], m[6], m[7]);
-            vp[0] = make_float4(v[0], v[1], v[2], v[3]);
-            vp[1] = make_float4(v[4], v[5], v[6], v[7]);
-            if (d.copy) {
-                uint4 o;
-                o.x = f32_to_bf16(p[0]) | (f32_to_bf16(p[1]) << 16);
-                o.y = f32_to_bf16(p[2]) | (f32_to_bf16(p[3]) << 16);
-                o.z = f32_to_bf16(p[4]) | (f32_to_bf16(p[5]) << 16);
-                o.w = f32_to_bf16(p[6]) | (f32_to_bf16(p[7]) << 16);
-                *reinterpret_cast<uint4*>(d.copy + i) = o;
-            }
+        constexpr int64_t S = (int64_t)kBlock * 8;  // one pass of the block
+        int64_t i = e0 + (int64_t)threadIdx.x * 8;
+#if ELY_ADAM_UNROLL > 1
+        // two groups per thread in flight: 14 loads issued before the first use
+        for (; i + S < vend; i += 2 * S) {
+            Group<BF16G> A, B;
+            group_load(d, i, A);
+            group_load(d, i + S, B);
+            group_update_store<BF16G, ORDER, WD, CLIP>(d, i, A, c, coef);
+            group_update_store<BF16G, ORDER, WD, CLIP>(d, i + S, B, c, coef);
+        }
+#endif
+        for (; i < vend; i += S) {
+            Group<BF16G> A;
+            group_load(d, i, A);
+            group_update_store<BF16G, ORDER, WD, CLIP>(d, i, A, c, coef);
         }
     }
     // Scalar path: unaligned tensors entirely, aligned tensors' last < 8 elements.
     for (int64_t i = (d.aligned ? vend : e0) + threadIdx.x; i < e1; i += kBlock) {
-        float p = d.p[i], m = d.m[i], v = d.v[i];
-        float g = BF16G ? bf16_to_f32(static_cast<const uint16_t*>(d.g)[i]) : static_cast<const float*>(d.g)[i];
+        float p = *gp(d.p + i), m = *gp(d.m + i), v = *gp(d.v + i);
+        float g = BF16G ? bf16_to_f32(*gp(static_cast<const uint16_t*>(d.g) + i)) : *gp(static_cast<const float*>(d.g) + i);
         Op::elem(p, g, m, v, c, coef);
-        d.p[i] = p;
-        d.m[i] = m;
-        d.v[i] = v;
-        if (d.copy) d.copy[i] = (uint16_t)f32_to_bf16(p);
+        *gp(d.p + i) = p;
+        *gp(d.m + i) = m;
+        *gp(d.v + i) = v;
+        if (d.copy) *gp(d.copy + i) = (uint16_t)f32_to_bf16(p);
     }
 }
 
@@ -237,17 +378,13 @@ __global__ __launch_bounds__(kBlock) void adamw_kernel(const AdamDesc* __restric
                                                        int64_t total_tiles, const float* __restrict__ coef_ptr) {
     const int64_t G = gridDim.x;
     const int64_t b = blockIdx.x;
+    const float coef = CLIP ? *coef_ptr : 1.0f;
+#if ELY_ADAM_SCHED == 0
+    // contiguous tile range per block
     const int64_t t0 = b * total_tiles / G, t1 = (b + 1) * total_tiles / G;
     if (t0 >= t1) return;
-    const float coef = CLIP ? *coef_ptr : 1.0f;
-    int lo = 0, hi = n - 1;
-    while (lo < hi) {
-        int mid = (lo + hi + 1) >> 1;
-        if (desc[mid].tile_begin <= t0) lo = mid;
-        else hi = mid - 1;
-    }
     int64_t tile = t0;
-    for (int ti = lo; ti < n && tile < t1; ++ti) {
+    for (int ti = find_tensor(desc, n, t0); ti < n && tile < t1; ++ti) {
         const AdamDesc d = desc[ti];
         const int64_t ntiles = (d.numel + kAdamTile - 1) / kAdamTile;
         const int64_t tend = min(t1, d.tile_begin + ntiles);
@@ -258,6 +395,20 @@ __global__ __launch_bounds__(kBlock) void adamw_kernel(const AdamDesc* __restric
         adam_range<BF16G, ORDER, WD, CLIP>(d, c, coef, e0, e1);
         tile = tend;
     }
+#else
+    // interleaved: in round r block b takes tile r*G + b, so at any moment the
+    // whole grid streams one contiguous window of the shard
+    if (b >= total_tiles) return;
+    int ti = find_tensor(desc, n, b);
+    for (int64_t tile = b; tile < total_tiles; tile += G) {
+        while (ti + 1 < n && desc[ti + 1].tile_begin <= tile) ++ti;
+        const AdamDesc d = desc[ti];
+        const int64_t e0 = (tile - d.tile_begin) * kAdamTile;
+        const int64_t e1 = min(e0 + kAdamTile, d.numel);
+        const ely_adamw_consts c = consts[ti];
+        adam_range<BF16G, ORDER, WD, CLIP>(d, c, coef, e0, e1);
+    }
+#endif
 }
 
 typedef void (*AdamKernel)(const AdamDesc*, const ely_adamw_consts*, int32_t, int64_t, const float*);
@@ -323,7 +474,7 @@ int ely_grad_norm(const ely_tensor* grads, int32_t n, float max_norm, ely_norm_r
         double* partials = reinterpret_cast<double*>(ws + norm_table_bytes(n));
         if (tiles > 0) {
             upload(dtable, table.data(), table.size() * sizeof(NormDesc), s);
-            const int64_t waves = std::min<int64_t>(tiles, mt_blocks(8) * (kBlock / kWave));
+            const int64_t waves = std::min<int64_t>(tiles, mt_blocks(ELY_NORM_BPC) * (kBlock / kWave));
             const int64_t blocks = (waves + 3) / 4;
             hipLaunchKernelGGL(norm_partials_kernel, dim3((unsigned)blocks), dim3(kBlock), 0, s, dtable,
                                (int32_t)table.size(), tiles, partials);
@@ -407,7 +558,7 @@ int ely_adamw_step(const ely_tensor* params, const ely_tensor* grads, const ely_
         else
             k = order == ELY_ORDER_HOST ? pick_adam<false, ELY_ORDER_HOST>(wd, clip)
                                         : pick_adam<false, ELY_ORDER_TORCH>(wd, clip);
-        const int64_t blocks = std::min<int64_t>(tiles, mt_blocks(8));
+        const int64_t blocks = std::min<int64_t>(tiles, mt_blocks(ELY_ADAM_BPC));
         hipLaunchKernelGGL(k, dim3((unsigned)blocks), dim3(kBlock), 0, s, dtable, dconsts, (int32_t)table.size(),
                            tiles, coef_dev);
         check_launch("adamw_kernel");

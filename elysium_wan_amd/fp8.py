@@ -13,6 +13,8 @@ Inputs must be CUDA tensors of dtype bfloat16 or float32.
 
 from __future__ import annotations
 
+import math
+
 import torch
 
 from . import _lib
@@ -43,7 +45,7 @@ def _rows(x: torch.Tensor, what: str):
     if not x.is_contiguous():
         x = x.contiguous()
     cols = x.shape[-1]
-    rows = x.numel() // cols if cols else 0
+    rows = math.prod(x.shape[:-1])
     return x, rows, cols
 
 
@@ -107,7 +109,7 @@ def dequantize(q: torch.Tensor, k: torch.Tensor, dtype: torch.dtype = torch.floa
         raise ValueError("dequantize: a 0-d tensor has no rows")
     k = k.to(device=q.device, dtype=torch.int32).contiguous()
     cols = q.shape[-1]
-    rows = q.numel() // cols if cols else 0
+    rows = math.prod(q.shape[:-1])
     if k.numel() == 1 and rows != 1:
         # per-tensor exponent: one row of every element
         rows, cols = 1, q.numel()
@@ -137,3 +139,24 @@ def roundtrip(x: torch.Tensor, fmt: str = "e4m3", per_tensor: bool = False) -> t
         "roundtrip",
     )
     return out
+
+
+def recover_exp(t: torch.Tensor, fmt: str = "e4m3") -> torch.Tensor:
+    """Per-row exponent k making t * 2^-k exactly fp8-representable, from the
+    dequantized tensor alone: the first of base + (0, -1, 1, -2, 2) that works
+    for the whole row (model/fp8.py:66-93).  Raises ValueError when some row
+    has none ("recipe mismatch"), as the reference does.  One device
+    synchronization (the bad-row count) per call."""
+    f = _fmt(fmt)
+    t, rows, cols = _rows(t, "recover_exp")
+    k = torch.empty(_k_shape(t), dtype=torch.int32, device=t.device)
+    bad = torch.zeros(1, dtype=torch.int64, device=t.device)
+    L = _lib.load()
+    ws = _lib.workspace(t.device, L.ely_fp8_recover_workspace_bytes(rows))
+    _lib.check(
+        L.ely_fp8_recover_exp(t.data_ptr(), _lib.dtype_code(t), rows, cols, f, k.data_ptr(), bad.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_ptr(t.device)),
+        "recover_exp",
+    )
+    if int(bad.item()):
+        raise ValueError("boundary tensor is not scaled-FP8 representable: recipe mismatch")
+    return k

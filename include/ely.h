@@ -125,6 +125,24 @@ int ely_fp8_roundtrip(const void* x, int32_t x_dtype, int64_t rows, int64_t cols
                       void* out, uint8_t* q, int32_t* k, void* workspace, int64_t ws_bytes,
                       void* stream);
 
+/* Workspace bytes ely_fp8_recover_exp needs for `rows` rows. */
+int64_t ely_fp8_recover_workspace_bytes(int64_t rows);
+
+/* fp8.recover_exp (model/fp8.py:66-93): per row, base = the scale_exp
+ * exponent of t's own |t|max, then the first k of base + (0, -1, 1, -2, 2)
+ * for which every element satisfies fp8(t * 2^-k) * 2^k == t in t's dtype.
+ * k: [rows] int32; a row with no such k keeps base + 2 and adds 1 to
+ * *bad_rows_dev (the caller zeroes it; the reference raises ValueError, which
+ * the Python layer does when the count is non-zero). */
+int ely_fp8_recover_exp(const void* t, int32_t t_dtype, int64_t rows, int64_t cols, int32_t fmt,
+                        int32_t* k, unsigned long long* bad_rows_dev, void* workspace, int64_t ws_bytes,
+                        void* stream);
+
+/* q = fp8(x * 2^-k[row]) with the caller's exponents, the multiply in x's
+ * dtype: the byte image of the scaled-fp8 wire (codec/planes.py:110-111). */
+int ely_fp8_quantize_k(const void* x, int32_t x_dtype, int64_t rows, int64_t cols, int32_t fmt,
+                       const int32_t* k, uint8_t* q, void* stream);
+
 /* ------------------------------------------------------------ casts/fold */
 
 /* pieces.cast_piece (runtime/pieces.py:192-195): fp32 -> bf16, RNE,

@@ -73,7 +73,10 @@ def _oracle_steps(oracle, params, grads_per_step, lr, wd, max_norm, copies=True)
     m, v = np.zeros_like(p), np.zeros_like(p)
     cp = np.zeros(p.size, dtype=np.uint16) if copies else None
     for step, grads in enumerate(grads_per_step):
-        gflat = np.concatenate([bits(t).reshape(-1) for t in grads])
+        if all(t.dtype == torch.bfloat16 for t in grads):
+            gflat = np.concatenate([bits(t).reshape(-1) for t in grads])
+        else:  # mixed dtypes: the exact fp32 widening of each part
+            gflat = np.concatenate([bits(t.float()).reshape(-1) for t in grads])
         coef = 1.0
         if max_norm is not None:
             norm = float(np.float32(np.sqrt(oracle.sumsq([gflat]))))

@@ -1,0 +1,91 @@
+"""recover_exp and the scaled-fp8 wire image on the GPU against the
+reference's own outputs (tests/golden: payload bytes made by
+codec/planes.py:85-117 with zlib-1, per-row recovered exponents of
+model/fp8.py:66-93) and the oracle."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import golden
+from gpu_util import activation, bits, f32_equal, from_bits_bf16, say
+
+pytestmark = pytest.mark.gpu
+
+
+def _tensor(raw, dname_or_dtype):
+    if "bf16" in str(dname_or_dtype) or "bfloat16" in str(dname_or_dtype):
+        return from_bits_bf16(raw, "cuda")
+    return torch.from_numpy(raw.astype(np.float32)).cuda()
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+@pytest.mark.parametrize("dname", ["f32", "bf16"])
+def test_recover_exp_equals_the_reference_golden(fmt, dname):
+    from elysium_wan_amd import fp8
+
+    g = golden("fp8_rows.npz")
+    pre = f"{fmt}_{dname}"
+    for src, kk, ok in (("rt", "rec", "rec_ok"), ("cand", "cand_k", "cand_ok")):
+        t = _tensor(g[f"{pre}_{src}"], dname)
+        say("recover_exp golden", pre, src, tuple(t.shape))
+        want_k, want_ok = g[f"{pre}_{kk}"], g[f"{pre}_{ok}"]
+        good = np.nonzero(want_ok)[0]
+        k = fp8.recover_exp(t[torch.from_numpy(good).cuda()], fmt)
+        assert np.array_equal(bits(k).reshape(-1), want_k[good])
+        for r in np.nonzero(want_ok == 0)[0][:8]:
+            with pytest.raises(ValueError, match="recipe mismatch"):
+                fp8.recover_exp(t[int(r) : int(r) + 1], fmt)
+
+
+def test_wire_payloads_equal_the_reference_bytes():
+    from elysium_wan_amd import planes
+
+    g = golden("wire.npz")
+    for name in g["names"]:
+        name = str(name)
+        fmt = "e5m2" if name.endswith("e5m2") else "e4m3"
+        shape = tuple(int(s) for s in g[f"{name}_shape"])
+        t = _tensor(g[f"{name}_t"], str(g[f"{name}_dtype"])).reshape(shape)
+        say("wire golden", name, shape)
+        payload, sh = planes.encode_scaled_fp8(t, fmt)
+        assert sh == shape
+        assert payload == g[f"{name}_payload"].tobytes(), name
+        out = planes.decode(payload, shape)
+        assert f32_equal(bits(out).reshape(-1), g[f"{name}_decoded"].reshape(-1))
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+def test_wire_round_trip_of_a_c1_activation_and_its_refusal(oracle, fmt):
+    """tests/unit/test_codecs_identity.py:59-68 at C1's boundary shape: the
+    recipe's round trip crosses the wire exactly; an un-narrowed tensor is
+    refused."""
+    from elysium_wan_amd import fp8, planes
+
+    x = activation((8, 2048, 2560), seed=21 if fmt == "e4m3" else 22)
+    rt = fp8.roundtrip(x, fmt)
+    say("wire C1", fmt)
+    payload, shape = planes.encode_scaled_fp8(rt, fmt)
+    back = planes.decode(payload, shape)
+    assert torch.equal(back, rt.float())
+    k = fp8.recover_exp(rt, fmt)
+    ok, bad = oracle.recover_exp(bits(rt[0, :64]), fmt)
+    assert bad == 0 and np.array_equal(bits(k[0, :64]).reshape(-1), ok)
+    with pytest.raises(ValueError, match="recipe mismatch"):
+        planes.encode_scaled_fp8(x, fmt)
+
+
+def test_gradient_scale_values_survive_the_wire():
+    """test_codecs_identity.py:62: randn * 1e-4, values an unscaled cast zeroes."""
+    from elysium_wan_amd import fp8, planes
+
+    x = torch.randn(3, 8, 32, device="cuda") * 1e-4
+    for fmt in ("e4m3", "e5m2"):
+        q = fp8.roundtrip(x, fmt)
+        assert float(q.abs().sum()) > 0
+        payload, shape = planes.encode_scaled_fp8(q, fmt)
+        assert torch.equal(planes.decode(payload, shape), q)
+        with pytest.raises(ValueError):
+            planes.encode_scaled_fp8(x, fmt)
