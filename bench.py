@@ -42,6 +42,7 @@ LR, BETAS, EPS, WD, MAX_NORM = 3e-4, (0.9, 0.95), 1e-8, 0.1, 1.0
 ADAM_BYTES_PER_ELEM = 28  # bf16 grads, bf16 copy out
 NORM_BYTES_PER_ELEM = 2
 CODEC_BYTES_PER_ELEM = 3  # bf16 in / fp8 out (quantize); fp8 in / bf16 out (dequantize)
+CAL_ELEMS = 1 << 28  # calibration cast of the --pmc passes
 
 
 def log(*a):
@@ -199,6 +200,125 @@ def cpu_baseline(sample_elems: int, steps: int = 2):
     return sample_elems * steps / dt, dt
 
 
+def profile_pass(device):
+    """A short run of every kernel bench.py measures, for rocprofv3 --pmc
+    passes (one counter set per run): a plain streaming kernel of known size
+    (the fp32 -> bf16 cast of 2^28 elements: reads 1 GiB, writes 512 MiB)
+    to calibrate the counters, three optimizer steps over C1's shard and
+    three quantize / dequantize launches of C1's activation."""
+    from elysium_wan_amd import _lib, optim
+
+    L = _lib.load()
+    sptr = _lib.stream_ptr(device)
+    x = torch.empty(CAL_ELEMS, dtype=torch.float32, device=device).normal_()
+    y = torch.empty(CAL_ELEMS, dtype=torch.bfloat16, device=device)
+    for _ in range(3):
+        _lib.check(L.ely_cast_bf16(x.data_ptr(), y.data_ptr(), CAL_ELEMS, sptr), "cast")
+    torch.cuda.synchronize()
+    del x, y
+    log("profile pass: calibration done")
+    params, grads = make_shard(device)
+    opt = optim.FusedAdamW(params, lr=LR, betas=BETAS, eps=EPS, weight_decay=WD, order="host", max_norm=MAX_NORM, working_copy=True)
+    for _ in range(3):
+        opt.step(grads=grads)
+    torch.cuda.synchronize()
+    del opt, params, grads
+    log("profile pass: optimizer done")
+    rows, cols = 8 * 2048, D_MODEL
+    xa = torch.randn(rows, cols, device=device).to(torch.bfloat16)
+    q = torch.empty(rows, cols, dtype=torch.uint8, device=device)
+    k = torch.empty(rows, dtype=torch.int32, device=device)
+    out = torch.empty(rows, cols, dtype=torch.bfloat16, device=device)
+    ws = _lib.workspace(device, L.ely_fp8_workspace_bytes(rows, cols, _lib.BF16))
+    for _ in range(3):
+        _lib.check(L.ely_fp8_quantize(xa.data_ptr(), _lib.BF16, rows, cols, _lib.E4M3, q.data_ptr(), k.data_ptr(), ws.data_ptr(), ws.numel(), sptr), "q")
+        _lib.check(L.ely_fp8_dequantize(q.data_ptr(), k.data_ptr(), rows, cols, _lib.E4M3, out.data_ptr(), _lib.BF16, sptr), "dq")
+    torch.cuda.synchronize()
+    log("profile pass: codec done")
+
+
+# Kernels the traffic summary reports: name fragment -> (algorithmic bytes per
+# launch, what they are).  C1 sizes.
+def _traffic_kernels():
+    n = sum(int(np.prod(s)) for s in block_shapes(D_MODEL)) * N_BLOCKS
+    act = 8 * 2048 * D_MODEL
+    return {
+        "adamw_kernel": (n * ADAM_BYTES_PER_ELEM, "fused clip + AdamW, C1 shard, 28 B/elem"),
+        "norm_partials_kernel": (n * NORM_BYTES_PER_ELEM, "grad-norm partials, C1 bf16 grads, 2 B/elem"),
+        "quant_rows_kernel": (act * CODEC_BYTES_PER_ELEM, "fp8 e4m3 quantize, C1 activation, 3 B/elem"),
+        "dequant_kernel": (act * CODEC_BYTES_PER_ELEM, "fp8 e4m3 dequantize -> bf16, C1 activation, 3 B/elem"),
+    }
+
+
+def _pmc_means(directory: str, counter: str) -> dict:
+    """Mean per-dispatch value of `counter` for each kernel name in a
+    rocprofv3 --pmc output directory (every *counter_collection.csv under it)."""
+    import csv
+    import glob
+
+    sums: dict = {}
+    files = glob.glob(os.path.join(directory, "**", "*counter_collection.csv"), recursive=True)
+    if not files:
+        raise SystemExit(f"no counter_collection.csv under {directory}")
+    for path in files:
+        with open(path, newline="") as f:
+            for row in csv.DictReader(f):
+                if row.get("Counter_Name") != counter:
+                    continue
+                name = row["Kernel_Name"]
+                s = sums.setdefault(name, [0.0, 0])
+                s[0] += float(row["Counter_Value"])
+                s[1] += 1
+    return {name: v[0] / v[1] for name, v in sums.items()}
+
+
+def _pick(means: dict, fragment: str):
+    hits = [v for name, v in means.items() if fragment in name]
+    if not hits:
+        return None
+    return sum(hits) / len(hits)
+
+
+def traffic_summary(fetch_dir: str, write_dir: str, command: str) -> None:
+    """HBM bytes per launch of each measured kernel from two rocprofv3 --pmc
+    runs of `bench.py --profile-pass` (FETCH_SIZE, then WRITE_SIZE; KiB per
+    dispatch), each scaled by the same counter's reading on the calibration
+    cast (known: 4 B read + 2 B written per element).  Writes
+    profiles/adamw_c1_traffic.json (read back by bench.py) and a text
+    summary beside it."""
+    fetch = _pmc_means(fetch_dir, "FETCH_SIZE")
+    write = _pmc_means(write_dir, "WRITE_SIZE")
+    cf = _pick(fetch, "cast_bf16_kernel") * 1024.0 / (CAL_ELEMS * 4)
+    cw = _pick(write, "cast_bf16_kernel") * 1024.0 / (CAL_ELEMS * 2)
+    out = {"fetch_factor": cf, "write_factor": cw, "command": command, "kernels": {}}
+    lines = [
+        "# HBM traffic per launch (rocprofv3 --pmc), C1 workload",
+        "",
+        f"Command: `{command}`",
+        "",
+        f"Calibration: cast_bf16_kernel over {CAL_ELEMS} fp32 -> bf16 (reads {CAL_ELEMS * 4} B, writes {CAL_ELEMS * 2} B);",
+        f"FETCH_SIZE reads {cf:.4f} x the known bytes, WRITE_SIZE {cw:.4f} x.  Every figure below is divided by these factors.",
+        "",
+        "| kernel | FETCH_SIZE KiB | WRITE_SIZE KiB | traffic (B) | algorithmic (B) | traffic / algorithmic | what |",
+        "|---|---|---|---|---|---|---|",
+    ]
+    for frag, (alg, what) in _traffic_kernels().items():
+        fk, wk = _pick(fetch, frag), _pick(write, frag)
+        if fk is None or wk is None:
+            continue
+        t = fk * 1024.0 / cf + wk * 1024.0 / cw
+        out["kernels"][frag] = {"fetch_kib": fk, "write_kib": wk, "traffic_bytes": t, "algorithmic_bytes": alg, "ratio": t / alg}
+        lines.append(f"| {frag} | {fk:.0f} | {wk:.0f} | {t:.4g} | {alg:.4g} | {t / alg:.3f} | {what} |")
+    adam = out["kernels"].get("adamw_kernel")
+    out["traffic_bytes_per_launch"] = adam["traffic_bytes"] if adam else None
+    os.makedirs(os.path.join(HERE, "profiles"), exist_ok=True)
+    with open(os.path.join(HERE, "profiles", "adamw_c1_traffic.json"), "w") as f:
+        json.dump(out, f, indent=1)
+    with open(os.path.join(HERE, "profiles", "adamw_c1_traffic.md"), "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
 def read_traffic():
     """HBM bytes per AdamW launch measured by rocprofv3 --pmc (FETCH_SIZE +
     WRITE_SIZE, scaled by a plain copy's reading), if that profile is
@@ -218,7 +338,13 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-codec", action="store_true", help="skip the fp8 codec leg")
     ap.add_argument("--cpu-sample", type=int, default=256 * 1024 * 1024)
+    ap.add_argument("--profile-pass", action="store_true", help="launch each measured kernel a few times, untimed, for rocprofv3 --pmc runs")
+    ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"), help="summarize two --pmc runs of --profile-pass into profiles/")
+    ap.add_argument("--traffic-command", default="", help="the command line recorded in the traffic summary")
     args = ap.parse_args()
+    if args.traffic_summary:
+        traffic_summary(*args.traffic_summary, args.traffic_command)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
@@ -228,6 +354,10 @@ def main():
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)
     stream = torch.cuda.Stream(device)
+    if args.profile_pass:
+        with torch.cuda.stream(stream):
+            profile_pass(device)
+        return
     with torch.cuda.stream(stream):
         log("optimizer leg")
         o = bench_optimizer(args, device, stream)
