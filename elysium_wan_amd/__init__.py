@@ -9,10 +9,11 @@ Modules mirror the reference's:
              recover_exp)
   pieces  -- runtime/pieces.py  (cast_piece, fold_start, fold_add, fold)
   planes  -- codec/planes.py    (encode_scaled_fp8, decode: the scaled-fp8 wire)
+  boundary -- model/gpt.py:284-317 (narrow, Boundary: the codec's caller)
 The kernels live in libelyhip.so (C ABI: include/ely.h), built by
 elysium_wan_amd.build for gfx950.
 """
 
-from . import fp8, optim, pieces, planes  # noqa: F401
+from . import boundary, fp8, optim, pieces, planes  # noqa: F401
 
-__all__ = ["fp8", "optim", "pieces", "planes"]
+__all__ = ["boundary", "fp8", "optim", "pieces", "planes"]

@@ -1,19 +1,23 @@
-"""The elementwise kernels of the sharded "pieces" update on MI355X: the
-drop-in for wantrain's runtime/pieces.py:192-227 (same names and semantics).
+"""The elementwise kernels and the optimizer of the sharded "pieces" update
+on MI355X: the drop-in for wantrain's runtime/pieces.py:192-256 (same names
+and semantics).
 
 cast_piece: fp32 master -> working copy (bf16 RNE, or a plain copy for fp32).
 fold_start / fold_add / fold: the fixed-order fp32 gradient fold, widening
 bf16 parts exactly.  int64 count lanes stay on torch's exact integer add, as
 the reference does (runtime/pieces.py:198-214).
+adamw / step_unit: the reference's AdamW over master pieces (the fused
+kernel in torch's op order) and the per-unit step.
 """
 
 from __future__ import annotations
 
-from collections.abc import Iterable
+from collections.abc import Iterable, Sequence
 
 import torch
 
 from . import _lib
+from . import optim as _optim
 
 
 def cast_piece(p: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
@@ -70,3 +74,36 @@ def fold(gs: Iterable[torch.Tensor]) -> torch.Tensor:
     if acc is None:
         raise ValueError("a fold over zero microbatches")
     return acc
+
+
+def adamw(params: Iterable[torch.Tensor], lr: float):
+    """runtime/pieces.py:230-232: the reference's optimizer over owned pieces
+    -- torch.optim.AdamW(lr, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.0),
+    here the fused kernel in torch's op order."""
+    return _optim.build("adamw", params, lr)
+
+
+def step_unit(opt, params: Sequence[torch.Tensor], grads: Sequence[torch.Tensor]) -> None:
+    """runtime/pieces.py:235-256: one unit's update.  Only `params` carry
+    gradients during the step, so every other parameter's state and step
+    counter are left untouched; gradients are cleared afterwards."""
+    if len(params) != len(grads):
+        raise ValueError(f"{len(params)} params, {len(grads)} grads")
+    ids = {id(p) for p in params}
+    held = {id(p) for group in opt.param_groups for p in group["params"]}
+    if not ids <= held:
+        raise ValueError("step_unit: a parameter outside this optimizer")
+    for group in opt.param_groups:
+        for p in group["params"]:
+            if id(p) not in ids:
+                p.grad = None
+    if isinstance(opt, _optim.FusedAdamW):
+        # bf16 gradients cannot sit in an fp32 parameter's .grad: hand them in
+        by_id = {id(p): g for p, g in zip(params, grads)}
+        opt.step(grads=[by_id.get(id(p)) for p in opt.params])
+    else:
+        for p, g in zip(params, grads):
+            p.grad = g
+        opt.step()
+    for p in params:
+        p.grad = None

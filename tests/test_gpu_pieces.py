@@ -46,3 +46,31 @@ def test_fold_is_widen_then_add_in_order(oracle):
     want = a + b.float()
     pieces.fold_add(a, b)
     assert torch.equal(a, want)
+
+
+def test_step_unit_steps_only_its_unit():
+    """runtime/pieces.py:235-256 with pieces.adamw (torch's AdamW op order):
+    the unit's params move exactly as a whole-list step over them would;
+    the other unit's params, moments and step counters stay untouched."""
+    from elysium_wan_amd import pieces
+
+    gen = torch.Generator().manual_seed(11)
+    shapes = [(64, 48), (48,), (300,), (17, 5)]
+    init = [torch.randn(s, generator=gen) for s in shapes]
+    ps = [t.clone().cuda().requires_grad_(True) for t in init]
+    solo = [t.clone().cuda().requires_grad_(True) for t in init[:2]]
+    opt = pieces.adamw(ps, 1e-2)
+    opt_solo = pieces.adamw(solo, 1e-2)
+    say("step_unit")
+    for step in range(3):
+        gs = [(torch.randn(s, generator=gen) * 1e-2).cuda() for s in shapes[:2]]
+        pieces.step_unit(opt, ps[:2], gs)
+        pieces.step_unit(opt_solo, solo, [g.clone() for g in gs])
+    for a, b in zip(ps[:2], solo):
+        assert torch.equal(a.detach().view(torch.int32), b.detach().view(torch.int32))
+    for a, b in zip(ps[2:], init[2:]):
+        assert torch.equal(a.detach().cpu(), b)
+    assert set(opt.state) == {0, 1} and all(float(opt.state[i]["step"]) == 3.0 for i in (0, 1))
+    assert all(p.grad is None for p in ps)
+    with pytest.raises(ValueError, match="outside"):
+        pieces.step_unit(opt, [torch.zeros(3, device="cuda", requires_grad=True)], [torch.zeros(3, device="cuda")])
