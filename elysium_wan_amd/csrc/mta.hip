@@ -45,13 +45,13 @@ namespace ely {
 #define ELY_NORM_UNROLL 4        // 16-byte loads a grad-norm lane keeps in flight
 #endif
 #ifndef ELY_NT
-#define ELY_NT 0                 // bit 0: nontemporal AdamW loads, bit 1: nontemporal stores
+#define ELY_NT 3                 // bit 0: nontemporal AdamW loads, bit 1: nontemporal stores
 #endif
 #ifndef ELY_ADAM_UNROLL
-#define ELY_ADAM_UNROLL 1        // 8-element groups a thread keeps in flight (1 or 2)
+#define ELY_ADAM_UNROLL 2        // 2,048-element block steps a thread keeps in flight (1, 2, 4 or 8)
 #endif
 #ifndef ELY_ADAM_BPC
-#define ELY_ADAM_BPC 8           // AdamW blocks per compute unit
+#define ELY_ADAM_BPC 1           // AdamW blocks per compute unit
 #endif
 #ifndef ELY_NORM_BPC
 #define ELY_NORM_BPC 8           // grad-norm blocks (of 4 waves) per compute unit
@@ -273,66 +273,67 @@ __device__ __forceinline__ void st_stream(ELY_GLOBAL T* p, T v) {
 #endif
 }
 
-// One 8-element group of AdamW at element i (all pointers 16-byte aligned).
+// The vector path's unit of work is a block step of kStep = 2,048 elements.
+// Thread t owns the quads [4t, 4t+4) and [1024+4t, 1024+4t+4) of the step,
+// so each load or store instruction of a wave covers one contiguous 1 KB
+// (fp32) or 512 B (bf16) run: every request is a full, aligned line, and the
+// two halves of a step never share a line.  ELY_ADAM_UNROLL steps are loaded
+// before the first is updated, keeping 14 * U 16- or 8-byte loads per thread
+// in flight.
+constexpr int64_t kStep = (int64_t)kBlock * 8;
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
 template <bool BF16G>
-struct Group {
-    f32x4 p0, p1, m0, m1, v0, v1;
+struct Quad2 {
+    f32x4 p[2], m[2], v[2];
     float g[8];
 };
 
 template <bool BF16G>
-__device__ __forceinline__ void group_load(const AdamDesc& d, int64_t i, Group<BF16G>& G) {
-    const ELY_GLOBAL f32x4* pp = gp(reinterpret_cast<const f32x4*>(d.p + i));
-    const ELY_GLOBAL f32x4* mp = gp(reinterpret_cast<const f32x4*>(d.m + i));
-    const ELY_GLOBAL f32x4* vp = gp(reinterpret_cast<const f32x4*>(d.v + i));
-    G.p0 = ld_stream(pp); G.p1 = ld_stream(pp + 1);
-    G.m0 = ld_stream(mp); G.m1 = ld_stream(mp + 1);
-    G.v0 = ld_stream(vp); G.v1 = ld_stream(vp + 1);
-    if (BF16G) {
-        const u32x4 w = ld_stream(gp(reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(d.g) + i)));
+__device__ __forceinline__ void quad_load(const AdamDesc& d, int64_t i, Quad2<BF16G>& Q) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            G.g[2 * j] = bf16_to_f32(w[j] & 0xFFFFu);
-            G.g[2 * j + 1] = bf16_to_f32(w[j] >> 16);
-        }
-    } else {
-        const ELY_GLOBAL f32x4* q = gp(reinterpret_cast<const f32x4*>(static_cast<const float*>(d.g) + i));
-        const f32x4 a = ld_stream(q), b = ld_stream(q + 1);
+    for (int h = 0; h < 2; ++h) {
+        const int64_t e = i + h * (kStep / 2);
+        Q.p[h] = ld_stream(gp(reinterpret_cast<const f32x4*>(d.p + e)));
+        Q.m[h] = ld_stream(gp(reinterpret_cast<const f32x4*>(d.m + e)));
+        Q.v[h] = ld_stream(gp(reinterpret_cast<const f32x4*>(d.v + e)));
+        if (BF16G) {
+            const u32x2 w = ld_stream(gp(reinterpret_cast<const u32x2*>(static_cast<const uint16_t*>(d.g) + e)));
+            Q.g[4 * h + 0] = bf16_to_f32(w[0] & 0xFFFFu);
+            Q.g[4 * h + 1] = bf16_to_f32(w[0] >> 16);
+            Q.g[4 * h + 2] = bf16_to_f32(w[1] & 0xFFFFu);
+            Q.g[4 * h + 3] = bf16_to_f32(w[1] >> 16);
+        } else {
+            const f32x4 a = ld_stream(gp(reinterpret_cast<const f32x4*>(static_cast<const float*>(d.g) + e)));
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            G.g[j] = a[j];
-            G.g[4 + j] = b[j];
+            for (int j = 0; j < 4; ++j) Q.g[4 * h + j] = a[j];
         }
     }
 }
 
 template <bool BF16G, int ORDER, bool WD, bool CLIP>
-__device__ __forceinline__ void group_update_store(const AdamDesc& d, int64_t i, Group<BF16G>& G,
-                                                   const ely_adamw_consts& c, float coef) {
+__device__ __forceinline__ void quad_update_store(const AdamDesc& d, int64_t i, Quad2<BF16G>& Q,
+                                                  const ely_adamw_consts& c, float coef) {
     using Op = AdamOp<BF16G, ORDER, WD, CLIP>;
-    float p[8], m[8], v[8];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        p[j] = G.p0[j]; p[4 + j] = G.p1[j];
-        m[j] = G.m0[j]; m[4 + j] = G.m1[j];
-        v[j] = G.v0[j]; v[4 + j] = G.v1[j];
-    }
+    for (int h = 0; h < 2; ++h) {
+        float p[4], m[4], v[4];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) Op::elem(p[j], G.g[j], m[j], v[j], c, coef);
-    ELY_GLOBAL f32x4* pp = gp(reinterpret_cast<f32x4*>(d.p + i));
-    ELY_GLOBAL f32x4* mp = gp(reinterpret_cast<f32x4*>(d.m + i));
-    ELY_GLOBAL f32x4* vp = gp(reinterpret_cast<f32x4*>(d.v + i));
-    st_stream(pp, f32x4{p[0], p[1], p[2], p[3]});
-    st_stream(pp + 1, f32x4{p[4], p[5], p[6], p[7]});
-    st_stream(mp, f32x4{m[0], m[1], m[2], m[3]});
-    st_stream(mp + 1, f32x4{m[4], m[5], m[6], m[7]});
-    st_stream(vp, f32x4{v[0], v[1], v[2], v[3]});
-    st_stream(vp + 1, f32x4{v[4], v[5], v[6], v[7]});
-    if (d.copy) {
-        u32x4 o;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) o[j] = f32_to_bf16(p[2 * j]) | (f32_to_bf16(p[2 * j + 1]) << 16);
-        st_stream(gp(reinterpret_cast<u32x4*>(d.copy + i)), o);
+        for (int j = 0; j < 4; ++j) {
+            p[j] = Q.p[h][j];
+            m[j] = Q.m[h][j];
+            v[j] = Q.v[h][j];
+            Op::elem(p[j], Q.g[4 * h + j], m[j], v[j], c, coef);
+        }
+        const int64_t e = i + h * (kStep / 2);
+        st_stream(gp(reinterpret_cast<f32x4*>(d.p + e)), f32x4{p[0], p[1], p[2], p[3]});
+        st_stream(gp(reinterpret_cast<f32x4*>(d.m + e)), f32x4{m[0], m[1], m[2], m[3]});
+        st_stream(gp(reinterpret_cast<f32x4*>(d.v + e)), f32x4{v[0], v[1], v[2], v[3]});
+        if (d.copy) {
+            const u32x2 o = {f32_to_bf16(p[0]) | (f32_to_bf16(p[1]) << 16), f32_to_bf16(p[2]) | (f32_to_bf16(p[3]) << 16)};
+            st_stream(gp(reinterpret_cast<u32x2*>(d.copy + e)), o);
+        }
     }
 }
 
@@ -340,28 +341,28 @@ template <bool BF16G, int ORDER, bool WD, bool CLIP>
 __device__ __forceinline__ void adam_range(const AdamDesc& d, const ely_adamw_consts& c, float coef, int64_t e0,
                                            int64_t e1) {
     using Op = AdamOp<BF16G, ORDER, WD, CLIP>;
-    const int64_t vend = e0 + ((e1 - e0) & ~(int64_t)7);
+    constexpr int U = ELY_ADAM_UNROLL;
+    int64_t done = e0;
     if (d.aligned) {
-        constexpr int64_t S = (int64_t)kBlock * 8;  // one pass of the block
-        int64_t i = e0 + (int64_t)threadIdx.x * 8;
-#if ELY_ADAM_UNROLL > 1
-        // two groups per thread in flight: 14 loads issued before the first use
-        for (; i + S < vend; i += 2 * S) {
-            Group<BF16G> A, B;
-            group_load(d, i, A);
-            group_load(d, i + S, B);
-            group_update_store<BF16G, ORDER, WD, CLIP>(d, i, A, c, coef);
-            group_update_store<BF16G, ORDER, WD, CLIP>(d, i + S, B, c, coef);
+        const int64_t steps = (e1 - e0) / kStep;
+        const int64_t t4 = (int64_t)threadIdx.x * 4;
+        int64_t s = 0;
+        for (; s + U <= steps; s += U) {
+            Quad2<BF16G> Q[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) quad_load(d, e0 + (s + u) * kStep + t4, Q[u]);
+#pragma unroll
+            for (int u = 0; u < U; ++u) quad_update_store<BF16G, ORDER, WD, CLIP>(d, e0 + (s + u) * kStep + t4, Q[u], c, coef);
         }
-#endif
-        for (; i < vend; i += S) {
-            Group<BF16G> A;
-            group_load(d, i, A);
-            group_update_store<BF16G, ORDER, WD, CLIP>(d, i, A, c, coef);
+        for (; s < steps; ++s) {
+            Quad2<BF16G> Q;
+            quad_load(d, e0 + s * kStep + t4, Q);
+            quad_update_store<BF16G, ORDER, WD, CLIP>(d, e0 + s * kStep + t4, Q, c, coef);
         }
+        done = e0 + steps * kStep;
     }
-    // Scalar path: unaligned tensors entirely, aligned tensors' last < 8 elements.
-    for (int64_t i = (d.aligned ? vend : e0) + threadIdx.x; i < e1; i += kBlock) {
+    // Scalar path: unaligned tensors entirely, aligned tensors' last partial step.
+    for (int64_t i = done + threadIdx.x; i < e1; i += kBlock) {
         float p = *gp(d.p + i), m = *gp(d.m + i), v = *gp(d.v + i);
         float g = BF16G ? bf16_to_f32(*gp(static_cast<const uint16_t*>(d.g) + i)) : *gp(static_cast<const float*>(d.g) + i);
         Op::elem(p, g, m, v, c, coef);

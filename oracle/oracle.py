@@ -323,3 +323,92 @@ def cast_bf16(x: np.ndarray) -> np.ndarray:
 def fold_add(acc: np.ndarray, g: np.ndarray) -> None:
     g = np.ascontiguousarray(g)
     lib().orc_fold_add(_ptr(acc), _ptr(g), _dt(g), acc.size)
+
+
+# ----------------------------------------------------------- plane codecs
+
+# codec/planes.py:63-70: wire dtype ids and element sizes (torch dtype names).
+PLANE_IDS = {"float32": 0, "bfloat16": 1, "float16": 2, "float8_e4m3fn": 3, "float8_e5m2": 4, "int64": 5}
+PLANE_ESZ = {0: 4, 1: 2, 2: 2, 3: 1, 4: 1, 5: 8}
+
+
+def byte_planes(raw: np.ndarray, esz: int) -> list:
+    """codec/planes.py:152-158: the little-endian elements of `raw` (bytes,
+    esz per element) split into esz planes, most significant byte first; one
+    interleaved plane for single-byte elements."""
+    b = np.ascontiguousarray(raw, dtype=np.uint8).reshape(-1, esz)
+    if esz == 1:
+        return [b.reshape(-1).copy()]
+    return [b[:, j].copy() for j in range(esz - 1, -1, -1)]
+
+
+def planes_encode(raw: np.ndarray, dtype_name: str) -> bytes:
+    """codec/planes.py:141-160: header <BBQ> (id, plane count, elements),
+    one <I> size per plane, then each plane compressed (zlib-1)."""
+    did = PLANE_IDS[dtype_name]
+    esz = PLANE_ESZ[did]
+    blobs = [zlib.compress(p.tobytes(), 1) for p in byte_planes(raw, esz)]
+    head = struct.pack("<BBQ", did, len(blobs), raw.size // esz)
+    head += b"".join(struct.pack("<I", len(b)) for b in blobs)
+    return head + b"".join(blobs)
+
+
+def planes_decode(payload: bytes) -> tuple:
+    """codec/planes.py:163-190 for the plain ids -> (dtype id, element bytes)."""
+    did, nplanes, n = struct.unpack_from("<BBQ", payload, 0)
+    off = struct.calcsize("<BBQ")
+    sizes = []
+    for _ in range(nplanes):
+        sizes.append(struct.unpack_from("<I", payload, off)[0])
+        off += 4
+    esz = PLANE_ESZ[did]
+    planes = []
+    for sz in sizes:
+        planes.append(np.frombuffer(zlib.decompress(payload[off : off + sz]), dtype=np.uint8))
+        off += sz
+    if nplanes == 1:
+        return did, planes[0].copy()
+    out = np.empty((n, esz), dtype=np.uint8)
+    for i, p in enumerate(planes):
+        out[:, esz - 1 - i] = p
+    return did, out.reshape(-1)
+
+
+def nibble_planes(codes: np.ndarray):
+    """codec/fp8_planes.py:27-30: each e4m3 code's high and low nibble, two
+    nibbles per byte in element order (element 2i in the high half), the last
+    byte's low half zero for an odd count."""
+    c = np.ascontiguousarray(codes, dtype=np.uint8).reshape(-1)
+    n = c.size
+    hi, lo = c >> 4, c & 0x0F
+    if n % 2:
+        hi = np.append(hi, np.uint8(0))
+        lo = np.append(lo, np.uint8(0))
+    return ((hi[0::2] << 4) | hi[1::2]).astype(np.uint8), ((lo[0::2] << 4) | lo[1::2]).astype(np.uint8)
+
+
+def fp8_planes_encode(t: np.ndarray) -> bytes:
+    """codec/fp8_planes.py:19-32: t (float32, or bf16 bits as uint16) must be
+    exactly e4m3-representable (AssertionError otherwise, as the reference's
+    assert); payload <QII> + zlib(high nibbles) + zlib(low nibbles)."""
+    t = np.ascontiguousarray(t)
+    x = t.astype(np.float32) if t.dtype == np.float32 else bf16_bits_to_f32(t)
+    codes = fp8_encode(x.reshape(-1), "e4m3")
+    back = fp8_decode_table("e4m3")[codes]
+    if not np.array_equal(back, x.reshape(-1)):  # NaN never equal, -0 == 0 (torch.equal)
+        raise AssertionError("boundary is not FP8-representable: recipe mismatch")
+    hi_p, lo_p = nibble_planes(codes)
+    c_hi, c_lo = zlib.compress(hi_p.tobytes(), 1), zlib.compress(lo_p.tobytes(), 1)
+    return struct.pack("<QII", codes.size, len(c_hi), len(c_lo)) + c_hi + c_lo
+
+
+def fp8_planes_decode(payload: bytes) -> np.ndarray:
+    """codec/fp8_planes.py:35-52: -> float32 values."""
+    n, nhi, nlo = struct.unpack_from("<QII", payload, 0)
+    off = struct.calcsize("<QII")
+    hi_p = np.frombuffer(zlib.decompress(payload[off : off + nhi]), dtype=np.uint8)
+    lo_p = np.frombuffer(zlib.decompress(payload[off + nhi : off + nhi + nlo]), dtype=np.uint8)
+    hi = np.stack([hi_p >> 4, hi_p & 0x0F], axis=1).reshape(-1)[:n]
+    lo = np.stack([lo_p >> 4, lo_p & 0x0F], axis=1).reshape(-1)[:n]
+    codes = ((hi << 4) | lo).astype(np.uint8)
+    return fp8_decode_table("e4m3")[codes]

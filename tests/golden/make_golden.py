@@ -19,6 +19,10 @@ routine or invariant pins bit for bit:
 * planes.encode_scaled_fp8 / decode (codec/planes.py:85-133): the complete
   payload bytes (zlib-1 container, zstandard being absent) for the inputs of
   tests/unit/test_codecs_identity.py:59-68 and a bf16 activation.
+* planes.encode / decode (codec/planes.py:141-190), the lossless byte-plane
+  wire, for every wire dtype, and fp8_planes.encode / decode
+  (codec/fp8_planes.py:19-52), the unscaled e4m3 nibble-plane wire, on even
+  and odd element counts, plus the inputs each refuses.
 
 The fixtures are data only (.npz, no pickles): inputs and the reference's
 outputs.  The torch version they were made with is recorded in each file.
@@ -40,7 +44,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 REF = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
 sys.path.insert(0, os.path.join(REF, "src"))
 
-from wantrain.codec import planes  # noqa: E402
+from wantrain.codec import fp8_planes, planes  # noqa: E402
 from wantrain.model import fp8  # noqa: E402
 from wantrain.runtime import optim  # noqa: E402
 
@@ -285,8 +289,81 @@ def make_wire():
     np.savez_compressed(os.path.join(HERE, "wire.npz"), **arrays)
 
 
+# ----------------------------------------------------------- plane codecs
+
+
+def _plane_inputs():
+    """One small tensor per wire dtype (codec/planes.py:63-70), with the
+    values a byte split must carry: signs, zeros, NaN/Inf, extremes."""
+    g = torch.Generator().manual_seed(41)
+    x = torch.randn(3, 7, 33, generator=g) * 4
+    x.view(-1)[:6] = torch.tensor([0.0, -0.0, float("inf"), -float("inf"), float("nan"), 1e-40])
+    out = [
+        ("f32", x.clone()),
+        ("bf16", x.to(torch.bfloat16)),
+        ("f16", (x / 8).to(torch.float16)),
+        ("e4m3", (x / 8).clamp(-400, 400).to(torch.float8_e4m3fn)),
+        ("e5m2", (x / 8).to(torch.float8_e5m2)),
+        ("i64", torch.randint(-(1 << 62), 1 << 62, (5, 13), generator=g, dtype=torch.int64)),
+        ("bf16_one", torch.tensor([1.5], dtype=torch.bfloat16)),
+    ]
+    return out
+
+
+def _fp8_plane_inputs():
+    """e4m3-representable tensors (the fp8_planes precondition), even and
+    odd element counts, fp32 and bf16."""
+    g = torch.Generator().manual_seed(43)
+    codes = torch.randint(0, 256, (4, 9, 27), generator=g, dtype=torch.int64)
+    codes[(codes & 0x7F) == 0x7F] = 0x11  # no NaN codes
+    q = codes.to(torch.uint8).view(torch.float8_e4m3fn)
+    return [
+        ("odd_f32", q.to(torch.float32)),
+        ("odd_bf16", q.to(torch.bfloat16)),
+        ("even_f32", q.to(torch.float32).reshape(-1)[:512].reshape(16, 32)),
+        ("one_f32", q.to(torch.float32).reshape(-1)[:1]),
+    ]
+
+
+def make_planes():
+    arrays = dict(META)
+    names = []
+    for name, t in _plane_inputs():
+        payload, shape = planes.encode(t)
+        arrays[f"p_{name}_t"] = np.frombuffer(t.contiguous().view(torch.uint8).numpy().tobytes(), dtype=np.uint8).copy()
+        arrays[f"p_{name}_dtype"] = np.array(str(t.dtype))
+        arrays[f"p_{name}_shape"] = np.array(shape, dtype=np.int64)
+        arrays[f"p_{name}_payload"] = np.frombuffer(payload, dtype=np.uint8).copy()
+        back = planes.decode(payload, shape)
+        arrays[f"p_{name}_decoded"] = np.frombuffer(back.contiguous().view(torch.uint8).numpy().tobytes(), dtype=np.uint8).copy()
+        names.append(name)
+    arrays["plane_names"] = np.array(names)
+    names = []
+    for name, t in _fp8_plane_inputs():
+        payload, shape = fp8_planes.encode(t)
+        arrays[f"n_{name}_t"] = _bits(t)
+        arrays[f"n_{name}_dtype"] = np.array(str(t.dtype))
+        arrays[f"n_{name}_shape"] = np.array(shape, dtype=np.int64)
+        arrays[f"n_{name}_payload"] = np.frombuffer(payload, dtype=np.uint8).copy()
+        arrays[f"n_{name}_decoded"] = _bits(fp8_planes.decode(payload, shape))
+        names.append(name)
+    arrays["nibble_names"] = np.array(names)
+    # inputs fp8_planes.encode refuses (not e4m3-representable), one per row
+    bad = torch.tensor([[1.0, 2.0, 3.0, 1.0 + 2.0**-5], [0.0, float("nan"), 1.0, 2.0], [500.0, 1.0, 2.0, 3.0], [2.0**-10, 0, 0, 0]])
+    refused = []
+    for r in bad:
+        try:
+            fp8_planes.encode(r)
+            refused.append(0)
+        except AssertionError:
+            refused.append(1)
+    arrays["n_bad_t"] = _bits(bad)
+    arrays["n_bad_refused"] = np.array(refused, dtype=np.int8)
+    np.savez_compressed(os.path.join(HERE, "planes.npz"), **arrays)
+
+
 if __name__ == "__main__":
-    make_adamw()
-    make_fp8()
-    make_wire()
-    print("golden vectors written to", HERE)
+    which = sys.argv[2:] or ["adamw", "fp8", "wire", "planes"]
+    for w in which:
+        {"adamw": make_adamw, "fp8": make_fp8, "wire": make_wire, "planes": make_planes}[w]()
+    print("golden vectors written to", HERE, which)

@@ -358,3 +358,58 @@ def test_a_wrong_format_bias_fails_the_fp8_golden(oracle):
     assert not np.array_equal(k, g["e4m3_f32_k"])
     q, _ = oracle.quantize(x, "e5m2")
     assert not np.array_equal(q, g["e4m3_f32_q"])
+
+
+# ----------------------------------------------------------- plane codecs
+
+
+def test_byte_plane_payloads_match_reference_golden(oracle):
+    """codec/planes.py:141-190: the oracle's payload equals the reference's,
+    byte for byte, for every wire dtype; decoding restores the bytes."""
+    g = golden("planes.npz")
+    for name in g["plane_names"]:
+        name = str(name)
+        raw = g[f"p_{name}_t"]
+        dname = str(g[f"p_{name}_dtype"]).replace("torch.", "")
+        payload = oracle.planes_encode(raw, dname)
+        assert payload == g[f"p_{name}_payload"].tobytes(), name
+        did, back = oracle.planes_decode(payload)
+        assert did == oracle.PLANE_IDS[dname] and np.array_equal(back, g[f"p_{name}_decoded"]), name
+
+
+def test_byte_planes_are_the_textbook_split(oracle):
+    """Plane j of a 4-byte little-endian element is byte 3 - j: the same as
+    numpy's big-endian view of the elements, read column by column."""
+    x = np.random.default_rng(0).integers(0, 2**32, 1001, dtype=np.uint64).astype(np.uint32)
+    planes = oracle.byte_planes(x.view(np.uint8), 4)
+    be = x.astype(">u4").view(np.uint8).reshape(-1, 4)
+    for j in range(4):
+        assert np.array_equal(planes[j], be[:, j])
+
+
+def test_nibble_payloads_match_reference_golden(oracle):
+    """codec/fp8_planes.py:19-52: payload bytes and decoded values equal the
+    reference's; the inputs it refuses are refused."""
+    g = golden("planes.npz")
+    for name in g["nibble_names"]:
+        name = str(name)
+        t = g[f"n_{name}_t"]
+        payload = oracle.fp8_planes_encode(t)
+        assert payload == g[f"n_{name}_payload"].tobytes(), name
+        assert np.array_equal(oracle.fp8_planes_decode(payload).view(np.uint32), g[f"n_{name}_decoded"].reshape(-1).view(np.uint32))
+    for row, refused in zip(g["n_bad_t"], g["n_bad_refused"]):
+        if refused:
+            with pytest.raises(AssertionError):
+                oracle.fp8_planes_encode(row)
+
+
+def test_nibble_packing_is_numpys_packbits(oracle):
+    """fp8_planes.py:27-30 packs 4-bit values with np.packbits: the oracle's
+    nibble arithmetic equals that library routine on odd and even counts."""
+    rng = np.random.default_rng(1)
+    for n in (1, 2, 7, 1000, 1001):
+        c = rng.integers(0, 256, n, dtype=np.uint8)
+        hi, lo = oracle.nibble_planes(c)
+        for plane, nib in ((hi, c >> 4), (lo, c & 0x0F)):
+            ref = np.packbits(np.unpackbits(nib.reshape(-1, 1), axis=1, count=8)[:, 4:])
+            assert np.array_equal(plane, ref)
