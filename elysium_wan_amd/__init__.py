@@ -8,12 +8,14 @@ Modules mirror the reference's:
   fp8     -- model/fp8.py       (scale_exp, quantize, dequantize, roundtrip,
              recover_exp)
   pieces  -- runtime/pieces.py  (cast_piece, fold_start, fold_add, fold)
-  planes  -- codec/planes.py    (encode_scaled_fp8, decode: the scaled-fp8 wire)
+  planes  -- codec/planes.py    (encode, decode, encode_scaled_fp8: the
+             byte-plane and scaled-fp8 wires)
+  fp8_planes -- codec/fp8_planes.py (encode, decode: the e4m3 nibble wire)
   boundary -- model/gpt.py:284-317 (narrow, Boundary: the codec's caller)
 The kernels live in libelyhip.so (C ABI: include/ely.h), built by
 elysium_wan_amd.build for gfx950.
 """
 
-from . import boundary, fp8, optim, pieces, planes  # noqa: F401
+from . import boundary, fp8, fp8_planes, optim, pieces, planes  # noqa: F401
 
-__all__ = ["boundary", "fp8", "optim", "pieces", "planes"]
+__all__ = ["boundary", "fp8", "fp8_planes", "optim", "pieces", "planes"]

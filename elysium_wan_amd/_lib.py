@@ -28,8 +28,10 @@ EXPORTS = (
     "ely_last_error",
     "ely_grad_norm_workspace_bytes",
     "ely_grad_norm",
+    "ely_grad_norm_fold",
     "ely_adamw_workspace_bytes",
     "ely_adamw_step",
+    "ely_adamw_fold_step",
     "ely_fp8_workspace_bytes",
     "ely_fp8_quantize",
     "ely_fp8_dequantize",
@@ -41,6 +43,10 @@ EXPORTS = (
     "ely_fold_add",
     "ely_scale_inplace",
     "ely_set_max_blocks",
+    "ely_byteplanes_split",
+    "ely_byteplanes_join",
+    "ely_fp8_nibbles_encode",
+    "ely_fp8_nibbles_decode",
     "ely_selftest_fp8_cvt",
     "ely_selftest_sqrt",
 )
@@ -83,9 +89,11 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
         L.ely_grad_norm_workspace_bytes.restype = I64
         L.ely_grad_norm_workspace_bytes.argtypes = [TP, I32]
         L.ely_grad_norm.argtypes = [TP, I32, F, P, P, I64, P]
+        L.ely_grad_norm_fold.argtypes = [TP, TP, I32, F, P, P, I64, P]
         L.ely_adamw_workspace_bytes.restype = I64
         L.ely_adamw_workspace_bytes.argtypes = [I32]
         L.ely_adamw_step.argtypes = [TP, TP, TP, TP, TP, I32, ctypes.POINTER(ElyConsts), I32, I32, P, P, I64, P]
+        L.ely_adamw_fold_step.argtypes = [TP, TP, TP, TP, TP, TP, I32, ctypes.POINTER(ElyConsts), I32, I32, P, P, I64, P]
         L.ely_fp8_workspace_bytes.restype = I64
         L.ely_fp8_workspace_bytes.argtypes = [I64, I64, I32]
         L.ely_fp8_quantize.argtypes = [P, I32, I64, I64, I32, P, P, P, I64, P]
@@ -99,6 +107,10 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
         L.ely_fold_add.argtypes = [P, P, I32, I64, P]
         L.ely_scale_inplace.argtypes = [TP, I32, P, P]
         L.ely_set_max_blocks.argtypes = [I32]
+        L.ely_byteplanes_split.argtypes = [P, I64, I32, P, P]
+        L.ely_byteplanes_join.argtypes = [P, I64, I32, P, P]
+        L.ely_fp8_nibbles_encode.argtypes = [P, I32, I64, P, P, P, P]
+        L.ely_fp8_nibbles_decode.argtypes = [P, P, I64, P, P]
         L.ely_selftest_fp8_cvt.argtypes = [ctypes.c_uint32, ctypes.c_uint64, I32, P, P]
         L.ely_selftest_sqrt.argtypes = [ctypes.c_uint32, ctypes.c_uint64, P, P]
         _lib = L

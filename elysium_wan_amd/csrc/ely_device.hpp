@@ -163,6 +163,12 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
     return v;
 }
 
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += (uint32_t)__shfl_xor((int)v, o, kWave);
+    return v;
+}
+
 // Butterfly sum: every lane ends with the same value, in a fixed order.
 __device__ __forceinline__ double wave_sum_f64(double v) {
 #pragma unroll

@@ -77,12 +77,13 @@ __device__ __forceinline__ int find_tensor(const Desc* desc, int n, int64_t tile
 }
 
 
-struct NormDesc {          // 32 bytes
+struct NormDesc {          // 40 bytes
     const void* g;
+    const float* acc;      // FOLD: the fp32 fold of the earlier microbatches
     int64_t numel;
     int64_t tile_begin;
     int32_t dtype;         // ELY_F32 | ELY_BF16
-    int32_t aligned;       // g is 16-byte aligned
+    int32_t aligned;       // g (and acc) 16-byte aligned
 };
 
 // Sum of squares of 8 values by a fixed fp32 tree.
@@ -117,7 +118,9 @@ __device__ __forceinline__ T ld_norm(const ELY_GLOBAL T* p) {
 #endif
 }
 
-// 8 consecutive gradient values from a 16-byte aligned address.
+// 8 consecutive gradient values from a 16-byte aligned address.  With FOLD
+// each is acc + widen(g) rounded once to fp32 (pieces.fold_add).
+template <bool FOLD>
 __device__ __forceinline__ void load8_vec(const NormDesc& d, int64_t i, float (&x)[8]) {
     if (d.dtype == ELY_BF16) {
         const nu32x4 w = ld_norm(gp(reinterpret_cast<const nu32x4*>(static_cast<const uint16_t*>(d.g) + i)));
@@ -135,9 +138,19 @@ __device__ __forceinline__ void load8_vec(const NormDesc& d, int64_t i, float (&
             x[4 + j] = b[j];
         }
     }
+    if (FOLD) {
+        const ELY_GLOBAL nf32x4* q = gp(reinterpret_cast<const nf32x4*>(d.acc + i));
+        const nf32x4 a = ld_norm(q), b = ld_norm(q + 1);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            x[j] = a[j] + x[j];
+            x[4 + j] = b[j] + x[4 + j];
+        }
+    }
 }
 
 // The same 8 values element by element (0 past `end`): any alignment.
+template <bool FOLD>
 __device__ __forceinline__ void load8_any(const NormDesc& d, int64_t i, int64_t end, float (&x)[8]) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -146,11 +159,13 @@ __device__ __forceinline__ void load8_any(const NormDesc& d, int64_t i, int64_t 
         if (e < end) {
             v = d.dtype == ELY_BF16 ? bf16_to_f32(*gp(static_cast<const uint16_t*>(d.g) + e))
                                     : *gp(static_cast<const float*>(d.g) + e);
+            if (FOLD) v = *gp(d.acc + e) + v;
         }
         x[j] = v;
     }
 }
 
+template <bool FOLD>
 __global__ __launch_bounds__(kBlock) void norm_partials_kernel(const NormDesc* __restrict__ desc, int32_t n,
                                                                int64_t total_tiles, double* __restrict__ partials) {
     const int lane = threadIdx.x & (kWave - 1);
@@ -174,13 +189,13 @@ __global__ __launch_bounds__(kBlock) void norm_partials_kernel(const NormDesc* _
 #pragma unroll ELY_NORM_UNROLL
             for (int j = 0; j < (int)(kNormTile / (kWave * 8)); ++j) {
                 float x[8];
-                load8_vec(d, e0 + ((int64_t)j * kWave + lane) * 8, x);
+                load8_vec<FOLD>(d, e0 + ((int64_t)j * kWave + lane) * 8, x);
                 acc += (double)sq8(x);
             }
         } else {
             for (int j = 0; j < (int)(kNormTile / (kWave * 8)); ++j) {
                 float x[8];
-                load8_any(d, e0 + ((int64_t)j * kWave + lane) * 8, e1, x);
+                load8_any<FOLD>(d, e0 + ((int64_t)j * kWave + lane) * 8, e1, x);
                 acc += (double)sq8(x);
             }
         }
@@ -226,9 +241,10 @@ static size_t norm_table_bytes(int32_t n) { return align_up((size_t)n * sizeof(N
 
 // ------------------------------------------------------------- (b) AdamW
 
-struct AdamDesc {          // 64 bytes
+struct AdamDesc {          // 72 bytes
     float* p;
     const void* g;
+    const float* acc;      // FOLD: the fp32 fold of the earlier microbatches
     float* m;
     float* v;
     uint16_t* copy;        // bf16 working copy or null
@@ -238,7 +254,7 @@ struct AdamDesc {          // 64 bytes
     int32_t pad;
 };
 
-template <bool BF16G, int ORDER, bool WD, bool CLIP>
+template <bool BF16G, int ORDER, bool WD, bool CLIP, bool FOLD>
 struct AdamOp {
     __device__ __forceinline__ static void elem(float& p, float g, float& m, float& v, const ely_adamw_consts& c,
                                                 float coef) {
@@ -290,7 +306,7 @@ struct Quad2 {
     float g[8];
 };
 
-template <bool BF16G>
+template <bool BF16G, bool FOLD>
 __device__ __forceinline__ void quad_load(const AdamDesc& d, int64_t i, Quad2<BF16G>& Q) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -309,13 +325,19 @@ __device__ __forceinline__ void quad_load(const AdamDesc& d, int64_t i, Quad2<BF
 #pragma unroll
             for (int j = 0; j < 4; ++j) Q.g[4 * h + j] = a[j];
         }
+        if (FOLD) {
+            // the last microbatch folded in: acc + widen(g), one fp32 rounding
+            const f32x4 a = ld_stream(gp(reinterpret_cast<const f32x4*>(d.acc + e)));
+#pragma unroll
+            for (int j = 0; j < 4; ++j) Q.g[4 * h + j] = a[j] + Q.g[4 * h + j];
+        }
     }
 }
 
-template <bool BF16G, int ORDER, bool WD, bool CLIP>
+template <bool BF16G, int ORDER, bool WD, bool CLIP, bool FOLD>
 __device__ __forceinline__ void quad_update_store(const AdamDesc& d, int64_t i, Quad2<BF16G>& Q,
                                                   const ely_adamw_consts& c, float coef) {
-    using Op = AdamOp<BF16G, ORDER, WD, CLIP>;
+    using Op = AdamOp<BF16G, ORDER, WD, CLIP, FOLD>;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         float p[4], m[4], v[4];
@@ -337,10 +359,10 @@ __device__ __forceinline__ void quad_update_store(const AdamDesc& d, int64_t i, 
     }
 }
 
-template <bool BF16G, int ORDER, bool WD, bool CLIP>
+template <bool BF16G, int ORDER, bool WD, bool CLIP, bool FOLD>
 __device__ __forceinline__ void adam_range(const AdamDesc& d, const ely_adamw_consts& c, float coef, int64_t e0,
                                            int64_t e1) {
-    using Op = AdamOp<BF16G, ORDER, WD, CLIP>;
+    using Op = AdamOp<BF16G, ORDER, WD, CLIP, FOLD>;
     constexpr int U = ELY_ADAM_UNROLL;
     int64_t done = e0;
     if (d.aligned) {
@@ -350,14 +372,15 @@ __device__ __forceinline__ void adam_range(const AdamDesc& d, const ely_adamw_co
         for (; s + U <= steps; s += U) {
             Quad2<BF16G> Q[U];
 #pragma unroll
-            for (int u = 0; u < U; ++u) quad_load(d, e0 + (s + u) * kStep + t4, Q[u]);
+            for (int u = 0; u < U; ++u) quad_load<BF16G, FOLD>(d, e0 + (s + u) * kStep + t4, Q[u]);
 #pragma unroll
-            for (int u = 0; u < U; ++u) quad_update_store<BF16G, ORDER, WD, CLIP>(d, e0 + (s + u) * kStep + t4, Q[u], c, coef);
+            for (int u = 0; u < U; ++u)
+                quad_update_store<BF16G, ORDER, WD, CLIP, FOLD>(d, e0 + (s + u) * kStep + t4, Q[u], c, coef);
         }
         for (; s < steps; ++s) {
             Quad2<BF16G> Q;
-            quad_load(d, e0 + s * kStep + t4, Q);
-            quad_update_store<BF16G, ORDER, WD, CLIP>(d, e0 + s * kStep + t4, Q, c, coef);
+            quad_load<BF16G, FOLD>(d, e0 + s * kStep + t4, Q);
+            quad_update_store<BF16G, ORDER, WD, CLIP, FOLD>(d, e0 + s * kStep + t4, Q, c, coef);
         }
         done = e0 + steps * kStep;
     }
@@ -365,6 +388,7 @@ __device__ __forceinline__ void adam_range(const AdamDesc& d, const ely_adamw_co
     for (int64_t i = done + threadIdx.x; i < e1; i += kBlock) {
         float p = *gp(d.p + i), m = *gp(d.m + i), v = *gp(d.v + i);
         float g = BF16G ? bf16_to_f32(*gp(static_cast<const uint16_t*>(d.g) + i)) : *gp(static_cast<const float*>(d.g) + i);
+        if (FOLD) g = *gp(d.acc + i) + g;
         Op::elem(p, g, m, v, c, coef);
         *gp(d.p + i) = p;
         *gp(d.m + i) = m;
@@ -373,7 +397,7 @@ __device__ __forceinline__ void adam_range(const AdamDesc& d, const ely_adamw_co
     }
 }
 
-template <bool BF16G, int ORDER, bool WD, bool CLIP>
+template <bool BF16G, int ORDER, bool WD, bool CLIP, bool FOLD>
 __global__ __launch_bounds__(kBlock) void adamw_kernel(const AdamDesc* __restrict__ desc,
                                                        const ely_adamw_consts* __restrict__ consts, int32_t n,
                                                        int64_t total_tiles, const float* __restrict__ coef_ptr) {
@@ -393,7 +417,7 @@ __global__ __launch_bounds__(kBlock) void adamw_kernel(const AdamDesc* __restric
         const int64_t e0 = (tile - d.tile_begin) * kAdamTile;
         const int64_t e1 = min((tend - d.tile_begin) * kAdamTile, d.numel);
         const ely_adamw_consts c = consts[ti];
-        adam_range<BF16G, ORDER, WD, CLIP>(d, c, coef, e0, e1);
+        adam_range<BF16G, ORDER, WD, CLIP, FOLD>(d, c, coef, e0, e1);
         tile = tend;
     }
 #else
@@ -407,17 +431,17 @@ __global__ __launch_bounds__(kBlock) void adamw_kernel(const AdamDesc* __restric
         const int64_t e0 = (tile - d.tile_begin) * kAdamTile;
         const int64_t e1 = min(e0 + kAdamTile, d.numel);
         const ely_adamw_consts c = consts[ti];
-        adam_range<BF16G, ORDER, WD, CLIP>(d, c, coef, e0, e1);
+        adam_range<BF16G, ORDER, WD, CLIP, FOLD>(d, c, coef, e0, e1);
     }
 #endif
 }
 
 typedef void (*AdamKernel)(const AdamDesc*, const ely_adamw_consts*, int32_t, int64_t, const float*);
 
-template <bool BF16G, int ORDER>
+template <bool BF16G, int ORDER, bool FOLD>
 static AdamKernel pick_adam(bool wd, bool clip) {
-    if (wd) return clip ? adamw_kernel<BF16G, ORDER, true, true> : adamw_kernel<BF16G, ORDER, true, false>;
-    return clip ? adamw_kernel<BF16G, ORDER, false, true> : adamw_kernel<BF16G, ORDER, false, false>;
+    if (wd) return clip ? adamw_kernel<BF16G, ORDER, true, true, FOLD> : adamw_kernel<BF16G, ORDER, true, false, FOLD>;
+    return clip ? adamw_kernel<BF16G, ORDER, false, true, FOLD> : adamw_kernel<BF16G, ORDER, false, false, FOLD>;
 }
 
 static size_t adam_table_bytes(int32_t n) {
@@ -435,9 +459,153 @@ static void check_list(const ely_tensor* t, int32_t n, const char* what) {
     }
 }
 
+// Fold accumulators: fp32, one per gradient, of its numel.
+static void check_folds(const ely_tensor* accs, const ely_tensor* grads, int32_t n, const char* what) {
+    for (int32_t i = 0; i < n; ++i) {
+        if (accs[i].dtype != ELY_F32 || accs[i].numel != grads[i].numel)
+            fail(ELY_EINVAL, std::string(what) + ": accumulator " + std::to_string(i) + " must be fp32 of the gradient's numel");
+        if (accs[i].numel > 0 && !accs[i].ptr) fail(ELY_EINVAL, std::string(what) + ": null accumulator pointer");
+    }
+}
+
+template <bool FOLD>
+static AdamKernel pick_adam_order(bool bf16g, int32_t order, bool wd, bool clip) {
+    if (bf16g)
+        return order == ELY_ORDER_HOST ? pick_adam<true, ELY_ORDER_HOST, FOLD>(wd, clip)
+                                       : pick_adam<true, ELY_ORDER_TORCH, FOLD>(wd, clip);
+    return order == ELY_ORDER_HOST ? pick_adam<false, ELY_ORDER_HOST, FOLD>(wd, clip)
+                                   : pick_adam<false, ELY_ORDER_TORCH, FOLD>(wd, clip);
+}
+
 }  // namespace ely
 
 using namespace ely;
+
+// ws query used by the implementations below
+extern "C" int64_t ely_grad_norm_workspace_bytes(const ely_tensor* grads, int32_t n);
+extern "C" int64_t ely_adamw_workspace_bytes(int32_t n);
+
+namespace ely {
+
+// The norm of grads (FOLD: of accs[i] + widen(grads[i])): see ely_grad_norm.
+static void grad_norm_impl(const ely_tensor* accs, const ely_tensor* grads, int32_t n, float max_norm,
+                           ely_norm_result* out_dev, void* workspace, int64_t ws_bytes, void* stream) {
+    check_list(grads, n, "ely_grad_norm grads");
+    if (accs) check_folds(accs, grads, n, "ely_grad_norm_fold");
+    if (!out_dev) fail(ELY_EINVAL, "ely_grad_norm: null result pointer");
+    const int64_t need = ely_grad_norm_workspace_bytes(grads, n);
+    if (!workspace || ws_bytes < need)
+        fail(ELY_EWORKSPACE, "ely_grad_norm: workspace of " + std::to_string(ws_bytes) + " bytes, need " +
+                                 std::to_string(need));
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    std::vector<NormDesc> table;
+    table.reserve(n);
+    int64_t tiles = 0;
+    for (int32_t i = 0; i < n; ++i) {
+        if (grads[i].numel == 0) continue;
+        NormDesc d;
+        d.g = grads[i].ptr;
+        d.acc = accs ? static_cast<const float*>(accs[i].ptr) : nullptr;
+        d.numel = grads[i].numel;
+        d.tile_begin = tiles;
+        d.dtype = grads[i].dtype;
+        d.aligned = aligned16(grads[i].ptr) && (!accs || aligned16(accs[i].ptr)) ? 1 : 0;
+        table.push_back(d);
+        tiles += (d.numel + kNormTile - 1) / kNormTile;
+    }
+    char* ws = static_cast<char*>(workspace);
+    NormDesc* dtable = reinterpret_cast<NormDesc*>(ws);
+    double* partials = reinterpret_cast<double*>(ws + norm_table_bytes(n));
+    if (tiles > 0) {
+        upload(dtable, table.data(), table.size() * sizeof(NormDesc), s);
+        const int64_t waves = std::min<int64_t>(tiles, mt_blocks(ELY_NORM_BPC) * (kBlock / kWave));
+        const int64_t blocks = (waves + 3) / 4;
+        if (accs)
+            hipLaunchKernelGGL(norm_partials_kernel<true>, dim3((unsigned)blocks), dim3(kBlock), 0, s, dtable,
+                               (int32_t)table.size(), tiles, partials);
+        else
+            hipLaunchKernelGGL(norm_partials_kernel<false>, dim3((unsigned)blocks), dim3(kBlock), 0, s, dtable,
+                               (int32_t)table.size(), tiles, partials);
+        check_launch("norm_partials_kernel");
+    }
+    hipLaunchKernelGGL(norm_final_kernel, dim3(1), dim3(kFinalThreads), 0, s, partials, tiles, max_norm,
+                       out_dev);
+    check_launch("norm_final_kernel");
+}
+
+// One fused step (FOLD: the gradient of tensor i is accs[i] + widen(grads[i])).
+static void adamw_impl(const ely_tensor* params, const ely_tensor* accs, const ely_tensor* grads,
+                       const ely_tensor* exp_avg, const ely_tensor* exp_avg_sq, const ely_tensor* copies, int32_t n,
+                       const ely_adamw_consts* consts, int32_t order, int32_t weight_decay_nonzero,
+                       const float* coef_dev, void* workspace, int64_t ws_bytes, void* stream) {
+    check_list(params, n, "ely_adamw_step params");
+    check_list(grads, n, "ely_adamw_step grads");
+    if (accs) check_folds(accs, grads, n, "ely_adamw_fold_step");
+    check_list(exp_avg, n, "ely_adamw_step exp_avg");
+    check_list(exp_avg_sq, n, "ely_adamw_step exp_avg_sq");
+    if (order != ELY_ORDER_HOST && order != ELY_ORDER_TORCH)
+        fail(ELY_EINVAL, "ely_adamw_step: order must be ELY_ORDER_HOST or ELY_ORDER_TORCH");
+    if (n > 0 && !consts) fail(ELY_EINVAL, "ely_adamw_step: null constants");
+    const int64_t need = ely_adamw_workspace_bytes(n);
+    if (!workspace || ws_bytes < need)
+        fail(ELY_EWORKSPACE, "ely_adamw_step: workspace of " + std::to_string(ws_bytes) + " bytes, need " +
+                                 std::to_string(need));
+    int gdt = -1;
+    std::vector<AdamDesc> table;
+    std::vector<ely_adamw_consts> cs;
+    table.reserve(n);
+    cs.reserve(n);
+    int64_t tiles = 0;
+    for (int32_t i = 0; i < n; ++i) {
+        const int64_t ne = params[i].numel;
+        if (params[i].dtype != ELY_F32 || exp_avg[i].dtype != ELY_F32 || exp_avg_sq[i].dtype != ELY_F32)
+            fail(ELY_EINVAL, "ely_adamw_step: params and moments must be fp32 (tensor " + std::to_string(i) + ")");
+        if (grads[i].numel != ne || exp_avg[i].numel != ne || exp_avg_sq[i].numel != ne)
+            fail(ELY_EINVAL, "ely_adamw_step: numel mismatch at tensor " + std::to_string(i));
+        if (copies && copies[i].ptr) {
+            if (copies[i].dtype != ELY_BF16 || copies[i].numel != ne)
+                fail(ELY_EINVAL, "ely_adamw_step: working copy " + std::to_string(i) + " must be bf16 of numel " +
+                                     std::to_string(ne));
+        }
+        if (ne == 0) continue;
+        if (gdt < 0) gdt = grads[i].dtype;
+        else if (gdt != grads[i].dtype)
+            fail(ELY_EINVAL, "ely_adamw_step: grads of one call share one dtype");
+        AdamDesc d;
+        d.p = static_cast<float*>(params[i].ptr);
+        d.g = grads[i].ptr;
+        d.acc = accs ? static_cast<const float*>(accs[i].ptr) : nullptr;
+        d.m = static_cast<float*>(exp_avg[i].ptr);
+        d.v = static_cast<float*>(exp_avg_sq[i].ptr);
+        d.copy = copies ? static_cast<uint16_t*>(copies[i].ptr) : nullptr;
+        d.numel = ne;
+        d.tile_begin = tiles;
+        d.aligned = aligned16(d.p) && aligned16(d.g) && aligned16(d.m) && aligned16(d.v) &&
+                    (!d.copy || aligned16(d.copy)) && (!d.acc || aligned16(d.acc));
+        d.pad = 0;
+        table.push_back(d);
+        cs.push_back(consts[i]);
+        tiles += (ne + kAdamTile - 1) / kAdamTile;
+    }
+    if (tiles == 0) return;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    char* ws = static_cast<char*>(workspace);
+    AdamDesc* dtable = reinterpret_cast<AdamDesc*>(ws);
+    ely_adamw_consts* dconsts = reinterpret_cast<ely_adamw_consts*>(ws + align_up((size_t)n * sizeof(AdamDesc), 256));
+    upload(dtable, table.data(), table.size() * sizeof(AdamDesc), s);
+    upload(dconsts, cs.data(), cs.size() * sizeof(ely_adamw_consts), s);
+    const bool wd = weight_decay_nonzero != 0;
+    const bool clip = coef_dev != nullptr;
+    AdamKernel k;
+    if (accs) k = pick_adam_order<true>(gdt == ELY_BF16, order, wd, clip);
+    else k = pick_adam_order<false>(gdt == ELY_BF16, order, wd, clip);
+    const int64_t blocks = std::min<int64_t>(tiles, mt_blocks(ELY_ADAM_BPC));
+    hipLaunchKernelGGL(k, dim3((unsigned)blocks), dim3(kBlock), 0, s, dtable, dconsts, (int32_t)table.size(),
+                       tiles, coef_dev);
+    check_launch("adamw_kernel");
+}
+
+}  // namespace ely
 
 extern "C" {
 
@@ -448,42 +616,14 @@ int64_t ely_grad_norm_workspace_bytes(const ely_tensor* grads, int32_t n) {
 
 int ely_grad_norm(const ely_tensor* grads, int32_t n, float max_norm, ely_norm_result* out_dev, void* workspace,
                   int64_t ws_bytes, void* stream) {
+    return guarded([&] { grad_norm_impl(nullptr, grads, n, max_norm, out_dev, workspace, ws_bytes, stream); });
+}
+
+int ely_grad_norm_fold(const ely_tensor* accs, const ely_tensor* grads, int32_t n, float max_norm,
+                       ely_norm_result* out_dev, void* workspace, int64_t ws_bytes, void* stream) {
     return guarded([&] {
-        check_list(grads, n, "ely_grad_norm grads");
-        if (!out_dev) fail(ELY_EINVAL, "ely_grad_norm: null result pointer");
-        const int64_t need = ely_grad_norm_workspace_bytes(grads, n);
-        if (!workspace || ws_bytes < need)
-            fail(ELY_EWORKSPACE, "ely_grad_norm: workspace of " + std::to_string(ws_bytes) + " bytes, need " +
-                                     std::to_string(need));
-        hipStream_t s = static_cast<hipStream_t>(stream);
-        std::vector<NormDesc> table;
-        table.reserve(n);
-        int64_t tiles = 0;
-        for (int32_t i = 0; i < n; ++i) {
-            if (grads[i].numel == 0) continue;
-            NormDesc d;
-            d.g = grads[i].ptr;
-            d.numel = grads[i].numel;
-            d.tile_begin = tiles;
-            d.dtype = grads[i].dtype;
-            d.aligned = aligned16(grads[i].ptr) ? 1 : 0;
-            table.push_back(d);
-            tiles += (d.numel + kNormTile - 1) / kNormTile;
-        }
-        char* ws = static_cast<char*>(workspace);
-        NormDesc* dtable = reinterpret_cast<NormDesc*>(ws);
-        double* partials = reinterpret_cast<double*>(ws + norm_table_bytes(n));
-        if (tiles > 0) {
-            upload(dtable, table.data(), table.size() * sizeof(NormDesc), s);
-            const int64_t waves = std::min<int64_t>(tiles, mt_blocks(ELY_NORM_BPC) * (kBlock / kWave));
-            const int64_t blocks = (waves + 3) / 4;
-            hipLaunchKernelGGL(norm_partials_kernel, dim3((unsigned)blocks), dim3(kBlock), 0, s, dtable,
-                               (int32_t)table.size(), tiles, partials);
-            check_launch("norm_partials_kernel");
-        }
-        hipLaunchKernelGGL(norm_final_kernel, dim3(1), dim3(kFinalThreads), 0, s, partials, tiles, max_norm,
-                           out_dev);
-        check_launch("norm_final_kernel");
+        if (n > 0 && !accs) fail(ELY_EINVAL, "ely_grad_norm_fold: null accumulator list");
+        grad_norm_impl(accs, grads, n, max_norm, out_dev, workspace, ws_bytes, stream);
     });
 }
 
@@ -497,72 +637,19 @@ int ely_adamw_step(const ely_tensor* params, const ely_tensor* grads, const ely_
                    int32_t order, int32_t weight_decay_nonzero, const float* coef_dev, void* workspace,
                    int64_t ws_bytes, void* stream) {
     return guarded([&] {
-        check_list(params, n, "ely_adamw_step params");
-        check_list(grads, n, "ely_adamw_step grads");
-        check_list(exp_avg, n, "ely_adamw_step exp_avg");
-        check_list(exp_avg_sq, n, "ely_adamw_step exp_avg_sq");
-        if (order != ELY_ORDER_HOST && order != ELY_ORDER_TORCH)
-            fail(ELY_EINVAL, "ely_adamw_step: order must be ELY_ORDER_HOST or ELY_ORDER_TORCH");
-        if (n > 0 && !consts) fail(ELY_EINVAL, "ely_adamw_step: null constants");
-        const int64_t need = ely_adamw_workspace_bytes(n);
-        if (!workspace || ws_bytes < need)
-            fail(ELY_EWORKSPACE, "ely_adamw_step: workspace of " + std::to_string(ws_bytes) + " bytes, need " +
-                                     std::to_string(need));
-        int gdt = -1;
-        std::vector<AdamDesc> table;
-        std::vector<ely_adamw_consts> cs;
-        table.reserve(n);
-        cs.reserve(n);
-        int64_t tiles = 0;
-        for (int32_t i = 0; i < n; ++i) {
-            const int64_t ne = params[i].numel;
-            if (params[i].dtype != ELY_F32 || exp_avg[i].dtype != ELY_F32 || exp_avg_sq[i].dtype != ELY_F32)
-                fail(ELY_EINVAL, "ely_adamw_step: params and moments must be fp32 (tensor " + std::to_string(i) + ")");
-            if (grads[i].numel != ne || exp_avg[i].numel != ne || exp_avg_sq[i].numel != ne)
-                fail(ELY_EINVAL, "ely_adamw_step: numel mismatch at tensor " + std::to_string(i));
-            if (copies && copies[i].ptr) {
-                if (copies[i].dtype != ELY_BF16 || copies[i].numel != ne)
-                    fail(ELY_EINVAL, "ely_adamw_step: working copy " + std::to_string(i) + " must be bf16 of numel " +
-                                         std::to_string(ne));
-            }
-            if (ne == 0) continue;
-            if (gdt < 0) gdt = grads[i].dtype;
-            else if (gdt != grads[i].dtype)
-                fail(ELY_EINVAL, "ely_adamw_step: grads of one call share one dtype");
-            AdamDesc d;
-            d.p = static_cast<float*>(params[i].ptr);
-            d.g = grads[i].ptr;
-            d.m = static_cast<float*>(exp_avg[i].ptr);
-            d.v = static_cast<float*>(exp_avg_sq[i].ptr);
-            d.copy = copies ? static_cast<uint16_t*>(copies[i].ptr) : nullptr;
-            d.numel = ne;
-            d.tile_begin = tiles;
-            d.aligned = aligned16(d.p) && aligned16(d.g) && aligned16(d.m) && aligned16(d.v) &&
-                        (!d.copy || aligned16(d.copy));
-            d.pad = 0;
-            table.push_back(d);
-            cs.push_back(consts[i]);
-            tiles += (ne + kAdamTile - 1) / kAdamTile;
-        }
-        if (tiles == 0) return;
-        hipStream_t s = static_cast<hipStream_t>(stream);
-        char* ws = static_cast<char*>(workspace);
-        AdamDesc* dtable = reinterpret_cast<AdamDesc*>(ws);
-        ely_adamw_consts* dconsts = reinterpret_cast<ely_adamw_consts*>(ws + align_up((size_t)n * sizeof(AdamDesc), 256));
-        upload(dtable, table.data(), table.size() * sizeof(AdamDesc), s);
-        upload(dconsts, cs.data(), cs.size() * sizeof(ely_adamw_consts), s);
-        const bool wd = weight_decay_nonzero != 0;
-        const bool clip = coef_dev != nullptr;
-        AdamKernel k;
-        if (gdt == ELY_BF16)
-            k = order == ELY_ORDER_HOST ? pick_adam<true, ELY_ORDER_HOST>(wd, clip) : pick_adam<true, ELY_ORDER_TORCH>(wd, clip);
-        else
-            k = order == ELY_ORDER_HOST ? pick_adam<false, ELY_ORDER_HOST>(wd, clip)
-                                        : pick_adam<false, ELY_ORDER_TORCH>(wd, clip);
-        const int64_t blocks = std::min<int64_t>(tiles, mt_blocks(ELY_ADAM_BPC));
-        hipLaunchKernelGGL(k, dim3((unsigned)blocks), dim3(kBlock), 0, s, dtable, dconsts, (int32_t)table.size(),
-                           tiles, coef_dev);
-        check_launch("adamw_kernel");
+        adamw_impl(params, nullptr, grads, exp_avg, exp_avg_sq, copies, n, consts, order, weight_decay_nonzero, coef_dev,
+                   workspace, ws_bytes, stream);
+    });
+}
+
+int ely_adamw_fold_step(const ely_tensor* params, const ely_tensor* accs, const ely_tensor* grads,
+                        const ely_tensor* exp_avg, const ely_tensor* exp_avg_sq, const ely_tensor* copies, int32_t n,
+                        const ely_adamw_consts* consts, int32_t order, int32_t weight_decay_nonzero,
+                        const float* coef_dev, void* workspace, int64_t ws_bytes, void* stream) {
+    return guarded([&] {
+        if (n > 0 && !accs) fail(ELY_EINVAL, "ely_adamw_fold_step: null accumulator list");
+        adamw_impl(params, accs, grads, exp_avg, exp_avg_sq, copies, n, consts, order, weight_decay_nonzero, coef_dev,
+                   workspace, ws_bytes, stream);
     });
 }
 

@@ -149,6 +149,7 @@ class FusedAdamW:
         self.recipe = "adamw-host" if order == "host" else "adamw"
         devices = set()
         for p in self.params:
+            # a frozen tensor never has a gradient and is never stepped (runtime/optim.py:98-99)
             if p.requires_grad and p.dtype != torch.float32:
                 raise ValueError(f"{self.recipe} trains fp32 parameters, got {p.dtype}")
             if p.requires_grad:
@@ -156,6 +157,12 @@ class FusedAdamW:
                 devices.add(p.device)
         if len(devices) > 1:
             raise ValueError(f"{self.recipe}: parameters span devices {sorted(map(str, devices))}; build one optimizer per device")
+        if not devices:
+            # no parameter requires grad: the moments follow the GPU tensors
+            devices = {p.device for p in self.params if p.device.type == "cuda"}
+            if len(devices) > 1:
+                raise ValueError(f"{self.recipe}: parameters span devices {sorted(map(str, devices))}; build one optimizer per device")
+        # the device of the moments (set by the first stepped parameter if still unknown)
         self.device = devices.pop() if devices else None
         self.lr, self.betas, self.eps, self.weight_decay = lr, tuple(betas), eps, weight_decay
         self.max_norm = None if max_norm is None else float(max_norm)
@@ -193,6 +200,8 @@ class FusedAdamW:
             offs.append(total)
             total += -(-p.numel() // _ALIGN) * _ALIGN
         dev = self.device
+        if dev is None or dev.type != "cuda":
+            raise ValueError(f"{self.recipe}: the moments live on the parameters' GPU, got device {dev}")
         self._flat_m = torch.zeros(max(total, 1), dtype=torch.float32, device=dev)
         self._flat_v = torch.zeros(max(total, 1), dtype=torch.float32, device=dev)
         self._offs = offs
@@ -218,17 +227,24 @@ class FusedAdamW:
         return torch_consts(self.lr, self.betas, self.eps, self.weight_decay, t)
 
     @torch.no_grad()
-    def step(self, on_param=None, grads=None) -> None:
+    def step(self, on_param=None, grads=None, acc=None) -> None:
         """One AdamW step over every parameter with a gradient, in order;
         `on_param(i)` runs after parameter i's update is issued
         (runtime/optim.py:145-170).  Nothing here waits for the GPU.
 
         grads: optional list aligned with the parameters (None entries skip
         a parameter) used instead of p.grad -- the way to hand in bf16
-        gradients, which torch does not let an fp32 parameter's .grad hold."""
+        gradients, which torch does not let an fp32 parameter's .grad hold.
+        acc: optional list aligned with the parameters of fp32 fold
+        accumulators (runtime/accumulate.py:93-104) holding the sum of the
+        earlier microbatches; the step's gradient is then acc[i] + grads[i]
+        rounded once to fp32 (pieces.fold_add), folded inside the update
+        without writing acc."""
         if grads is not None and len(grads) != len(self.params):
             raise ValueError(f"{len(grads)} gradients for {len(self.params)} parameters")
-        idx, ps, gs, ms, vs, cs, consts = [], [], [], [], [], [], []
+        if acc is not None and len(acc) != len(self.params):
+            raise ValueError(f"{len(acc)} accumulators for {len(self.params)} parameters")
+        idx, ps, gs, accs, ms, vs, cs, consts = [], [], [], [], [], [], [], []
         cache: dict = {}
         for i, p in enumerate(self.params):
             g = p.grad if grads is None else grads[i]
@@ -240,6 +256,18 @@ class FusedAdamW:
                 raise ValueError(f"{self.recipe}: the gradient of parameter {i} must be contiguous, shaped like it, on its device")
             if g.dtype not in (torch.float32, torch.bfloat16):
                 raise ValueError(f"{self.recipe}: gradients are float32 or bfloat16, got {g.dtype}")
+            if p.dtype != torch.float32:
+                raise ValueError(f"{self.recipe} trains fp32 parameters, got {p.dtype}")
+            _lib.require_gpu(p, self.recipe)
+            if self.device is None:
+                self.device = p.device
+            elif p.device != self.device:
+                raise ValueError(f"{self.recipe}: parameter {i} is on {p.device}, the optimizer's moments on {self.device}")
+            if acc is not None:
+                a = acc[i]
+                if a is None or a.dtype != torch.float32 or a.shape != p.shape or not a.is_contiguous() or a.device != p.device:
+                    raise ValueError(f"{self.recipe}: the fold accumulator of parameter {i} must be a contiguous float32 tensor shaped like it, on its device")
+                accs.append(a)
             st = self._slot(i, p)
             st["step"] += 1
             t = float(st["step"])
@@ -255,34 +283,38 @@ class FusedAdamW:
             consts.append(c)
         if idx:
             dev = ps[0].device
+            fold = accs if acc is not None else None
             with torch.cuda.device(dev):
-                coef_ptr = self._clip_coef(gs) if self.max_norm is not None else None
+                coef_ptr = self._clip_coef(gs, fold) if self.max_norm is not None else None
                 # one launch per gradient dtype (torch groups by dtype the same way)
                 for gdt in (torch.bfloat16, torch.float32):
                     sel = [j for j, g in enumerate(gs) if g.dtype == gdt]
                     if sel:
                         self._launch([ps[j] for j in sel], [gs[j] for j in sel], [ms[j] for j in sel],
-                                     [vs[j] for j in sel], [cs[j] for j in sel], [consts[j] for j in sel], coef_ptr)
+                                     [vs[j] for j in sel], [cs[j] for j in sel], [consts[j] for j in sel], coef_ptr,
+                                     None if fold is None else [fold[j] for j in sel])
         if on_param is not None:
             for i in idx:
                 on_param(i)
 
-    def _clip_coef(self, grads) -> int:
+    def _clip_coef(self, grads, accs=None) -> int:
         """Launch the deterministic norm of every gradient of the step (any
-        dtype); returns the device address of its fp32 clip coefficient."""
+        dtype; with accs, of the folded sums); returns the device address of
+        its fp32 clip coefficient."""
         L = _lib.load()
         dev = grads[0].device
         if self._norm is None or self._norm.device != dev:
             self._norm = torch.empty(16, dtype=torch.uint8, device=dev)
         garr = _lib.tensor_array(grads)
         ws = _lib.workspace(dev, L.ely_grad_norm_workspace_bytes(garr, len(grads)))
-        _lib.check(
-            L.ely_grad_norm(garr, len(grads), self.max_norm, self._norm.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_ptr(dev)),
-            "grad norm",
-        )
+        if accs is None:
+            rc = L.ely_grad_norm(garr, len(grads), self.max_norm, self._norm.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_ptr(dev))
+        else:
+            rc = L.ely_grad_norm_fold(_lib.tensor_array(accs), garr, len(grads), self.max_norm, self._norm.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_ptr(dev))
+        _lib.check(rc, "grad norm")
         return self._norm.data_ptr() + 12
 
-    def _launch(self, ps, gs, ms, vs, cs, consts, coef_ptr) -> None:
+    def _launch(self, ps, gs, ms, vs, cs, consts, coef_ptr, accs=None) -> None:
         L = _lib.load()
         dev = ps[0].device
         stream = _lib.stream_ptr(dev)
@@ -292,14 +324,20 @@ class FusedAdamW:
             carr[j].c[:] = c
         copies = [(_lib.ely_tensor(c) if c is not None else _lib.ElyTensor(None, 0, _lib.BF16, 0)) for c in cs]
         ws = _lib.workspace(dev, L.ely_adamw_workspace_bytes(n))
-        _lib.check(
-            L.ely_adamw_step(
+        order = _lib.ORDER_HOST if self.order == "host" else _lib.ORDER_TORCH
+        wd = int(self.weight_decay != 0)
+        if accs is None:
+            rc = L.ely_adamw_step(
                 _lib.tensor_array(ps), _lib.tensor_array(gs), _lib.tensor_array(ms), _lib.tensor_array(vs),
-                _lib.tensor_array(copies), n, carr, _lib.ORDER_HOST if self.order == "host" else _lib.ORDER_TORCH,
-                int(self.weight_decay != 0), coef_ptr, ws.data_ptr(), ws.numel(), stream,
-            ),
-            f"{self.recipe} step",
-        )
+                _lib.tensor_array(copies), n, carr, order, wd, coef_ptr, ws.data_ptr(), ws.numel(), stream,
+            )
+        else:
+            rc = L.ely_adamw_fold_step(
+                _lib.tensor_array(ps), _lib.tensor_array(accs), _lib.tensor_array(gs), _lib.tensor_array(ms),
+                _lib.tensor_array(vs), _lib.tensor_array(copies), n, carr, order, wd, coef_ptr, ws.data_ptr(),
+                ws.numel(), stream,
+            )
+        _lib.check(rc, f"{self.recipe} step")
 
     def grad_norm(self) -> torch.Tensor | None:
         """The fp32 global gradient norm of the last clipped step (a device

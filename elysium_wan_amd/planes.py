@@ -1,7 +1,13 @@
-"""The scaled-fp8 wire codec of a stage boundary on MI355X: the drop-in for
-wantrain's codec/planes.py:85-138 (encode_scaled_fp8, decode and the wire
-ids), with the exponent recovery, the byte image and the dequantization on
-the GPU.  Only the compressed bytes cross to the host.
+"""The lossless wire codecs of a stage boundary on MI355X: the drop-in for
+wantrain's codec/planes.py (encode, decode, encode_scaled_fp8 and the wire
+ids).  The byte work runs on the GPU -- the byte-plane split and join, the
+scaled-fp8 exponent recovery, byte image and dequantization -- and only the
+planes cross PCIe, to be compressed on the host.
+
+Plain dtypes (codec/planes.py:141-190): header "<BBQ" (dtype id, plane
+count, element count), one "<I" compressed size per plane, then the planes;
+multi-byte elements travel as byte planes, most significant byte first,
+single-byte elements interleaved.
 
 Payload layout, unchanged (codec/planes.py:115-117): struct "<BBQ" (wire id
 32 for e4m3 / 33 for e5m2, plane count 2, element count), "<I" length of the
@@ -25,6 +31,16 @@ from . import _lib
 from . import fp8 as _fp8
 
 _ZSTD_MAGIC = b"\x28\xb5\x2f\xfd"
+# wire dtype ids; append only, never renumber (codec/planes.py:63-70)
+_DT = {
+    0: torch.float32,
+    1: torch.bfloat16,
+    2: torch.float16,
+    3: torch.float8_e4m3fn,
+    4: torch.float8_e5m2,
+    5: torch.int64,
+}
+_ID = {v: k for k, v in _DT.items()}
 _HDR = struct.Struct("<BBQ")  # dtype id, plane count, element count
 # Scaled-fp8 wire ids live above the plain dtype ids; append only (codec/planes.py:137-138).
 _SCALED_ID = {"e4m3": 32, "e5m2": 33}
@@ -77,14 +93,76 @@ def encode_scaled_fp8(t: torch.Tensor, fmt: str = "e4m3"):
     return head + c_v + c_k, tuple(t.shape)
 
 
+def encode(t: torch.Tensor):
+    """codec/planes.py:141-160: a tensor in its declared boundary dtype ->
+    (payload, shape), lossless.  The byte planes are split on the GPU."""
+    if t.dtype not in _ID:
+        raise ValueError(f"no wire encoding for dtype {t.dtype}")
+    _lib.require_gpu(t, "encode")
+    t = t.detach().contiguous()
+    esz = t.element_size()
+    n = t.numel()
+    raw = t.reshape(-1).view(torch.uint8)
+    if esz == 1:
+        blobs = [_compress(raw.cpu().numpy().tobytes())]
+    else:
+        planes = torch.empty(esz * n, dtype=torch.uint8, device=t.device)
+        L = _lib.load()
+        _lib.check(L.ely_byteplanes_split(raw.data_ptr(), n, esz, planes.data_ptr(), _lib.stream_ptr(t.device)), "encode")
+        host = planes.cpu().numpy()
+        blobs = [_compress(host[j * n : (j + 1) * n].tobytes()) for j in range(esz)]
+    head = _HDR.pack(_ID[t.dtype], len(blobs), n)
+    head += b"".join(struct.pack("<I", len(b)) for b in blobs)
+    return head + b"".join(blobs), tuple(t.shape)
+
+
+def _device(device):
+    return torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+
+
 def decode(payload: bytes, shape, device=None) -> torch.Tensor:
-    """codec/planes.py:141-190 for the scaled-fp8 ids: payload -> float32
-    tensor of `shape` (on `device`, default the current CUDA device),
-    dequantized on the GPU.  Plain-dtype byte-plane payloads are not part of
-    this build."""
+    """codec/planes.py:163-190: payload -> tensor of `shape` on `device`
+    (default the current CUDA device), bit-identical to what was encoded.
+    Scaled-fp8 payloads decode to float32 (codec/planes.py:120-133)."""
     did, nplanes, n = _HDR.unpack_from(payload, 0)
-    if did not in _SCALED_FMT:
-        raise ValueError(f"wire id {did} is not a scaled-fp8 payload (ids {sorted(_SCALED_FMT)})")
+    if did in _SCALED_FMT:
+        return _decode_scaled(payload, shape, device)
+    if did not in _DT:
+        raise ValueError(f"unknown wire dtype id {did}")
+    off = _HDR.size
+    sizes = []
+    for _ in range(nplanes):
+        sizes.append(struct.unpack_from("<I", payload, off)[0])
+        off += 4
+    dtype = _DT[did]
+    esz = torch.empty(0, dtype=dtype).element_size()
+    if math.prod(shape) != n:
+        raise ValueError(f"shape {tuple(shape)} does not hold {n} elements")
+    planes = []
+    for sz in sizes:
+        planes.append(_decompress(payload[off : off + sz]))
+        off += sz
+    dev = _device(device)
+    if nplanes == 1:
+        if len(planes[0]) != n * esz:
+            raise ValueError(f"payload holds {len(planes[0])} bytes, header says {n * esz}")
+        buf = torch.frombuffer(bytearray(planes[0]), dtype=torch.uint8).to(dev) if n else torch.empty(0, dtype=torch.uint8, device=dev)
+        return buf.view(dtype).reshape(shape)
+    if nplanes != esz or any(len(p) != n for p in planes):
+        raise ValueError(f"{nplanes} planes of sizes {[len(p) for p in planes]} do not hold {n} elements of {esz} bytes")
+    out = torch.empty(n * esz, dtype=torch.uint8, device=dev)
+    if n:
+        src = torch.frombuffer(bytearray(b"".join(planes)), dtype=torch.uint8).to(dev)
+        L = _lib.load()
+        with torch.cuda.device(dev):
+            _lib.check(L.ely_byteplanes_join(src.data_ptr(), n, esz, out.data_ptr(), _lib.stream_ptr(dev)), "decode")
+    return out.view(dtype).reshape(shape)
+
+
+def _decode_scaled(payload: bytes, shape, device=None) -> torch.Tensor:
+    """codec/planes.py:120-133: a scaled-fp8 payload -> float32 tensor of
+    `shape` on `device`, dequantized on the GPU."""
+    did, nplanes, n = _HDR.unpack_from(payload, 0)
     off = _HDR.size
     sizes = []
     for _ in range(nplanes):
@@ -101,7 +179,7 @@ def decode(payload: bytes, shape, device=None) -> torch.Tensor:
         raise ValueError(f"{n} elements do not split into {rows} rows")
     if math.prod(shape) != n:
         raise ValueError(f"shape {tuple(shape)} does not hold {n} elements")
-    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    dev = _device(device)
     q = torch.from_numpy(raw.copy()).to(dev).view(_fp8.FORMATS[fmt][0]).reshape(rows, n // rows)
     k = torch.from_numpy(exps.astype(np.int32)).to(dev).reshape(rows, 1)
     return _fp8.dequantize(q, k, torch.float32).reshape(shape)

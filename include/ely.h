@@ -81,6 +81,14 @@ int64_t ely_grad_norm_workspace_bytes(const ely_tensor* grads, int32_t n);
 int ely_grad_norm(const ely_tensor* grads, int32_t n, float max_norm,
                   ely_norm_result* out_dev, void* workspace, int64_t ws_bytes, void* stream);
 
+/* ely_grad_norm of the folded gradients accs[i] + widen(grads[i]) (each sum
+ * rounded once to fp32, pieces.fold_add, runtime/pieces.py:206-214): the
+ * norm of the step's gradient when the last microbatch has not been folded
+ * into the fp32 accumulators yet.  accs: n fp32 tensors of the grads' numel;
+ * nothing is written to them.  Same order and determinism as ely_grad_norm. */
+int ely_grad_norm_fold(const ely_tensor* accs, const ely_tensor* grads, int32_t n, float max_norm,
+                       ely_norm_result* out_dev, void* workspace, int64_t ws_bytes, void* stream);
+
 /* ---------------------------------------------------------------- (b) */
 
 int64_t ely_adamw_workspace_bytes(int32_t n);
@@ -100,6 +108,18 @@ int ely_adamw_step(const ely_tensor* params, const ely_tensor* grads,
                    const ely_tensor* copies, int32_t n,
                    const ely_adamw_consts* consts, int32_t order, int32_t weight_decay_nonzero,
                    const float* coef_dev, void* workspace, int64_t ws_bytes, void* stream);
+
+/* ely_adamw_step whose gradient is the ordered fold finished inside the
+ * update: g = accs[i] + widen(grads[i]), rounded once to fp32 as
+ * pieces.fold_add does (runtime/pieces.py:206-214, runtime/accumulate.py:
+ * 93-104), then clipped and applied.  The accumulator of the earlier
+ * microbatches is read, never written, so the fold costs 4 read bytes per
+ * element instead of a 10-byte fold pass plus the update's gradient read.
+ * Results equal ely_fold_add followed by ely_adamw_step bit for bit. */
+int ely_adamw_fold_step(const ely_tensor* params, const ely_tensor* accs, const ely_tensor* grads,
+                        const ely_tensor* exp_avg, const ely_tensor* exp_avg_sq, const ely_tensor* copies, int32_t n,
+                        const ely_adamw_consts* consts, int32_t order, int32_t weight_decay_nonzero,
+                        const float* coef_dev, void* workspace, int64_t ws_bytes, void* stream);
 
 /* ---------------------------------------------------------------- (c) */
 
@@ -163,6 +183,33 @@ int ely_scale_inplace(const ely_tensor* tensors, int32_t n, const float* coef_de
  * restores the default (8 per compute unit).  For tuning and for the tests
  * that prove results do not depend on the grid.  Process-wide. */
 int ely_set_max_blocks(int32_t max_blocks);
+
+/* ---------------------------------------------------------- wire planes */
+
+/* The byte split of codec/planes.py:152-158 (encode's plain-dtype path):
+ * n elements of esz bytes (1, 2, 4 or 8; little-endian) at x become esz
+ * planes of n bytes at planes[j * n + i], plane j holding byte esz-1-j of
+ * every element (most significant first).  esz 1 is a copy. */
+int ely_byteplanes_split(const void* x, int64_t n, int32_t esz, uint8_t* planes, void* stream);
+
+/* The byte join of codec/planes.py:174-186 (decode's plain-dtype path): the
+ * inverse of ely_byteplanes_split. */
+int ely_byteplanes_join(const uint8_t* planes, int64_t n, int32_t esz, void* out, void* stream);
+
+/* codec/fp8_planes.py:19-30: the float8_e4m3fn code of each of the n
+ * elements of t (ELY_F32 or ELY_BF16, torch's rounding), written as two
+ * nibble planes of (n + 1) / 2 bytes: hi[i] = (code[2i] >> 4) << 4 |
+ * code[2i+1] >> 4, lo[i] likewise with the low nibbles, a missing odd
+ * element as 0.  Every element whose code does not convert back to it
+ * exactly (NaN, Inf, beyond 448, off the e4m3 grid; -0 == 0 as in
+ * torch.equal) adds 1 to *bad_dev (the caller zeroes it; the reference
+ * asserts, which the Python layer does when the count is non-zero). */
+int ely_fp8_nibbles_encode(const void* t, int32_t t_dtype, int64_t n, uint8_t* hi, uint8_t* lo,
+                           unsigned long long* bad_dev, void* stream);
+
+/* codec/fp8_planes.py:35-52: nibble planes -> n fp32 values of the e4m3
+ * codes. */
+int ely_fp8_nibbles_decode(const uint8_t* hi, const uint8_t* lo, int64_t n, float* out, void* stream);
 
 /* ------------------------------------------------------------ self-test */
 

@@ -232,3 +232,51 @@ def test_mixed_grad_dtypes_take_one_launch_each(oracle):
     p, _, _, _ = _oracle_steps(oracle, init, [grads], 1e-3, 0.0, 1.0, copies=False)
     got = torch.cat([x.detach().cpu() for x in ps]).numpy()
     assert np.array_equal(got.view(np.uint32), p.view(np.uint32))
+
+
+@pytest.mark.parametrize("order", ["host", "torch"])
+@pytest.mark.parametrize("gdtype", [torch.bfloat16, torch.float32])
+def test_fold_inside_the_update_equals_fold_then_step(order, gdtype):
+    """ely_adamw_fold_step / ely_grad_norm_fold: finishing the ordered fold
+    (runtime/accumulate.py:93-104) inside the update gives, bit for bit, the
+    parameters, moments, working copy and norm of pieces.fold_add followed
+    by a plain step; the accumulators are left unwritten."""
+    from elysium_wan_amd import optim, pieces
+
+    gen = torch.Generator().manual_seed(21)
+    shapes = [(96, 64), (64,), (1000,), (33, 7), (4096,)]
+    init = [torch.randn(s, generator=gen) * 0.02 for s in shapes]
+    mb = [[(torch.randn(s, generator=gen) * 1e-2).to(gdtype) for s in shapes] for _ in range(3)]
+    a_ps = [t.clone().cuda() for t in init]
+    b_ps = [t.clone().cuda() for t in init]
+    a = optim.FusedAdamW(a_ps, lr=1e-2, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, order=order, max_norm=0.5, working_copy=True)
+    b = optim.FusedAdamW(b_ps, lr=1e-2, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, order=order, max_norm=0.5, working_copy=True)
+    say("fold inside the update", order, gdtype)
+    for step in range(2):
+        parts = [[g.cuda() for g in m] for m in mb]
+        accs = [pieces.fold([parts[0][i], parts[1][i]]) for i in range(len(shapes))]
+        before = [x.clone() for x in accs]
+        a.step(grads=parts[2], acc=accs)
+        full = [x.clone() for x in accs]
+        for x, g in zip(full, parts[2]):
+            pieces.fold_add(x, g)
+        b.step(grads=full)
+        assert all(torch.equal(x, y) for x, y in zip(accs, before))
+    torch.cuda.synchronize()
+    assert torch.equal(a.grad_norm().view(torch.int32), b.grad_norm().view(torch.int32))
+    for x, y in zip(a_ps, b_ps):
+        assert torch.equal(x.view(torch.int32), y.view(torch.int32))
+    for i in range(len(shapes)):
+        for k in ("exp_avg", "exp_avg_sq"):
+            assert torch.equal(a.state[i][k].view(torch.int32), b.state[i][k].view(torch.int32))
+        assert torch.equal(a.working_copies[i].view(torch.int16), b.working_copies[i].view(torch.int16))
+    # an unaligned view takes the element path and still matches
+    big = torch.randn(4097, generator=gen)
+    pa, pb = big.clone().cuda()[1:], big.clone().cuda()[1:]
+    accv = torch.randn(4097, generator=gen).cuda()[1:]
+    gv = torch.randn(4097, generator=gen).cuda()[1:]
+    oa = optim.FusedAdamW([pa], lr=1e-3, order=order)
+    ob = optim.FusedAdamW([pb], lr=1e-3, order=order)
+    oa.step(grads=[gv], acc=[accv])
+    ob.step(grads=[accv + gv])
+    assert torch.equal(pa.view(torch.int32), pb.view(torch.int32))

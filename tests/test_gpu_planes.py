@@ -1,0 +1,146 @@
+"""The lossless wire codecs on the GPU: the byte-plane wire
+(codec/planes.py:141-190) for every wire dtype and the unscaled e4m3
+nibble-plane wire (codec/fp8_planes.py:19-52), against the reference's own
+payload bytes (tests/golden/planes.npz, zlib-1 containers) and the oracle,
+at golden sizes and at C1's boundary size, aligned and not."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import golden
+from gpu_util import activation, bits, say
+
+pytestmark = pytest.mark.gpu
+
+_TORCH = {
+    "torch.float32": torch.float32,
+    "torch.bfloat16": torch.bfloat16,
+    "torch.float16": torch.float16,
+    "torch.float8_e4m3fn": torch.float8_e4m3fn,
+    "torch.float8_e5m2": torch.float8_e5m2,
+    "torch.int64": torch.int64,
+}
+
+
+def _from_bytes(raw: np.ndarray, dtype, shape, device="cuda") -> torch.Tensor:
+    return torch.from_numpy(raw.copy()).to(device).view(dtype).reshape(shape)
+
+
+def _raw(t: torch.Tensor) -> np.ndarray:
+    return t.detach().contiguous().reshape(-1).view(torch.uint8).cpu().numpy()
+
+
+def test_byte_plane_payloads_equal_the_reference_bytes():
+    from elysium_wan_amd import planes
+
+    g = golden("planes.npz")
+    for name in g["plane_names"]:
+        name = str(name)
+        dtype = _TORCH[str(g[f"p_{name}_dtype"])]
+        shape = tuple(int(s) for s in g[f"p_{name}_shape"])
+        t = _from_bytes(g[f"p_{name}_t"], dtype, shape)
+        say("byte planes golden", name, shape)
+        payload, sh = planes.encode(t)
+        assert sh == shape
+        assert payload == g[f"p_{name}_payload"].tobytes(), name
+        back = planes.decode(payload, shape)
+        assert back.dtype == dtype and tuple(back.shape) == shape and back.device.type == "cuda"
+        assert np.array_equal(_raw(back), g[f"p_{name}_decoded"]), name
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16, torch.int64])
+def test_split_and_join_equal_the_oracle_aligned_and_not(oracle, dtype):
+    """ely_byteplanes_split through the C ABI against the oracle's byte
+    split, on the vector path (aligned, n % 16 == 0) and the element-wise
+    path (4 bytes off, odd n); join inverts it."""
+    from elysium_wan_amd import _lib
+
+    L = _lib.load()
+    gen = torch.Generator().manual_seed(5)
+    base = torch.randint(-(1 << 62), 1 << 62, (200_016,), generator=gen, dtype=torch.int64).view(torch.uint8).cuda()
+    esz = torch.empty(0, dtype=dtype).element_size()
+    for off, n in ((0, 200_000 * 8 // esz), (4, 1001)):
+        x = base[off : off + n * esz]
+        say("split/join", dtype, "offset", off, "n", n)
+        planes = torch.empty(n * esz, dtype=torch.uint8, device="cuda")
+        _lib.check(L.ely_byteplanes_split(x.data_ptr(), n, esz, planes.data_ptr(), _lib.stream_ptr(x.device)), "split")
+        want = np.concatenate(oracle.byte_planes(x.cpu().numpy(), esz))
+        assert np.array_equal(planes.cpu().numpy(), want)
+        dst = torch.empty(n * esz + 4, dtype=torch.uint8, device="cuda")[off : off + n * esz]
+        _lib.check(L.ely_byteplanes_join(planes.data_ptr(), n, esz, dst.data_ptr(), _lib.stream_ptr(x.device)), "join")
+        assert torch.equal(dst, x)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_byte_plane_wire_round_trip_at_c1_size(oracle, dtype):
+    """The C1 boundary activation [8, 2048, 2560] crosses the byte-plane wire
+    bit for bit; its payload equals the oracle's."""
+    from elysium_wan_amd import planes
+
+    x = activation((8, 2048, 2560), seed=51, dtype=dtype)
+    say("byte-plane wire C1", dtype)
+    payload, shape = planes.encode(x)
+    back = planes.decode(payload, shape)
+    assert torch.equal(back.view(torch.uint8), x.view(torch.uint8))
+    assert payload == oracle.planes_encode(_raw(x), str(dtype).replace("torch.", ""))
+
+
+def test_nibble_payloads_equal_the_reference_bytes():
+    from elysium_wan_amd import fp8_planes
+
+    g = golden("planes.npz")
+    for name in g["nibble_names"]:
+        name = str(name)
+        shape = tuple(int(s) for s in g[f"n_{name}_shape"])
+        raw = g[f"n_{name}_t"]
+        if "bfloat16" in str(g[f"n_{name}_dtype"]):
+            t = torch.from_numpy(raw.view(np.int16).copy()).view(torch.bfloat16).cuda().reshape(shape)
+        else:
+            t = torch.from_numpy(raw.copy()).cuda().reshape(shape)
+        say("nibble planes golden", name, shape)
+        payload, sh = fp8_planes.encode(t)
+        assert sh == shape
+        assert payload == g[f"n_{name}_payload"].tobytes(), name
+        back = fp8_planes.decode(payload, shape)
+        assert back.dtype == torch.float32
+        assert np.array_equal(bits(back).reshape(-1).view(np.uint32), g[f"n_{name}_decoded"].reshape(-1).view(np.uint32))
+    for row, refused in zip(g["n_bad_t"], g["n_bad_refused"]):
+        if refused:
+            with pytest.raises(AssertionError, match="recipe mismatch"):
+                fp8_planes.encode(torch.from_numpy(row.copy()).cuda())
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_nibble_wire_at_c1_size_and_odd_counts(oracle, dtype):
+    """An e4m3-representable C1 boundary tensor: nibble planes equal the
+    oracle's, the wire round trip is exact; odd counts and unaligned views
+    take the element-wise path; one value off the grid is refused."""
+    from elysium_wan_amd import fp8_planes
+
+    gen = torch.Generator().manual_seed(52)
+    codes = torch.randint(0, 256, (8, 2048, 2560), generator=gen, dtype=torch.int64)
+    codes[(codes & 0x7F) == 0x7F] = 0x3C
+    t = codes.to(torch.uint8).view(torch.float8_e4m3fn).to(dtype).cuda()
+    for view in (t, t.reshape(-1)[1:100_002]):
+        say("nibble wire", dtype, tuple(view.shape))
+        payload, shape = fp8_planes.encode(view)
+        back = fp8_planes.decode(payload, shape)
+        assert torch.equal(back, view.float())
+        assert payload == oracle.fp8_planes_encode(bits(view))
+    bad = t.reshape(-1)[:4097].clone()
+    bad[4096] = 1.0 + 2.0**-5 if dtype == torch.float32 else 1.0 + 2.0**-6
+    with pytest.raises(AssertionError):
+        fp8_planes.encode(bad)
+
+
+def test_empty_and_scalar_tensors():
+    from elysium_wan_amd import fp8_planes, planes
+
+    for t in (torch.empty(0, device="cuda"), torch.tensor(2.5, device="cuda"), torch.empty(3, 0, dtype=torch.bfloat16, device="cuda")):
+        payload, shape = planes.encode(t)
+        assert torch.equal(planes.decode(payload, shape), t)
+        payload, shape = fp8_planes.encode(t)
+        assert torch.equal(fp8_planes.decode(payload, shape), t.float())
