@@ -136,37 +136,45 @@ def bench_optimizer(args, device, stream):
     }
 
 
-def bench_codec(device, stream, iters=20):
+def _activations(device, rows, cols, copies, seed):
+    """bf16 N(0, 1) with 0.1% of the elements x50 (BASELINE's C1 recipe)."""
+    gen = torch.Generator(device=device).manual_seed(seed)
+    xs = []
+    for _ in range(copies):
+        x = torch.empty(rows, cols, device=device)
+        x.normal_(generator=gen)
+        mask = torch.rand(rows, cols, device=device, generator=gen) < 1e-3
+        xs.append(torch.where(mask, x * 50.0, x).to(torch.bfloat16))
+        del x, mask
+    return xs
+
+
+def bench_codec(device, stream, rows, cols, copies, iters=20, per_tensor=False):
+    """Quantize and dequantize (bf16 <-> fp8, per-row or per-tensor) of a
+    [rows, cols] activation, rotating through `copies` inputs so that
+    launches stream from HBM rather than the 256 MB MALL."""
     from elysium_wan_amd import _lib
 
     L = _lib.load()
     sptr = _lib.stream_ptr(device)
-    rows, cols = 8 * 2048, D_MODEL
     n = rows * cols
-    copies = 8  # 8 x 84 MB inputs + outputs: every launch reads HBM, not the MALL
-    gen = torch.Generator(device=device).manual_seed(7)
-    xs, qs, ks, outs = [], [], [], []
-    for i in range(copies):
-        x = torch.empty(rows, cols, device=device)
-        x.normal_(generator=gen)
-        mask = torch.rand(rows, cols, device=device, generator=gen) < 1e-3
-        x = torch.where(mask, x * 50.0, x).to(torch.bfloat16)
-        xs.append(x)
-        qs.append(torch.empty(rows, cols, dtype=torch.uint8, device=device))
-        ks.append(torch.empty(rows, dtype=torch.int32, device=device))
-        outs.append(torch.empty(rows, cols, dtype=torch.bfloat16, device=device))
-    ws = _lib.workspace(device, L.ely_fp8_workspace_bytes(rows, cols, _lib.BF16))
+    xs = _activations(device, rows, cols, copies, 7)
+    qs = [torch.empty(rows, cols, dtype=torch.uint8, device=device) for _ in range(copies)]
+    ks = [torch.empty(rows, dtype=torch.int32, device=device) for _ in range(copies)]
+    outs = [torch.empty(rows, cols, dtype=torch.bfloat16, device=device) for _ in range(copies)]
+    qr, qc = (1, n) if per_tensor else (rows, cols)
+    ws = _lib.workspace(device, L.ely_fp8_workspace_bytes(qr, qc, _lib.BF16))
     out = {}
     for fmt in ("e4m3", "e5m2"):
         f = _lib.FMT[fmt]
 
         def quant(i, f=f):
             j = i % copies
-            _lib.check(L.ely_fp8_quantize(xs[j].data_ptr(), _lib.BF16, rows, cols, f, qs[j].data_ptr(), ks[j].data_ptr(), ws.data_ptr(), ws.numel(), sptr), "q")
+            _lib.check(L.ely_fp8_quantize(xs[j].data_ptr(), _lib.BF16, qr, qc, f, qs[j].data_ptr(), ks[j].data_ptr(), ws.data_ptr(), ws.numel(), sptr), "q")
 
         def deq(i, f=f):
             j = i % copies
-            _lib.check(L.ely_fp8_dequantize(qs[j].data_ptr(), ks[j].data_ptr(), rows, cols, f, outs[j].data_ptr(), _lib.BF16, sptr), "dq")
+            _lib.check(L.ely_fp8_dequantize(qs[j].data_ptr(), ks[j].data_ptr(), qr, qc, f, outs[j].data_ptr(), _lib.BF16, sptr), "dq")
 
         for i in range(copies):
             quant(i)
@@ -178,7 +186,71 @@ def bench_codec(device, stream, iters=20):
             "dequantize_ms": d_ms,
             "dequantize_GBs": n * CODEC_BYTES_PER_ELEM / d_ms / 1e6,
         }
+    del xs, qs, outs
     return out
+
+
+def bench_fold(device, stream, iters=5):
+    """The ordered fold finished inside the update (ely_adamw_fold_step:
+    read acc 4 + g 2, p m v 12; write p m v 12 + copy 2 = 32 B/elem) against
+    the fold pass (ely_fold_add, 10 B/elem) followed by the plain step on the
+    fp32 sum (30 B/elem), over C1's shard with bf16 last-microbatch grads."""
+    from elysium_wan_amd import _lib, optim
+
+    params, grads = make_shard(device)
+    n = len(params)
+    n_elem = sum(p.numel() for p in params)
+    accs = [torch.empty_like(p).normal_(0.0, 1e-4) for p in params]
+    opt = optim.FusedAdamW(params, lr=LR, betas=BETAS, eps=EPS, weight_decay=WD, order="host", working_copy=True)
+    opt.step(grads=grads, acc=accs)  # allocates the moments
+    torch.cuda.synchronize()
+    L = _lib.load()
+    sptr = _lib.stream_ptr(device)
+    parr, garr, aarr = _lib.tensor_array(params), _lib.tensor_array(grads), _lib.tensor_array(accs)
+    marr = _lib.tensor_array([opt.state[i]["exp_avg"] for i in range(n)])
+    varr = _lib.tensor_array([opt.state[i]["exp_avg_sq"] for i in range(n)])
+    carr = _lib.tensor_array(opt.working_copies)
+    consts = (_lib.ElyConsts * n)()
+    for j in range(n):
+        consts[j].c[:] = optim.host_consts(LR, BETAS, EPS, WD, 2.0)
+    aws = torch.empty(L.ely_adamw_workspace_bytes(n), dtype=torch.uint8, device=device)
+
+    def fused(_):
+        _lib.check(L.ely_adamw_fold_step(parr, aarr, garr, marr, varr, carr, n, consts, _lib.ORDER_HOST, 1, None, aws.data_ptr(), aws.numel(), sptr), "fold step")
+
+    def fold_then_step(_):
+        for a, g in zip(accs, grads):
+            _lib.check(L.ely_fold_add(a.data_ptr(), g.data_ptr(), _lib.BF16, a.numel(), sptr), "fold")
+        _lib.check(L.ely_adamw_step(parr, aarr, marr, varr, carr, n, consts, _lib.ORDER_HOST, 1, None, aws.data_ptr(), aws.numel(), sptr), "step")
+
+    fused_ms = time_events(fused, iters, stream)
+    unfused_ms = time_events(fold_then_step, iters, stream)
+    del opt, params, grads, accs
+    return {
+        "fused_ms": fused_ms,
+        "fused_GBs": n_elem * 32 / fused_ms / 1e6,
+        "fold_then_step_ms": unfused_ms,
+        "saved_frac": 1.0 - fused_ms / unfused_ms,
+    }
+
+
+def bench_host_moments(device, steps=3):
+    """adamw-host with its moments in pinned host memory (the reference's
+    recipe), streamed through HBM in 2^24-element chunks over 3 slots: the
+    PCIe-inclusive rate of C1's step (m and v cross PCIe both ways, 16 B per
+    element), for comparison with the HBM-resident `value`."""
+    from elysium_wan_amd import optim
+
+    params, grads = make_shard(device)
+    n_elem = sum(p.numel() for p in params)
+    opt = optim.FusedAdamW(params, lr=LR, betas=BETAS, eps=EPS, weight_decay=WD, order="host", max_norm=MAX_NORM, working_copy=True, moments="host")
+    opt.step(grads=grads)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        opt.step(grads=grads)  # synchronizes at its end, as the reference's does
+    dt = (time.perf_counter() - t0) / steps
+    del opt, params, grads
+    return {"step_s": dt, "params_per_s": n_elem / dt, "pcie_GBs": n_elem * 16 / dt / 1e9}
 
 
 def cpu_baseline(sample_elems: int, steps: int = 2):
@@ -337,6 +409,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-codec", action="store_true", help="skip the fp8 codec leg")
+    ap.add_argument("--no-extra", action="store_true", help="skip the fused-fold and host-moment legs")
     ap.add_argument("--cpu-sample", type=int, default=256 * 1024 * 1024)
     ap.add_argument("--profile-pass", action="store_true", help="launch each measured kernel a few times, untimed, for rocprofv3 --pmc runs")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"), help="summarize two --pmc runs of --profile-pass into profiles/")
@@ -361,10 +434,21 @@ def main():
     with torch.cuda.stream(stream):
         log("optimizer leg")
         o = bench_optimizer(args, device, stream)
-        codec = None
+        codec = extra = None
         if not args.no_codec:
             log("codec leg")
-            codec = bench_codec(device, stream)
+            codec = {"c1_per_row": bench_codec(device, stream, 8 * 2048, D_MODEL, 8)}
+            torch.cuda.empty_cache()
+            codec["c4_per_row"] = bench_codec(device, stream, 16 * 4096, 8192, 2, iters=10)
+            codec["c4_per_tensor"] = bench_codec(device, stream, 16 * 4096, 8192, 2, iters=10, per_tensor=True)
+            torch.cuda.empty_cache()
+        if not args.no_extra:
+            log("fold leg")
+            extra = {"fold": bench_fold(device, stream)}
+            torch.cuda.empty_cache()
+            log("host-moments leg")
+            extra["host_moments"] = bench_host_moments(device)
+            torch.cuda.empty_cache()
     n = o["n_elem"]
     adam_bytes = n * ADAM_BYTES_PER_ELEM
     achieved = adam_bytes / (o["adam_ms"] * 1e-3) / 1e9
@@ -416,6 +500,7 @@ def main():
             "step_GBs": n * (ADAM_BYTES_PER_ELEM + NORM_BYTES_PER_ELEM) / o["step_s"] / 1e9,
         },
         "fp8_codec": codec,
+        "extra": extra,
         "grad_norm": o["grad_norm"],
     }
     print(json.dumps(result), flush=True)

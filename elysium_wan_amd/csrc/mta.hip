@@ -59,6 +59,7 @@ namespace ely {
 
 constexpr int64_t kAdamTile = ELY_ADAM_TILE;
 constexpr int64_t kNormTile = 16384;    // elements per grad-norm tile (one wave): fixes the summation order
+constexpr int kNormUnroll = ELY_NORM_UNROLL;
 constexpr int kBlock = 256;
 constexpr int kFinalThreads = 1024;
 
@@ -186,7 +187,7 @@ __global__ __launch_bounds__(kBlock) void norm_partials_kernel(const NormDesc* _
         double acc = 0.0;
         // lane l owns groups j*64 + l of 8 elements, in the same order on both paths
         if (d.aligned && e1 - e0 == kNormTile) {
-#pragma unroll ELY_NORM_UNROLL
+#pragma unroll kNormUnroll
             for (int j = 0; j < (int)(kNormTile / (kWave * 8)); ++j) {
                 float x[8];
                 load8_vec<FOLD>(d, e0 + ((int64_t)j * kWave + lane) * 8, x);

@@ -5,10 +5,13 @@
 
 * "adamw"      -> FusedAdamW(order="torch"): torch.optim.AdamW's arithmetic
                   (TORCH/optim/adam.py:554-800), within 1 ulp of it.
-* "adamw-host" -> FusedAdamW(order="host"): HostAdamW's single-rounding op
-                  order (runtime/optim.py:277-298), bit for bit.  The moments
-                  stay in HBM (a 288 GB MI355X holds a stage's fp32
-                  p/m/v/g); checkpoints keep the reference's host layout.
+* "adamw-host" -> FusedAdamW(order="host", moments="host"): HostAdamW's
+                  single-rounding op order (runtime/optim.py:277-298), bit for
+                  bit, with its moments in pinned host memory streamed through
+                  the GPU in chunks (runtime/optim.py:176-204, 301-363).
+                  moments="device" keeps them in HBM instead: a 288 GB
+                  MI355X holds a stage's fp32 p/m/v/g, and the step is then
+                  HBM-bound rather than PCIe-bound.
 
 Either way one step is at most two launches over the whole parameter list:
 the deterministic grad-norm (when max_norm is set) and the fused
@@ -52,7 +55,9 @@ def build(optimizer: str, params: Iterable[torch.Tensor], lr: float, **kw):
     if optimizer == "adamw":
         return FusedAdamW(params, lr=lr, order="torch", **{**ADAMW, **kw})
     if optimizer == "adamw-host":
-        return FusedAdamW(params, lr=lr, order="host", **{**ADAMW, **kw})
+        # the reference's memory contract (8 device bytes per element): moments
+        # in host memory, streamed through the GPU; moments="device" keeps them in HBM
+        return FusedAdamW(params, lr=lr, order="host", **{**ADAMW, "moments": "host", **kw})
     raise ValueError(f"optimizer {optimizer!r} is not one of {OPTIMIZERS}")
 
 
@@ -141,10 +146,22 @@ class FusedAdamW:
         order: str = "host",
         max_norm: float | None = None,
         working_copy=None,
+        moments: str = "device",
+        chunk: int = CHUNK,
+        pipeline: bool | None = None,
+        slots: int = 3,
     ):
         self.params = list(params)
         if order not in ("host", "torch"):
             raise ValueError(f"order {order!r} is not 'host' or 'torch'")
+        if moments not in ("device", "host"):
+            raise ValueError(f"moments {moments!r} is not 'device' or 'host'")
+        if int(chunk) < 1 or int(slots) < 1:
+            raise ValueError("chunk and slots are positive")
+        self.moments = moments
+        self.chunk, self.pipeline, self.slots = int(chunk), pipeline, int(slots)
+        self.resident: set = set()  # host mode: indices whose moments were promoted to the GPU
+        self._staging = None  # host mode: per-step streaming buffers, streams and events
         self.order = order
         self.recipe = "adamw-host" if order == "host" else "adamw"
         devices = set()
@@ -194,7 +211,9 @@ class FusedAdamW:
 
     def _alloc_state(self) -> None:
         """Moments live in two flat fp32 buffers in parameter order, each
-        tensor's slice starting on a 256-byte boundary; state[i] holds views."""
+        tensor's slice starting on a 256-byte boundary; state[i] holds views.
+        moments="device": in HBM.  moments="host": in pinned host memory
+        (runtime/optim.py:121-130), streamed through the GPU at every step."""
         offs, total = [], 0
         for p in self.params:
             offs.append(total)
@@ -202,8 +221,12 @@ class FusedAdamW:
         dev = self.device
         if dev is None or dev.type != "cuda":
             raise ValueError(f"{self.recipe}: the moments live on the parameters' GPU, got device {dev}")
-        self._flat_m = torch.zeros(max(total, 1), dtype=torch.float32, device=dev)
-        self._flat_v = torch.zeros(max(total, 1), dtype=torch.float32, device=dev)
+        if self.moments == "host":
+            self._flat_m = torch.zeros(max(total, 1), dtype=torch.float32, pin_memory=True)
+            self._flat_v = torch.zeros(max(total, 1), dtype=torch.float32, pin_memory=True)
+        else:
+            self._flat_m = torch.zeros(max(total, 1), dtype=torch.float32, device=dev)
+            self._flat_v = torch.zeros(max(total, 1), dtype=torch.float32, device=dev)
         self._offs = offs
 
     def _slot(self, i: int, p: torch.Tensor) -> dict:
@@ -284,18 +307,138 @@ class FusedAdamW:
         if idx:
             dev = ps[0].device
             fold = accs if acc is not None else None
+            streamed = [j for j, m in enumerate(ms) if m.device.type != "cuda"]
+            direct = [j for j, m in enumerate(ms) if m.device.type == "cuda"]
             with torch.cuda.device(dev):
                 coef_ptr = self._clip_coef(gs, fold) if self.max_norm is not None else None
                 # one launch per gradient dtype (torch groups by dtype the same way)
                 for gdt in (torch.bfloat16, torch.float32):
-                    sel = [j for j, g in enumerate(gs) if g.dtype == gdt]
+                    sel = [j for j in direct if gs[j].dtype == gdt]
                     if sel:
                         self._launch([ps[j] for j in sel], [gs[j] for j in sel], [ms[j] for j in sel],
                                      [vs[j] for j in sel], [cs[j] for j in sel], [consts[j] for j in sel], coef_ptr,
                                      None if fold is None else [fold[j] for j in sel])
+                if streamed:
+                    self._stream_host_moments([idx[j] for j in streamed], [ps[j] for j in streamed], [gs[j] for j in streamed],
+                                              [cs[j] for j in streamed], [consts[j] for j in streamed], coef_ptr,
+                                              None if fold is None else [fold[j] for j in streamed])
+                    # the host copies are the state: they land before the step returns (runtime/optim.py:171-174)
+                    torch.cuda.synchronize(dev)
         if on_param is not None:
             for i in idx:
                 on_param(i)
+
+    def _stream_host_moments(self, idx, ps, gs, cs, consts, coef_ptr, accs) -> None:
+        """The update of parameters whose moments live in host memory
+        (runtime/optim.py:176-204, 301-363): the flat moment buffers are cut
+        into chunks of at most `chunk` elements along parameter order (a
+        chunk may span several parameters); chunk k goes through staging
+        slot k % slots -- its copy in on the h2d stream, the fused update of
+        every parameter piece it holds on the current stream, its copy out on
+        the d2h stream, ordered by events, so copies in, updates and copies
+        out of neighbouring chunks overlap (PCIe is full duplex).  With
+        pipeline=False the copies run on the current stream."""
+        dev = self.device
+        chunk = self.chunk
+        pieces = []  # (j, s, e): elements [s, e) of stepped parameter j
+        for j, p in enumerate(ps):
+            n = p.numel()
+            for s0 in range(0, n, chunk):
+                pieces.append((j, s0, min(n, s0 + chunk)))
+        groups = []  # [flat start, flat end, pieces]
+        for j, s0, e0 in pieces:
+            a, b = self._offs[idx[j]] + s0, self._offs[idx[j]] + e0
+            if groups and b - groups[-1][0] <= chunk:
+                groups[-1][1] = b
+                groups[-1][2].append((j, s0, e0))
+            else:
+                groups.append([a, b, [(j, s0, e0)]])
+        staged = self.pipeline is not False
+        st = self._staging_buffers(dev, max(b - a for a, b, _ in groups))
+        compute = torch.cuda.current_stream(dev)
+        mh, vh = self._flat_m, self._flat_v
+        for k, (a, b, members) in enumerate(groups):
+            slot = k % len(st["bufs"])
+            md, vd = st["bufs"][slot][0][: b - a], st["bufs"][slot][1][: b - a]
+            if staged:
+                if st["used"][slot]:
+                    st["h2d"].wait_event(st["ev_back"][slot])
+                with torch.cuda.stream(st["h2d"]):
+                    md.copy_(mh[a:b], non_blocking=True)
+                    vd.copy_(vh[a:b], non_blocking=True)
+                    st["ev_in"][slot].record(st["h2d"])
+                compute.wait_event(st["ev_in"][slot])
+            else:
+                md.copy_(mh[a:b], non_blocking=True)
+                vd.copy_(vh[a:b], non_blocking=True)
+            for gdt in (torch.bfloat16, torch.float32):
+                sel = [(j, s0, e0) for j, s0, e0 in members if gs[j].dtype == gdt]
+                if not sel:
+                    continue
+                views = lambda ts: [ts[j].view(-1)[s0:e0] for j, s0, e0 in sel]  # noqa: E731
+                off = [self._offs[idx[j]] - a for j, _, _ in sel]
+                self._launch(
+                    views(ps), views(gs),
+                    [md[o + s0 : o + e0] for o, (_, s0, e0) in zip(off, sel)],
+                    [vd[o + s0 : o + e0] for o, (_, s0, e0) in zip(off, sel)],
+                    [None if cs[j] is None else cs[j].view(-1)[s0:e0] for j, s0, e0 in sel],
+                    [consts[j] for j, _, _ in sel], coef_ptr,
+                    None if accs is None else views(accs),
+                )
+            if staged:
+                st["ev_done"][slot].record(compute)
+                st["d2h"].wait_event(st["ev_done"][slot])
+                with torch.cuda.stream(st["d2h"]):
+                    mh[a:b].copy_(md, non_blocking=True)
+                    vh[a:b].copy_(vd, non_blocking=True)
+                    st["ev_back"][slot].record(st["d2h"])
+                st["used"][slot] = True
+            else:
+                mh[a:b].copy_(md, non_blocking=True)
+                vh[a:b].copy_(vd, non_blocking=True)
+        if staged:
+            compute.wait_stream(st["d2h"])
+            st["used"] = [False] * len(st["bufs"])
+
+    def _staging_buffers(self, dev, need: int) -> dict:
+        """`slots` pairs of fp32 device buffers of `chunk` elements, the copy
+        streams (default priority) and the per-slot events, made once."""
+        st = self._staging
+        if st is None or st["bufs"][0][0].numel() < need:
+            n = max(need, 1)
+            st = self._staging = {
+                "bufs": [(torch.empty(n, dtype=torch.float32, device=dev), torch.empty(n, dtype=torch.float32, device=dev)) for _ in range(self.slots)],
+                "h2d": torch.cuda.Stream(dev),
+                "d2h": torch.cuda.Stream(dev),
+                "ev_in": [torch.cuda.Event() for _ in range(self.slots)],
+                "ev_done": [torch.cuda.Event() for _ in range(self.slots)],
+                "ev_back": [torch.cuda.Event() for _ in range(self.slots)],
+                "used": [False] * self.slots,
+            }
+        return st
+
+    def promote(self, budget_bytes: int) -> int:
+        """runtime/optim.py:208-227: move the host moments of parameters, in
+        order, onto the GPU while they fit `budget_bytes` (8 bytes per
+        element); the update reads and writes the same values wherever they
+        live, so no bit changes.  -> bytes moved (0 for device moments)."""
+        if self.moments != "host":
+            return 0
+        moved = 0
+        for i, p in enumerate(self.params):
+            if i in self.resident or not p.requires_grad or p.device.type != "cuda":
+                continue
+            need = 8 * p.numel()
+            if moved + need > budget_bytes:
+                continue
+            st = self._slot(i, p)
+            st["exp_avg"] = st["exp_avg"].to(p.device)
+            st["exp_avg_sq"] = st["exp_avg_sq"].to(p.device)
+            self.resident.add(i)
+            moved += need
+        if moved:
+            torch.cuda.synchronize()
+        return moved
 
     def _clip_coef(self, grads, accs=None) -> int:
         """Launch the deterministic norm of every gradient of the step (any

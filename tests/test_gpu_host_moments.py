@@ -1,0 +1,117 @@
+"""The "adamw-host" recipe with its moments in pinned host memory, streamed
+through the GPU in chunks (runtime/optim.py:176-204, 301-363): the
+reference's own contracts (tests/unit/test_host_adamw.py) on the GPU --
+chunking, staging slots and the copy pipeline move no bit, so the streamed
+step equals the HBM-resident step; the moments live in host memory and
+checkpoint in torch's layout; promote moves them to the GPU without changing
+a bit; the planner prices the recipe at 8 device bytes per element."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from gpu_util import gpt_block_shapes, say
+
+pytestmark = pytest.mark.gpu
+
+
+def _params(seed=3, shapes=((37, 19), (19,), (5, 3, 7), (1001,))):
+    """tests/unit/test_host_adamw.py:20-23 (moved to the GPU)."""
+    g = torch.Generator().manual_seed(seed)
+    return [torch.randn(s, generator=g).cuda().requires_grad_(True) for s in shapes]
+
+
+def _grads(params, step, seed=5, dtype=torch.float32):
+    """tests/unit/test_host_adamw.py:26-28."""
+    g = torch.Generator().manual_seed(seed + step)
+    return [(torch.randn(p.shape, generator=g) * 10.0 ** (-step % 4)).to(dtype).cuda() for p in params]
+
+
+def _train(make, params, steps=4, dtype=torch.float32, fold=False):
+    opt = make(params)
+    for step in range(steps):
+        gs = _grads(params, step, dtype=dtype)
+        if fold:
+            accs = [(torch.randn(p.shape, generator=torch.Generator().manual_seed(90 + step)) * 1e-2).cuda() for p in params]
+            opt.step(grads=gs, acc=accs)
+        else:
+            opt.step(grads=gs)
+    torch.cuda.synchronize()
+    return opt
+
+
+def _same(a, b) -> bool:
+    for i, (x, y) in enumerate(zip(a.params, b.params)):
+        if not torch.equal(x.detach().view(torch.int32), y.detach().view(torch.int32)):
+            return False
+        for k in ("exp_avg", "exp_avg_sq"):
+            if not torch.equal(a.state[i][k].cpu().view(torch.int32), b.state[i][k].cpu().view(torch.int32)):
+                return False
+        if a.working_copies is not None and not torch.equal(a.working_copies[i].view(torch.int16), b.working_copies[i].view(torch.int16)):
+            return False
+    return True
+
+
+@pytest.mark.parametrize("chunk,slots,pipeline", [(7, 2, True), (7, 3, False), (64, 3, None), (1 << 24, 3, None)])
+def test_streamed_moments_equal_resident_moments(chunk, slots, pipeline):
+    """test_host_adamw.py:50-55, 154-167: chunk k in slot k % slots,
+    refilled across parameter boundaries, staged or direct -- the parameters
+    and moments equal the HBM-resident run's, bit for bit."""
+    from elysium_wan_amd import optim
+
+    hp = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, order="host", max_norm=1.0, working_copy=True)
+    say("host moments", chunk, slots, pipeline)
+    dev = _train(lambda ps: optim.FusedAdamW(ps, **hp), _params())
+    host = _train(lambda ps: optim.FusedAdamW(ps, moments="host", chunk=chunk, slots=slots, pipeline=pipeline, **hp), _params())
+    assert all(host.state[i]["exp_avg"].device.type == "cpu" for i in host.state)
+    assert _same(dev, host)
+
+
+@pytest.mark.parametrize("order", ["host", "torch"])
+def test_streamed_c0_shard_with_bf16_grads_and_fold(order):
+    """Config C0's layout (3 GPT blocks at d = 768, 21.3M elements) in chunks
+    of 2^20 through 3 slots, bf16 gradients folded into fp32 accumulators
+    inside the update: equal to the resident run."""
+    from elysium_wan_amd import optim
+
+    shapes = tuple(gpt_block_shapes(768) * 3 + [(768,), (768,)])
+    hp = dict(lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, order=order, max_norm=1.0, working_copy=True)
+    say("host moments C0", order)
+    dev = _train(lambda ps: optim.FusedAdamW(ps, **hp), _params(7, shapes), steps=2, dtype=torch.bfloat16, fold=True)
+    host = _train(lambda ps: optim.FusedAdamW(ps, moments="host", chunk=1 << 20, **hp), _params(7, shapes), steps=2, dtype=torch.bfloat16, fold=True)
+    assert _same(dev, host)
+
+
+def test_recipe_lives_in_host_memory_checkpoints_and_promotes():
+    """test_host_adamw.py:80-96, 170-185: build("adamw-host") keeps its
+    moments in host memory, checkpoints host tensors in torch's layout, and
+    promote() moves them to the GPU without moving a bit."""
+    from elysium_wan_amd import optim
+
+    assert optim.state_bytes_per_param("adamw-host") == 8 and optim.state_bytes_per_param("adamw") == 16
+    ref = _train(lambda ps: optim.build("adamw-host", ps, 1e-3, moments="device"), _params(), steps=6)
+    params = _params()
+    opt = optim.build("adamw-host", params, 1e-3)
+    for step in range(3):
+        opt.step(grads=_grads(params, step))
+    sd = opt.state_dict()
+    assert sd["param_groups"][0]["moments"] == "host"
+    assert all(sd["state"][i]["exp_avg"].device.type == "cpu" for i in range(4))
+    moved = opt.promote(8 * (37 * 19 + 19))
+    assert moved == 8 * (37 * 19 + 19) and opt.resident == {0, 1}
+    assert opt.state[0]["exp_avg"].device.type == "cuda" and opt.state[2]["exp_avg"].device.type == "cpu"
+    for step in range(3, 6):
+        opt.step(grads=_grads(params, step))
+    torch.cuda.synchronize()
+    assert _same(ref, opt)
+    sd = opt.state_dict()
+    assert all(sd["state"][i]["exp_avg"].device.type == "cpu" for i in range(4))
+    # a resumed host-moment optimizer continues bit for bit
+    params2 = [p.detach().clone().requires_grad_(True) for p in params]
+    opt2 = optim.build("adamw-host", params2, 1e-3)
+    opt2.load_state_dict(sd)
+    ref.step(grads=_grads(params, 6))
+    opt2.step(grads=_grads(params2, 6))
+    torch.cuda.synchronize()
+    assert all(torch.equal(a.detach().view(torch.int32), b.detach().view(torch.int32)) for a, b in zip(ref.params, params2))
