@@ -39,10 +39,10 @@ namespace ely {
 #define ELY_NORM_SCHED 0         // same choice for the grad-norm waves
 #endif
 #ifndef ELY_NORM_NT
-#define ELY_NORM_NT 0            // nontemporal grad-norm loads
+#define ELY_NORM_NT 1            // nontemporal grad-norm loads
 #endif
 #ifndef ELY_NORM_UNROLL
-#define ELY_NORM_UNROLL 4        // 16-byte loads a grad-norm lane keeps in flight
+#define ELY_NORM_UNROLL 8        // 8-element groups a grad-norm lane loads before summing (divides 32)
 #endif
 #ifndef ELY_NT
 #define ELY_NT 3                 // bit 0: nontemporal AdamW loads, bit 1: nontemporal stores
@@ -119,11 +119,12 @@ __device__ __forceinline__ T ld_norm(const ELY_GLOBAL T* p) {
 #endif
 }
 
-// 8 consecutive gradient values from a 16-byte aligned address.  With FOLD
+// 8 consecutive gradient values from a 16-byte aligned address, the dtype
+// fixed at compile time so that a tile's loads issue back to back.  With FOLD
 // each is acc + widen(g) rounded once to fp32 (pieces.fold_add).
-template <bool FOLD>
+template <bool BF16, bool FOLD>
 __device__ __forceinline__ void load8_vec(const NormDesc& d, int64_t i, float (&x)[8]) {
-    if (d.dtype == ELY_BF16) {
+    if (BF16) {
         const nu32x4 w = ld_norm(gp(reinterpret_cast<const nu32x4*>(static_cast<const uint16_t*>(d.g) + i)));
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -148,6 +149,25 @@ __device__ __forceinline__ void load8_vec(const NormDesc& d, int64_t i, float (&
             x[4 + j] = b[j] + x[4 + j];
         }
     }
+}
+
+// Sum of squares of one full, aligned tile: lane l owns the 8-element groups
+// j*64 + l, j = 0..31, added in order; kNormUnroll groups are loaded before
+// the first of them is summed.
+template <bool BF16, bool FOLD>
+__device__ __forceinline__ double tile_sumsq_vec(const NormDesc& d, int64_t e0, int lane) {
+    constexpr int G = (int)(kNormTile / (kWave * 8));
+    constexpr int U = kNormUnroll;
+    static_assert(G % U == 0, "unroll divides the groups of a tile");
+    double acc = 0.0;
+    for (int j0 = 0; j0 < G; j0 += U) {
+        float x[U][8];
+#pragma unroll
+        for (int u = 0; u < U; ++u) load8_vec<BF16, FOLD>(d, e0 + ((int64_t)(j0 + u) * kWave + lane) * 8, x[u]);
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc += (double)sq8(x[u]);
+    }
+    return acc;
 }
 
 // The same 8 values element by element (0 past `end`): any alignment.
@@ -187,12 +207,7 @@ __global__ __launch_bounds__(kBlock) void norm_partials_kernel(const NormDesc* _
         double acc = 0.0;
         // lane l owns groups j*64 + l of 8 elements, in the same order on both paths
         if (d.aligned && e1 - e0 == kNormTile) {
-#pragma unroll kNormUnroll
-            for (int j = 0; j < (int)(kNormTile / (kWave * 8)); ++j) {
-                float x[8];
-                load8_vec<FOLD>(d, e0 + ((int64_t)j * kWave + lane) * 8, x);
-                acc += (double)sq8(x);
-            }
+            acc = d.dtype == ELY_BF16 ? tile_sumsq_vec<true, FOLD>(d, e0, lane) : tile_sumsq_vec<false, FOLD>(d, e0, lane);
         } else {
             for (int j = 0; j < (int)(kNormTile / (kWave * 8)); ++j) {
                 float x[8];
@@ -209,7 +224,16 @@ __global__ __launch_bounds__(kFinalThreads) void norm_final_kernel(const double*
                                                                    float max_norm, ely_norm_result* out) {
     __shared__ double red[kFinalThreads];
     double s = 0.0;
-    for (int64_t i = threadIdx.x; i < tiles; i += kFinalThreads) s += partials[i];
+    int64_t i = threadIdx.x;
+    // partials i, i + 1024, ... added in that order; 8 loads in flight
+    for (; i + 7 * kFinalThreads < tiles; i += 8 * kFinalThreads) {
+        double v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = partials[i + u * kFinalThreads];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) s += v[u];
+    }
+    for (; i < tiles; i += kFinalThreads) s += partials[i];
     red[threadIdx.x] = s;
     for (int o = kFinalThreads / 2; o > 0; o >>= 1) {
         __syncthreads();
