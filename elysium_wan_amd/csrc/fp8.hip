@@ -8,9 +8,11 @@
 //     wave, and codes are written from the same registers: one HBM read and
 //     one write per element (3 B/elem for bf16 -> fp8).
 //   * longer rows (per-tensor scaling is rows = 1): the row is cut into
-//     2048-element segments, one wave each; a first launch folds each
-//     segment's |x|max into the row's slot with an integer atomicMax (order
-//     free, so deterministic), a second converts.  Two reads of x.
+//     2048-element segments.  A first launch reduces the row's |x|max into
+//     at most 8,192 partial maxima (each wave strides over its row's
+//     segments; integer max, so order-free), a small second launch folds the
+//     partials per row, a third converts one segment per wave.  Two reads
+//     of x, no atomics.
 //   * any other shape (unaligned, columns not a multiple of the vector):
 //     the same two launches with element-wise loads.
 // Every row whose exponent keeps 2^-k, 2^k and every product exact
@@ -38,6 +40,21 @@ constexpr int64_t kDeqSegCodes = 4096;         // dequantize segment, codes
 constexpr int kFastK = 110;                    // |k| bound of the instruction path
 
 // ----------------------------------------------------------- element helpers
+
+#ifndef ELY_FP8_NT
+#define ELY_FP8_NT 0  // nontemporal codec loads
+#endif
+
+// One 16-byte load of streamed data.
+__device__ __forceinline__ uint4 ld_vec(const uint4* p) {
+#if ELY_FP8_NT
+    typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+    const v4u v = __builtin_nontemporal_load(reinterpret_cast<const __attribute__((address_space(1))) v4u*>(p));
+    return make_uint4(v[0], v[1], v[2], v[3]);
+#else
+    return *p;
+#endif
+}
 
 template <bool BF16>
 __device__ __forceinline__ float load_x(const void* x, int64_t i) {
@@ -189,12 +206,19 @@ __global__ __launch_bounds__(kQBlock) void quant_rows_kernel(const void* __restr
     if (row >= rows) return;  // whole waves leave; the kernel has no block barrier
     const int64_t nvec = cols / EPV;
     const uint4* xr = reinterpret_cast<const uint4*>(static_cast<const char*>(x) + row * cols * ESZ);
+    // every load is issued before the first is used: lanes past the row's end
+    // load its last vector (in bounds) and zero it afterwards
     uint4 buf[VPL];
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+        const int64_t vi = lane + (int64_t)kWave * j;
+        buf[j] = ld_vec(xr + (vi < nvec ? vi : nvec - 1));
+    }
     uint32_t amax = 0;
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
         const int64_t vi = lane + (int64_t)kWave * j;
-        buf[j] = vi < nvec ? xr[vi] : make_uint4(0u, 0u, 0u, 0u);
+        if (vi >= nvec) buf[j] = make_uint4(0u, 0u, 0u, 0u);
         amax = vec_absmax<BF16>(buf[j], amax);
     }
     amax = wave_max_u32(amax);
@@ -223,23 +247,43 @@ __global__ void fill_u32_kernel(uint32_t* p, int64_t n, uint32_t value) {
         p[i] = value;
 }
 
-// |x|max of each 2048-element segment, folded into rowmax[row] (fp32 bits of
-// |x|max for fp32 input, bf16 bits for bf16 input).
+// Long rows (and per-tensor scaling, one row) go through segments of
+// kSegElems elements.  The row's |x|max is reduced without atomics: wave
+// (r, j) of the rowmax_partial_kernel folds segments j, j + wpr, ... of row r
+// into partial[r * wpr + j]; rowmax_reduce_kernel folds a row's wpr partials
+// (wpr == 1: the partials are the row maxima).  Values are |x| bit patterns
+// (fp32 bits for fp32 input, bf16 bits for bf16), so max is an integer max.
+constexpr int64_t kSplitWaves = 8192;  // waves of the partial-max launch (at most)
+
+static int64_t split_wpr(int64_t rows, int64_t segs) {
+    return std::max<int64_t>(1, std::min<int64_t>(segs, kSplitWaves / std::max<int64_t>(rows, 1)));
+}
+
+// Vectors of one segment a lane holds: 2048 bf16 = 256 x 16 B -> 4 per lane.
 template <bool BF16>
-__global__ __launch_bounds__(kQBlock) void rowmax_split_kernel(const void* __restrict__ x, int64_t rows, int64_t cols,
-                                                               int64_t segs, int vec, uint32_t* __restrict__ rowmax) {
-    constexpr int EPV = BF16 ? 8 : 4;
-    constexpr int ESZ = BF16 ? 2 : 4;
-    const int lane = threadIdx.x & (kWave - 1);
-    const int64_t gw = (int64_t)blockIdx.x * kWavesPerBlock + wave_uniform(threadIdx.x / kWave);
-    const int64_t row = gw / segs, seg = gw % segs;
-    if (row >= rows) return;
-    const int64_t e0 = seg * kSegElems, e1 = min(e0 + kSegElems, cols);
+struct Seg {
+    static constexpr int EPV = BF16 ? 8 : 4;
+    static constexpr int VPL = (int)(kSegElems / EPV / kWave);
+};
+
+// |x|max bits of elements [e0, e1) of row `row` (e1 - e0 <= kSegElems).
+template <bool BF16>
+__device__ __forceinline__ uint32_t seg_absmax(const void* x, int64_t row, int64_t cols, int64_t e0, int64_t e1,
+                                               int vec, int lane) {
+    constexpr int EPV = Seg<BF16>::EPV, VPL = Seg<BF16>::VPL, ESZ = BF16 ? 2 : 4;
     uint32_t amax = 0;
     if (vec) {
         const uint4* xr = reinterpret_cast<const uint4*>(static_cast<const char*>(x) + (row * cols + e0) * ESZ);
         const int64_t nv = (e1 - e0) / EPV;
-        for (int64_t vi = lane; vi < nv; vi += kWave) amax = vec_absmax<BF16>(xr[vi], amax);
+        uint4 buf[VPL];
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) {
+            const int64_t vi = lane + (int64_t)kWave * j;
+            buf[j] = ld_vec(xr + (vi < nv ? vi : nv - 1));
+        }
+#pragma unroll
+        for (int j = 0; j < VPL; ++j)
+            if (lane + (int64_t)kWave * j < nv) amax = vec_absmax<BF16>(buf[j], amax);
     } else {
         for (int64_t e = e0 + lane; e < e1; e += kWave) {
             uint32_t b = BF16 ? (uint32_t)static_cast<const uint16_t*>(x)[row * cols + e] & 0x7FFFu
@@ -247,8 +291,43 @@ __global__ __launch_bounds__(kQBlock) void rowmax_split_kernel(const void* __res
             amax = max(amax, b);
         }
     }
+    return amax;
+}
+
+template <bool BF16>
+__global__ __launch_bounds__(kQBlock) void rowmax_partial_kernel(const void* __restrict__ x, int64_t rows, int64_t cols,
+                                                                 int64_t segs, int64_t wpr, int vec,
+                                                                 uint32_t* __restrict__ partial) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t gw = (int64_t)blockIdx.x * kWavesPerBlock + wave_uniform(threadIdx.x / kWave);
+    if (gw >= rows * wpr) return;
+    const int64_t row = gw / wpr, j = gw % wpr;
+    uint32_t amax = 0;
+    for (int64_t seg = j; seg < segs; seg += wpr) {
+        const int64_t e0 = seg * kSegElems;
+        amax = max(amax, seg_absmax<BF16>(x, row, cols, e0, min(e0 + kSegElems, cols), vec, lane));
+    }
     amax = wave_max_u32(amax);
-    if (lane == 0) atomicMax(rowmax + row, amax);
+    if (lane == 0) partial[gw] = amax;
+}
+
+__global__ __launch_bounds__(kQBlock) void rowmax_reduce_kernel(const uint32_t* __restrict__ partial, int64_t rows,
+                                                                int64_t wpr, uint32_t* __restrict__ rowmax) {
+    __shared__ uint32_t red[kWavesPerBlock];
+    const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
+    for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+        uint32_t m = 0;
+        for (int64_t i = threadIdx.x; i < wpr; i += kQBlock) m = max(m, partial[r * wpr + i]);
+        m = wave_max_u32(m);
+        if (lane == 0) red[w] = m;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            uint32_t t = red[0];
+            for (int k = 1; k < kWavesPerBlock; ++k) t = max(t, red[k]);
+            rowmax[r] = t;
+        }
+        __syncthreads();
+    }
 }
 
 template <int FMT, bool BF16>
@@ -257,8 +336,7 @@ __global__ __launch_bounds__(kQBlock) void quant_split_kernel(const void* __rest
                                                               const uint32_t* __restrict__ rowmax,
                                                               uint8_t* __restrict__ q, int32_t* __restrict__ k,
                                                               void* __restrict__ out) {
-    constexpr int EPV = BF16 ? 8 : 4;
-    constexpr int ESZ = BF16 ? 2 : 4;
+    constexpr int EPV = Seg<BF16>::EPV, VPL = Seg<BF16>::VPL, ESZ = BF16 ? 2 : 4;
     const int lane = threadIdx.x & (kWave - 1);
     const int64_t gw = (int64_t)blockIdx.x * kWavesPerBlock + wave_uniform(threadIdx.x / kWave);
     const int64_t row = gw / segs, seg = gw % segs;
@@ -270,10 +348,19 @@ __global__ __launch_bounds__(kQBlock) void quant_split_kernel(const void* __rest
     if (vec) {
         const uint4* xr = reinterpret_cast<const uint4*>(static_cast<const char*>(x) + (base + e0) * ESZ);
         const int64_t nv = (e1 - e0) / EPV;
-        for (int64_t vi = lane; vi < nv; vi += kWave) {
+        uint4 buf[VPL];
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) {
+            const int64_t vi = lane + (int64_t)kWave * j;
+            buf[j] = ld_vec(xr + (vi < nv ? vi : nv - 1));
+        }
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) {
+            const int64_t vi = lane + (int64_t)kWave * j;
+            if (vi >= nv) continue;
             uint32_t words[2];
             const int64_t e = e0 + vi * EPV;
-            quant_vec<FMT, BF16>(xr[vi], rs, words, out ? static_cast<char*>(out) + (base + e) * ESZ : nullptr);
+            quant_vec<FMT, BF16>(buf[j], rs, words, out ? static_cast<char*>(out) + (base + e) * ESZ : nullptr);
             if (q) {
                 if (BF16) *reinterpret_cast<uint2*>(q + base + e) = make_uint2(words[0], words[1]);
                 else *reinterpret_cast<uint32_t*>(q + base + e) = words[0];
@@ -311,8 +398,18 @@ __global__ __launch_bounds__(kQBlock) void dequant_kernel(const uint8_t* __restr
     if (vec) {
         const uint4* qr = reinterpret_cast<const uint4*>(q + base + e0);
         const int64_t nv = (e1 - e0) / 16;
-        for (int64_t vi = lane; vi < nv; vi += kWave) {
-            const uint4 w = qr[vi];
+        constexpr int VPL = (int)(kDeqSegCodes / 16 / kWave);
+        uint4 buf[VPL];
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) {
+            const int64_t vi = lane + (int64_t)kWave * j;
+            buf[j] = ld_vec(qr + (vi < nv ? vi : nv - 1));
+        }
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) {
+            const int64_t vi = lane + (int64_t)kWave * j;
+            if (vi >= nv) continue;
+            const uint4 w = buf[j];
             const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
             float o[16];
 #pragma unroll
@@ -563,7 +660,29 @@ static int rows_vpl(int64_t cols, int32_t dtype, const void* x, const uint8_t* q
     return 0;
 }
 
-static size_t split_ws_bytes(int64_t rows) { return align_up((size_t)std::max<int64_t>(rows, 1) * 4, 256); }
+// Row maxima, then the partial maxima (at most max(rows, kSplitWaves) of them).
+static size_t rowmax_bytes(int64_t rows) { return align_up((size_t)std::max<int64_t>(rows, 1) * 4, 256); }
+static size_t split_ws_bytes(int64_t rows) {
+    return rowmax_bytes(rows) + align_up((size_t)std::max<int64_t>(rows, kSplitWaves) * 4, 256);
+}
+
+// rowmax[r] = |x|max bits of row r, through the split path's two launches.
+template <bool BF16>
+static void split_rowmax(const void* x, int64_t rows, int64_t cols, int vec, void* workspace, uint32_t* rowmax,
+                         hipStream_t s) {
+    const int64_t segs = (cols + kSegElems - 1) / kSegElems;
+    const int64_t wpr = split_wpr(rows, segs);
+    if (rows > INT64_MAX / wpr) fail(ELY_EINVAL, "too many rows");
+    uint32_t* partial = wpr == 1 ? rowmax : reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + rowmax_bytes(rows));
+    hipLaunchKernelGGL((rowmax_partial_kernel<BF16>), dim3(blocks_for_waves(rows * wpr)), dim3(kQBlock), 0, s, x, rows,
+                       cols, segs, wpr, vec, partial);
+    check_launch("rowmax_partial_kernel");
+    if (wpr > 1) {
+        hipLaunchKernelGGL(rowmax_reduce_kernel, dim3((unsigned)std::min<int64_t>(rows, 65536)), dim3(kQBlock), 0, s,
+                           (const uint32_t*)partial, rows, wpr, rowmax);
+        check_launch("rowmax_reduce_kernel");
+    }
+}
 
 template <int FMT, bool BF16>
 static void quantize_impl(const void* x, int64_t rows, int64_t cols, uint8_t* q, int32_t* k, void* out,
@@ -590,13 +709,8 @@ static void quantize_impl(const void* x, int64_t rows, int64_t cols, uint8_t* q,
     uint32_t* rowmax = static_cast<uint32_t*>(workspace);
     const int64_t segs = (cols + kSegElems - 1) / kSegElems;
     if (rows > INT64_MAX / segs) fail(ELY_EINVAL, "too many segments");
-    hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)std::min<int64_t>((rows + 255) / 256, 4096)), dim3(256), 0,
-                       s, rowmax, rows, 0u);
-    check_launch("fill_u32_kernel");
+    split_rowmax<BF16>(x, rows, cols, vec, workspace, rowmax, s);
     const unsigned blocks = blocks_for_waves(rows * segs);
-    hipLaunchKernelGGL((rowmax_split_kernel<BF16>), dim3(blocks), dim3(kQBlock), 0, s, x, rows, cols, segs, vec,
-                       rowmax);
-    check_launch("rowmax_split_kernel");
     hipLaunchKernelGGL((quant_split_kernel<FMT, BF16>), dim3(blocks), dim3(kQBlock), 0, s, x, rows, cols, segs, vec,
                        (const uint32_t*)rowmax, q, k, out);
     check_launch("quant_split_kernel");
@@ -715,7 +829,7 @@ int ely_selftest_sqrt(uint32_t start, uint64_t count, unsigned long long* mismat
 
 int64_t ely_fp8_recover_workspace_bytes(int64_t rows) {
     if (rows < 0) return -1;
-    return (int64_t)(2 * split_ws_bytes(rows));
+    return (int64_t)(split_ws_bytes(rows) + rowmax_bytes(rows));
 }
 
 int ely_fp8_recover_exp(const void* t, int32_t t_dtype, int64_t rows, int64_t cols, int32_t fmt, int32_t* k,
@@ -732,22 +846,19 @@ int ely_fp8_recover_exp(const void* t, int32_t t_dtype, int64_t rows, int64_t co
         uint32_t* rowmax = static_cast<uint32_t*>(workspace);
         uint32_t* rowmask = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + split_ws_bytes(rows));
         const unsigned fb = (unsigned)std::min<int64_t>((rows + 255) / 256, 4096);
-        hipLaunchKernelGGL(fill_u32_kernel, dim3(fb), dim3(256), 0, s, rowmax, rows, 0u);
-        check_launch("fill_u32_kernel");
         hipLaunchKernelGGL(fill_u32_kernel, dim3(fb), dim3(256), 0, s, rowmask, rows, 0x1Fu);
         check_launch("fill_u32_kernel");
         const bool bf16 = t_dtype == ELY_BF16;
-        if (cols > 0) {
+        if (cols == 0) {
+            hipLaunchKernelGGL(fill_u32_kernel, dim3(fb), dim3(256), 0, s, rowmax, rows, 0u);
+            check_launch("fill_u32_kernel");
+        } else {
             const int64_t segs = (cols + kSegElems - 1) / kSegElems;
             if (rows > INT64_MAX / segs) fail(ELY_EINVAL, "too many segments");
             const unsigned blocks = blocks_for_waves(rows * segs);
-            if (bf16)
-                hipLaunchKernelGGL(rowmax_split_kernel<true>, dim3(blocks), dim3(kQBlock), 0, s, t, rows, cols, segs, 0,
-                                   rowmax);
-            else
-                hipLaunchKernelGGL(rowmax_split_kernel<false>, dim3(blocks), dim3(kQBlock), 0, s, t, rows, cols, segs,
-                                   0, rowmax);
-            check_launch("rowmax_split_kernel");
+            const int vec = (cols % (bf16 ? 8 : 4) == 0) && aligned16(t);
+            if (bf16) split_rowmax<true>(t, rows, cols, vec, workspace, rowmax, s);
+            else split_rowmax<false>(t, rows, cols, vec, workspace, rowmax, s);
 #define ELY_RECOVER_MASK(F, B)                                                                                    \
     hipLaunchKernelGGL((recover_mask_kernel<F, B>), dim3(blocks), dim3(kQBlock), 0, s, t, rows, cols, segs,        \
                        (const uint32_t*)rowmax, rowmask)

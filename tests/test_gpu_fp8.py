@@ -174,3 +174,54 @@ def test_empty_inputs():
     z = torch.empty(3, 0, dtype=torch.bfloat16, device="cuda")
     q, k = fp8.quantize(z)
     assert k.shape == (3, 1) and int(k.abs().sum()) == 0
+
+
+def test_long_rows_beyond_the_partial_budget(oracle):
+    """More long rows (cols > 8192) than the partial-max launch has waves:
+    one wave per row strides over its segments."""
+    x = activation((9000, 8200), seed=12)
+    say("fp8 9000 long rows")
+    _check_against_oracle(oracle, x, "e4m3")
+
+
+def _c4_activation(seed: int) -> torch.Tensor:
+    """Config C4's activation [16, 4096, 8192] bf16: Student-t (df = 3) with
+    0.01% of the elements set to +-1e4, generated on the GPU."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    shape = (16, 4096, 8192)
+    z = torch.randn(shape, generator=g, device="cuda")
+    c = torch.zeros(shape, device="cuda")
+    for _ in range(3):
+        c.add_(torch.randn(shape, generator=g, device="cuda").square_())
+    z.div_(c.div_(3.0).sqrt_())
+    del c
+    n = z.numel()
+    idx = torch.randint(0, n, (n // 10000,), generator=g, device="cuda")
+    sign = torch.randint(0, 2, idx.shape, generator=g, device="cuda").float() * 2 - 1
+    z.view(-1)[idx] = 1e4 * sign
+    return z.to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+def test_c4_per_row_and_per_tensor_equal_torch_on_the_gpu(fmt):
+    """Config C4 at full size: bytes and exponents of per-row and per-tensor
+    scaling equal torch's own ops on the GPU running model/fp8.py:28-49's
+    arithmetic (frexp of |x|max, the pow2 product in bf16, torch's fp8
+    conversion); decode is exact."""
+    from elysium_wan_amd import fp8
+
+    x = _c4_activation(61 if fmt == "e4m3" else 62)
+    dt, ebias = fp8.FORMATS[fmt]
+    for per_tensor in (False, True):
+        say("fp8 C4", fmt, "per-tensor" if per_tensor else "per-row")
+        q, k = fp8.quantize(x, fmt, per_tensor=per_tensor)
+        amax = x.abs().amax() if per_tensor else x.abs().amax(dim=-1, keepdim=True)
+        kt = torch.frexp(amax.float()).exponent.to(torch.int32) - ebias
+        kt = torch.where(amax == 0, torch.zeros_like(kt), kt)
+        assert torch.equal(k.reshape(-1), kt.reshape(-1))
+        qt = (x * torch.exp2(-kt.to(torch.float32)).to(torch.bfloat16)).to(dt)
+        assert torch.equal(q.view(torch.uint8), qt.view(torch.uint8))
+        del qt
+        d = fp8.dequantize(q, k, torch.bfloat16)
+        assert torch.equal(d, (q.to(torch.bfloat16) * torch.exp2(kt.to(torch.float32)).to(torch.bfloat16)))
+        del q, d
