@@ -215,13 +215,15 @@ def test_c4_per_row_and_per_tensor_equal_torch_on_the_gpu(fmt):
     for per_tensor in (False, True):
         say("fp8 C4", fmt, "per-tensor" if per_tensor else "per-row")
         q, k = fp8.quantize(x, fmt, per_tensor=per_tensor)
-        amax = x.abs().amax() if per_tensor else x.abs().amax(dim=-1, keepdim=True)
-        kt = torch.frexp(amax.float()).exponent.to(torch.int32) - ebias
-        kt = torch.where(amax == 0, torch.zeros_like(kt), kt)
+        xs = x.reshape(1, -1) if per_tensor else x
+        amax = xs.abs().amax(dim=-1, keepdim=True)
+        kt = (torch.frexp(amax).exponent - ebias).to(torch.int32)
+        kt = torch.where(amax > 0, kt, torch.zeros_like(kt))
         assert torch.equal(k.reshape(-1), kt.reshape(-1))
-        qt = (x * torch.exp2(-kt.to(torch.float32)).to(torch.bfloat16)).to(dt)
-        assert torch.equal(q.view(torch.uint8), qt.view(torch.uint8))
+        qt = (xs * torch.exp2((-kt).to(xs.dtype))).to(dt)
+        assert torch.equal(q.reshape(-1).view(torch.uint8), qt.reshape(-1).view(torch.uint8))
         del qt
         d = fp8.dequantize(q, k, torch.bfloat16)
-        assert torch.equal(d, (q.to(torch.bfloat16) * torch.exp2(kt.to(torch.float32)).to(torch.bfloat16)))
+        dt_ = q.reshape(xs.shape).to(torch.bfloat16) * torch.exp2(kt.to(torch.bfloat16))
+        assert torch.equal(d.reshape(-1), dt_.reshape(-1))
         del q, d
