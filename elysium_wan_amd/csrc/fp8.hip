@@ -22,8 +22,10 @@
 // torch's arithmetic (pow2 rounded to the dtype, product rounded to the
 // dtype, software conversion), uniformly per row.
 //
-// dequantize (fp8.py:52-53): out = float(q) * 2^k in the output dtype,
-// 16 codes per lane per step; roundtrip (fp8.py:56-63) fuses both.
+// dequantize (fp8.py:52-53): out = float(q) * 2^k in the output dtype, the
+// codes taken as one flat array (a wave's 4,096 codes may span rows), 8 codes
+// per lane per step for bf16 output (4 for fp32) so every store instruction
+// covers a contiguous 1 KB; roundtrip (fp8.py:56-63) fuses both.
 #include <algorithm>
 
 #include "ely_device.hpp"
@@ -42,14 +44,57 @@ constexpr int kFastK = 110;                    // |k| bound of the instruction p
 // ----------------------------------------------------------- element helpers
 
 #ifndef ELY_FP8_NT
-#define ELY_FP8_NT 0  // nontemporal codec loads
+#define ELY_FP8_NT 3  // bit 0: nontemporal codec loads, bit 1: nontemporal stores
 #endif
+
+// Stores of streamed data; nontemporal when bit 1 of ELY_FP8_NT is set.
+typedef uint32_t ev4u __attribute__((ext_vector_type(4)));
+typedef uint32_t ev2u __attribute__((ext_vector_type(2)));
+#define ELY_G1 __attribute__((address_space(1)))
+__device__ __forceinline__ void st_vec(void* p, uint4 v) {
+#if ELY_FP8_NT & 2
+    __builtin_nontemporal_store(ev4u{v.x, v.y, v.z, v.w}, (ELY_G1 ev4u*)p);
+#else
+    *static_cast<uint4*>(p) = v;
+#endif
+}
+__device__ __forceinline__ void st_vec2(void* p, uint2 v) {
+#if ELY_FP8_NT & 2
+    __builtin_nontemporal_store(ev2u{v.x, v.y}, (ELY_G1 ev2u*)p);
+#else
+    *static_cast<uint2*>(p) = v;
+#endif
+}
+__device__ __forceinline__ void st_u32(void* p, uint32_t v) {
+#if ELY_FP8_NT & 2
+    __builtin_nontemporal_store(v, (ELY_G1 uint32_t*)p);
+#else
+    *static_cast<uint32_t*>(p) = v;
+#endif
+}
+
+// 8- and 4-byte loads of streamed data.
+__device__ __forceinline__ uint2 ld_vec2(const void* p) {
+#if ELY_FP8_NT & 1
+    const ev2u v = __builtin_nontemporal_load((const ELY_G1 ev2u*)p);
+    return make_uint2(v[0], v[1]);
+#else
+    return *static_cast<const uint2*>(p);
+#endif
+}
+__device__ __forceinline__ uint32_t ld_u32(const void* p) {
+#if ELY_FP8_NT & 1
+    return __builtin_nontemporal_load((const ELY_G1 uint32_t*)p);
+#else
+    return *static_cast<const uint32_t*>(p);
+#endif
+}
 
 // One 16-byte load of streamed data.
 __device__ __forceinline__ uint4 ld_vec(const uint4* p) {
-#if ELY_FP8_NT
+#if ELY_FP8_NT & 1
     typedef uint32_t v4u __attribute__((ext_vector_type(4)));
-    const v4u v = __builtin_nontemporal_load(reinterpret_cast<const __attribute__((address_space(1))) v4u*>(p));
+    const v4u v = __builtin_nontemporal_load((const __attribute__((address_space(1))) v4u*)(const void*)p);
     return make_uint4(v[0], v[1], v[2], v[3]);
 #else
     return *p;
@@ -139,57 +184,62 @@ __device__ __forceinline__ void unpack(const uint4& w, float* f) {
     }
 }
 
-// Quantize one 16-byte input vector (8 bf16 or 4 fp32) into codes packed in
-// words[0..1] (bf16: 8 codes) or words[0] (fp32: 4 codes); with `out`,
-// also write the dequantized values in the input dtype at out_vec.
+// Quantize one 16-byte input vector (8 bf16 or 4 fp32) of an instruction-path
+// row into codes packed in words[0..1] (bf16: 8 codes) or words[0] (fp32: 4
+// codes); with `out`, also write the dequantized values in the input dtype at
+// out_vec (exact there, so bf16 truncation is the rounding).
 template <int FMT, bool BF16>
-__device__ __forceinline__ void quant_vec(const uint4& w, const RowScale& rs, uint32_t* words, void* out_vec) {
+__device__ __forceinline__ void quant_vec_fast(const uint4& w, const RowScale& rs, uint32_t* words, void* out_vec) {
     constexpr int EPV = BF16 ? 8 : 4;
     float f[EPV];
     unpack<BF16>(w, f);
-    uint32_t codes[EPV];
-    if (rs.fast) {
 #pragma unroll
-        for (int j = 0; j < EPV; j += 4) {
-            uint32_t pk = cvt_pk_fp8<FMT, false>(f[j] * rs.s_down, f[j + 1] * rs.s_down, 0u);
-            pk = cvt_pk_fp8<FMT, true>(f[j + 2] * rs.s_down, f[j + 3] * rs.s_down, pk);
-            words[j / 4] = pk;
-        }
-    } else {
-#pragma unroll
-        for (int j = 0; j < EPV; ++j) codes[j] = quant_sw<FMT, BF16>(f[j], rs.s_down);
-#pragma unroll
-        for (int j = 0; j < EPV; j += 4)
-            words[j / 4] = codes[j] | (codes[j + 1] << 8) | (codes[j + 2] << 16) | (codes[j + 3] << 24);
+    for (int j = 0; j < EPV; j += 4) {
+        uint32_t pk = cvt_pk_fp8<FMT, false>(f[j] * rs.s_down, f[j + 1] * rs.s_down, 0u);
+        pk = cvt_pk_fp8<FMT, true>(f[j + 2] * rs.s_down, f[j + 3] * rs.s_down, pk);
+        words[j / 4] = pk;
     }
     if (out_vec) {
         float o[EPV];
-        if (rs.fast) {
 #pragma unroll
-            for (int j = 0; j < EPV; j += 4) {
-                float a, b, c, d;
-                cvt_pk_f32<FMT, false>(words[j / 4], a, b);
-                cvt_pk_f32<FMT, true>(words[j / 4], c, d);
-                o[j] = a * rs.s_up;
-                o[j + 1] = b * rs.s_up;
-                o[j + 2] = c * rs.s_up;
-                o[j + 3] = d * rs.s_up;
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < EPV; ++j) o[j] = dequant_sw<FMT, BF16>((words[j / 4] >> (8 * (j % 4))) & 0xFFu, rs.s_up);
+        for (int j = 0; j < EPV; j += 4) {
+            float a, b, c, d;
+            cvt_pk_f32<FMT, false>(words[j / 4], a, b);
+            cvt_pk_f32<FMT, true>(words[j / 4], c, d);
+            o[j] = a * rs.s_up;
+            o[j + 1] = b * rs.s_up;
+            o[j + 2] = c * rs.s_up;
+            o[j + 3] = d * rs.s_up;
         }
         uint4 r;
         if (BF16) {
             uint32_t b[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) b[j] = rs.fast ? fast_bf16_bits(o[j]) : f32_to_bf16(o[j]);
+            for (int j = 0; j < 8; ++j) b[j] = fast_bf16_bits(o[j]);
             r = make_uint4(b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16), b[6] | (b[7] << 16));
         } else {
             r = make_uint4(__float_as_uint(o[0]), __float_as_uint(o[1]), __float_as_uint(o[2]),
                            __float_as_uint(o[3]));
         }
-        *static_cast<uint4*>(out_vec) = r;
+        st_vec(out_vec, r);
+    }
+}
+
+// Elements [e0, e1) of a row at `base` through the bit-level restatement of
+// torch's arithmetic: the rows the instruction path does not cover (|k| >
+// 110 or a non-finite |x|max), one element per lane per step.
+template <int FMT, bool BF16>
+__device__ __forceinline__ void quant_slow(const void* x, int64_t base, int64_t e0, int64_t e1, const RowScale& rs,
+                                        uint8_t* q, void* out, int lane) {
+    for (int64_t e = e0 + lane; e < e1; e += kWave) {
+        const float xv = load_x<BF16>(x, base + e);
+        const uint32_t c = quant_sw<FMT, BF16>(xv, rs.s_down);
+        if (q) q[base + e] = (uint8_t)c;
+        if (out) {
+            const float o = dequant_sw<FMT, BF16>(c, rs.s_up);
+            if (BF16) static_cast<uint16_t*>(out)[base + e] = (uint16_t)f32_to_bf16(o);
+            else static_cast<float*>(out)[base + e] = o;
+        }
     }
 }
 
@@ -224,6 +274,7 @@ __global__ __launch_bounds__(kQBlock) void quant_rows_kernel(const void* __restr
     amax = wave_max_u32(amax);
     const RowScale rs = row_scale<FMT>(to_f32_bits<BF16>(amax), BF16, BF16);
     if (lane == 0 && k) k[row] = rs.k;
+    if (!rs.fast) return quant_slow<FMT, BF16>(x, row * cols, 0, cols, rs, q, out, lane);
     uint8_t* qr = q ? q + row * cols : nullptr;
     char* orow = out ? static_cast<char*>(out) + row * cols * ESZ : nullptr;
 #pragma unroll
@@ -231,10 +282,10 @@ __global__ __launch_bounds__(kQBlock) void quant_rows_kernel(const void* __restr
         const int64_t vi = lane + (int64_t)kWave * j;
         if (vi < nvec) {
             uint32_t words[2];
-            quant_vec<FMT, BF16>(buf[j], rs, words, orow ? orow + vi * 16 : nullptr);
+            quant_vec_fast<FMT, BF16>(buf[j], rs, words, orow ? orow + vi * 16 : nullptr);
             if (qr) {
-                if (BF16) *reinterpret_cast<uint2*>(qr + vi * 8) = make_uint2(words[0], words[1]);
-                else *reinterpret_cast<uint32_t*>(qr + vi * 4) = words[0];
+                if (BF16) st_vec2(qr + vi * 8, make_uint2(words[0], words[1]));
+                else st_u32(qr + vi * 4, words[0]);
             }
         }
     }
@@ -345,7 +396,7 @@ __global__ __launch_bounds__(kQBlock) void quant_split_kernel(const void* __rest
     if (seg == 0 && lane == 0 && k) k[row] = rs.k;
     const int64_t e0 = seg * kSegElems, e1 = min(e0 + kSegElems, cols);
     const int64_t base = row * cols;
-    if (vec) {
+    if (vec && rs.fast) {
         const uint4* xr = reinterpret_cast<const uint4*>(static_cast<const char*>(x) + (base + e0) * ESZ);
         const int64_t nv = (e1 - e0) / EPV;
         uint4 buf[VPL];
@@ -360,32 +411,102 @@ __global__ __launch_bounds__(kQBlock) void quant_split_kernel(const void* __rest
             if (vi >= nv) continue;
             uint32_t words[2];
             const int64_t e = e0 + vi * EPV;
-            quant_vec<FMT, BF16>(buf[j], rs, words, out ? static_cast<char*>(out) + (base + e) * ESZ : nullptr);
+            quant_vec_fast<FMT, BF16>(buf[j], rs, words, out ? static_cast<char*>(out) + (base + e) * ESZ : nullptr);
             if (q) {
-                if (BF16) *reinterpret_cast<uint2*>(q + base + e) = make_uint2(words[0], words[1]);
-                else *reinterpret_cast<uint32_t*>(q + base + e) = words[0];
+                if (BF16) st_vec2(q + base + e, make_uint2(words[0], words[1]));
+                else st_u32(q + base + e, words[0]);
             }
         }
     } else {
-        for (int64_t e = e0 + lane; e < e1; e += kWave) {
-            const float xv = load_x<BF16>(x, base + e);
-            const uint32_t c = quant_sw<FMT, BF16>(xv, rs.s_down);
-            if (q) q[base + e] = (uint8_t)c;
-            if (out) {
-                const float o = dequant_sw<FMT, BF16>(c, rs.s_up);
-                if (BF16) static_cast<uint16_t*>(out)[base + e] = (uint16_t)f32_to_bf16(o);
-                else static_cast<float*>(out)[base + e] = o;
-            }
-        }
+        quant_slow<FMT, BF16>(x, base, e0, e1, rs, q, out, lane);
     }
 }
 
 // -------------------------------------------------------------- dequantize
 
+// Codes in rows whose length is a multiple of 16 (and 16-byte aligned
+// buffers) are dequantized as one flat array: wave w takes codes
+// [4096 w, 4096 w + 4096), which may span rows.  A lane takes CPL codes per
+// step (8 for bf16 output, 4 for fp32), so that each store instruction of a
+// wave writes one contiguous 1 KB run; every lane issues all its loads
+// before the first is used, and each CPL-code vector lies in one row and
+// looks up that row's exponent.
+template <int FMT, bool BF16OUT, bool IDX32>
+__global__ __launch_bounds__(kQBlock) void dequant_flat_kernel(const uint8_t* __restrict__ q,
+                                                               const int32_t* __restrict__ k, int64_t n,
+                                                               int64_t cols, void* __restrict__ out) {
+    constexpr int CPL = BF16OUT ? 8 : 4;
+    constexpr int VPL = (int)(kDeqSegCodes / CPL / kWave);
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t gw = (int64_t)blockIdx.x * kWavesPerBlock + wave_uniform(threadIdx.x / kWave);
+    const int64_t e0 = gw * kDeqSegCodes;
+    if (e0 >= n) return;
+    const int64_t nv = min(kDeqSegCodes, n - e0) / CPL;
+    uint32_t buf[VPL][CPL / 4];
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+        const int64_t vi = lane + (int64_t)kWave * j;
+        const uint8_t* src = q + e0 + (vi < nv ? vi : nv - 1) * CPL;
+        if (CPL == 8) {
+            const uint2 w = ld_vec2(src);
+            buf[j][0] = w.x;
+            buf[j][CPL / 4 - 1] = w.y;
+        } else {
+            buf[j][0] = ld_u32(src);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+        const int64_t vi = lane + (int64_t)kWave * j;
+        if (vi >= nv) continue;
+        const int64_t e = e0 + vi * CPL;
+        const int64_t row = IDX32 ? (int64_t)((uint32_t)e / (uint32_t)cols) : e / cols;
+        const int kk = k[row];
+        if (kk >= -kFastK && kk <= kFastK) {
+            const float s_up = __uint_as_float((uint32_t)(127 + kk) << 23);
+            float o[CPL];
+#pragma unroll
+            for (int h = 0; h < CPL / 4; ++h) {
+                float a, b, c, d;
+                cvt_pk_f32<FMT, false>(buf[j][h], a, b);
+                cvt_pk_f32<FMT, true>(buf[j][h], c, d);
+                o[4 * h] = a * s_up;
+                o[4 * h + 1] = b * s_up;
+                o[4 * h + 2] = c * s_up;
+                o[4 * h + 3] = d * s_up;
+            }
+            if (BF16OUT) {
+                uint32_t b[8];
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    // an fp8 NaN is the only non-exact value the instruction path sees
+                    const float v = o[t];
+                    b[t] = v != v ? 0x7FC0u : fast_bf16_bits(v);
+                }
+                st_vec(static_cast<uint16_t*>(out) + e,
+                       make_uint4(b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16), b[6] | (b[7] << 16)));
+            } else {
+                st_vec(static_cast<float*>(out) + e, make_uint4(__float_as_uint(o[0]), __float_as_uint(o[1]),
+                                                                __float_as_uint(o[2]), __float_as_uint(o[3])));
+            }
+        } else {
+            // the restatement of torch's arithmetic (|k| > 110), code by code
+            const float s_up = pow2_dtype(kk, BF16OUT);
+#pragma unroll 1
+            for (int t = 0; t < CPL; ++t) {
+                const float o = dequant_sw<FMT, BF16OUT>((buf[j][t / 4] >> (8 * (t % 4))) & 0xFFu, s_up);
+                if (BF16OUT) static_cast<uint16_t*>(out)[e + t] = (uint16_t)f32_to_bf16(o);
+                else static_cast<float*>(out)[e + t] = o;
+            }
+        }
+    }
+}
+
+// Any other shape: one wave per (row, 4096-code segment), element by element.
 template <int FMT, bool BF16OUT>
-__global__ __launch_bounds__(kQBlock) void dequant_kernel(const uint8_t* __restrict__ q, const int32_t* __restrict__ k,
-                                                          int64_t rows, int64_t cols, int64_t segs, int vec,
-                                                          void* __restrict__ out) {
+__global__ __launch_bounds__(kQBlock) void dequant_any_kernel(const uint8_t* __restrict__ q,
+                                                              const int32_t* __restrict__ k, int64_t rows,
+                                                              int64_t cols, int64_t segs, void* __restrict__ out) {
     const int lane = threadIdx.x & (kWave - 1);
     const int64_t gw = (int64_t)blockIdx.x * kWavesPerBlock + wave_uniform(threadIdx.x / kWave);
     const int64_t row = gw / segs, seg = gw % segs;
@@ -395,65 +516,10 @@ __global__ __launch_bounds__(kQBlock) void dequant_kernel(const uint8_t* __restr
     const float s_up = fast ? __uint_as_float((uint32_t)(127 + kk) << 23) : pow2_dtype(kk, BF16OUT);
     const int64_t e0 = seg * kDeqSegCodes, e1 = min(e0 + kDeqSegCodes, cols);
     const int64_t base = row * cols;
-    if (vec) {
-        const uint4* qr = reinterpret_cast<const uint4*>(q + base + e0);
-        const int64_t nv = (e1 - e0) / 16;
-        constexpr int VPL = (int)(kDeqSegCodes / 16 / kWave);
-        uint4 buf[VPL];
-#pragma unroll
-        for (int j = 0; j < VPL; ++j) {
-            const int64_t vi = lane + (int64_t)kWave * j;
-            buf[j] = ld_vec(qr + (vi < nv ? vi : nv - 1));
-        }
-#pragma unroll
-        for (int j = 0; j < VPL; ++j) {
-            const int64_t vi = lane + (int64_t)kWave * j;
-            if (vi >= nv) continue;
-            const uint4 w = buf[j];
-            const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-            float o[16];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                if (fast) {
-                    float a, b, c, d;
-                    cvt_pk_f32<FMT, false>(ws[j], a, b);
-                    cvt_pk_f32<FMT, true>(ws[j], c, d);
-                    o[4 * j] = a * s_up;
-                    o[4 * j + 1] = b * s_up;
-                    o[4 * j + 2] = c * s_up;
-                    o[4 * j + 3] = d * s_up;
-                } else {
-#pragma unroll
-                    for (int t = 0; t < 4; ++t) o[4 * j + t] = dequant_sw<FMT, BF16OUT>((ws[j] >> (8 * t)) & 0xFFu, s_up);
-                }
-            }
-            const int64_t e = e0 + vi * 16;
-            if (BF16OUT) {
-                uint32_t b[16];
-#pragma unroll
-                for (int j = 0; j < 16; ++j) {
-                    // an fp8 NaN is the only non-exact value the instruction path sees
-                    const float v = o[j];
-                    b[j] = fast ? (v != v ? 0x7FC0u : fast_bf16_bits(v)) : f32_to_bf16(v);
-                }
-                uint4* op = reinterpret_cast<uint4*>(static_cast<uint16_t*>(out) + base + e);
-                op[0] = make_uint4(b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16), b[6] | (b[7] << 16));
-                op[1] = make_uint4(b[8] | (b[9] << 16), b[10] | (b[11] << 16), b[12] | (b[13] << 16),
-                                   b[14] | (b[15] << 16));
-            } else {
-                float4* op = reinterpret_cast<float4*>(static_cast<float*>(out) + base + e);
-                op[0] = make_float4(o[0], o[1], o[2], o[3]);
-                op[1] = make_float4(o[4], o[5], o[6], o[7]);
-                op[2] = make_float4(o[8], o[9], o[10], o[11]);
-                op[3] = make_float4(o[12], o[13], o[14], o[15]);
-            }
-        }
-    } else {
-        for (int64_t e = e0 + lane; e < e1; e += kWave) {
-            const float o = dequant_sw<FMT, BF16OUT>(q[base + e], s_up);
-            if (BF16OUT) static_cast<uint16_t*>(out)[base + e] = (uint16_t)f32_to_bf16(o);
-            else static_cast<float*>(out)[base + e] = o;
-        }
+    for (int64_t e = e0 + lane; e < e1; e += kWave) {
+        const float o = dequant_sw<FMT, BF16OUT>(q[base + e], s_up);
+        if (BF16OUT) static_cast<uint16_t*>(out)[base + e] = (uint16_t)f32_to_bf16(o);
+        else static_cast<float*>(out)[base + e] = o;
     }
 }
 
@@ -720,12 +786,23 @@ template <int FMT, bool BF16OUT>
 static void dequantize_impl(const uint8_t* q, const int32_t* k, int64_t rows, int64_t cols, void* out,
                             hipStream_t s) {
     if (rows == 0 || cols == 0) return;
-    const int vec = (cols % 16 == 0) && aligned16(q) && aligned16(out);
+    if ((cols % 16 == 0) && aligned16(q) && aligned16(out)) {
+        const int64_t n = rows * cols;
+        const unsigned blocks = blocks_for_waves((n + kDeqSegCodes - 1) / kDeqSegCodes);
+        if (n < ((int64_t)1 << 32))
+            hipLaunchKernelGGL((dequant_flat_kernel<FMT, BF16OUT, true>), dim3(blocks), dim3(kQBlock), 0, s, q, k, n,
+                               cols, out);
+        else
+            hipLaunchKernelGGL((dequant_flat_kernel<FMT, BF16OUT, false>), dim3(blocks), dim3(kQBlock), 0, s, q, k, n,
+                               cols, out);
+        check_launch("dequant_flat_kernel");
+        return;
+    }
     const int64_t segs = (cols + kDeqSegCodes - 1) / kDeqSegCodes;
     if (rows > INT64_MAX / segs) fail(ELY_EINVAL, "too many segments");
-    hipLaunchKernelGGL((dequant_kernel<FMT, BF16OUT>), dim3(blocks_for_waves(rows * segs)), dim3(kQBlock), 0, s, q, k,
-                       rows, cols, segs, vec, out);
-    check_launch("dequant_kernel");
+    hipLaunchKernelGGL((dequant_any_kernel<FMT, BF16OUT>), dim3(blocks_for_waves(rows * segs)), dim3(kQBlock), 0, s, q,
+                       k, rows, cols, segs, out);
+    check_launch("dequant_any_kernel");
 }
 
 }  // namespace ely

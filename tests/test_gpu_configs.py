@@ -1,0 +1,135 @@
+"""BASELINE configs C2 and C3 at their full sizes on one MI355X, checked
+through properties that do not need a CPU pass over billions of elements:
+
+* C2 (the 15.8B model's stage: ~7.9B fp32 elements, p/m/v/g resident in
+  HBM, 1% of the tensors' gradients x100 so that clipping triggers): the
+  global norm against an fp64 sum of squares (within 1e-6), the clip
+  coefficient against the oracle's clip_grad_norm_ formula, and a random
+  sample of one million elements stepped by the oracle from their gathered
+  inputs, bit for bit;
+* C3 (the 25.1B model's 4-stage shard: 1,000 vectors of 6,144 interleaved
+  with 100 matrices of 6,144 x 10,240, bf16 Student-t gradients): five runs
+  from the same seeded inputs give bitwise-identical norms, parameters and
+  moments, and a sampled oracle check.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import say
+
+pytestmark = pytest.mark.gpu
+
+LR, BETAS, EPS, WD, MAX_NORM = 3e-4, (0.9, 0.95), 1e-8, 0.1, 1.0
+
+
+def _fp64_sumsq(grads) -> float:
+    return float(sum(float(g.double().square().sum()) for g in grads))
+
+
+def test_c2_full_shard_clips_and_steps_exactly(oracle):
+    """C2: 25 GPT blocks at d = 5120 (300 tensors, 7,865,984,000 fp32
+    elements; p, g, m, v = 126 GB in HBM), fp32 grads N(0, 1e-4) with 3 of
+    the 300 tensors (1%) x100."""
+    from elysium_wan_amd import optim
+
+    d = 5120
+    shapes = [(d,), (d,), (3 * d, d), (3 * d,), (d, d), (d,), (d,), (d,), (4 * d, d), (4 * d,), (d, 4 * d), (d,)] * 25
+    gen = torch.Generator(device="cuda").manual_seed(2)
+    params, grads = [], []
+    hot = {30, 150, 270}
+    for i, s in enumerate(shapes):
+        params.append(torch.empty(s, device="cuda").normal_(0.0, 0.02, generator=gen).requires_grad_(True))
+        grads.append(torch.empty(s, device="cuda").normal_(0.0, 1e-4 * (100.0 if i in hot else 1.0), generator=gen))
+    n = sum(p.numel() for p in params)
+    assert n == 7_865_984_000
+    say("C2 full shard", n)
+    opt = optim.FusedAdamW(params, lr=LR, betas=BETAS, eps=EPS, weight_decay=WD, order="host", max_norm=MAX_NORM)
+    # the inputs of one million sampled elements, saved before the step
+    sizes = torch.tensor([p.numel() for p in params], dtype=torch.int64)
+    cum = torch.cumsum(sizes, 0)
+    flat_idx = torch.randint(0, n, (1_000_000,), generator=torch.Generator().manual_seed(77))
+    t_idx = torch.searchsorted(cum, flat_idx, right=True)
+    local = flat_idx - (cum[t_idx] - sizes[t_idx])
+    saved = {}
+    for t in torch.unique(t_idx).tolist():
+        sel = local[t_idx == t].cuda()
+        saved[t] = (sel, params[t].detach().view(-1)[sel].clone(), grads[t].view(-1)[sel].clone())
+    want = _fp64_sumsq(grads)
+    opt.step(grads=grads)
+    torch.cuda.synchronize()
+    norm = float(opt.grad_norm())
+    assert abs(norm - want**0.5) <= 1e-6 * want**0.5
+    coef = float(opt._norm[12:16].view(torch.float32))
+    assert coef < 1.0, "C2's hot tensors make clipping trigger"
+    assert coef == oracle.clip_coef(norm, MAX_NORM)
+    p_in = np.concatenate([saved[t][1].cpu().numpy() for t in sorted(saved)])
+    g_in = np.concatenate([saved[t][2].cpu().numpy() for t in sorted(saved)])
+    got_p = np.concatenate([params[t].detach().view(-1)[saved[t][0]].cpu().numpy() for t in sorted(saved)])
+    got_m = np.concatenate([opt.state[t]["exp_avg"].view(-1)[saved[t][0]].cpu().numpy() for t in sorted(saved)])
+    got_v = np.concatenate([opt.state[t]["exp_avg_sq"].view(-1)[saved[t][0]].cpu().numpy() for t in sorted(saved)])
+    m = np.zeros_like(p_in)
+    v = np.zeros_like(p_in)
+    oracle.adamw_host(p_in, g_in, m, v, np.array(optim.host_consts(LR, BETAS, EPS, WD, 1.0), dtype=np.float32), True, coef)
+    assert np.array_equal(got_p.view(np.uint32), p_in.view(np.uint32))
+    assert np.array_equal(got_m.view(np.uint32), m.view(np.uint32))
+    assert np.array_equal(got_v.view(np.uint32), v.view(np.uint32))
+    del opt, params, grads, saved
+    torch.cuda.empty_cache()
+
+
+def _c3_shard(seed: int):
+    """C3: 1,000 vectors of 6,144 interleaved with 100 matrices of
+    6,144 x 10,240 (ten vectors, then one matrix), 6,297,600,000 elements;
+    params N(0, 0.02) fp32, grads Student-t(df = 3) x 1e-4 in bf16."""
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    shapes = []
+    for _ in range(100):
+        shapes += [(6144,)] * 10 + [(6144, 10240)]
+    params, grads = [], []
+    for s in shapes:
+        params.append(torch.empty(s, device="cuda").normal_(0.0, 0.02, generator=gen).requires_grad_(True))
+        z = torch.empty(s, device="cuda").normal_(generator=gen)
+        c = torch.zeros(s, device="cuda")
+        for _ in range(3):
+            c.add_(torch.empty(s, device="cuda").normal_(generator=gen).square_())
+        grads.append(z.div_(c.div_(3.0).sqrt_()).mul_(1e-4).to(torch.bfloat16))
+        del z, c
+    return params, grads
+
+
+def test_c3_ragged_shard_is_bitwise_reproducible(oracle):
+    """C3's 1,100-tensor ragged list: five runs of grad-norm + clipped step
+    from the same seeded inputs give bit-identical norms and checksums of
+    p, m and v; the first run's sampled elements equal the oracle's."""
+    from elysium_wan_amd import optim
+
+    sums = []
+    for run in range(5):
+        params, grads = _c3_shard(33)
+        if run == 0:
+            n = sum(p.numel() for p in params)
+            assert n == 6_297_600_000 and len(params) == 1100
+            keep_p = {t: params[t].detach().view(-1)[:4096].clone() for t in range(0, 1100, 37)}
+            keep_g = {t: grads[t].view(-1)[:4096].clone() for t in keep_p}
+        say("C3 run", run)
+        opt = optim.FusedAdamW(params, lr=LR, betas=BETAS, eps=EPS, weight_decay=WD, order="host", max_norm=MAX_NORM)
+        opt.step(grads=grads)
+        torch.cuda.synchronize()
+        ck = lambda ts: int(sum(int(t.detach().view(torch.int32).to(torch.int64).sum()) for t in ts))  # noqa: E731
+        sums.append((float(opt.grad_norm()), ck(params), ck([opt.state[i]["exp_avg"] for i in range(1100)]), ck([opt.state[i]["exp_avg_sq"] for i in range(1100)])))
+        if run == 0:
+            coef = float(opt._norm[12:16].view(torch.float32))
+            p_in = np.concatenate([keep_p[t].cpu().numpy() for t in keep_p])
+            g_in = np.concatenate([keep_g[t].view(torch.int16).cpu().numpy().view(np.uint16) for t in keep_p])
+            got = np.concatenate([params[t].detach().view(-1)[:4096].cpu().numpy() for t in keep_p])
+            m = np.zeros_like(p_in)
+            v = np.zeros_like(p_in)
+            oracle.adamw_host(p_in, g_in, m, v, np.array(optim.host_consts(LR, BETAS, EPS, WD, 1.0), dtype=np.float32), True, coef)
+            assert np.array_equal(got.view(np.uint32), p_in.view(np.uint32))
+        del opt, params, grads
+        torch.cuda.empty_cache()
+    assert all(s == sums[0] for s in sums), sums
