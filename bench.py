@@ -318,7 +318,7 @@ def _traffic_kernels():
         "adamw_kernel": (n * ADAM_BYTES_PER_ELEM, "fused clip + AdamW, C1 shard, 28 B/elem"),
         "norm_partials_kernel": (n * NORM_BYTES_PER_ELEM, "grad-norm partials, C1 bf16 grads, 2 B/elem"),
         "quant_rows_kernel": (act * CODEC_BYTES_PER_ELEM, "fp8 e4m3 quantize, C1 activation, 3 B/elem"),
-        "dequant_kernel": (act * CODEC_BYTES_PER_ELEM, "fp8 e4m3 dequantize -> bf16, C1 activation, 3 B/elem"),
+        "dequant_flat_kernel": (act * CODEC_BYTES_PER_ELEM, "fp8 e4m3 dequantize -> bf16, C1 activation, 3 B/elem"),
     }
 
 
@@ -410,6 +410,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-codec", action="store_true", help="skip the fp8 codec leg")
     ap.add_argument("--no-extra", action="store_true", help="skip the fused-fold and host-moment legs")
+    ap.add_argument("--codec", choices=("c1", "c4", "all"), default="all", help="activation sizes of the codec leg")
+    ap.add_argument("--no-optimizer", action="store_true", help="skip the optimizer leg (profiling the other legs alone)")
     ap.add_argument("--cpu-sample", type=int, default=256 * 1024 * 1024)
     ap.add_argument("--profile-pass", action="store_true", help="launch each measured kernel a few times, untimed, for rocprofv3 --pmc runs")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"), help="summarize two --pmc runs of --profile-pass into profiles/")
@@ -432,16 +434,26 @@ def main():
             profile_pass(device)
         return
     with torch.cuda.stream(stream):
+        if args.no_optimizer:
+            log("codec-only run")
+            for size in ("c1", "c4"):
+                if args.codec in (size, "all"):
+                    rows, cols, copies = (8 * 2048, D_MODEL, 8) if size == "c1" else (16 * 4096, 8192, 2)
+                    print(json.dumps({size: bench_codec(device, stream, rows, cols, copies, iters=10)}), flush=True)
+            return
         log("optimizer leg")
         o = bench_optimizer(args, device, stream)
         codec = extra = None
         if not args.no_codec:
             log("codec leg")
-            codec = {"c1_per_row": bench_codec(device, stream, 8 * 2048, D_MODEL, 8)}
-            torch.cuda.empty_cache()
-            codec["c4_per_row"] = bench_codec(device, stream, 16 * 4096, 8192, 2, iters=10)
-            codec["c4_per_tensor"] = bench_codec(device, stream, 16 * 4096, 8192, 2, iters=10, per_tensor=True)
-            torch.cuda.empty_cache()
+            codec = {}
+            if args.codec in ("c1", "all"):
+                codec["c1_per_row"] = bench_codec(device, stream, 8 * 2048, D_MODEL, 8)
+                torch.cuda.empty_cache()
+            if args.codec in ("c4", "all"):
+                codec["c4_per_row"] = bench_codec(device, stream, 16 * 4096, 8192, 2, iters=10)
+                codec["c4_per_tensor"] = bench_codec(device, stream, 16 * 4096, 8192, 2, iters=10, per_tensor=True)
+                torch.cuda.empty_cache()
         if not args.no_extra:
             log("fold leg")
             extra = {"fold": bench_fold(device, stream)}

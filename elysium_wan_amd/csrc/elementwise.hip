@@ -1,8 +1,10 @@
-// elementwise.hip -- the two stand-alone elementwise ops of the sharded
-// "pieces" update: the fp32 master -> bf16 working-copy cast
-// (pieces.cast_piece, runtime/pieces.py:192-195) and the fp32 fold of a
-// microbatch gradient (pieces.fold_add, runtime/pieces.py:206-214).  Both
-// are one HBM pass, 16-byte vectors, grid-stride over a persistent grid.
+// elementwise.hip -- the stand-alone elementwise ops of the sharded "pieces"
+// update: the fp32 master -> bf16 working-copy cast (pieces.cast_piece,
+// runtime/pieces.py:192-195), the fp32 fold of a microbatch gradient
+// (pieces.fold_add, runtime/pieces.py:206-214) and the clip's in-place
+// scaling (clip_grad_norm_).  Each is one HBM pass over 4-element quads
+// (16-byte fp32, 8-byte bf16 vectors, nontemporal), four quads in flight per
+// thread, on a persistent grid.
 #include <algorithm>
 
 #include "ely_device.hpp"
@@ -13,61 +15,82 @@
 namespace ely {
 
 constexpr int kEwBlock = 256;
+constexpr int kEwUnroll = 4;  // quads of 4 elements a thread has in flight
 
-__global__ __launch_bounds__(kEwBlock) void cast_bf16_kernel(const float* __restrict__ x, uint16_t* __restrict__ out,
-                                                             int64_t n, int vec) {
-    const int64_t tid = (int64_t)blockIdx.x * kEwBlock + threadIdx.x;
-    const int64_t stride = (int64_t)gridDim.x * kEwBlock;
-    int64_t done = 0;
-    if (vec) {
-        const int64_t nv = n / 8;
-        for (int64_t i = tid; i < nv; i += stride) {
-            const float4* xp = reinterpret_cast<const float4*>(x + i * 8);
-            const float4 a = xp[0], b = xp[1];
-            uint4 o;
-            o.x = f32_to_bf16(a.x) | (f32_to_bf16(a.y) << 16);
-            o.y = f32_to_bf16(a.z) | (f32_to_bf16(a.w) << 16);
-            o.z = f32_to_bf16(b.x) | (f32_to_bf16(b.y) << 16);
-            o.w = f32_to_bf16(b.z) | (f32_to_bf16(b.w) << 16);
-            *reinterpret_cast<uint4*>(out + i * 8) = o;
-        }
-        done = nv * 8;
-    }
-    for (int64_t i = done + tid; i < n; i += stride) out[i] = (uint16_t)f32_to_bf16(x[i]);
+typedef float ef4 __attribute__((ext_vector_type(4)));
+typedef uint32_t eu2 __attribute__((ext_vector_type(2)));
+#define EW_G1 __attribute__((address_space(1)))
+
+// Streamed (nontemporal) 16-byte fp32 quads and 8-byte bf16 quads.
+__device__ __forceinline__ ef4 ld4(const float* p) { return __builtin_nontemporal_load((const EW_G1 ef4*)p); }
+__device__ __forceinline__ void st4(float* p, ef4 v) { __builtin_nontemporal_store(v, (EW_G1 ef4*)p); }
+__device__ __forceinline__ eu2 ldh4(const uint16_t* p) { return __builtin_nontemporal_load((const EW_G1 eu2*)p); }
+__device__ __forceinline__ void sth4(uint16_t* p, eu2 v) { __builtin_nontemporal_store(v, (EW_G1 eu2*)p); }
+
+__device__ __forceinline__ ef4 widen4(eu2 w) {
+    return ef4{bf16_to_f32(w[0] & 0xFFFFu), bf16_to_f32(w[0] >> 16), bf16_to_f32(w[1] & 0xFFFFu), bf16_to_f32(w[1] >> 16)};
+}
+__device__ __forceinline__ eu2 narrow4(ef4 v) {
+    return eu2{f32_to_bf16(v[0]) | (f32_to_bf16(v[1]) << 16), f32_to_bf16(v[2]) | (f32_to_bf16(v[3]) << 16)};
 }
 
+// The quad loop shared by the kernels below: thread t of T takes quads
+// t, t + T, ..., kEwUnroll of them loaded before the first is computed, so
+// each load or store instruction of a wave covers one contiguous run.
+// load(q) reads quad q into registers, store(q, regs) computes and writes it;
+// returns the elements covered.
+template <class Load, class Store>
+__device__ __forceinline__ int64_t quad_loop(int64_t nq, Load load, Store store) {
+    const int64_t T = (int64_t)gridDim.x * kEwBlock;
+    const int64_t t = (int64_t)blockIdx.x * kEwBlock + threadIdx.x;
+    for (int64_t base = t; base < nq; base += T * kEwUnroll) {
+        decltype(load(0)) r[kEwUnroll];
+#pragma unroll
+        for (int u = 0; u < kEwUnroll; ++u) {
+            const int64_t q = base + u * T;
+            r[u] = load(q < nq ? q : nq - 1);
+        }
+#pragma unroll
+        for (int u = 0; u < kEwUnroll; ++u) {
+            const int64_t q = base + u * T;
+            if (q < nq) store(q, r[u]);
+        }
+    }
+    return nq * 4;
+}
+
+// pieces.cast_piece: fp32 -> bf16 (RNE, NaN -> 0x7FC0).
+__global__ __launch_bounds__(kEwBlock) void cast_bf16_kernel(const float* __restrict__ x, uint16_t* __restrict__ out,
+                                                             int64_t n, int vec) {
+    int64_t done = 0;
+    if (vec)
+        done = quad_loop(
+            n / 4, [&](int64_t q) { return ld4(x + 4 * q); }, [&](int64_t q, ef4 v) { sth4(out + 4 * q, narrow4(v)); });
+    const int64_t T = (int64_t)gridDim.x * kEwBlock;
+    for (int64_t i = done + (int64_t)blockIdx.x * kEwBlock + threadIdx.x; i < n; i += T) out[i] = (uint16_t)f32_to_bf16(x[i]);
+}
+
+struct AccG {
+    ef4 acc, g;
+};
+
+// pieces.fold_add: acc += widen(g), one fp32 rounding per element.
 template <bool BF16G>
 __global__ __launch_bounds__(kEwBlock) void fold_add_kernel(float* __restrict__ acc, const void* __restrict__ g,
                                                             int64_t n, int vec) {
-    const int64_t tid = (int64_t)blockIdx.x * kEwBlock + threadIdx.x;
-    const int64_t stride = (int64_t)gridDim.x * kEwBlock;
     int64_t done = 0;
-    if (vec) {
-        const int64_t nv = n / 8;
-        for (int64_t i = tid; i < nv; i += stride) {
-            float4* ap = reinterpret_cast<float4*>(acc + i * 8);
-            float4 a = ap[0], b = ap[1];
-            float gv[8];
-            if (BF16G) {
-                const uint4 w = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(g) + i * 8);
-                gv[0] = bf16_to_f32(w.x & 0xFFFFu); gv[1] = bf16_to_f32(w.x >> 16);
-                gv[2] = bf16_to_f32(w.y & 0xFFFFu); gv[3] = bf16_to_f32(w.y >> 16);
-                gv[4] = bf16_to_f32(w.z & 0xFFFFu); gv[5] = bf16_to_f32(w.z >> 16);
-                gv[6] = bf16_to_f32(w.w & 0xFFFFu); gv[7] = bf16_to_f32(w.w >> 16);
-            } else {
-                const float4* gp = reinterpret_cast<const float4*>(static_cast<const float*>(g) + i * 8);
-                const float4 c = gp[0], d = gp[1];
-                gv[0] = c.x; gv[1] = c.y; gv[2] = c.z; gv[3] = c.w;
-                gv[4] = d.x; gv[5] = d.y; gv[6] = d.z; gv[7] = d.w;
-            }
-            a.x = a.x + gv[0]; a.y = a.y + gv[1]; a.z = a.z + gv[2]; a.w = a.w + gv[3];
-            b.x = b.x + gv[4]; b.y = b.y + gv[5]; b.z = b.z + gv[6]; b.w = b.w + gv[7];
-            ap[0] = a;
-            ap[1] = b;
-        }
-        done = nv * 8;
-    }
-    for (int64_t i = done + tid; i < n; i += stride) {
+    if (vec)
+        done = quad_loop(
+            n / 4,
+            [&](int64_t q) {
+                AccG r;
+                r.acc = ld4(acc + 4 * q);
+                r.g = BF16G ? widen4(ldh4(static_cast<const uint16_t*>(g) + 4 * q)) : ld4(static_cast<const float*>(g) + 4 * q);
+                return r;
+            },
+            [&](int64_t q, AccG r) { st4(acc + 4 * q, ef4{r.acc[0] + r.g[0], r.acc[1] + r.g[1], r.acc[2] + r.g[2], r.acc[3] + r.g[3]}); });
+    const int64_t T = (int64_t)gridDim.x * kEwBlock;
+    for (int64_t i = done + (int64_t)blockIdx.x * kEwBlock + threadIdx.x; i < n; i += T) {
         const float gv = BF16G ? bf16_to_f32(static_cast<const uint16_t*>(g)[i]) : static_cast<const float*>(g)[i];
         acc[i] = acc[i] + gv;
     }
@@ -76,12 +99,25 @@ __global__ __launch_bounds__(kEwBlock) void fold_add_kernel(float* __restrict__ 
 // g <- g * coef (coef read from device memory), one fp32 multiply rounded to
 // g's dtype: torch's _foreach_mul_(grads, clip_coef) (clip_grad.py:170-177).
 template <bool BF16G>
-__global__ __launch_bounds__(kEwBlock) void scale_kernel(void* __restrict__ g, int64_t n,
+__global__ __launch_bounds__(kEwBlock) void scale_kernel(void* __restrict__ g, int64_t n, int vec,
                                                          const float* __restrict__ coef_ptr) {
     const float coef = *coef_ptr;
-    const int64_t tid = (int64_t)blockIdx.x * kEwBlock + threadIdx.x;
-    const int64_t stride = (int64_t)gridDim.x * kEwBlock;
-    for (int64_t i = tid; i < n; i += stride) {
+    int64_t done = 0;
+    if (vec) {
+        if (BF16G) {
+            uint16_t* p = static_cast<uint16_t*>(g);
+            done = quad_loop(
+                n / 4, [&](int64_t q) { return widen4(ldh4(p + 4 * q)); },
+                [&](int64_t q, ef4 v) { sth4(p + 4 * q, narrow4(ef4{v[0] * coef, v[1] * coef, v[2] * coef, v[3] * coef})); });
+        } else {
+            float* p = static_cast<float*>(g);
+            done = quad_loop(
+                n / 4, [&](int64_t q) { return ld4(p + 4 * q); },
+                [&](int64_t q, ef4 v) { st4(p + 4 * q, ef4{v[0] * coef, v[1] * coef, v[2] * coef, v[3] * coef}); });
+        }
+    }
+    const int64_t T = (int64_t)gridDim.x * kEwBlock;
+    for (int64_t i = done + (int64_t)blockIdx.x * kEwBlock + threadIdx.x; i < n; i += T) {
         if (BF16G) {
             uint16_t* p = static_cast<uint16_t*>(g);
             p[i] = (uint16_t)f32_to_bf16(bf16_to_f32(p[i]) * coef);
@@ -94,7 +130,7 @@ __global__ __launch_bounds__(kEwBlock) void scale_kernel(void* __restrict__ g, i
 
 static unsigned ew_blocks(int64_t n) {
     const DeviceInfo& dev = device_info();
-    const int64_t want = (n + (int64_t)kEwBlock * 8 - 1) / ((int64_t)kEwBlock * 8);
+    const int64_t want = (n + (int64_t)kEwBlock * 4 * kEwUnroll - 1) / ((int64_t)kEwBlock * 4 * kEwUnroll);
     return (unsigned)std::max<int64_t>(1, std::min<int64_t>(want, (int64_t)dev.cus * 8));
 }
 
@@ -109,7 +145,7 @@ int ely_cast_bf16(const float* x, uint16_t* out, int64_t n, void* stream) {
         if (n < 0) fail(ELY_EINVAL, "ely_cast_bf16: negative n");
         if (n == 0) return;
         if (!x || !out) fail(ELY_EINVAL, "ely_cast_bf16: null pointer");
-        const int vec = aligned16(x) && aligned16(out);
+        const int vec = aligned16(x) && (reinterpret_cast<uintptr_t>(out) % 8 == 0);
         hipLaunchKernelGGL(cast_bf16_kernel, dim3(ew_blocks(n)), dim3(kEwBlock), 0, static_cast<hipStream_t>(stream),
                            x, out, n, vec);
         check_launch("cast_bf16_kernel");
@@ -122,7 +158,7 @@ int ely_fold_add(float* acc, const void* g, int32_t g_dtype, int64_t n, void* st
         if (g_dtype != ELY_F32 && g_dtype != ELY_BF16) fail(ELY_EINVAL, "ely_fold_add: g_dtype");
         if (n == 0) return;
         if (!acc || !g) fail(ELY_EINVAL, "ely_fold_add: null pointer");
-        const int vec = aligned16(acc) && aligned16(g);
+        const int vec = aligned16(acc) && (reinterpret_cast<uintptr_t>(g) % (g_dtype == ELY_BF16 ? 8 : 16) == 0);
         hipStream_t s = static_cast<hipStream_t>(stream);
         if (g_dtype == ELY_BF16)
             hipLaunchKernelGGL(fold_add_kernel<true>, dim3(ew_blocks(n)), dim3(kEwBlock), 0, s, acc, g, n, vec);
@@ -141,12 +177,13 @@ int ely_scale_inplace(const ely_tensor* ts, int32_t n, const float* coef_dev, vo
             const ely_tensor& t = ts[i];
             if (t.numel < 0 || (t.numel > 0 && !t.ptr)) fail(ELY_EINVAL, "ely_scale_inplace: bad tensor");
             if (t.numel == 0) continue;
+            const int vec = reinterpret_cast<uintptr_t>(t.ptr) % (t.dtype == ELY_BF16 ? 8 : 16) == 0;
             if (t.dtype == ELY_BF16)
                 hipLaunchKernelGGL(scale_kernel<true>, dim3(ew_blocks(t.numel)), dim3(kEwBlock), 0, s, t.ptr, t.numel,
-                                   coef_dev);
+                                   vec, coef_dev);
             else if (t.dtype == ELY_F32)
                 hipLaunchKernelGGL(scale_kernel<false>, dim3(ew_blocks(t.numel)), dim3(kEwBlock), 0, s, t.ptr, t.numel,
-                                   coef_dev);
+                                   vec, coef_dev);
             else
                 fail(ELY_EINVAL, "ely_scale_inplace: dtype");
             check_launch("scale_kernel");
