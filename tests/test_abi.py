@@ -81,6 +81,35 @@ def test_argument_errors_are_status_codes(lib):
     assert lib.ely_selftest_fp8_cvt(0, 1 << 33, 0, None, None) == _lib.EINVAL
 
 
+def test_argument_errors_of_the_fold_wire_and_recover_entry_points(lib):
+    """Every check fails before the HIP runtime is touched."""
+    from elysium_wan_amd import _lib
+
+    one = _lib.tensor_array([_lib.ElyTensor(1 << 20, 5, _lib.F32, 0)])
+    bf = _lib.tensor_array([_lib.ElyTensor(1 << 20, 5, _lib.BF16, 0)])
+    c = (_lib.ElyConsts * 1)()
+    st = lib.ely_adamw_fold_step(one, None, bf, one, one, None, 1, c, 0, 0, None, None, 0, None)
+    assert st == _lib.EINVAL and b"accumulator" in lib.ely_last_error()
+    st = lib.ely_adamw_fold_step(one, bf, bf, one, one, None, 1, c, 0, 0, None, None, 0, None)
+    assert st == _lib.EINVAL and b"must be fp32" in lib.ely_last_error()
+    short = _lib.tensor_array([_lib.ElyTensor(1 << 20, 4, _lib.F32, 0)])
+    st = lib.ely_grad_norm_fold(short, bf, 1, 1.0, None, None, 0, None)
+    assert st == _lib.EINVAL and b"numel" in lib.ely_last_error()
+    assert lib.ely_grad_norm_fold(None, bf, 1, 1.0, None, None, 0, None) == _lib.EINVAL
+    assert lib.ely_byteplanes_split(None, 10, 3, None, None) == _lib.EINVAL
+    assert b"esz" in lib.ely_last_error()
+    assert lib.ely_byteplanes_split(None, -1, 4, None, None) == _lib.EINVAL
+    assert lib.ely_byteplanes_split(None, 10, 4, None, None) == _lib.EINVAL
+    assert lib.ely_byteplanes_join(None, 10, 2, None, None) == _lib.EINVAL
+    assert lib.ely_byteplanes_split(None, 0, 4, None, None) == _lib.OK  # nothing to do
+    assert lib.ely_fp8_nibbles_encode(None, 7, 4, None, None, None, None) == _lib.EINVAL
+    assert lib.ely_fp8_nibbles_encode(None, _lib.F32, 4, None, None, None, None) == _lib.EINVAL
+    assert lib.ely_fp8_nibbles_decode(None, None, 4, None, None) == _lib.EINVAL
+    assert lib.ely_fp8_recover_exp(None, _lib.BF16, 2, 8, 9, None, None, None, 0, None) == _lib.EINVAL
+    assert lib.ely_fp8_recover_exp(None, _lib.BF16, 2, 8, _lib.E4M3, None, None, None, 0, None) == _lib.EINVAL
+    assert lib.ely_fp8_quantize_k(None, _lib.F32, 2, 8, _lib.E5M2, None, None, None) == _lib.EINVAL
+
+
 def test_workspace_queries_are_host_arithmetic(lib):
     from elysium_wan_amd import _lib
 
@@ -90,6 +119,9 @@ def test_workspace_queries_are_host_arithmetic(lib):
     assert lib.ely_grad_norm_workspace_bytes(arr, -1) == -1
     assert lib.ely_adamw_workspace_bytes(192) >= 192 * (64 + 32)
     assert lib.ely_fp8_workspace_bytes(16384, 2560, _lib.BF16) >= 16384 * 4
+    # row maxima plus at most 8,192 partial maxima, whatever the row length
+    assert lib.ely_fp8_workspace_bytes(1, 1 << 40, _lib.BF16) >= 8192 * 4
+    assert lib.ely_fp8_recover_workspace_bytes(100) >= lib.ely_fp8_workspace_bytes(100, 0, _lib.BF16) + 400
 
 
 def test_python_surface_fails_loudly_off_the_gpu():

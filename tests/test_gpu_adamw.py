@@ -280,3 +280,48 @@ def test_fold_inside_the_update_equals_fold_then_step(order, gdtype):
     oa.step(grads=[gv], acc=[accv])
     ob.step(grads=[accv + gv])
     assert torch.equal(pa.view(torch.int32), pb.view(torch.int32))
+
+
+def test_step_on_a_side_thread_and_stream():
+    """runtime/stage.py:3094-3099 runs step() on a side thread inside
+    torch.cuda.stream(side): the launches go to that stream (the main stream
+    stays free) and the result equals a step on the main stream."""
+    import threading
+
+    from elysium_wan_amd import optim
+
+    gen = torch.Generator().manual_seed(31)
+    shapes = [(512, 384), (384,), (70001,)]
+    init = [torch.randn(s, generator=gen) for s in shapes]
+    grads = [(torch.randn(s, generator=gen) * 1e-2).to(torch.bfloat16).cuda() for s in shapes]
+    main = [t.clone().cuda().requires_grad_(True) for t in init]
+    side_ps = [t.clone().cuda().requires_grad_(True) for t in init]
+    a = optim.FusedAdamW(main, lr=1e-3, betas=(0.9, 0.95), order="host", max_norm=1.0, working_copy=True)
+    b = optim.FusedAdamW(side_ps, lr=1e-3, betas=(0.9, 0.95), order="host", max_norm=1.0, working_copy=True)
+    side = torch.cuda.Stream()
+    seen = []
+    errors = []
+
+    def run():
+        try:
+            with torch.cuda.stream(side):
+                for _ in range(3):
+                    b.step(grads=grads, on_param=seen.append)
+        except Exception as e:  # surfaced below
+            errors.append(e)
+
+    say("step on a side thread")
+    torch.cuda.synchronize()
+    t = threading.Thread(target=run)
+    t.start()
+    t.join()
+    assert not errors, errors
+    side.synchronize()
+    for _ in range(3):
+        a.step(grads=grads)
+    torch.cuda.synchronize()
+    assert seen == [0, 1, 2] * 3
+    for x, y in zip(main, side_ps):
+        assert torch.equal(x.detach().view(torch.int32), y.detach().view(torch.int32))
+    for x, y in zip(a.working_copies, b.working_copies):
+        assert torch.equal(x.view(torch.int16), y.view(torch.int16))
