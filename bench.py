@@ -391,6 +391,39 @@ def traffic_summary(fetch_dir: str, write_dir: str, command: str) -> None:
     print("\n".join(lines))
 
 
+def cpu_context(sample_elems: int = 1 << 25):
+    """More CPU reference points on the same host: torch.optim.AdamW
+    (foreach=False, the reference's "adamw" CPU path) over a 32M-element
+    sample at one thread and at torch's default thread count, and the
+    oracle's fp8 quantize of a bf16 activation sample (one thread)."""
+    from oracle import oracle as O
+
+    out = {}
+    threads0 = torch.get_num_threads()
+    try:
+        for threads in sorted({1, threads0}):
+            torch.set_num_threads(threads)
+            p = torch.randn(sample_elems) * 0.02
+            p.requires_grad_(True)
+            p.grad = torch.randn(sample_elems) * 1e-4
+            opt = torch.optim.AdamW([p], lr=LR, betas=BETAS, eps=EPS, weight_decay=WD, foreach=False)
+            opt.step()
+            t0 = time.perf_counter()
+            opt.step()
+            out[f"torch_adamw_params_per_s_{threads}t"] = sample_elems / (time.perf_counter() - t0)
+            del opt, p
+    finally:
+        torch.set_num_threads(threads0)
+    x = (np.random.default_rng(1).standard_normal((4096, D_MODEL)) ).astype(np.float32)
+    xb = O.f32_to_bf16_bits(x).reshape(x.shape)
+    t0 = time.perf_counter()
+    O.quantize(xb, "e4m3")
+    dt = time.perf_counter() - t0
+    out["oracle_fp8_quantize_GBs_1t"] = xb.size * CODEC_BYTES_PER_ELEM / dt / 1e9
+    out["sample"] = f"torch AdamW over {sample_elems} fp32 elements (threads: 1 and {threads0}); oracle quantize of [4096, {D_MODEL}] bf16"
+    return out
+
+
 def read_traffic():
     """HBM bytes per AdamW launch measured by rocprofv3 --pmc (FETCH_SIZE +
     WRITE_SIZE, scaled by a plain copy's reading), if that profile is
@@ -468,6 +501,8 @@ def main():
     if not args.no_cpu:
         log("cpu baseline leg")
         rate, secs = cpu_baseline(args.cpu_sample)
+        extra = extra or {}
+        extra["cpu_context"] = cpu_context()
         cpu = {
             "value": rate,
             "unit": "params/s",
