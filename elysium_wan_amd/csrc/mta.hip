@@ -54,7 +54,7 @@ namespace ely {
 #define ELY_ADAM_BPC 1           // AdamW blocks per compute unit
 #endif
 #ifndef ELY_NORM_BPC
-#define ELY_NORM_BPC 8           // grad-norm blocks (of 4 waves) per compute unit
+#define ELY_NORM_BPC 24          // grad-norm blocks (of 4 waves) per compute unit
 #endif
 
 constexpr int64_t kAdamTile = ELY_ADAM_TILE;
@@ -119,41 +119,56 @@ __device__ __forceinline__ T ld_norm(const ELY_GLOBAL T* p) {
 #endif
 }
 
-// 8 consecutive gradient values from a 16-byte aligned address, the dtype
-// fixed at compile time so that a tile's loads issue back to back.  With FOLD
-// each is acc + widen(g) rounded once to fp32 (pieces.fold_add).
+// The raw 16-byte vectors of one 8-element group: 1 (bf16) or 2 (fp32)
+// gradient vectors, plus 2 accumulator vectors with FOLD.
 template <bool BF16, bool FOLD>
-__device__ __forceinline__ void load8_vec(const NormDesc& d, int64_t i, float (&x)[8]) {
-    if (BF16) {
-        const nu32x4 w = ld_norm(gp(reinterpret_cast<const nu32x4*>(static_cast<const uint16_t*>(d.g) + i)));
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            x[2 * j] = bf16_to_f32(w[j] & 0xFFFFu);
-            x[2 * j + 1] = bf16_to_f32(w[j] >> 16);
-        }
-    } else {
-        const ELY_GLOBAL nf32x4* p = gp(reinterpret_cast<const nf32x4*>(static_cast<const float*>(d.g) + i));
-        const nf32x4 a = ld_norm(p), b = ld_norm(p + 1);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            x[j] = a[j];
-            x[4 + j] = b[j];
-        }
-    }
+struct Raw8 {
+    nu32x4 g[BF16 ? 1 : 2];
+    nf32x4 a[FOLD ? 2 : 1];
+};
+
+template <bool BF16, bool FOLD>
+__device__ __forceinline__ void raw8_load(const NormDesc& d, int64_t i, Raw8<BF16, FOLD>& r) {
+    const ELY_GLOBAL nu32x4* p = gp(reinterpret_cast<const nu32x4*>(static_cast<const char*>(d.g) + i * (BF16 ? 2 : 4)));
+    r.g[0] = ld_norm(p);
+    if (!BF16) r.g[BF16 ? 0 : 1] = ld_norm(p + 1);
     if (FOLD) {
         const ELY_GLOBAL nf32x4* q = gp(reinterpret_cast<const nf32x4*>(d.acc + i));
-        const nf32x4 a = ld_norm(q), b = ld_norm(q + 1);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            x[j] = a[j] + x[j];
-            x[4 + j] = b[j] + x[4 + j];
-        }
+        r.a[0] = ld_norm(q);
+        r.a[FOLD ? 1 : 0] = ld_norm(q + 1);
     }
 }
 
+// The group's values (acc + widen(g) with FOLD), squared and summed by sq8.
+template <bool BF16, bool FOLD>
+__device__ __forceinline__ float raw8_sumsq(const Raw8<BF16, FOLD>& r) {
+    float x[8];
+    if (BF16) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            x[2 * j] = bf16_to_f32(r.g[0][j] & 0xFFFFu);
+            x[2 * j + 1] = bf16_to_f32(r.g[0][j] >> 16);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            x[j] = __uint_as_float(r.g[0][j]);
+            x[4 + j] = __uint_as_float(r.g[BF16 ? 0 : 1][j]);
+        }
+    }
+    if (FOLD) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            x[j] = r.a[0][j] + x[j];
+            x[4 + j] = r.a[FOLD ? 1 : 0][j] + x[4 + j];
+        }
+    }
+    return sq8(x);
+}
+
 // Sum of squares of one full, aligned tile: lane l owns the 8-element groups
-// j*64 + l, j = 0..31, added in order; kNormUnroll groups are loaded before
-// the first of them is summed.
+// j*64 + l, j = 0..31, added in order; kNormUnroll groups' raw vectors are
+// loaded before the first of them is summed.
 template <bool BF16, bool FOLD>
 __device__ __forceinline__ double tile_sumsq_vec(const NormDesc& d, int64_t e0, int lane) {
     constexpr int G = (int)(kNormTile / (kWave * 8));
@@ -161,11 +176,11 @@ __device__ __forceinline__ double tile_sumsq_vec(const NormDesc& d, int64_t e0, 
     static_assert(G % U == 0, "unroll divides the groups of a tile");
     double acc = 0.0;
     for (int j0 = 0; j0 < G; j0 += U) {
-        float x[U][8];
+        Raw8<BF16, FOLD> r[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) load8_vec<BF16, FOLD>(d, e0 + ((int64_t)(j0 + u) * kWave + lane) * 8, x[u]);
+        for (int u = 0; u < U; ++u) raw8_load<BF16, FOLD>(d, e0 + ((int64_t)(j0 + u) * kWave + lane) * 8, r[u]);
 #pragma unroll
-        for (int u = 0; u < U; ++u) acc += (double)sq8(x[u]);
+        for (int u = 0; u < U; ++u) acc += (double)raw8_sumsq<BF16, FOLD>(r[u]);
     }
     return acc;
 }
@@ -186,7 +201,11 @@ __device__ __forceinline__ void load8_any(const NormDesc& d, int64_t i, int64_t 
     }
 }
 
-template <bool FOLD>
+// DT: the gradients' dtype when one call's are all ELY_F32 or all ELY_BF16
+// (the tile loop is then compiled for that dtype only, which keeps the
+// kernel's registers, and so its occupancy, to what that dtype needs), or -1
+// for a mixed list, dispatched per tile.
+template <bool FOLD, int DT>
 __global__ __launch_bounds__(kBlock) void norm_partials_kernel(const NormDesc* __restrict__ desc, int32_t n,
                                                                int64_t total_tiles, double* __restrict__ partials) {
     const int lane = threadIdx.x & (kWave - 1);
@@ -207,7 +226,8 @@ __global__ __launch_bounds__(kBlock) void norm_partials_kernel(const NormDesc* _
         double acc = 0.0;
         // lane l owns groups j*64 + l of 8 elements, in the same order on both paths
         if (d.aligned && e1 - e0 == kNormTile) {
-            acc = d.dtype == ELY_BF16 ? tile_sumsq_vec<true, FOLD>(d, e0, lane) : tile_sumsq_vec<false, FOLD>(d, e0, lane);
+            if (DT == ELY_BF16 || (DT < 0 && d.dtype == ELY_BF16)) acc = tile_sumsq_vec<true, FOLD>(d, e0, lane);
+            else acc = tile_sumsq_vec<false, FOLD>(d, e0, lane);
         } else {
             for (int j = 0; j < (int)(kNormTile / (kWave * 8)); ++j) {
                 float x[8];
@@ -545,12 +565,19 @@ static void grad_norm_impl(const ely_tensor* accs, const ely_tensor* grads, int3
         upload(dtable, table.data(), table.size() * sizeof(NormDesc), s);
         const int64_t waves = std::min<int64_t>(tiles, mt_blocks(ELY_NORM_BPC) * (kBlock / kWave));
         const int64_t blocks = (waves + 3) / 4;
+        int dt = table[0].dtype;
+        for (const NormDesc& d : table)
+            if (d.dtype != dt) dt = -1;
+        typedef void (*NormKernel)(const NormDesc*, int32_t, int64_t, double*);
+        NormKernel kern;
         if (accs)
-            hipLaunchKernelGGL(norm_partials_kernel<true>, dim3((unsigned)blocks), dim3(kBlock), 0, s, dtable,
-                               (int32_t)table.size(), tiles, partials);
+            kern = dt == ELY_BF16 ? norm_partials_kernel<true, ELY_BF16>
+                                  : dt == ELY_F32 ? norm_partials_kernel<true, ELY_F32> : norm_partials_kernel<true, -1>;
         else
-            hipLaunchKernelGGL(norm_partials_kernel<false>, dim3((unsigned)blocks), dim3(kBlock), 0, s, dtable,
-                               (int32_t)table.size(), tiles, partials);
+            kern = dt == ELY_BF16 ? norm_partials_kernel<false, ELY_BF16>
+                                  : dt == ELY_F32 ? norm_partials_kernel<false, ELY_F32> : norm_partials_kernel<false, -1>;
+        hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(kBlock), 0, s, dtable, (int32_t)table.size(), tiles,
+                           partials);
         check_launch("norm_partials_kernel");
     }
     hipLaunchKernelGGL(norm_final_kernel, dim3(1), dim3(kFinalThreads), 0, s, partials, tiles, max_norm,
