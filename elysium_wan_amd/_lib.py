@@ -12,6 +12,7 @@ import ctypes
 import os
 import threading
 
+import numpy as np
 import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -148,11 +149,30 @@ def ely_tensor(t: torch.Tensor | None, dtype: int | None = None) -> ElyTensor:
     return ElyTensor(t.data_ptr() or None, t.numel(), dtype_code(t) if dtype is None else dtype, 0)
 
 
+_TENSOR_NP = np.dtype([("ptr", "<u8"), ("numel", "<i8"), ("dtype", "<i4"), ("reserved", "<i4")])
+_DTYPE_CODE = {torch.float32: F32, torch.bfloat16: BF16}
+
+
 def tensor_array(ts) -> ctypes.Array:
-    arr = (ElyTensor * max(1, len(ts)))()
-    for i, t in enumerate(ts):
-        arr[i] = t if isinstance(t, ElyTensor) else ely_tensor(t)
-    return arr
+    """An ely_tensor[] over torch tensors (or ElyTensor entries), built
+    column-wise in numpy: a step over a few hundred tensors spends tens of
+    microseconds here, not milliseconds."""
+    n = len(ts)
+    table = np.zeros(max(1, n), dtype=_TENSOR_NP)
+    if n:
+        if any(isinstance(t, ElyTensor) for t in ts):
+            for i, t in enumerate(ts):
+                e = t if isinstance(t, ElyTensor) else ely_tensor(t)
+                table[i] = (e.ptr or 0, e.numel, e.dtype, 0)
+        else:
+            try:
+                table["dtype"][:n] = [_DTYPE_CODE[t.dtype] for t in ts]
+            except KeyError:
+                for t in ts:
+                    dtype_code(t)  # raises the TypeError naming the dtype
+            table["ptr"][:n] = [t.data_ptr() for t in ts]
+            table["numel"][:n] = [t.numel() for t in ts]
+    return (ElyTensor * max(1, n)).from_buffer(table)
 
 
 def stream_ptr(device: torch.device) -> int:

@@ -30,7 +30,7 @@ namespace ely {
 
 // Compile-time tunables (chosen by measurement on MI355X; see the defaults).
 #ifndef ELY_ADAM_TILE
-#define ELY_ADAM_TILE 16384      // elements per AdamW tile
+#define ELY_ADAM_TILE 4096       // elements per AdamW tile (two unrolled block steps)
 #endif
 #ifndef ELY_ADAM_SCHED
 #define ELY_ADAM_SCHED 1         // 0: contiguous tile range per block, 1: interleaved rounds

@@ -189,6 +189,8 @@ class FusedAdamW:
         self.param_groups = [{**group, "params": self.params}]
         self.state: dict = {}
         self._flat_m = self._flat_v = None
+        self._steps = None  # flat fp32 step counters; state[i]["step"] are 0-d views of it
+        self._tables = None  # descriptor arrays kept between steps (_launch_cached)
         self._norm = None  # device ely_norm_result of the last clipped step
         self.working_copies = self._init_copies(working_copy)
 
@@ -228,6 +230,8 @@ class FusedAdamW:
             self._flat_m = torch.zeros(max(total, 1), dtype=torch.float32, device=dev)
             self._flat_v = torch.zeros(max(total, 1), dtype=torch.float32, device=dev)
         self._offs = offs
+        self._steps = torch.zeros(max(len(self.params), 1), dtype=torch.float32)
+        self._tables = None
 
     def _slot(self, i: int, p: torch.Tensor) -> dict:
         st = self.state.get(i)
@@ -236,7 +240,7 @@ class FusedAdamW:
                 self._alloc_state()
             o, n = self._offs[i], p.numel()
             st = self.state[i] = {
-                "step": torch.tensor(0.0, dtype=torch.float32),
+                "step": self._steps[i],  # a 0-d view of the flat counters
                 "exp_avg": self._flat_m[o : o + n].view(p.shape),
                 "exp_avg_sq": self._flat_v[o : o + n].view(p.shape),
             }
@@ -267,54 +271,41 @@ class FusedAdamW:
             raise ValueError(f"{len(grads)} gradients for {len(self.params)} parameters")
         if acc is not None and len(acc) != len(self.params):
             raise ValueError(f"{len(acc)} accumulators for {len(self.params)} parameters")
-        idx, ps, gs, accs, ms, vs, cs, consts = [], [], [], [], [], [], [], []
-        cache: dict = {}
-        for i, p in enumerate(self.params):
-            g = p.grad if grads is None else grads[i]
-            if g is None:
-                continue  # as torch: a parameter without a gradient is not stepped
-            if not p.is_contiguous():
-                raise ValueError(f"{self.recipe} steps contiguous parameters only")
-            if g.shape != p.shape or not g.is_contiguous() or g.device != p.device:
-                raise ValueError(f"{self.recipe}: the gradient of parameter {i} must be contiguous, shaped like it, on its device")
-            if g.dtype not in (torch.float32, torch.bfloat16):
-                raise ValueError(f"{self.recipe}: gradients are float32 or bfloat16, got {g.dtype}")
-            if p.dtype != torch.float32:
-                raise ValueError(f"{self.recipe} trains fp32 parameters, got {p.dtype}")
-            _lib.require_gpu(p, self.recipe)
-            if self.device is None:
-                self.device = p.device
-            elif p.device != self.device:
-                raise ValueError(f"{self.recipe}: parameter {i} is on {p.device}, the optimizer's moments on {self.device}")
-            if acc is not None:
-                a = acc[i]
-                if a is None or a.dtype != torch.float32 or a.shape != p.shape or not a.is_contiguous() or a.device != p.device:
-                    raise ValueError(f"{self.recipe}: the fold accumulator of parameter {i} must be a contiguous float32 tensor shaped like it, on its device")
-                accs.append(a)
-            st = self._slot(i, p)
-            st["step"] += 1
-            t = float(st["step"])
-            c = cache.get(t)
-            if c is None:
-                c = cache[t] = self._consts(t)
-            idx.append(i)
-            ps.append(p)
-            gs.append(g)
-            ms.append(st["exp_avg"])
-            vs.append(st["exp_avg_sq"])
-            cs.append(self.working_copies[i] if self.working_copies is not None else None)
-            consts.append(c)
+        gl = [p.grad for p in self.params] if grads is None else grads
+        # as torch: a parameter without a gradient is not stepped
+        idx = [i for i, g in enumerate(gl) if g is not None]
+        ps = [self.params[i] for i in idx]
+        gs = [gl[i] for i in idx]
+        accs = None if acc is None else [acc[i] for i in idx]
+        self._check_inputs(idx, ps, gs, accs)
         if idx:
+            sts = [self._slot(i, p) for i, p in zip(idx, ps)]
+            # the step counters are views of one flat tensor: one increment for all
+            it = torch.tensor(idx, dtype=torch.int64)
+            self._steps[it] += 1
+            ts = self._steps[it].tolist()
+            ms = [st["exp_avg"] for st in sts]
+            vs = [st["exp_avg_sq"] for st in sts]
+            cs = [self.working_copies[i] if self.working_copies is not None else None for i in idx]
+            per_t = {t: self._consts(t) for t in set(ts)}
+            consts = [per_t[t] for t in ts]
             dev = ps[0].device
-            fold = accs if acc is not None else None
-            streamed = [j for j, m in enumerate(ms) if m.device.type != "cuda"]
-            direct = [j for j, m in enumerate(ms) if m.device.type == "cuda"]
+            fold = accs
+            if self.moments == "host":
+                streamed = [j for j, m in enumerate(ms) if m.device.type != "cuda"]
+                direct = [j for j, m in enumerate(ms) if m.device.type == "cuda"]
+            else:
+                streamed, direct = [], list(range(len(idx)))
             with torch.cuda.device(dev):
                 coef_ptr = self._clip_coef(gs, fold) if self.max_norm is not None else None
                 # one launch per gradient dtype (torch groups by dtype the same way)
                 for gdt in (torch.bfloat16, torch.float32):
                     sel = [j for j in direct if gs[j].dtype == gdt]
-                    if sel:
+                    if not sel:
+                        continue
+                    if len(sel) == len(idx):
+                        self._launch_cached(idx, ps, gs, ms, vs, cs, consts, coef_ptr, fold)
+                    else:
                         self._launch([ps[j] for j in sel], [gs[j] for j in sel], [ms[j] for j in sel],
                                      [vs[j] for j in sel], [cs[j] for j in sel], [consts[j] for j in sel], coef_ptr,
                                      None if fold is None else [fold[j] for j in sel])
@@ -327,6 +318,56 @@ class FusedAdamW:
         if on_param is not None:
             for i in idx:
                 on_param(i)
+
+    _GRAD_DTYPES = (torch.float32, torch.bfloat16)
+
+    def _check_inputs(self, idx, ps, gs, accs) -> None:
+        """The reference's refusals (runtime/optim.py:98-99, 177-178) plus the
+        GPU-side contract, one pass over the stepped parameters."""
+        f32, gdts = torch.float32, self._GRAD_DTYPES
+        for k, (i, p, g) in enumerate(zip(idx, ps, gs)):
+            pd = p.device
+            if p.dtype != f32:
+                raise ValueError(f"{self.recipe} trains fp32 parameters, got {p.dtype}")
+            if not p.is_contiguous():
+                raise ValueError(f"{self.recipe} steps contiguous parameters only")
+            if g.shape != p.shape or not g.is_contiguous() or g.device != pd:
+                raise ValueError(f"{self.recipe}: the gradient of parameter {i} must be contiguous, shaped like it, on its device")
+            if g.dtype not in gdts:
+                raise ValueError(f"{self.recipe}: gradients are float32 or bfloat16, got {g.dtype}")
+            if pd.type != "cuda":
+                _lib.require_gpu(p, self.recipe)
+            if self.device is None:
+                self.device = pd
+            elif pd != self.device:
+                raise ValueError(f"{self.recipe}: parameter {i} is on {pd}, the optimizer's moments on {self.device}")
+            if accs is not None:
+                a = accs[k]
+                if a is None or a.dtype != f32 or a.shape != p.shape or not a.is_contiguous() or a.device != pd:
+                    raise ValueError(f"{self.recipe}: the fold accumulator of parameter {i} must be a contiguous float32 tensor shaped like it, on its device")
+
+    def _launch_cached(self, idx, ps, gs, ms, vs, cs, consts, coef_ptr, accs) -> None:
+        """_launch over every stepped parameter, with the descriptor arrays
+        of the tensors the optimizer owns (moments, working copies) and of
+        the parameters kept from the last step with the same parameters: the
+        parameters' data pointers are compared each step, the moments' and
+        copies' change only through _alloc_state and promote (which drop the
+        cache).  Gradients and accumulators are new every step."""
+        key = tuple(idx)
+        pptrs = [p.data_ptr() for p in ps]
+        t = self._tables
+        if t is None or t["key"] != key or t["pptrs"] != pptrs:
+            copies = [(_lib.ely_tensor(c) if c is not None else _lib.ElyTensor(None, 0, _lib.BF16, 0)) for c in cs]
+            t = self._tables = {
+                "key": key,
+                "pptrs": pptrs,
+                "p": _lib.tensor_array(ps),
+                "m": _lib.tensor_array(ms),
+                "v": _lib.tensor_array(vs),
+                "c": _lib.tensor_array(copies),
+            }
+        self._launch_arrays(len(ps), t["p"], _lib.tensor_array(gs), t["m"], t["v"], t["c"], consts, coef_ptr,
+                            None if accs is None else _lib.tensor_array(accs), ps[0].device)
 
     def _stream_host_moments(self, idx, ps, gs, cs, consts, coef_ptr, accs) -> None:
         """The update of parameters whose moments live in host memory
@@ -434,6 +475,7 @@ class FusedAdamW:
             st = self._slot(i, p)
             st["exp_avg"] = st["exp_avg"].to(p.device)
             st["exp_avg_sq"] = st["exp_avg_sq"].to(p.device)
+            self._tables = None
             self.resident.add(i)
             moved += need
         if moved:
@@ -458,28 +500,27 @@ class FusedAdamW:
         return self._norm.data_ptr() + 12
 
     def _launch(self, ps, gs, ms, vs, cs, consts, coef_ptr, accs=None) -> None:
-        L = _lib.load()
-        dev = ps[0].device
-        stream = _lib.stream_ptr(dev)
-        n = len(ps)
-        carr = (_lib.ElyConsts * n)()
-        for j, c in enumerate(consts):
-            carr[j].c[:] = c
         copies = [(_lib.ely_tensor(c) if c is not None else _lib.ElyTensor(None, 0, _lib.BF16, 0)) for c in cs]
+        self._launch_arrays(len(ps), _lib.tensor_array(ps), _lib.tensor_array(gs), _lib.tensor_array(ms),
+                            _lib.tensor_array(vs), _lib.tensor_array(copies), consts, coef_ptr,
+                            None if accs is None else _lib.tensor_array(accs), ps[0].device)
+
+    def _launch_arrays(self, n, parr, garr, marr, varr, carr, consts, coef_ptr, aarr, dev) -> None:
+        L = _lib.load()
+        stream = _lib.stream_ptr(dev)
+        ctab = np.asarray(consts, dtype=np.float32).reshape(n, -1)
+        if ctab.shape[1] < 8:
+            ctab = np.pad(ctab, ((0, 0), (0, 8 - ctab.shape[1])))
+        ctab = np.ascontiguousarray(ctab)
+        carr_c = (_lib.ElyConsts * n).from_buffer(ctab)
         ws = _lib.workspace(dev, L.ely_adamw_workspace_bytes(n))
         order = _lib.ORDER_HOST if self.order == "host" else _lib.ORDER_TORCH
         wd = int(self.weight_decay != 0)
-        if accs is None:
-            rc = L.ely_adamw_step(
-                _lib.tensor_array(ps), _lib.tensor_array(gs), _lib.tensor_array(ms), _lib.tensor_array(vs),
-                _lib.tensor_array(copies), n, carr, order, wd, coef_ptr, ws.data_ptr(), ws.numel(), stream,
-            )
+        if aarr is None:
+            rc = L.ely_adamw_step(parr, garr, marr, varr, carr, n, carr_c, order, wd, coef_ptr, ws.data_ptr(), ws.numel(), stream)
         else:
-            rc = L.ely_adamw_fold_step(
-                _lib.tensor_array(ps), _lib.tensor_array(accs), _lib.tensor_array(gs), _lib.tensor_array(ms),
-                _lib.tensor_array(vs), _lib.tensor_array(copies), n, carr, order, wd, coef_ptr, ws.data_ptr(),
-                ws.numel(), stream,
-            )
+            rc = L.ely_adamw_fold_step(parr, aarr, garr, marr, varr, carr, n, carr_c, order, wd, coef_ptr, ws.data_ptr(),
+                                       ws.numel(), stream)
         _lib.check(rc, f"{self.recipe} step")
 
     def grad_norm(self) -> torch.Tensor | None:
@@ -533,10 +574,12 @@ class FusedAdamW:
                 if tuple(st[k].shape) != tuple(p.shape):
                     raise ValueError(f"optimizer state {i}.{k} has shape {tuple(st[k].shape)}")
         self.state = {}
+        if self._flat_m is not None:
+            self._steps.zero_()
         for i, st in sd.get("state", {}).items():
             i = int(i)
             slot = self._slot(i, self.params[i])
-            slot["step"] = torch.as_tensor(st["step"], dtype=torch.float32).clone().cpu()
+            slot["step"].copy_(torch.as_tensor(st["step"], dtype=torch.float32).cpu())
             slot["exp_avg"].copy_(st["exp_avg"])
             slot["exp_avg_sq"].copy_(st["exp_avg_sq"])
 
