@@ -4,10 +4,11 @@
 //
 // Work decomposition.  Every tensor is cut into fixed tiles (kAdamTile /
 // kNormTile elements; a tensor's last tile may be short) numbered
-// consecutively across the list.  A launch gets a persistent grid; block
-// (AdamW) or wave (norm) w takes the contiguous tile range
-// [w*T/W, (w+1)*T/W), so every worker streams long contiguous runs of one
-// or a few tensors and the ragged list costs one launch.  A table of tensor
+// consecutively across the list, so the ragged list costs one launch on a
+// persistent grid.  AdamW: in round r block b takes tile r*G + b, so at any
+// moment the whole chip streams one small window of the shard (4,096-element
+// tiles measured best: a smaller window keeps DRAM pages busy).  Norm: wave
+// w takes the contiguous tile range [w*T/W, (w+1)*T/W).  A table of tensor
 // descriptors is staged into the caller's workspace per call.
 //
 // Determinism of (a): a tile's partial sum is a fixed function of its
