@@ -1,5 +1,5 @@
-"""Benchmark of the per-stage update path on one MI355X (config C1 of
-BASELINE.json: one of the 2 pipeline stages of the 2.8B model).
+"""Benchmark of the per-stage update path on one MI355X (benchmark config C1:
+one of the 2 pipeline stages of the 2.8B model).
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
 
@@ -137,7 +137,7 @@ def bench_optimizer(args, device, stream):
 
 
 def _activations(device, rows, cols, copies, seed):
-    """bf16 N(0, 1) with 0.1% of the elements x50 (BASELINE's C1 recipe)."""
+    """bf16 N(0, 1) with 0.1% of the elements x50 (config C1's activation recipe)."""
     gen = torch.Generator(device=device).manual_seed(seed)
     xs = []
     for _ in range(copies):

@@ -1,4 +1,4 @@
-"""BASELINE configs C2 and C3 at their full sizes on one MI355X, checked
+"""Benchmark configs C2 and C3 at their full sizes on one MI355X, checked
 through properties that do not need a CPU pass over billions of elements:
 
 * C2 (the 15.8B model's stage: ~7.9B fp32 elements, p/m/v/g resident in
