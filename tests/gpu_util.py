@@ -46,8 +46,8 @@ def ulp_distance(a: np.ndarray, b: np.ndarray) -> np.ndarray:
 
 
 def activation(shape, seed: int, dtype=torch.bfloat16, outlier_frac=1e-3, outlier_scale=50.0, device="cuda"):
-    """N(0,1) with a seeded fraction of elements scaled (the benchmark configs
-    activation recipe), generated on the CPU so the bytes are reproducible."""
+    """N(0,1) with a seeded fraction of elements scaled (the benchmark
+    configs' activation recipe), generated on the CPU so the bytes are reproducible."""
     g = torch.Generator().manual_seed(seed)
     x = torch.randn(shape, generator=g)
     n = x.numel()
