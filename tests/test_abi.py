@@ -166,3 +166,21 @@ def test_host_constants_equal_the_reference_golden():
         for step in range(int(steps)):
             c = optim.host_consts(lr, (b1, b2), eps, wd, float(step + 1))
             assert [float(x) for x in g[f"{case}_consts"][step][0]] == c
+
+
+def test_a_missing_library_fails_loudly():
+    """No fallback: without libelyhip.so the package raises instead of
+    computing anything another way."""
+    import subprocess
+    import sys
+
+    code = (
+        "import sys; sys.path.insert(0, %r)\n"
+        "from elysium_wan_amd import _lib\n"
+        "try:\n"
+        "    _lib.load('/nonexistent/libelyhip.so')\n"
+        "except RuntimeError as e:\n"
+        "    print('raised', 'build the HIP library' in str(e))\n"
+    ) % ROOT
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
+    assert r.stdout.strip() == "raised True", r.stdout + r.stderr
