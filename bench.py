@@ -391,6 +391,20 @@ def traffic_summary(fetch_dir: str, write_dir: str, command: str) -> None:
     print("\n".join(lines))
 
 
+def hbm_reference(device, stream, n: int = 1 << 28, iters: int = 10):
+    """What the vendor stack itself reaches on this box for mixed read/write
+    traffic, beside the analytic peak: torch's device-to-device copy_ of
+    1 GiB (read 4 B + write 4 B per element) and torch.add(a, b, out=c)
+    (read 8 B + write 4 B), HIP events on the bench stream."""
+    a = torch.empty(n, device=device).normal_()
+    b = torch.empty(n, device=device).normal_()
+    c = torch.empty(n, device=device)
+    copy_ms = time_events(lambda i: c.copy_(a), iters, stream)
+    add_ms = time_events(lambda i: torch.add(a, b, out=c), iters, stream)
+    del a, b, c
+    return {"torch_copy_GBs": 8 * n / copy_ms / 1e6, "torch_add_GBs": 12 * n / add_ms / 1e6, "elements": n}
+
+
 def cpu_context(sample_elems: int = 1 << 25):
     """More CPU reference points on the same host: torch.optim.AdamW
     (foreach=False, the reference's "adamw" CPU path) over a 32M-element
@@ -493,6 +507,9 @@ def main():
             torch.cuda.empty_cache()
             log("host-moments leg")
             extra["host_moments"] = bench_host_moments(device)
+            torch.cuda.empty_cache()
+            log("vendor-kernel reference leg")
+            extra["hbm_reference"] = hbm_reference(device, stream)
             torch.cuda.empty_cache()
     n = o["n_elem"]
     adam_bytes = n * ADAM_BYTES_PER_ELEM
