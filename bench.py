@@ -391,6 +391,60 @@ def traffic_summary(fetch_dir: str, write_dir: str, command: str) -> None:
     print("\n".join(lines))
 
 
+def bench_wire(device, stream, iters: int = 10):
+    """The GPU half of the lossless boundary wires on C1's activation
+    [8, 2048, 2560] bf16 (the host half, zlib, is not timed): the byte-plane
+    split and join (4 B/elem), the e4m3 nibble encode (2 B read + 1 B written)
+    and decode (1 B + 4 B fp32), and the scaled-fp8 wire's exponent recovery
+    plus byte image (2 + 2 B read, 1 B written), rotating through 4 inputs."""
+    from elysium_wan_amd import _lib, fp8
+
+    L = _lib.load()
+    sptr = _lib.stream_ptr(device)
+    rows, cols = 8 * 2048, D_MODEL
+    n = rows * cols
+    copies = 4
+    xs = _activations(device, rows, cols, copies, 11)
+    planes = [torch.empty(2 * n, dtype=torch.uint8, device=device) for _ in range(copies)]
+    back = [torch.empty(n, dtype=torch.bfloat16, device=device) for _ in range(copies)]
+    out = {}
+    ms = time_events(lambda i: _lib.check(L.ely_byteplanes_split(xs[i % copies].data_ptr(), n, 2, planes[i % copies].data_ptr(), sptr), "split"), iters, stream)
+    out["byteplanes_split_GBs"] = 4 * n / ms / 1e6
+    ms = time_events(lambda i: _lib.check(L.ely_byteplanes_join(planes[i % copies].data_ptr(), n, 2, back[i % copies].data_ptr(), sptr), "join"), iters, stream)
+    out["byteplanes_join_GBs"] = 4 * n / ms / 1e6
+    reps = [x.clamp(-448, 448).to(torch.float8_e4m3fn).to(torch.bfloat16) for x in xs]  # e4m3-representable boundaries
+    hi = [torch.empty((n + 1) // 2, dtype=torch.uint8, device=device) for _ in range(copies)]
+    lo = [torch.empty((n + 1) // 2, dtype=torch.uint8, device=device) for _ in range(copies)]
+    f32 = [torch.empty(n, dtype=torch.float32, device=device) for _ in range(2)]
+    nbad = torch.zeros(1, dtype=torch.int64, device=device)
+    ms = time_events(lambda i: _lib.check(L.ely_fp8_nibbles_encode(reps[i % copies].data_ptr(), _lib.BF16, n, hi[i % copies].data_ptr(), lo[i % copies].data_ptr(), nbad.data_ptr(), sptr), "nibbles"), iters, stream)
+    out["nibbles_encode_GBs"] = 3 * n / ms / 1e6
+    ms = time_events(lambda i: _lib.check(L.ely_fp8_nibbles_decode(hi[i % copies].data_ptr(), lo[i % copies].data_ptr(), n, f32[i % 2].data_ptr(), sptr), "nibbles"), iters, stream)
+    out["nibbles_decode_GBs"] = 5 * n / ms / 1e6
+    torch.cuda.synchronize()
+    if int(nbad.item()):
+        raise RuntimeError("bench_wire: an e4m3 cast was not e4m3-representable")
+    del reps, hi, lo, f32
+    bad = torch.zeros(1, dtype=torch.int64, device=device)
+    rts = [fp8.roundtrip(x, "e4m3") for x in xs]
+    ks = [torch.empty(rows, dtype=torch.int32, device=device) for _ in range(copies)]
+    q = torch.empty(n, dtype=torch.uint8, device=device)
+    ws = _lib.workspace(device, L.ely_fp8_recover_workspace_bytes(rows))
+
+    def recover_and_image(i):
+        j = i % copies
+        _lib.check(L.ely_fp8_recover_exp(rts[j].data_ptr(), _lib.BF16, rows, cols, _lib.E4M3, ks[j].data_ptr(), bad.data_ptr(), ws.data_ptr(), ws.numel(), sptr), "recover")
+        _lib.check(L.ely_fp8_quantize_k(rts[j].data_ptr(), _lib.BF16, rows, cols, _lib.E4M3, ks[j].data_ptr(), q.data_ptr(), sptr), "image")
+
+    ms = time_events(recover_and_image, iters, stream)
+    out["scaled_fp8_image_GBs"] = 5 * n / ms / 1e6
+    torch.cuda.synchronize()
+    if int(bad.item()):
+        raise RuntimeError("bench_wire: a recipe round trip was not recoverable")
+    del xs, planes, back, rts, ks, q
+    return out
+
+
 def hbm_reference(device, stream, n: int = 1 << 28, iters: int = 10):
     """What the vendor stack itself reaches on this box for mixed read/write
     traffic, beside the analytic peak: torch's device-to-device copy_ of
@@ -507,6 +561,9 @@ def main():
             torch.cuda.empty_cache()
             log("host-moments leg")
             extra["host_moments"] = bench_host_moments(device)
+            torch.cuda.empty_cache()
+            log("wire leg")
+            extra["wire"] = bench_wire(device, stream)
             torch.cuda.empty_cache()
             log("vendor-kernel reference leg")
             extra["hbm_reference"] = hbm_reference(device, stream)
