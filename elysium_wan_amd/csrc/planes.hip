@@ -8,10 +8,11 @@
 //     of high nibbles and a plane of low nibbles, two nibbles per byte
 //     (element 2i in the high half), and back to fp32.
 //
-// All four are one HBM pass.  The vector paths move 16 elements per lane per
-// step: each plane store is one 16-byte (byte planes) or 8-byte (nibbles)
-// vector, contiguous across the wave.  Shapes the vector path cannot take
-// (unaligned pointers, n not a multiple of 16) run element-wise.
+// All four are one HBM pass.  The vector paths keep every load and store
+// instruction of a wave on one contiguous run (a lane moves one 16-byte
+// vector of elements for the byte planes, 4 codes for the nibble decode).
+// Shapes the vector path cannot take (unaligned pointers, n not a multiple
+// of 16) run element-wise.
 #include <algorithm>
 
 #include "ely_device.hpp"
@@ -31,36 +32,76 @@ static unsigned grid_for(int64_t work, int per_cu = 8) {
 
 // ------------------------------------------------------------ byte planes
 
-// Byte b (little-endian index within an element) of the 16 elements whose
-// bytes are the words w[0 .. 4*ESZ), packed in element order.
-template <int ESZ>
-__device__ __forceinline__ uint4 gather_byte(const uint32_t (&w)[4 * ESZ], int b) {
-    uint32_t o[4] = {0u, 0u, 0u, 0u};
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-        const int byte = e * ESZ + b;  // byte offset within the 16 elements
-        o[e / 4] |= ((w[byte / 4] >> (8 * (byte % 4))) & 0xFFu) << (8 * (e % 4));
+// The vector paths move one 16-byte vector of elements per lane (EPL =
+// 16 / esz elements): a lane's plane share is EPL bytes, so every load and
+// every store instruction of a wave covers one contiguous run.  kPUnroll
+// vectors per lane are loaded before the first is used; all streams are
+// nontemporal.
+constexpr int kPUnroll = 4;
+
+typedef uint32_t pv4 __attribute__((ext_vector_type(4)));
+typedef uint32_t pv2 __attribute__((ext_vector_type(2)));
+#define PL_G1 __attribute__((address_space(1)))
+
+__device__ __forceinline__ pv4 ld16(const void* p) { return __builtin_nontemporal_load((const PL_G1 pv4*)p); }
+__device__ __forceinline__ void st16(void* p, pv4 v) { __builtin_nontemporal_store(v, (PL_G1 pv4*)p); }
+
+// EPL bytes (EPL = 16, 8, 4 or 2) packed little-endian in w[0..EPL/4) (or
+// the low half of w[0] for 2), stored at p.
+template <int EPL>
+__device__ __forceinline__ void st_plane(uint8_t* p, const uint32_t (&w)[4]) {
+    if (EPL == 16) st16(p, pv4{w[0], w[1], w[2], w[3]});
+    else if (EPL == 8) __builtin_nontemporal_store(pv2{w[0], w[1]}, (PL_G1 pv2*)p);
+    else if (EPL == 4) __builtin_nontemporal_store(w[0], (PL_G1 uint32_t*)p);
+    else __builtin_nontemporal_store((uint16_t)w[0], (PL_G1 uint16_t*)p);
+}
+
+template <int EPL>
+__device__ __forceinline__ void ld_plane(const uint8_t* p, uint32_t (&w)[4]) {
+    w[0] = w[1] = w[2] = w[3] = 0;
+    if (EPL == 16) {
+        const pv4 v = ld16(p);
+        w[0] = v[0]; w[1] = v[1]; w[2] = v[2]; w[3] = v[3];
+    } else if (EPL == 8) {
+        const pv2 v = __builtin_nontemporal_load((const PL_G1 pv2*)p);
+        w[0] = v[0]; w[1] = v[1];
+    } else if (EPL == 4) {
+        w[0] = __builtin_nontemporal_load((const PL_G1 uint32_t*)p);
+    } else {
+        w[0] = __builtin_nontemporal_load((const PL_G1 uint16_t*)p);
     }
-    return make_uint4(o[0], o[1], o[2], o[3]);
 }
 
 template <int ESZ>
-__global__ __launch_bounds__(kPBlock) void split_vec_kernel(const uint4* __restrict__ x, int64_t n16,
+__global__ __launch_bounds__(kPBlock) void split_vec_kernel(const uint8_t* __restrict__ x, int64_t nvec,
                                                             uint8_t* __restrict__ planes, int64_t n) {
-    const int64_t stride = (int64_t)gridDim.x * kPBlock;
-    for (int64_t c = (int64_t)blockIdx.x * kPBlock + threadIdx.x; c < n16; c += stride) {
-        uint32_t w[4 * ESZ];
+    constexpr int EPL = 16 / ESZ;
+    const int64_t T = (int64_t)gridDim.x * kPBlock;
+    const int64_t t = (int64_t)blockIdx.x * kPBlock + threadIdx.x;
+    for (int64_t base = t; base < nvec; base += T * kPUnroll) {
+        pv4 v[kPUnroll];
 #pragma unroll
-        for (int j = 0; j < ESZ; ++j) {
-            const uint4 v = x[c * ESZ + j];
-            w[4 * j] = v.x;
-            w[4 * j + 1] = v.y;
-            w[4 * j + 2] = v.z;
-            w[4 * j + 3] = v.w;
+        for (int u = 0; u < kPUnroll; ++u) {
+            const int64_t vi = base + u * T;
+            v[u] = ld16(x + (vi < nvec ? vi : nvec - 1) * 16);
         }
 #pragma unroll
-        for (int j = 0; j < ESZ; ++j)
-            *reinterpret_cast<uint4*>(planes + (int64_t)j * n + c * 16) = gather_byte<ESZ>(w, ESZ - 1 - j);
+        for (int u = 0; u < kPUnroll; ++u) {
+            const int64_t vi = base + u * T;
+            if (vi >= nvec) continue;
+            const uint32_t in[4] = {v[u][0], v[u][1], v[u][2], v[u][3]};
+#pragma unroll
+            for (int j = 0; j < ESZ; ++j) {
+                const int b = ESZ - 1 - j;  // plane j holds byte esz-1-j of every element
+                uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) {
+                    const int byte = e * ESZ + b;
+                    w[e / 4] |= ((in[byte / 4] >> (8 * (byte % 4))) & 0xFFu) << (8 * (e % 4));
+                }
+                st_plane<EPL>(planes + (int64_t)j * n + vi * EPL, w);
+            }
+        }
     }
 }
 
@@ -72,35 +113,37 @@ __global__ __launch_bounds__(kPBlock) void split_any_kernel(const uint8_t* __res
 }
 
 template <int ESZ>
-__global__ __launch_bounds__(kPBlock) void join_vec_kernel(const uint8_t* __restrict__ planes, int64_t n16, int64_t n,
-                                                           uint4* __restrict__ out) {
-    const int64_t stride = (int64_t)gridDim.x * kPBlock;
-    for (int64_t c = (int64_t)blockIdx.x * kPBlock + threadIdx.x; c < n16; c += stride) {
-        uint32_t pl[ESZ][4];
+__global__ __launch_bounds__(kPBlock) void join_vec_kernel(const uint8_t* __restrict__ planes, int64_t nvec, int64_t n,
+                                                           uint8_t* __restrict__ out) {
+    constexpr int EPL = 16 / ESZ;
+    const int64_t T = (int64_t)gridDim.x * kPBlock;
+    const int64_t t = (int64_t)blockIdx.x * kPBlock + threadIdx.x;
+    for (int64_t base = t; base < nvec; base += T * kPUnroll) {
+        uint32_t pl[kPUnroll][ESZ][4];
 #pragma unroll
-        for (int j = 0; j < ESZ; ++j) {
-            const uint4 v = *reinterpret_cast<const uint4*>(planes + (int64_t)j * n + c * 16);
-            pl[j][0] = v.x;
-            pl[j][1] = v.y;
-            pl[j][2] = v.z;
-            pl[j][3] = v.w;
+        for (int u = 0; u < kPUnroll; ++u) {
+            const int64_t vi = base + u * T;
+            const int64_t vc = vi < nvec ? vi : nvec - 1;
+#pragma unroll
+            for (int j = 0; j < ESZ; ++j) ld_plane<EPL>(planes + (int64_t)j * n + vc * EPL, pl[u][j]);
         }
-        uint32_t words[ESZ * 4];
 #pragma unroll
-        for (int q = 0; q < ESZ * 4; ++q) words[q] = 0;
+        for (int u = 0; u < kPUnroll; ++u) {
+            const int64_t vi = base + u * T;
+            if (vi >= nvec) continue;
+            uint32_t words[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
-        for (int j = 0; j < ESZ; ++j) {
-            const int b = ESZ - 1 - j;  // the plane's byte within an element
+            for (int j = 0; j < ESZ; ++j) {
+                const int b = ESZ - 1 - j;
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const uint32_t byte = (pl[j][e / 4] >> (8 * (e % 4))) & 0xFFu;
-                const int off = e * ESZ + b;
-                words[off / 4] |= byte << (8 * (off % 4));
+                for (int e = 0; e < EPL; ++e) {
+                    const uint32_t byte = (pl[u][j][e / 4] >> (8 * (e % 4))) & 0xFFu;
+                    const int off = e * ESZ + b;
+                    words[off / 4] |= byte << (8 * (off % 4));
+                }
             }
+            st16(out + vi * 16, pv4{words[0], words[1], words[2], words[3]});
         }
-#pragma unroll
-        for (int j = 0; j < ESZ; ++j)
-            out[c * ESZ + j] = make_uint4(words[4 * j], words[4 * j + 1], words[4 * j + 2], words[4 * j + 3]);
     }
 }
 
@@ -137,57 +180,68 @@ __device__ __forceinline__ float load_elem(const void* t, int64_t i) {
     return static_cast<const float*>(t)[i];
 }
 
+// Nibble index of element e within its byte: element 2i is the high half.
+__device__ __forceinline__ int nib_shift(int e) { return 8 * ((e / 2) % 4) + ((e & 1) ? 0 : 4); }
+
+// Encode: a lane converts one 16-byte vector of t (8 bf16 or 4 fp32), so its
+// share of each nibble plane is EPL/2 bytes (4 or 2) and every load and
+// store instruction of a wave covers one contiguous run.
 template <bool BF16>
 __global__ __launch_bounds__(kPBlock) void nibbles_encode_kernel(const void* __restrict__ t, int64_t n, int vec,
                                                                  uint8_t* __restrict__ hi, uint8_t* __restrict__ lo,
                                                                  unsigned long long* __restrict__ bad) {
-    const int64_t stride = (int64_t)gridDim.x * kPBlock;
+    constexpr int EPL = BF16 ? 8 : 4;
+    const int64_t T = (int64_t)gridDim.x * kPBlock;
     const int64_t tid = (int64_t)blockIdx.x * kPBlock + threadIdx.x;
     uint32_t nbad = 0;
     int64_t done = 0;  // elements covered by the vector path
     if (vec) {
-        const int64_t n16 = n / 16;
-        for (int64_t c = tid; c < n16; c += stride) {
-            float f[16];
-            if (BF16) {
-                const uint4* p = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(t) + c * 16);
-                const uint4 a = p[0], b = p[1];
-                const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        const int64_t nvec = n / 16 * (16 / EPL);  // whole 16-element groups only
+        const uint8_t* tb = static_cast<const uint8_t*>(t);
+        for (int64_t base = tid; base < nvec; base += T * kPUnroll) {
+            pv4 v[kPUnroll];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    f[2 * j] = bf16_to_f32(w[j] & 0xFFFFu);
-                    f[2 * j + 1] = bf16_to_f32(w[j] >> 16);
-                }
-            } else {
-                const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(t) + c * 16);
+            for (int u = 0; u < kPUnroll; ++u) {
+                const int64_t vi = base + u * T;
+                v[u] = ld16(tb + (vi < nvec ? vi : nvec - 1) * 16);
+            }
+#pragma unroll
+            for (int u = 0; u < kPUnroll; ++u) {
+                const int64_t vi = base + u * T;
+                if (vi >= nvec) continue;
+                float f[EPL];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    const float4 a = p[j];
-                    f[4 * j] = a.x;
-                    f[4 * j + 1] = a.y;
-                    f[4 * j + 2] = a.z;
-                    f[4 * j + 3] = a.w;
+                    if (BF16) {
+                        f[2 * j] = bf16_to_f32(v[u][j] & 0xFFFFu);
+                        f[2 * j + 1] = bf16_to_f32(v[u][j] >> 16);
+                    } else {
+                        f[j] = __uint_as_float(v[u][j]);
+                    }
+                }
+                uint32_t hw = 0u, lw = 0u;
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) {
+                    bool ok;
+                    const uint32_t code = e4m3_exact(f[e], ok);
+                    nbad += ok ? 0u : 1u;
+                    hw |= (code >> 4) << nib_shift(e);
+                    lw |= (code & 0xFu) << nib_shift(e);
+                }
+                if (BF16) {
+                    __builtin_nontemporal_store(hw, (PL_G1 uint32_t*)(hi + vi * 4));
+                    __builtin_nontemporal_store(lw, (PL_G1 uint32_t*)(lo + vi * 4));
+                } else {
+                    __builtin_nontemporal_store((uint16_t)hw, (PL_G1 uint16_t*)(hi + vi * 2));
+                    __builtin_nontemporal_store((uint16_t)lw, (PL_G1 uint16_t*)(lo + vi * 2));
                 }
             }
-            uint32_t hw[2] = {0u, 0u}, lw[2] = {0u, 0u};
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                bool ok;
-                const uint32_t code = e4m3_exact(f[e], ok);
-                nbad += ok ? 0u : 1u;
-                // element 2i -> high half of byte i; byte i sits at bits 8*(i%4) of word i/4
-                const int sh = 8 * ((e / 2) % 4) + ((e & 1) ? 0 : 4);
-                hw[e / 8] |= (code >> 4) << sh;
-                lw[e / 8] |= (code & 0xFu) << sh;
-            }
-            *reinterpret_cast<uint2*>(hi + c * 8) = make_uint2(hw[0], hw[1]);
-            *reinterpret_cast<uint2*>(lo + c * 8) = make_uint2(lw[0], lw[1]);
         }
-        done = n16 * 16;
+        done = nvec * EPL;
     }
     // one output byte (two elements) per thread from `done` on
     const int64_t nbytes = (n + 1) / 2;
-    for (int64_t b = done / 2 + tid; b < nbytes; b += stride) {
+    for (int64_t b = done / 2 + tid; b < nbytes; b += T) {
         uint32_t h = 0, l = 0;
         for (int k = 0; k < 2; ++k) {
             const int64_t i = 2 * b + k;
@@ -207,40 +261,44 @@ __global__ __launch_bounds__(kPBlock) void nibbles_encode_kernel(const void* __r
     if ((threadIdx.x & (kWave - 1)) == 0 && wave_bad) atomicAdd(bad, (unsigned long long)wave_bad);
 }
 
+// Decode: a lane takes 4 codes (2 bytes of each plane) and writes one 16-byte
+// fp32 vector, so every store instruction covers one contiguous 1 KB.
 __global__ __launch_bounds__(kPBlock) void nibbles_decode_kernel(const uint8_t* __restrict__ hi,
                                                                  const uint8_t* __restrict__ lo, int64_t n, int vec,
                                                                  float* __restrict__ out) {
-    const int64_t stride = (int64_t)gridDim.x * kPBlock;
+    const int64_t T = (int64_t)gridDim.x * kPBlock;
     const int64_t tid = (int64_t)blockIdx.x * kPBlock + threadIdx.x;
     int64_t done = 0;
     if (vec) {
-        const int64_t n16 = n / 16;
-        for (int64_t c = tid; c < n16; c += stride) {
-            const uint2 h = *reinterpret_cast<const uint2*>(hi + c * 8);
-            const uint2 l = *reinterpret_cast<const uint2*>(lo + c * 8);
-            const uint32_t hw[2] = {h.x, h.y}, lw[2] = {l.x, l.y};
-            float f[16];
+        const int64_t nq = n / 4;
+        for (int64_t base = tid; base < nq; base += T * kPUnroll) {
+            uint32_t h[kPUnroll], l[kPUnroll];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                // codes of elements 4q .. 4q+3 packed into one word for the instruction
-                uint32_t word = 0;
+            for (int u = 0; u < kPUnroll; ++u) {
+                const int64_t q = base + u * T;
+                const int64_t qc = q < nq ? q : nq - 1;
+                h[u] = __builtin_nontemporal_load((const PL_G1 uint16_t*)(hi + qc * 2));
+                l[u] = __builtin_nontemporal_load((const PL_G1 uint16_t*)(lo + qc * 2));
+            }
+#pragma unroll
+            for (int u = 0; u < kPUnroll; ++u) {
+                const int64_t q = base + u * T;
+                if (q >= nq) continue;
+                uint32_t word = 0;  // codes of elements 4q .. 4q+3, one per byte
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
-                    const int e = 4 * q + k;
-                    const int sh = 8 * ((e / 2) % 4) + ((e & 1) ? 0 : 4);
-                    const uint32_t code = (((hw[e / 8] >> sh) & 0xFu) << 4) | ((lw[e / 8] >> sh) & 0xFu);
-                    word |= code << (8 * k);
+                    const int sh = nib_shift(k);
+                    word |= ((((h[u] >> sh) & 0xFu) << 4) | ((l[u] >> sh) & 0xFu)) << (8 * k);
                 }
-                cvt_pk_f32<kE4M3, false>(word, f[4 * q], f[4 * q + 1]);
-                cvt_pk_f32<kE4M3, true>(word, f[4 * q + 2], f[4 * q + 3]);
+                float a, b, c, d;
+                cvt_pk_f32<kE4M3, false>(word, a, b);
+                cvt_pk_f32<kE4M3, true>(word, c, d);
+                st16(out + q * 4, pv4{__float_as_uint(a), __float_as_uint(b), __float_as_uint(c), __float_as_uint(d)});
             }
-            float4* o = reinterpret_cast<float4*>(out + c * 16);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) o[j] = make_float4(f[4 * j], f[4 * j + 1], f[4 * j + 2], f[4 * j + 3]);
         }
-        done = n16 * 16;
+        done = nq * 4;
     }
-    for (int64_t i = done + tid; i < n; i += stride) {
+    for (int64_t i = done + tid; i < n; i += T) {
         const int sh = (i & 1) ? 0 : 4;
         const uint32_t code = (((uint32_t)hi[i / 2] >> sh) & 0xFu) << 4 | (((uint32_t)lo[i / 2] >> sh) & 0xFu);
         float a, unused;
@@ -268,14 +326,14 @@ int ely_byteplanes_split(const void* x, int64_t n, int32_t esz, uint8_t* planes,
         if (n > INT64_MAX / 8) fail(ELY_EINVAL, "ely_byteplanes_split: n too large");
         hipStream_t s = static_cast<hipStream_t>(stream);
         if (n % 16 == 0 && aligned16(x) && aligned16(planes)) {
-            const int64_t n16 = n / 16;
-            const unsigned g = grid_for(n16);
-            const uint4* xv = static_cast<const uint4*>(x);
+            const int64_t nvec = n * esz / 16;
+            const unsigned g = grid_for((nvec + kPUnroll - 1) / kPUnroll);
+            const uint8_t* xb = static_cast<const uint8_t*>(x);
             switch (esz) {
-                case 1: hipLaunchKernelGGL(split_vec_kernel<1>, dim3(g), dim3(kPBlock), 0, s, xv, n16, planes, n); break;
-                case 2: hipLaunchKernelGGL(split_vec_kernel<2>, dim3(g), dim3(kPBlock), 0, s, xv, n16, planes, n); break;
-                case 4: hipLaunchKernelGGL(split_vec_kernel<4>, dim3(g), dim3(kPBlock), 0, s, xv, n16, planes, n); break;
-                default: hipLaunchKernelGGL(split_vec_kernel<8>, dim3(g), dim3(kPBlock), 0, s, xv, n16, planes, n); break;
+                case 1: hipLaunchKernelGGL(split_vec_kernel<1>, dim3(g), dim3(kPBlock), 0, s, xb, nvec, planes, n); break;
+                case 2: hipLaunchKernelGGL(split_vec_kernel<2>, dim3(g), dim3(kPBlock), 0, s, xb, nvec, planes, n); break;
+                case 4: hipLaunchKernelGGL(split_vec_kernel<4>, dim3(g), dim3(kPBlock), 0, s, xb, nvec, planes, n); break;
+                default: hipLaunchKernelGGL(split_vec_kernel<8>, dim3(g), dim3(kPBlock), 0, s, xb, nvec, planes, n); break;
             }
             check_launch("split_vec_kernel");
         } else {
@@ -295,14 +353,14 @@ int ely_byteplanes_join(const uint8_t* planes, int64_t n, int32_t esz, void* out
         if (n > INT64_MAX / 8) fail(ELY_EINVAL, "ely_byteplanes_join: n too large");
         hipStream_t s = static_cast<hipStream_t>(stream);
         if (n % 16 == 0 && aligned16(out) && aligned16(planes)) {
-            const int64_t n16 = n / 16;
-            const unsigned g = grid_for(n16);
-            uint4* ov = static_cast<uint4*>(out);
+            const int64_t nvec = n * esz / 16;
+            const unsigned g = grid_for((nvec + kPUnroll - 1) / kPUnroll);
+            uint8_t* ob = static_cast<uint8_t*>(out);
             switch (esz) {
-                case 1: hipLaunchKernelGGL(join_vec_kernel<1>, dim3(g), dim3(kPBlock), 0, s, planes, n16, n, ov); break;
-                case 2: hipLaunchKernelGGL(join_vec_kernel<2>, dim3(g), dim3(kPBlock), 0, s, planes, n16, n, ov); break;
-                case 4: hipLaunchKernelGGL(join_vec_kernel<4>, dim3(g), dim3(kPBlock), 0, s, planes, n16, n, ov); break;
-                default: hipLaunchKernelGGL(join_vec_kernel<8>, dim3(g), dim3(kPBlock), 0, s, planes, n16, n, ov); break;
+                case 1: hipLaunchKernelGGL(join_vec_kernel<1>, dim3(g), dim3(kPBlock), 0, s, planes, nvec, n, ob); break;
+                case 2: hipLaunchKernelGGL(join_vec_kernel<2>, dim3(g), dim3(kPBlock), 0, s, planes, nvec, n, ob); break;
+                case 4: hipLaunchKernelGGL(join_vec_kernel<4>, dim3(g), dim3(kPBlock), 0, s, planes, nvec, n, ob); break;
+                default: hipLaunchKernelGGL(join_vec_kernel<8>, dim3(g), dim3(kPBlock), 0, s, planes, nvec, n, ob); break;
             }
             check_launch("join_vec_kernel");
         } else {
@@ -321,8 +379,8 @@ int ely_fp8_nibbles_encode(const void* t, int32_t t_dtype, int64_t n, uint8_t* h
         if (n == 0) return;
         if (!t || !hi || !lo || !bad_dev) fail(ELY_EINVAL, "ely_fp8_nibbles_encode: null pointer");
         hipStream_t s = static_cast<hipStream_t>(stream);
-        const int vec = aligned16(t) && (reinterpret_cast<uintptr_t>(hi) % 8 == 0) && (reinterpret_cast<uintptr_t>(lo) % 8 == 0);
-        const unsigned g = grid_for(std::max<int64_t>(n / 16, 1));
+        const int vec = aligned16(t) && (reinterpret_cast<uintptr_t>(hi) % 4 == 0) && (reinterpret_cast<uintptr_t>(lo) % 4 == 0);
+        const unsigned g = grid_for(std::max<int64_t>(n / 8 / kPUnroll, 1));
         if (t_dtype == ELY_BF16)
             hipLaunchKernelGGL(nibbles_encode_kernel<true>, dim3(g), dim3(kPBlock), 0, s, t, n, vec, hi, lo, bad_dev);
         else
@@ -337,9 +395,9 @@ int ely_fp8_nibbles_decode(const uint8_t* hi, const uint8_t* lo, int64_t n, floa
         if (n == 0) return;
         if (!out || !hi || !lo) fail(ELY_EINVAL, "ely_fp8_nibbles_decode: null pointer");
         hipStream_t s = static_cast<hipStream_t>(stream);
-        const int vec = aligned16(out) && (reinterpret_cast<uintptr_t>(hi) % 8 == 0) && (reinterpret_cast<uintptr_t>(lo) % 8 == 0);
-        hipLaunchKernelGGL(nibbles_decode_kernel, dim3(grid_for(std::max<int64_t>(n / 16, 1))), dim3(kPBlock), 0, s, hi, lo,
-                           n, vec, out);
+        const int vec = aligned16(out) && (reinterpret_cast<uintptr_t>(hi) % 2 == 0) && (reinterpret_cast<uintptr_t>(lo) % 2 == 0);
+        hipLaunchKernelGGL(nibbles_decode_kernel, dim3(grid_for(std::max<int64_t>(n / 4 / kPUnroll, 1))), dim3(kPBlock), 0, s,
+                           hi, lo, n, vec, out);
         check_launch("nibbles_decode_kernel");
     });
 }
