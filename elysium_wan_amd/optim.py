@@ -127,12 +127,19 @@ class FusedAdamW:
     max_norm: clip the global L2 norm of the gradients to this value before
         the update (torch.nn.utils.clip_grad_norm_'s coefficient), fused into
         the same launch; None disables clipping.
-    working_copy: None, True (allocate a bf16 copy of every parameter) or a
-        list of bf16 tensors shaped like the parameters; refreshed with the
-        RNE bf16 cast of the updated parameter (pieces.cast_piece) in the
-        update's own pass.
-    Gradients (p.grad) may be float32 or bfloat16 (the bf16 fold start of
-    runtime/pieces.py:198-203 happens in registers).
+    working_copy: None, True (allocate a bf16 copy of every trainable
+        parameter) or a list of bf16 tensors shaped like the parameters;
+        refreshed with the RNE bf16 cast of the updated parameter
+        (pieces.cast_piece) in the update's own pass.
+    moments: "device" (HBM) or "host" (pinned host memory streamed through
+        the GPU in `chunk`-element pieces over `slots` staging buffers,
+        pipelined unless pipeline=False: HostAdamW's memory contract).
+    Gradients (p.grad, or step(grads=...)) may be float32 or bfloat16 (the
+    bf16 fold start of runtime/pieces.py:198-203 happens in registers);
+    step(acc=...) folds the last microbatch into fp32 accumulators inside the
+    update.  Moments exist for trainable (requires_grad) parameters only,
+    allocated at the first step, as the reference allocates them per stepped
+    parameter.
     """
 
     def __init__(
@@ -218,6 +225,11 @@ class FusedAdamW:
         (runtime/optim.py:121-130), streamed through the GPU at every step."""
         offs, total = [], 0
         for p in self.params:
+            # frozen tensors (a LoRA base) get no slice: they are never stepped
+            # through p.grad, and one stepped anyway gets its own moments (_slot)
+            if not p.requires_grad:
+                offs.append(None)
+                continue
             offs.append(total)
             total += -(-p.numel() // _ALIGN) * _ALIGN
         dev = self.device
@@ -239,10 +251,21 @@ class FusedAdamW:
             if self._flat_m is None:
                 self._alloc_state()
             o, n = self._offs[i], p.numel()
+            if o is None:
+                # a tensor outside the flat layout (no requires_grad) stepped
+                # through grads=: moments of its own, in HBM (taking the
+                # direct path in host mode)
+                m = torch.zeros(p.shape, dtype=torch.float32, device=self.device)
+                v = torch.zeros(p.shape, dtype=torch.float32, device=self.device)
+                if self.moments == "host":
+                    self.resident.add(i)
+            else:
+                m = self._flat_m[o : o + n].view(p.shape)
+                v = self._flat_v[o : o + n].view(p.shape)
             st = self.state[i] = {
                 "step": self._steps[i],  # a 0-d view of the flat counters
-                "exp_avg": self._flat_m[o : o + n].view(p.shape),
-                "exp_avg_sq": self._flat_v[o : o + n].view(p.shape),
+                "exp_avg": m,
+                "exp_avg_sq": v,
             }
         return st
 

@@ -325,3 +325,24 @@ def test_step_on_a_side_thread_and_stream():
         assert torch.equal(x.detach().view(torch.int32), y.detach().view(torch.int32))
     for x, y in zip(a.working_copies, b.working_copies):
         assert torch.equal(x.view(torch.int16), y.view(torch.int16))
+
+
+def test_frozen_parameters_get_no_moments():
+    """A frozen tensor (a LoRA base, runtime/optim.py:97-99) is never
+    stepped through p.grad and takes no moment memory; one stepped anyway
+    through grads= gets moments of its own and the same update."""
+    from elysium_wan_amd import optim
+
+    train = torch.randn(1000, device="cuda").requires_grad_(True)
+    frozen = torch.randn(1 << 22, device="cuda")  # no requires_grad
+    opt = optim.FusedAdamW([train, frozen], lr=1e-3, order="host")
+    train.grad = torch.randn(1000, device="cuda")
+    opt.step()
+    assert opt._flat_m.numel() == 1024 and set(opt.state) == {0}
+    g = torch.randn(1 << 22, device="cuda")
+    twin = frozen.clone()
+    opt.step(grads=[None, g])
+    ref = optim.FusedAdamW([twin], lr=1e-3, order="host")
+    ref.step(grads=[g])
+    assert torch.equal(frozen.view(torch.int32), twin.view(torch.int32))
+    assert torch.equal(opt.state[1]["exp_avg_sq"], ref.state[0]["exp_avg_sq"])
