@@ -554,29 +554,64 @@ __device__ __forceinline__ uint32_t wave_and_u32(uint32_t v) {
     return v;
 }
 
-// Per (row, segment): AND of the exactness masks of the segment's elements,
-// folded into rowmask[row] (set to all candidates beforehand).
-template <int FMT, bool BF16>
+// The segment's elements, one callback per element (lanes past the end make
+// none): vectorized loads, all issued before the first is used, when `vec`
+// (16-byte aligned rows whose length is a multiple of the vector), element
+// loads otherwise.
+template <bool BF16, class F>
+__device__ __forceinline__ void for_seg_elems(const void* t, int64_t row, int64_t cols, int64_t e0, int64_t e1,
+                                              int vec, int lane, F f) {
+    constexpr int EPV = Seg<BF16>::EPV, VPL = Seg<BF16>::VPL, ESZ = BF16 ? 2 : 4;
+    if (vec) {
+        const uint4* tr = reinterpret_cast<const uint4*>(static_cast<const char*>(t) + (row * cols + e0) * ESZ);
+        const int64_t nv = (e1 - e0) / EPV;
+        uint4 buf[VPL];
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) {
+            const int64_t vi = lane + (int64_t)kWave * j;
+            buf[j] = ld_vec(tr + (vi < nv ? vi : nv - 1));
+        }
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) {
+            if (lane + (int64_t)kWave * j >= nv) continue;
+            float v[EPV];
+            unpack<BF16>(buf[j], v);
+#pragma unroll
+            for (int e = 0; e < EPV; ++e) f(v[e]);
+        }
+    } else {
+        for (int64_t e = e0 + lane; e < e1; e += kWave) f(load_x<BF16>(t, row * cols + e));
+    }
+}
+
+// Per (row, segment): the exactness of the candidates over the segment's
+// elements, ANDed into rowmask[row] (all candidates set beforehand).  PHASE
+// 0 tests the base candidate only; PHASE 1 runs only for rows whose base
+// candidate failed somewhere and tests the other four, so a row the base
+// exponent recovers (the common case) costs one test per element.
+template <int FMT, bool BF16, int PHASE>
 __global__ __launch_bounds__(kQBlock) void recover_mask_kernel(const void* __restrict__ t, int64_t rows, int64_t cols,
-                                                               int64_t segs, const uint32_t* __restrict__ rowmax,
+                                                               int64_t segs, int vec,
+                                                               const uint32_t* __restrict__ rowmax,
                                                                uint32_t* __restrict__ rowmask) {
     const int lane = threadIdx.x & (kWave - 1);
     const int64_t gw = (int64_t)blockIdx.x * kWavesPerBlock + wave_uniform(threadIdx.x / kWave);
     const int64_t row = gw / segs, seg = gw % segs;
     if (row >= rows) return;
+    if (PHASE == 1 && (rowmask[row] & 1u)) return;  // the base candidate holds for the whole row
     const int base = scale_exp_from_amax<FMT>(to_f32_bits<BF16>(rowmax[row]));
     const bool fast = base - 2 >= -kFastK && base + 2 <= kFastK;
     const int64_t e0 = seg * kSegElems, e1 = min(e0 + kSegElems, cols);
-    uint32_t mask = 0x1Fu;
-    for (int64_t e = e0 + lane; e < e1; e += kWave) {
-        const float v = load_x<BF16>(t, row * cols + e);
+    uint32_t mask = PHASE == 0 ? 0x1u : 0x1Eu;
+    for_seg_elems<BF16>(t, row, cols, e0, e1, vec, lane, [&](float v) {
 #pragma unroll
-        for (int i = 0; i < 5; ++i)
+        for (int i = (PHASE == 0 ? 0 : 1); i < (PHASE == 0 ? 1 : 5); ++i)
             if ((mask >> i) & 1u)
                 if (!exact_at<FMT, BF16>(v, base + kDeltas[i], fast)) mask &= ~(1u << i);
-    }
+    });
     mask = wave_and_u32(mask);
-    if (lane == 0 && mask != 0x1Fu) atomicAnd(rowmask + row, mask);
+    const uint32_t keep = PHASE == 0 ? ~0x1u : ~0x1Eu;  // the bits this phase does not test
+    if (lane == 0 && (mask | keep) != 0xFFFFFFFFu) atomicAnd(rowmask + row, mask | keep);
 }
 
 // k = base + the first exact offset; a row with none counts as bad and keeps
@@ -602,8 +637,9 @@ __global__ void recover_final_kernel(int64_t rows, const uint32_t* __restrict__ 
 // wire image of a tensor whose exponents recover_exp found.
 template <int FMT, bool BF16>
 __global__ __launch_bounds__(kQBlock) void quant_k_kernel(const void* __restrict__ x, int64_t rows, int64_t cols,
-                                                          int64_t segs, const int32_t* __restrict__ kin,
+                                                          int64_t segs, int vec, const int32_t* __restrict__ kin,
                                                           uint8_t* __restrict__ q) {
+    constexpr int EPV = Seg<BF16>::EPV, VPL = Seg<BF16>::VPL, ESZ = BF16 ? 2 : 4;
     const int lane = threadIdx.x & (kWave - 1);
     const int64_t gw = (int64_t)blockIdx.x * kWavesPerBlock + wave_uniform(threadIdx.x / kWave);
     const int64_t row = gw / segs, seg = gw % segs;
@@ -612,12 +648,48 @@ __global__ __launch_bounds__(kQBlock) void quant_k_kernel(const void* __restrict
     const bool fast = kk >= -kFastK && kk <= kFastK;
     const float s_down = fast ? __uint_as_float((uint32_t)(127 - kk) << 23) : pow2_dtype(-kk, BF16);
     const int64_t e0 = seg * kSegElems, e1 = min(e0 + kSegElems, cols);
-    for (int64_t e = e0 + lane; e < e1; e += kWave) {
-        const float v = load_x<BF16>(x, row * cols + e);
-        uint32_t c;
-        if (fast && __builtin_isfinite(v)) c = cvt_pk_fp8<FMT, false>(v * s_down, 0.0f, 0u) & 0xFFu;
-        else c = quant_sw<FMT, BF16>(v, s_down);
-        q[row * cols + e] = (uint8_t)c;
+    const int64_t base = row * cols;
+    if (vec && fast) {
+        const uint4* xr = reinterpret_cast<const uint4*>(static_cast<const char*>(x) + (base + e0) * ESZ);
+        const int64_t nv = (e1 - e0) / EPV;
+        uint4 buf[VPL];
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) {
+            const int64_t vi = lane + (int64_t)kWave * j;
+            buf[j] = ld_vec(xr + (vi < nv ? vi : nv - 1));
+        }
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) {
+            const int64_t vi = lane + (int64_t)kWave * j;
+            if (vi >= nv) continue;
+            float f[EPV];
+            unpack<BF16>(buf[j], f);
+            uint32_t words[2];
+#pragma unroll
+            for (int h = 0; h < EPV; h += 4) {
+                uint32_t w = 0;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    // non-finite values follow the restatement (NaN, Inf codes)
+                    const uint32_t c = __builtin_isfinite(f[h + e])
+                                           ? cvt_pk_fp8<FMT, false>(f[h + e] * s_down, 0.0f, 0u) & 0xFFu
+                                           : quant_sw<FMT, BF16>(f[h + e], s_down);
+                    w |= c << (8 * e);
+                }
+                words[h / 4] = w;
+            }
+            const int64_t e = e0 + vi * EPV;
+            if (BF16) st_vec2(q + base + e, make_uint2(words[0], words[1]));
+            else st_u32(q + base + e, words[0]);
+        }
+    } else {
+        for (int64_t e = e0 + lane; e < e1; e += kWave) {
+            const float v = load_x<BF16>(x, base + e);
+            uint32_t c;
+            if (fast && __builtin_isfinite(v)) c = cvt_pk_fp8<FMT, false>(v * s_down, 0.0f, 0u) & 0xFFu;
+            else c = quant_sw<FMT, BF16>(v, s_down);
+            q[base + e] = (uint8_t)c;
+        }
     }
 }
 
@@ -937,8 +1009,12 @@ int ely_fp8_recover_exp(const void* t, int32_t t_dtype, int64_t rows, int64_t co
             if (bf16) split_rowmax<true>(t, rows, cols, vec, workspace, rowmax, s);
             else split_rowmax<false>(t, rows, cols, vec, workspace, rowmax, s);
 #define ELY_RECOVER_MASK(F, B)                                                                                    \
-    hipLaunchKernelGGL((recover_mask_kernel<F, B>), dim3(blocks), dim3(kQBlock), 0, s, t, rows, cols, segs,        \
-                       (const uint32_t*)rowmax, rowmask)
+    do {                                                                                                          \
+        hipLaunchKernelGGL((recover_mask_kernel<F, B, 0>), dim3(blocks), dim3(kQBlock), 0, s, t, rows, cols, segs, \
+                           vec, (const uint32_t*)rowmax, rowmask);                                                \
+        hipLaunchKernelGGL((recover_mask_kernel<F, B, 1>), dim3(blocks), dim3(kQBlock), 0, s, t, rows, cols, segs, \
+                           vec, (const uint32_t*)rowmax, rowmask);                                                \
+    } while (0)
             if (fmt == ELY_E4M3) {
                 if (bf16) ELY_RECOVER_MASK(kE4M3, true);
                 else ELY_RECOVER_MASK(kE4M3, false);
@@ -977,8 +1053,10 @@ int ely_fp8_quantize_k(const void* x, int32_t x_dtype, int64_t rows, int64_t col
         if (rows > INT64_MAX / segs) fail(ELY_EINVAL, "too many segments");
         const unsigned blocks = blocks_for_waves(rows * segs);
         const bool bf16 = x_dtype == ELY_BF16;
+        const int vec = (cols % (bf16 ? 8 : 4) == 0) && aligned16(x) &&
+                        (reinterpret_cast<uintptr_t>(q) % (bf16 ? 8 : 4) == 0);
 #define ELY_QK(F, B) \
-    hipLaunchKernelGGL((quant_k_kernel<F, B>), dim3(blocks), dim3(kQBlock), 0, s, x, rows, cols, segs, k, q)
+    hipLaunchKernelGGL((quant_k_kernel<F, B>), dim3(blocks), dim3(kQBlock), 0, s, x, rows, cols, segs, vec, k, q)
         if (fmt == ELY_E4M3) {
             if (bf16) ELY_QK(kE4M3, true);
             else ELY_QK(kE4M3, false);

@@ -89,3 +89,33 @@ def test_gradient_scale_values_survive_the_wire():
         assert torch.equal(planes.decode(payload, shape), q)
         with pytest.raises(ValueError):
             planes.encode_scaled_fp8(x, fmt)
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+@pytest.mark.parametrize("shape", [(5, 1001), (1, 100_000), (64, 8200)])
+def test_recover_exp_on_odd_and_long_rows_equals_the_oracle(oracle, fmt, shape):
+    """Element-wise rows (1001 is no multiple of the vector), one long row
+    over many segments, and rows past the register path: the exponents and
+    the byte image equal the oracle's, and rows off the fp8 grid are
+    refused."""
+    from elysium_wan_amd import _lib, fp8
+
+    x = activation(shape, seed=shape[1] % 97)
+    rt = fp8.roundtrip(x, fmt)
+    say("recover odd/long", fmt, shape)
+    k = fp8.recover_exp(rt, fmt)
+    ok, bad = oracle.recover_exp(bits(rt), fmt)
+    assert bad == 0 and np.array_equal(bits(k).reshape(-1), ok)
+    q = torch.empty(shape, dtype=torch.uint8, device="cuda")
+    L = _lib.load()
+    _lib.check(L.ely_fp8_quantize_k(rt.data_ptr(), _lib.BF16, shape[0], shape[1], _lib.FMT[fmt], k.data_ptr(), q.data_ptr(), _lib.stream_ptr(rt.device)), "quantize_k")
+    # the byte image with the recovered exponents: each product is exact
+    xf = oracle.bf16_bits_to_f32(bits(rt)).reshape(shape).astype(np.float64)
+    kk = bits(k).reshape(-1).astype(np.float64)
+    oq = oracle.fp8_encode((xf * np.exp2(-kk)[:, None]).astype(np.float32), fmt)
+    assert np.array_equal(q.cpu().numpy(), oq)
+    # one value with a 6-bit mantissa in row 0: no candidate exponent makes it fp8
+    off = rt.clone()
+    off[0, shape[1] // 2] = (1 + 2.0**-6) * 2.0 ** int(bits(k).reshape(-1)[0])
+    with pytest.raises(ValueError, match="recipe mismatch"):
+        fp8.recover_exp(off, fmt)
