@@ -11,7 +11,9 @@ the deterministic grad-norm launch plus the fused clip + AdamW launch.
 `value` is params/s of the whole timed step.  The fp8 boundary codec is
 timed beside it on C1's activation [8, 2048, 2560] (e4m3) and gradient
 (e5m2), per-row scaling, rotating through enough copies that no launch
-reads from the 256 MB MALL.
+reads from the 256 MB MALL, and swept over config C4 ([16, 4096, 8192]
+Student-t activation and N(0, 1e-5) gradient; e4m3 and e5m2; per-row and
+per-tensor) with relative error and digests of the exact bytes and scales.
 
 Prints one JSON line (rank 0):
   roofline      -- the fused AdamW kernel: algorithmic bytes per launch
@@ -71,7 +73,10 @@ def make_shard(device):
 
 
 def time_events(fn, iters, stream):
-    """Average duration (ms) of fn() over iters launches, HIP events on `stream`."""
+    """Average duration (ms) of fn() over iters launches, HIP events on
+    `stream`, after one untimed call (code-object load, first-touch)."""
+    fn(0)
+    torch.cuda.synchronize()
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
     for i in range(iters):
@@ -83,20 +88,28 @@ def time_events(fn, iters, stream):
 
 
 def bench_optimizer(args, device, stream):
+    params, grads = make_shard(device)
+    log(f"C1 shard: {len(params)} tensors, {sum(p.numel() for p in params)} elements")
+    return measure_shard(params, grads, device, stream, args.steps, args.warmup)
+
+
+def measure_shard(params, grads, device, stream, steps, warmup):
+    """Times optimizer steps of one shard (grad-norm launch + fused clip +
+    AdamW launch, bf16 working copy out) by wall clock around `steps` whole
+    steps, then each of the two launches alone with HIP events on the
+    launch stream."""
     from elysium_wan_amd import _lib, optim
 
-    params, grads = make_shard(device)
     n_elem = sum(p.numel() for p in params)
-    log(f"C1 shard: {len(params)} tensors, {n_elem} elements")
     opt = optim.FusedAdamW(params, lr=LR, betas=BETAS, eps=EPS, weight_decay=WD, order="host", max_norm=MAX_NORM, working_copy=True)
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         opt.step(grads=grads)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for _ in range(steps):
         opt.step(grads=grads)
     torch.cuda.synchronize()
-    step_s = (time.perf_counter() - t0) / args.steps
+    step_s = (time.perf_counter() - t0) / steps
 
     # Per-kernel durations: the same two launches through the C ABI, with HIP
     # events on the launch stream between them.
@@ -117,7 +130,7 @@ def bench_optimizer(args, device, stream):
     def norm(_):
         _lib.check(L.ely_grad_norm(garr, n, MAX_NORM, res.data_ptr(), nws.data_ptr(), nws.numel(), sptr), "norm")
 
-    iters = max(args.steps, 5)
+    iters = max(steps, 5)
     per_step = [optim.host_consts(LR, BETAS, EPS, WD, base_step + 1 + i) for i in range(iters)]
 
     def adam(i):
@@ -127,13 +140,122 @@ def bench_optimizer(args, device, stream):
 
     norm_ms = time_events(norm, iters, stream)
     adam_ms = time_events(adam, iters, stream)
-    return {
+    out = {
         "n_elem": n_elem,
         "step_s": step_s,
         "norm_ms": norm_ms,
         "adam_ms": adam_ms,
         "grad_norm": float(opt.grad_norm()),
+        "clip_coef": float(opt._norm[12:16].view(torch.float32)),
     }
+    del opt
+    return out
+
+
+def _shard_rates(o, grad_bytes, tensors):
+    """Rates of one measure_shard result: AdamW reads p, g, m, v and writes
+    p, m, v and the bf16 copy (26 + grad_bytes B/elem); the norm reads g."""
+    n = o["n_elem"]
+    adam_gbs = n * (26 + grad_bytes) / o["adam_ms"] / 1e6
+    return {
+        "tensors": tensors,
+        "n_elem": n,
+        "step_ms": o["step_s"] * 1e3,
+        "params_per_s": n / o["step_s"],
+        "adamw_ms": o["adam_ms"],
+        "adamw_GBs": adam_gbs,
+        "adamw_frac": adam_gbs / HBM_PEAK_GBS,
+        "grad_norm_ms": o["norm_ms"],
+        "grad_norm_GBs": n * grad_bytes / o["norm_ms"] / 1e6,
+        "clip_coef": o["clip_coef"],
+    }
+
+
+def config_shard(name, device):
+    """The other optimizer configs at their full sizes, generated on the
+    device (seeded):
+    C0 -- 3 GPT blocks at d = 768 + 2 vectors (38 tensors, 21,265,152
+          elements), fp32 grads N(0, 1e-3);
+    C2 -- 25 GPT blocks at d = 5120 (300 tensors, 7,865,984,000 elements),
+          fp32 grads N(0, 1e-4) with 3 tensors (1%) x100 so the clip triggers;
+    C3 -- 1,000 vectors of 6,144 interleaved with 100 matrices of
+          6,144 x 10,240 (1,100 tensors, 6,297,600,000 elements), bf16 grads
+          Student-t (df = 3) x 1e-4.
+    Params are N(0, 0.02) fp32 throughout."""
+    gen = torch.Generator(device=device).manual_seed({"c0": 10, "c2": 12, "c3": 13}[name])
+    if name == "c0":
+        shapes, gdt, scale, hot = block_shapes(768) * 3 + [(768,), (768,)], torch.float32, 1e-3, set()
+    elif name == "c2":
+        shapes, gdt, scale, hot = block_shapes(5120) * 25, torch.float32, 1e-4, {30, 150, 270}
+    else:
+        shapes, gdt, scale, hot = [], torch.bfloat16, 1e-4, set()
+        for _ in range(100):
+            shapes += [(6144,)] * 10 + [(6144, 10240)]
+    params, grads = [], []
+    for i, sh in enumerate(shapes):
+        params.append(torch.empty(sh, device=device).normal_(0.0, 0.02, generator=gen).requires_grad_(True))
+        if name == "c3":
+            z = torch.empty(sh, device=device).normal_(generator=gen)
+            c = torch.zeros(sh, device=device)
+            for _ in range(3):
+                c.add_(torch.empty(sh, device=device).normal_(generator=gen).square_())
+            grads.append(z.div_(c.div_(3.0).sqrt_()).mul_(scale).to(gdt))
+            del z, c
+        else:
+            g = torch.empty(sh, device=device).normal_(0.0, scale * (100.0 if i in hot else 1.0), generator=gen)
+            grads.append(g if gdt == torch.float32 else g.to(gdt))
+    return params, grads
+
+
+def bench_configs(device, stream, names=("c0", "c2", "c3"), steps=3, warmup=1):
+    """The fused step over configs C0, C2 and C3 at their full sizes: the
+    same launches as the headline C1 measurement, on a small
+    launch-bound shard (C0), a 126 GB resident shard whose clip triggers
+    (C2) and a 1,100-tensor ragged shard (C3)."""
+    out = {}
+    for name in names:
+        params, grads = config_shard(name, device)
+        log(f"{name} shard: {len(params)} tensors, {sum(p.numel() for p in params)} elements")
+        gbytes = grads[0].element_size()
+        o = measure_shard(params, grads, device, stream, steps, warmup)
+        out[name] = _shard_rates(o, gbytes, len(params))
+        del params, grads
+        torch.cuda.empty_cache()
+    return out
+
+
+def bench_placement(device, stream, hold_gib=150):
+    """C1's step with its shard allocated while `hold_gib` GiB of other device
+    memory are held, so that its pages come from another physical range
+    than a fresh process's first allocation. The kernel and the bytes are
+    the same; what changes is the DRAM side (the average EA read latency of
+    the AdamW launch, measured with rocprofv3 --pmc through
+    --placement-probe)."""
+    hold = torch.empty(hold_gib << 30, dtype=torch.uint8, device=device)
+    params, grads = make_shard(device)
+    o = measure_shard(params, grads, device, stream, 3, 1)
+    del params, grads, hold
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    r = _shard_rates(o, 2, 192)
+    r["held_GiB"] = hold_gib
+    return r
+
+
+def placement_probe(device, mode):
+    """Three C1 optimizer steps, for a rocprofv3 --pmc run: in a fresh
+    process ("fresh") or with the shard allocated while 150 GiB are held
+    ("hold150")."""
+    from elysium_wan_amd import optim
+
+    hold = torch.empty(150 << 30, dtype=torch.uint8, device=device) if mode == "hold150" else None
+    params, grads = make_shard(device)
+    opt = optim.FusedAdamW(params, lr=LR, betas=BETAS, eps=EPS, weight_decay=WD, order="host", max_norm=MAX_NORM, working_copy=True)
+    for _ in range(3):
+        opt.step(grads=grads)
+    torch.cuda.synchronize()
+    log(f"placement probe {mode}: 3 steps done")
+    del hold
 
 
 def _activations(device, rows, cols, copies, seed):
@@ -149,23 +271,51 @@ def _activations(device, rows, cols, copies, seed):
     return xs
 
 
-def bench_codec(device, stream, rows, cols, copies, iters=20, per_tensor=False):
+def _c4_inputs(device, seed):
+    """Config C4's two inputs of shape [16, 4096, 8192] bf16: the activation,
+    Student-t (df = 3) with 0.01% of the elements set to +-1e4, and the
+    gradient, N(0, 1e-5)."""
+    gen = torch.Generator(device=device).manual_seed(seed)
+    shape = (16 * 4096, 8192)
+    z = torch.empty(shape, device=device).normal_(generator=gen)
+    c = torch.zeros(shape, device=device)
+    for _ in range(3):
+        c.add_(torch.empty(shape, device=device).normal_(generator=gen).square_())
+    z.div_(c.div_(3.0).sqrt_())
+    del c
+    n = z.numel()
+    idx = torch.randint(0, n, (n // 10000,), generator=gen, device=device)
+    sign = torch.randint(0, 2, idx.shape, generator=gen, device=device).float() * 2 - 1
+    z.view(-1)[idx] = 1e4 * sign
+    act = z.to(torch.bfloat16)
+    del z
+    grad = torch.empty(shape, device=device).normal_(0.0, 1e-5, generator=gen).to(torch.bfloat16)
+    return {"activation": act, "gradient": grad}
+
+
+def bench_codec(device, stream, rows, cols, copies, iters=20, per_tensor=False, xs=None, fmts=("e4m3", "e5m2"), stats=False):
     """Quantize and dequantize (bf16 <-> fp8, per-row or per-tensor) of a
     [rows, cols] activation, rotating through `copies` inputs so that
-    launches stream from HBM rather than the 256 MB MALL."""
+    launches stream from HBM rather than the 256 MB MALL. With `stats`, the
+    round trip of the first input is also reported, outside the timed
+    region: relative L2 error of dequantize(quantize(x)) against x, the
+    range of the exponents k, and SHA-256 digests of the fp8 bytes and k."""
+    import hashlib
+
     from elysium_wan_amd import _lib
 
     L = _lib.load()
     sptr = _lib.stream_ptr(device)
     n = rows * cols
-    xs = _activations(device, rows, cols, copies, 7)
+    xs = xs if xs is not None else _activations(device, rows, cols, copies, 7)
+    copies = len(xs)
     qs = [torch.empty(rows, cols, dtype=torch.uint8, device=device) for _ in range(copies)]
-    ks = [torch.empty(rows, dtype=torch.int32, device=device) for _ in range(copies)]
-    outs = [torch.empty(rows, cols, dtype=torch.bfloat16, device=device) for _ in range(copies)]
     qr, qc = (1, n) if per_tensor else (rows, cols)
+    ks = [torch.empty(qr, dtype=torch.int32, device=device) for _ in range(copies)]
+    outs = [torch.empty(rows, cols, dtype=torch.bfloat16, device=device) for _ in range(copies)]
     ws = _lib.workspace(device, L.ely_fp8_workspace_bytes(qr, qc, _lib.BF16))
     out = {}
-    for fmt in ("e4m3", "e5m2"):
+    for fmt in fmts:
         f = _lib.FMT[fmt]
 
         def quant(i, f=f):
@@ -186,7 +336,37 @@ def bench_codec(device, stream, rows, cols, copies, iters=20, per_tensor=False):
             "dequantize_ms": d_ms,
             "dequantize_GBs": n * CODEC_BYTES_PER_ELEM / d_ms / 1e6,
         }
+        if stats:
+            quant(0)
+            deq(0)
+            torch.cuda.synchronize()
+            x64 = xs[0].double()
+            err = float((outs[0].double() - x64).norm() / x64.norm())
+            del x64
+            out[fmt].update({
+                "rel_l2_error": err,
+                "k_min": int(ks[0].min()),
+                "k_max": int(ks[0].max()),
+                "fp8_sha256": hashlib.sha256(qs[0].cpu().numpy().tobytes()).hexdigest(),
+                "k_sha256": hashlib.sha256(ks[0].cpu().numpy().tobytes()).hexdigest(),
+            })
     del xs, qs, outs
+    return out
+
+
+def bench_c4(device, stream, iters=10):
+    """Config C4's sweep: {activation, gradient} x {e4m3, e5m2} x {per-row
+    (8,192 wide), per-tensor}, encode -> decode, with timings, relative
+    error, exponent range and digests of the exact fp8 bytes and scales."""
+    inputs = _c4_inputs(device, 44)
+    rows, cols = inputs["activation"].shape
+    out = {}
+    for name, x in inputs.items():
+        out[name] = {}
+        for per_tensor in (False, True):
+            out[name]["per_tensor" if per_tensor else "per_row"] = bench_codec(device, stream, rows, cols, 2, iters=iters, per_tensor=per_tensor, xs=[x, x.clone()], stats=True)
+            torch.cuda.empty_cache()
+    del inputs
     return out
 
 
@@ -510,9 +690,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-codec", action="store_true", help="skip the fp8 codec leg")
-    ap.add_argument("--no-extra", action="store_true", help="skip the fused-fold and host-moment legs")
+    ap.add_argument("--no-extra", action="store_true", help="skip the fused-fold, host-moment, wire, vendor-reference and C0/C2/C3 legs")
     ap.add_argument("--codec", choices=("c1", "c4", "all"), default="all", help="activation sizes of the codec leg")
     ap.add_argument("--no-optimizer", action="store_true", help="skip the optimizer leg (profiling the other legs alone)")
+    ap.add_argument("--no-configs", action="store_true", help="skip the C0/C2/C3 optimizer leg (--no-extra skips it too)")
+    ap.add_argument("--placement-probe", choices=("fresh", "hold150"), help="three C1 steps only (for rocprofv3 --pmc)")
     ap.add_argument("--cpu-sample", type=int, default=256 * 1024 * 1024)
     ap.add_argument("--profile-pass", action="store_true", help="launch each measured kernel a few times, untimed, for rocprofv3 --pmc runs")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"), help="summarize two --pmc runs of --profile-pass into profiles/")
@@ -534,13 +716,17 @@ def main():
         with torch.cuda.stream(stream):
             profile_pass(device)
         return
+    if args.placement_probe:
+        with torch.cuda.stream(stream):
+            placement_probe(device, args.placement_probe)
+        return
     with torch.cuda.stream(stream):
         if args.no_optimizer:
             log("codec-only run")
-            for size in ("c1", "c4"):
-                if args.codec in (size, "all"):
-                    rows, cols, copies = (8 * 2048, D_MODEL, 8) if size == "c1" else (16 * 4096, 8192, 2)
-                    print(json.dumps({size: bench_codec(device, stream, rows, cols, copies, iters=10)}), flush=True)
+            if args.codec in ("c1", "all"):
+                print(json.dumps({"c1": bench_codec(device, stream, 8 * 2048, D_MODEL, 8, iters=10)}), flush=True)
+            if args.codec in ("c4", "all"):
+                print(json.dumps({"c4": bench_c4(device, stream)}), flush=True)
             return
         log("optimizer leg")
         o = bench_optimizer(args, device, stream)
@@ -552,8 +738,7 @@ def main():
                 codec["c1_per_row"] = bench_codec(device, stream, 8 * 2048, D_MODEL, 8)
                 torch.cuda.empty_cache()
             if args.codec in ("c4", "all"):
-                codec["c4_per_row"] = bench_codec(device, stream, 16 * 4096, 8192, 2, iters=10)
-                codec["c4_per_tensor"] = bench_codec(device, stream, 16 * 4096, 8192, 2, iters=10, per_tensor=True)
+                codec["c4"] = bench_c4(device, stream)
                 torch.cuda.empty_cache()
         if not args.no_extra:
             log("fold leg")
@@ -568,6 +753,11 @@ def main():
             log("vendor-kernel reference leg")
             extra["hbm_reference"] = hbm_reference(device, stream)
             torch.cuda.empty_cache()
+            if not args.no_configs:
+                log("configs leg (C0, C2, C3)")
+                extra["configs"] = bench_configs(device, stream)
+            log("placement leg (C1 allocated while 150 GiB are held)")
+            extra["c1_placement"] = bench_placement(device, stream)
     n = o["n_elem"]
     adam_bytes = n * ADAM_BYTES_PER_ELEM
     achieved = adam_bytes / (o["adam_ms"] * 1e-3) / 1e9

@@ -141,6 +141,55 @@ def test_unaligned_views_and_grid_sizes_do_not_move_a_bit(oracle):
     assert np.array_equal(results[0][1:].view(np.uint32), pf.view(np.uint32))
 
 
+_SPECIAL = [0.0, -0.0, 1e-45, -1e-45, 1.1754942e-38, 1e-30, 1e19, -1e19, 1.9e19, 2e19, 1e20, 3.4e38, -3.4e38,
+            float("inf"), float("-inf"), float("nan")]
+
+
+def _nan_as_nan_equal(a: np.ndarray, b: np.ndarray) -> bool:
+    """fp32 bits equal, except that any NaN equals any NaN (a NaN made inside
+    the arithmetic takes the device's default sign and payload)."""
+    na, nb = np.isnan(a), np.isnan(b)
+    return bool(np.array_equal(na, nb) and np.array_equal(a[~na].view(np.uint32), b[~nb].view(np.uint32)))
+
+
+@pytest.mark.parametrize("gdtype", [torch.float32, torch.bfloat16])
+def test_extreme_values_follow_the_oracle(oracle, gdtype):
+    """Zeros of both signs, subnormals, gradients whose square overflows fp32
+    (v = inf, so sqrt(v) = inf and m / d = 0), +-inf and NaN, in params and
+    grads, scattered over a tensor that has both a vector body and an
+    element tail: three steps with weight decay equal the oracle, NaN as NaN,
+    and the bf16 working copy too."""
+    from elysium_wan_amd import optim
+
+    rng = np.random.default_rng(5)
+    n = 3 * 4096 + 13
+    p0 = (rng.standard_normal(n) * 0.02).astype(np.float32)
+    pick = rng.choice(n, 200, replace=False)
+    p0[pick] = rng.choice(np.array(_SPECIAL, dtype=np.float32), 200)
+    gsteps = []
+    for _ in range(3):
+        g = (rng.standard_normal(n) * 1e-3).astype(np.float32)
+        pick = rng.choice(n, 400, replace=False)
+        g[pick] = rng.choice(np.array(_SPECIAL, dtype=np.float32), 400)
+        gsteps.append(torch.from_numpy(g).to(gdtype))
+    dev = torch.from_numpy(p0.copy()).cuda().requires_grad_(True)
+    say("adamw extreme values", gdtype)
+    opt = optim.FusedAdamW([dev], lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, order="host", working_copy=True)
+    for g in gsteps:
+        opt.step(grads=[g.cuda()])
+    torch.cuda.synchronize()
+    p, m, v = p0.copy(), np.zeros(n, np.float32), np.zeros(n, np.float32)
+    cp = np.zeros(n, dtype=np.uint16)
+    for t, g in enumerate(gsteps):
+        oracle.adamw_host(p, bits(g), m, v, oracle.host_adamw_consts(1e-3, (0.9, 0.95), 1e-8, 0.1, t + 1), True, 1.0, cp)
+    assert np.isnan(p).any() and np.isinf(v).any() and (np.isinf(p).any() or np.abs(p).max() > 1e38)
+    assert _nan_as_nan_equal(bits(dev.detach()), p)
+    assert _nan_as_nan_equal(bits(opt.state[0]["exp_avg"]), m)
+    assert _nan_as_nan_equal(bits(opt.state[0]["exp_avg_sq"]), v)
+    wc = bits(opt.working_copies[0]).astype(np.uint32) << 16
+    assert _nan_as_nan_equal(wc.view(np.float32), (cp.astype(np.uint32) << 16).view(np.float32))
+
+
 def test_torch_order_is_within_one_ulp_of_torch_adamw():
     """optim.build("adamw") against torch.optim.AdamW (foreach, the GPU
     default) on the same GPU, 5 steps, weight decay on."""
