@@ -171,6 +171,23 @@ class FusedAdamW:
         self._staging = None  # host mode: per-step streaming buffers, streams and events
         self.order = order
         self.recipe = "adamw-host" if order == "host" else "adamw"
+        if order == "torch":
+            # the "adamw" recipe is torch.optim.AdamW (runtime/optim.py:50-51):
+            # its argument checks and messages, hyperparameters first
+            # (TORCH/optim/adamw.py -> adam.py:58-67), then the empty list
+            # (TORCH/optim/optimizer.py); HostAdamW checks neither
+            if not 0.0 <= lr:
+                raise ValueError(f"Invalid learning rate: {lr}")
+            if not 0.0 <= eps:
+                raise ValueError(f"Invalid epsilon value: {eps}")
+            if not 0.0 <= betas[0] < 1.0:
+                raise ValueError(f"Invalid beta parameter at index 0: {betas[0]}")
+            if not 0.0 <= betas[1] < 1.0:
+                raise ValueError(f"Invalid beta parameter at index 1: {betas[1]}")
+            if not 0.0 <= weight_decay:
+                raise ValueError(f"Invalid weight_decay value: {weight_decay}")
+            if not self.params:
+                raise ValueError("optimizer got an empty parameter list")
         devices = set()
         for p in self.params:
             # a frozen tensor never has a gradient and is never stepped (runtime/optim.py:98-99)

@@ -154,6 +154,31 @@ def test_optimizer_bookkeeping_matches_the_reference():
     assert optim.ADAMW == {"betas": (0.9, 0.95), "eps": 1e-8, "weight_decay": 0.0}
 
 
+def test_recipes_refuse_what_the_reference_refuses():
+    """"adamw" is torch.optim.AdamW in the reference (runtime/optim.py:50-51):
+    the same ValueError, message for message, as torch's own AdamW on the
+    same arguments, including an empty parameter list (the ZeRO-1 owner of
+    no tensor, integration/test_zero1_empty_shard.py).  "adamw-host" checks
+    neither, as HostAdamW: over [] it builds, steps nothing and round-trips
+    an empty state."""
+    from elysium_wan_amd import optim
+
+    p = [torch.zeros(1, requires_grad=True)]
+    for params, kw in ((p, {"lr": -1.0}), (p, {"lr": float("nan")}), (p, {"lr": 1e-3, "eps": -1.0}),
+                       (p, {"lr": 1e-3, "betas": (1.0, 0.9)}), (p, {"lr": 1e-3, "betas": (0.9, -0.1)}),
+                       (p, {"lr": 1e-3, "weight_decay": -0.1}), ([], {"lr": 1e-3}), ([], {"lr": -1.0})):
+        with pytest.raises(ValueError) as want:
+            torch.optim.AdamW(params, **{**optim.ADAMW, **kw})
+        with pytest.raises(ValueError) as got:
+            optim.build("adamw", params, **kw)
+        assert str(got.value) == str(want.value)
+    host = optim.build("adamw-host", [], 1e-3)
+    host.step()
+    sd = host.state_dict()
+    assert sd["state"] == {} and sd["param_groups"][0]["params"] == [] and sd["param_groups"][0]["moments"] == "host"
+    host.load_state_dict(sd)
+
+
 def test_host_constants_equal_the_reference_golden():
     """The package's own constant code (not the oracle's) against the
     constants HostAdamW.step computed in the reference."""
