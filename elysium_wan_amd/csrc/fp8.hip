@@ -2,11 +2,15 @@
 //
 // quantize (fp8.py:28-49): per row, k = frexp(amax|x|).exponent - ebias and
 // q = fp8(x * 2^-k).  Three launch shapes:
-//   * rows that fit a wavefront's registers (<= 64 lanes x 16 vectors of
-//     16 bytes: 8192 bf16 / 4096 fp32 columns, 16-byte aligned): one wave per
-//     row, the row is read once into VGPRs, |x|max is a butterfly over the
-//     wave, and codes are written from the same registers: one HBM read and
-//     one write per element (3 B/elem for bf16 -> fp8).
+//   * rows that fit registers (<= 64 lanes x 16 vectors of 16 bytes: 8192
+//     bf16 / 4096 fp32 columns, 16-byte aligned): the row is read once into
+//     VGPRs, |x|max is a butterfly over the wave, and codes are written from
+//     the same registers: one HBM read and one write per element (3 B/elem
+//     for bf16 -> fp8).  Rows of up to 6 vectors per lane take one wave;
+//     longer ones are shared by a block's 4 waves, whose maxima meet in LDS,
+//     so that each wave holds at most 4 vectors and more rows stream at once.
+//     Each wave issues its loads one vector per lane at a time: fewer bytes
+//     in flight per CU keep the memory latency, and the bandwidth, up.
 //   * longer rows (per-tensor scaling is rows = 1): the row is cut into
 //     2048-element segments.  A first launch reduces the row's |x|max into
 //     at most 8,192 partial maxima (each wave strides over its row's
@@ -23,7 +27,7 @@
 // dtype, software conversion), uniformly per row.
 //
 // dequantize (fp8.py:52-53): out = float(q) * 2^k in the output dtype, the
-// codes taken as one flat array (a wave's 4,096 codes may span rows), 8 codes
+// codes taken as one flat array (a wave's 1,024 codes may span rows), 8 codes
 // per lane per step for bf16 output (4 for fp32) so every store instruction
 // covers a contiguous 1 KB; roundtrip (fp8.py:56-63) fuses both.
 #include <algorithm>
@@ -33,12 +37,22 @@
 
 #pragma clang fp contract(off)
 
+#ifndef ELY_DEQ_SEG
+#define ELY_DEQ_SEG 1024  // dequantize: codes per wave segment
+#endif
+#ifndef ELY_DEQ_BATCH
+#define ELY_DEQ_BATCH 0  // dequantize: vectors per lane per load batch (0: the whole segment at once)
+#endif
+#ifndef ELY_Q_BATCH
+#define ELY_Q_BATCH 1  // register paths: vectors per lane per load batch (0: the whole row at once)
+#endif
+
 namespace ely {
 
 constexpr int kQBlock = 256;                   // 4 waves, one row (or segment) each
 constexpr int kWavesPerBlock = kQBlock / kWave;
 constexpr int64_t kSegElems = 2048;            // split-path segment, elements
-constexpr int64_t kDeqSegCodes = 4096;         // dequantize segment, codes
+constexpr int64_t kDeqSegCodes = ELY_DEQ_SEG;  // dequantize segment, codes
 constexpr int kFastK = 110;                    // |k| bound of the instruction path
 
 // ----------------------------------------------------------- element helpers
@@ -256,20 +270,27 @@ __global__ __launch_bounds__(kQBlock) void quant_rows_kernel(const void* __restr
     if (row >= rows) return;  // whole waves leave; the kernel has no block barrier
     const int64_t nvec = cols / EPV;
     const uint4* xr = reinterpret_cast<const uint4*>(static_cast<const char*>(x) + row * cols * ESZ);
-    // every load is issued before the first is used: lanes past the row's end
-    // load its last vector (in bounds) and zero it afterwards
+    // the row's loads go out in batches of QB vectors per lane, each batch's
+    // loads back to back: lanes past the row's end load its last vector (in
+    // bounds) and zero it afterwards
+    constexpr int QB = (ELY_Q_BATCH <= 0 || ELY_Q_BATCH > VPL) ? VPL : ELY_Q_BATCH;
     uint4 buf[VPL];
-#pragma unroll
-    for (int j = 0; j < VPL; ++j) {
-        const int64_t vi = lane + (int64_t)kWave * j;
-        buf[j] = ld_vec(xr + (vi < nvec ? vi : nvec - 1));
-    }
     uint32_t amax = 0;
 #pragma unroll
-    for (int j = 0; j < VPL; ++j) {
-        const int64_t vi = lane + (int64_t)kWave * j;
-        if (vi >= nvec) buf[j] = make_uint4(0u, 0u, 0u, 0u);
-        amax = vec_absmax<BF16>(buf[j], amax);
+    for (int j0 = 0; j0 < VPL; j0 += QB) {
+#pragma unroll
+        for (int j = j0; j < j0 + QB && j < VPL; ++j) {
+            const int64_t vi = lane + (int64_t)kWave * j;
+            buf[j] = ld_vec(xr + (vi < nvec ? vi : nvec - 1));
+        }
+#pragma unroll
+        for (int j = j0; j < j0 + QB && j < VPL; ++j) {
+            const int64_t vi = lane + (int64_t)kWave * j;
+            if (vi >= nvec) buf[j] = make_uint4(0u, 0u, 0u, 0u);
+            amax = vec_absmax<BF16>(buf[j], amax);
+        }
+        // the next batch is issued only once this one has arrived
+        if (QB < VPL) __builtin_amdgcn_sched_barrier(0);
     }
     amax = wave_max_u32(amax);
     const RowScale rs = row_scale<FMT>(to_f32_bits<BF16>(amax), BF16, BF16);
@@ -280,6 +301,69 @@ __global__ __launch_bounds__(kQBlock) void quant_rows_kernel(const void* __restr
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
         const int64_t vi = lane + (int64_t)kWave * j;
+        if (vi < nvec) {
+            uint32_t words[2];
+            quant_vec_fast<FMT, BF16>(buf[j], rs, words, orow ? orow + vi * 16 : nullptr);
+            if (qr) {
+                if (BF16) st_vec2(qr + vi * 8, make_uint2(words[0], words[1]));
+                else st_u32(qr + vi * 4, words[0]);
+            }
+        }
+    }
+}
+
+// Long rows: the block's waves share one row, each wave a contiguous run of
+// kWave * VPLW vectors; the waves' |x|max meet in LDS across one barrier.
+// The host launches exactly one block per row, so every wave of a block
+// reaches the barrier.
+template <int FMT, bool BF16, int VPLW>
+__global__ __launch_bounds__(kQBlock) void quant_block_row_kernel(const void* __restrict__ x, int64_t cols,
+                                                                  uint8_t* __restrict__ q, int32_t* __restrict__ k,
+                                                                  void* __restrict__ out) {
+    constexpr int EPV = BF16 ? 8 : 4;
+    constexpr int ESZ = BF16 ? 2 : 4;
+    constexpr int QB = (ELY_Q_BATCH <= 0 || ELY_Q_BATCH > VPLW) ? VPLW : ELY_Q_BATCH;
+    __shared__ uint32_t wmax[kWavesPerBlock];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int w = wave_uniform(threadIdx.x / kWave);
+    const int64_t row = blockIdx.x;
+    const int64_t nvec = cols / EPV;
+    const int64_t v0 = (int64_t)w * kWave * VPLW;
+    const uint4* xr = reinterpret_cast<const uint4*>(static_cast<const char*>(x) + row * cols * ESZ);
+    uint4 buf[VPLW];
+    uint32_t amax = 0;
+#pragma unroll
+    for (int j0 = 0; j0 < VPLW; j0 += QB) {
+#pragma unroll
+        for (int j = j0; j < j0 + QB && j < VPLW; ++j) {
+            const int64_t vi = v0 + lane + (int64_t)kWave * j;
+            buf[j] = ld_vec(xr + (vi < nvec ? vi : nvec - 1));
+        }
+#pragma unroll
+        for (int j = j0; j < j0 + QB && j < VPLW; ++j) {
+            const int64_t vi = v0 + lane + (int64_t)kWave * j;
+            if (vi >= nvec) buf[j] = make_uint4(0u, 0u, 0u, 0u);
+            amax = vec_absmax<BF16>(buf[j], amax);
+        }
+        if (QB < VPLW) __builtin_amdgcn_sched_barrier(0);
+    }
+    amax = wave_max_u32(amax);
+    if (lane == 0) wmax[w] = amax;
+    __syncthreads();
+    amax = wmax[0];
+#pragma unroll
+    for (int i = 1; i < kWavesPerBlock; ++i) amax = max(amax, wmax[i]);
+    const RowScale rs = row_scale<FMT>(to_f32_bits<BF16>(amax), BF16, BF16);
+    if (threadIdx.x == 0 && k) k[row] = rs.k;
+    if (!rs.fast) {
+        const int64_t e0 = min(v0 * EPV, cols), e1 = min((v0 + (int64_t)kWave * VPLW) * EPV, cols);
+        return quant_slow<FMT, BF16>(x, row * cols, e0, e1, rs, q, out, lane);
+    }
+    uint8_t* qr = q ? q + row * cols : nullptr;
+    char* orow = out ? static_cast<char*>(out) + row * cols * ESZ : nullptr;
+#pragma unroll
+    for (int j = 0; j < VPLW; ++j) {
+        const int64_t vi = v0 + lane + (int64_t)kWave * j;
         if (vi < nvec) {
             uint32_t words[2];
             quant_vec_fast<FMT, BF16>(buf[j], rs, words, orow ? orow + vi * 16 : nullptr);
@@ -426,11 +510,12 @@ __global__ __launch_bounds__(kQBlock) void quant_split_kernel(const void* __rest
 
 // Codes in rows whose length is a multiple of 16 (and 16-byte aligned
 // buffers) are dequantized as one flat array: wave w takes codes
-// [4096 w, 4096 w + 4096), which may span rows.  A lane takes CPL codes per
-// step (8 for bf16 output, 4 for fp32), so that each store instruction of a
-// wave writes one contiguous 1 KB run; every lane issues all its loads
-// before the first is used, and each CPL-code vector lies in one row and
-// looks up that row's exponent.
+// [S w, S w + S) (S = kDeqSegCodes), which may span rows.  A lane takes CPL
+// codes per step (8 for bf16 output, 4 for fp32), so that each store
+// instruction of a wave writes one contiguous 1 KB run; every lane issues
+// its loads (all of them, or batches of ELY_DEQ_BATCH) before the first is
+// used, and each CPL-code vector lies in one row and looks up that row's
+// exponent.  Short segments (many short-lived waves) measured fastest.
 template <int FMT, bool BF16OUT, bool IDX32>
 __global__ __launch_bounds__(kQBlock) void dequant_flat_kernel(const uint8_t* __restrict__ q,
                                                                const int32_t* __restrict__ k, int64_t n,
@@ -442,67 +527,73 @@ __global__ __launch_bounds__(kQBlock) void dequant_flat_kernel(const uint8_t* __
     const int64_t e0 = gw * kDeqSegCodes;
     if (e0 >= n) return;
     const int64_t nv = min(kDeqSegCodes, n - e0) / CPL;
+    constexpr int DB = (ELY_DEQ_BATCH <= 0 || ELY_DEQ_BATCH > VPL) ? VPL : ELY_DEQ_BATCH;
     uint32_t buf[VPL][CPL / 4];
 #pragma unroll
-    for (int j = 0; j < VPL; ++j) {
-        const int64_t vi = lane + (int64_t)kWave * j;
-        const uint8_t* src = q + e0 + (vi < nv ? vi : nv - 1) * CPL;
-        if (CPL == 8) {
-            const uint2 w = ld_vec2(src);
-            buf[j][0] = w.x;
-            buf[j][CPL / 4 - 1] = w.y;
-        } else {
-            buf[j][0] = ld_u32(src);
-        }
-    }
+    for (int j0 = 0; j0 < VPL; j0 += DB) {
 #pragma unroll
-    for (int j = 0; j < VPL; ++j) {
-        const int64_t vi = lane + (int64_t)kWave * j;
-        if (vi >= nv) continue;
-        const int64_t e = e0 + vi * CPL;
-        const int64_t row = IDX32 ? (int64_t)((uint32_t)e / (uint32_t)cols) : e / cols;
-        const int kk = k[row];
-        if (kk >= -kFastK && kk <= kFastK) {
-            const float s_up = __uint_as_float((uint32_t)(127 + kk) << 23);
-            float o[CPL];
-#pragma unroll
-            for (int h = 0; h < CPL / 4; ++h) {
-                float a, b, c, d;
-                cvt_pk_f32<FMT, false>(buf[j][h], a, b);
-                cvt_pk_f32<FMT, true>(buf[j][h], c, d);
-                o[4 * h] = a * s_up;
-                o[4 * h + 1] = b * s_up;
-                o[4 * h + 2] = c * s_up;
-                o[4 * h + 3] = d * s_up;
-            }
-            if (BF16OUT) {
-                uint32_t b[8];
-#pragma unroll
-                for (int t = 0; t < 8; ++t) {
-                    // an fp8 NaN is the only non-exact value the instruction path sees
-                    const float v = o[t];
-                    b[t] = v != v ? 0x7FC0u : fast_bf16_bits(v);
-                }
-                st_vec(static_cast<uint16_t*>(out) + e,
-                       make_uint4(b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16), b[6] | (b[7] << 16)));
+        for (int j = j0; j < j0 + DB && j < VPL; ++j) {
+            const int64_t vi = lane + (int64_t)kWave * j;
+            const uint8_t* src = q + e0 + (vi < nv ? vi : nv - 1) * CPL;
+            if (CPL == 8) {
+                const uint2 w = ld_vec2(src);
+                buf[j][0] = w.x;
+                buf[j][CPL / 4 - 1] = w.y;
             } else {
-                st_vec(static_cast<float*>(out) + e, make_uint4(__float_as_uint(o[0]), __float_as_uint(o[1]),
-                                                                __float_as_uint(o[2]), __float_as_uint(o[3])));
-            }
-        } else {
-            // the restatement of torch's arithmetic (|k| > 110), code by code
-            const float s_up = pow2_dtype(kk, BF16OUT);
-#pragma unroll 1
-            for (int t = 0; t < CPL; ++t) {
-                const float o = dequant_sw<FMT, BF16OUT>((buf[j][t / 4] >> (8 * (t % 4))) & 0xFFu, s_up);
-                if (BF16OUT) static_cast<uint16_t*>(out)[e + t] = (uint16_t)f32_to_bf16(o);
-                else static_cast<float*>(out)[e + t] = o;
+                buf[j][0] = ld_u32(src);
             }
         }
+#pragma unroll
+        for (int j = j0; j < j0 + DB && j < VPL; ++j) {
+            const int64_t vi = lane + (int64_t)kWave * j;
+            if (vi >= nv) continue;
+            const int64_t e = e0 + vi * CPL;
+            const int64_t row = IDX32 ? (int64_t)((uint32_t)e / (uint32_t)cols) : e / cols;
+            const int kk = k[row];
+            if (kk >= -kFastK && kk <= kFastK) {
+                const float s_up = __uint_as_float((uint32_t)(127 + kk) << 23);
+                float o[CPL];
+#pragma unroll
+                for (int h = 0; h < CPL / 4; ++h) {
+                    float a, b, c, d;
+                    cvt_pk_f32<FMT, false>(buf[j][h], a, b);
+                    cvt_pk_f32<FMT, true>(buf[j][h], c, d);
+                    o[4 * h] = a * s_up;
+                    o[4 * h + 1] = b * s_up;
+                    o[4 * h + 2] = c * s_up;
+                    o[4 * h + 3] = d * s_up;
+                }
+                if (BF16OUT) {
+                    uint32_t b[8];
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) {
+                        // an fp8 NaN is the only non-exact value the instruction path sees
+                        const float v = o[t];
+                        b[t] = v != v ? 0x7FC0u : fast_bf16_bits(v);
+                    }
+                    st_vec(static_cast<uint16_t*>(out) + e, make_uint4(b[0] | (b[1] << 16), b[2] | (b[3] << 16),
+                                                                       b[4] | (b[5] << 16), b[6] | (b[7] << 16)));
+                } else {
+                    st_vec(static_cast<float*>(out) + e, make_uint4(__float_as_uint(o[0]), __float_as_uint(o[1]),
+                                                                    __float_as_uint(o[2]), __float_as_uint(o[3])));
+                }
+            } else {
+                // the restatement of torch's arithmetic (|k| > 110), code by code
+                const float s_up = pow2_dtype(kk, BF16OUT);
+#pragma unroll 1
+                for (int t = 0; t < CPL; ++t) {
+                    const float o = dequant_sw<FMT, BF16OUT>((buf[j][t / 4] >> (8 * (t % 4))) & 0xFFu, s_up);
+                    if (BF16OUT) static_cast<uint16_t*>(out)[e + t] = (uint16_t)f32_to_bf16(o);
+                    else static_cast<float*>(out)[e + t] = o;
+                }
+            }
+        }
+        // the next batch is issued only once this one has been stored
+        if (DB < VPL) __builtin_amdgcn_sched_barrier(0);
     }
 }
 
-// Any other shape: one wave per (row, 4096-code segment), element by element.
+// Any other shape: one wave per (row, kDeqSegCodes-code segment), element by element.
 template <int FMT, bool BF16OUT>
 __global__ __launch_bounds__(kQBlock) void dequant_any_kernel(const uint8_t* __restrict__ q,
                                                               const int32_t* __restrict__ k, int64_t rows,
@@ -758,7 +849,11 @@ static unsigned blocks_for_waves(int64_t waves) {
     return (unsigned)b;
 }
 
+// Vectors per lane of the register paths: a wave per row up to kMaxWaveVpl,
+// a block of kWavesPerBlock waves per row above (the block's loads in flight
+// per row stay the same, and more rows stream at once).
 constexpr int kVplChoices[] = {1, 2, 3, 4, 5, 6, 8, 10, 12, 16};
+constexpr int kMaxWaveVpl = 6;
 
 template <int FMT, bool BF16, int VPL>
 static void launch_rows(const void* x, int64_t rows, int64_t cols, uint8_t* q, int32_t* k, void* out, hipStream_t s) {
@@ -777,10 +872,6 @@ static void dispatch_rows(int vpl, const void* x, int64_t rows, int64_t cols, ui
         case 4: return launch_rows<FMT, BF16, 4>(x, rows, cols, q, k, out, s);
         case 5: return launch_rows<FMT, BF16, 5>(x, rows, cols, q, k, out, s);
         case 6: return launch_rows<FMT, BF16, 6>(x, rows, cols, q, k, out, s);
-        case 8: return launch_rows<FMT, BF16, 8>(x, rows, cols, q, k, out, s);
-        case 10: return launch_rows<FMT, BF16, 10>(x, rows, cols, q, k, out, s);
-        case 12: return launch_rows<FMT, BF16, 12>(x, rows, cols, q, k, out, s);
-        case 16: return launch_rows<FMT, BF16, 16>(x, rows, cols, q, k, out, s);
         default: fail(ELY_EINVAL, "internal: no register path for this row length");
     }
 }
@@ -837,6 +928,18 @@ static void quantize_impl(const void* x, int64_t rows, int64_t cols, uint8_t* q,
     }
     const int32_t dt = BF16 ? ELY_BF16 : ELY_F32;
     const int vpl = rows_vpl(cols, dt, x, q, out);
+    if (vpl > kMaxWaveVpl) {
+        // one block per row: kWavesPerBlock waves of ceil(vpl / kWavesPerBlock) vectors per lane
+        if (rows > 0x7FFFFFFF) fail(ELY_EINVAL, "fp8 quantize: too many rows for one launch");
+        switch ((vpl + kWavesPerBlock - 1) / kWavesPerBlock) {
+            case 2: hipLaunchKernelGGL((quant_block_row_kernel<FMT, BF16, 2>), dim3((unsigned)rows), dim3(kQBlock), 0, s, x, cols, q, k, out); break;
+            case 3: hipLaunchKernelGGL((quant_block_row_kernel<FMT, BF16, 3>), dim3((unsigned)rows), dim3(kQBlock), 0, s, x, cols, q, k, out); break;
+            case 4: hipLaunchKernelGGL((quant_block_row_kernel<FMT, BF16, 4>), dim3((unsigned)rows), dim3(kQBlock), 0, s, x, cols, q, k, out); break;
+            default: fail(ELY_EINVAL, "internal: no block-row path for this row length");
+        }
+        check_launch("quant_block_row_kernel");
+        return;
+    }
     if (vpl) return dispatch_rows<FMT, BF16>(vpl, x, rows, cols, q, k, out, s);
     const int64_t epv = BF16 ? 8 : 4;
     const int vec = (cols % epv == 0) && aligned16(x) && (!out || aligned16(out)) &&

@@ -54,7 +54,8 @@ def bits_t(t: torch.Tensor) -> torch.Tensor:
 @pytest.mark.parametrize("dname", ["bf16", "f32"])
 @pytest.mark.parametrize(
     "shape",
-    [(4, 1024, 768), (16, 2560), (7, 8192), (3, 4096 + 8), (5, 1000), (3, 7), (2, 1), (9, 16384 + 24), (1, 3 * 65536 + 5)],
+    [(4, 1024, 768), (16, 2560), (7, 8192), (3, 4096 + 8), (6, 4096), (5, 3200), (5, 1000), (3, 7), (2, 1), (9, 16384 + 24),
+     (1, 3 * 65536 + 5)],
 )
 def test_quantize_dequantize_roundtrip_equal_the_oracle(oracle, fmt, dname, shape):
     say("fp8 vs oracle", fmt, dname, shape)
@@ -108,6 +109,44 @@ def test_extreme_rows_equal_torch_on_the_gpu(oracle):
                     assert np.array_equal(bits(d), bits(dref))
                 else:
                     assert f32_equal(bits(d), bits(dref))
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+@pytest.mark.parametrize("dname", ["bf16", "f32"])
+@pytest.mark.parametrize("cols", [3200, 4104, 8192])
+def test_extreme_rows_on_the_block_row_path(fmt, dname, cols):
+    """Rows long enough to be shared by a block's waves (more than 6 vectors
+    per lane), each taking another branch: an ordinary row, a NaN, an Inf,
+    a row whose 2^-k leaves the instruction path (|x|max ~ 1e38), a tiny
+    row (|x|max ~ 1e-38), an all-zero row, and a row whose maximum sits in
+    the last wave's part.  k, bytes and the decode equal the reference's
+    torch expressions (model/fp8.py:28-53) on this GPU."""
+    from elysium_wan_amd import fp8
+
+    tdt = {"e4m3": torch.float8_e4m3fn, "e5m2": torch.float8_e5m2}[fmt]
+    x = activation((7, cols), seed=cols % 97, dtype=torch.float32).float()
+    x[1, cols // 3] = float("nan")
+    x[2, cols - 5] = float("-inf")
+    x[3] *= 5e35
+    x[4] *= 1e-39
+    x[5] = 0.0
+    x[6, cols - 1] = 3000.0
+    x = x.to(DT[dname])
+    say("fp8 block-row extremes", fmt, dname, cols)
+    _, eb = fp8.FORMATS[fmt]
+    amax = x.abs().amax(dim=-1, keepdim=True)
+    _, e = torch.frexp(amax)
+    kref = torch.where(amax > 0, (e - eb).to(torch.int32), torch.zeros_like(e, dtype=torch.int32))
+    qref = (x * torch.exp2((-kref).to(x.dtype))).to(tdt)
+    dref = qref.to(x.dtype) * torch.exp2(kref.to(x.dtype))
+    q, k = fp8.quantize(x, fmt)
+    assert torch.equal(k, kref)
+    assert np.array_equal(bits(q), bits(qref))
+    d = fp8.dequantize(q, k, x.dtype)
+    if dname == "bf16":
+        assert np.array_equal(bits(d), bits(dref))
+    else:
+        assert f32_equal(bits(d), bits(dref))
 
 
 @pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
