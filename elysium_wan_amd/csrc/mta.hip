@@ -51,6 +51,9 @@ namespace ely {
 #ifndef ELY_ADAM_UNROLL
 #define ELY_ADAM_UNROLL 2        // 2,048-element block steps a thread keeps in flight (1, 2, 4 or 8)
 #endif
+#ifndef ELY_ADAM_HALVES
+#define ELY_ADAM_HALVES 2        // 1,024-element halves per block step (1 or 2)
+#endif
 #ifndef ELY_ADAM_BPC
 #define ELY_ADAM_BPC 1           // AdamW blocks per compute unit
 #endif
@@ -335,28 +338,31 @@ __device__ __forceinline__ void st_stream(ELY_GLOBAL T* p, T v) {
 #endif
 }
 
-// The vector path's unit of work is a block step of kStep = 2,048 elements.
-// Thread t owns the quads [4t, 4t+4) and [1024+4t, 1024+4t+4) of the step,
-// so each load or store instruction of a wave covers one contiguous 1 KB
-// (fp32) or 512 B (bf16) run: every request is a full, aligned line, and the
-// two halves of a step never share a line.  ELY_ADAM_UNROLL steps are loaded
-// before the first is updated, keeping 14 * U 16- or 8-byte loads per thread
-// in flight.
-constexpr int64_t kStep = (int64_t)kBlock * 8;
+// The vector path's unit of work is a block step of kStep = kHalves * 1,024
+// elements.  Thread t owns the quads [4t, 4t+4), [1024+4t, 1024+4t+4), ...
+// of the step, one per 1,024-element half, so each load or store
+// instruction of a wave covers one contiguous 1 KB (fp32) or 512 B (bf16)
+// run: every request is a full, aligned line, and the halves of a step never
+// share a line.  ELY_ADAM_UNROLL steps are loaded before the first is
+// updated, keeping 7 * kHalves * U 16- or 8-byte loads per thread in flight.
+constexpr int kHalves = ELY_ADAM_HALVES;
+constexpr int64_t kHalf = (int64_t)kBlock * 4;
+constexpr int64_t kStep = kHalf * kHalves;
+static_assert(kAdamTile % kStep == 0, "an AdamW tile is a whole number of block steps");
 
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 template <bool BF16G>
 struct Quad2 {
-    f32x4 p[2], m[2], v[2];
-    float g[8];
+    f32x4 p[kHalves], m[kHalves], v[kHalves];
+    float g[4 * kHalves];
 };
 
 template <bool BF16G, bool FOLD>
 __device__ __forceinline__ void quad_load(const AdamDesc& d, int64_t i, Quad2<BF16G>& Q) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const int64_t e = i + h * (kStep / 2);
+    for (int h = 0; h < kHalves; ++h) {
+        const int64_t e = i + h * kHalf;
         Q.p[h] = ld_stream(gp(reinterpret_cast<const f32x4*>(d.p + e)));
         Q.m[h] = ld_stream(gp(reinterpret_cast<const f32x4*>(d.m + e)));
         Q.v[h] = ld_stream(gp(reinterpret_cast<const f32x4*>(d.v + e)));
@@ -385,7 +391,7 @@ __device__ __forceinline__ void quad_update_store(const AdamDesc& d, int64_t i, 
                                                   const ely_adamw_consts& c, float coef) {
     using Op = AdamOp<BF16G, ORDER, WD, CLIP, FOLD>;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < kHalves; ++h) {
         float p[4], m[4], v[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -394,7 +400,7 @@ __device__ __forceinline__ void quad_update_store(const AdamDesc& d, int64_t i, 
             v[j] = Q.v[h][j];
             Op::elem(p[j], Q.g[4 * h + j], m[j], v[j], c, coef);
         }
-        const int64_t e = i + h * (kStep / 2);
+        const int64_t e = i + h * kHalf;
         st_stream(gp(reinterpret_cast<f32x4*>(d.p + e)), f32x4{p[0], p[1], p[2], p[3]});
         st_stream(gp(reinterpret_cast<f32x4*>(d.m + e)), f32x4{m[0], m[1], m[2], m[3]});
         st_stream(gp(reinterpret_cast<f32x4*>(d.v + e)), f32x4{v[0], v[1], v[2], v[3]});
