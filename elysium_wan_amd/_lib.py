@@ -39,6 +39,7 @@ EXPORTS = (
     "ely_fp8_roundtrip",
     "ely_fp8_recover_workspace_bytes",
     "ely_fp8_recover_exp",
+    "ely_fp8_recover_image",
     "ely_fp8_quantize_k",
     "ely_cast_bf16",
     "ely_fold_add",
@@ -103,6 +104,7 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
         L.ely_fp8_recover_workspace_bytes.restype = I64
         L.ely_fp8_recover_workspace_bytes.argtypes = [I64]
         L.ely_fp8_recover_exp.argtypes = [P, I32, I64, I64, I32, P, P, P, I64, P]
+        L.ely_fp8_recover_image.argtypes = [P, I32, I64, I64, I32, P, P, P, P, I64, P]
         L.ely_fp8_quantize_k.argtypes = [P, I32, I64, I64, I32, P, P, P]
         L.ely_cast_bf16.argtypes = [P, P, I64, P]
         L.ely_fold_add.argtypes = [P, P, I32, I64, P]

@@ -784,6 +784,139 @@ __global__ __launch_bounds__(kQBlock) void quant_k_kernel(const void* __restrict
     }
 }
 
+// ---------------------------------------------- recover + image, registers
+
+// exact_at for a non-finite element of a row whose candidates are all on the
+// instruction path (|c| <= 112, so 2^+-c is finite and nonzero in either
+// dtype): the restatement turns NaN into a NaN code (never equal) and Inf
+// into a NaN code for e4m3 (no Inf there) or back into the same Inf for e5m2.
+template <int FMT>
+__device__ __forceinline__ bool exact_nonfinite(float v) {
+    return FMT == kE5M2 && __builtin_isinf(v);
+}
+
+// The first exact candidate of a row outside the instruction path, element
+// by element through the restatement, or -1 (the recover_mask_kernel test).
+template <int FMT, bool BF16>
+__device__ __forceinline__ int recover_slow_row(const void* t, int64_t row, int64_t cols, int base, int lane) {
+#pragma unroll 1
+    for (int i = 0; i < 5; ++i) {
+        bool ok = true;
+#pragma unroll 1
+        for (int64_t e = lane; e < cols; e += kWave)
+            ok = ok && exact_at<FMT, BF16>(load_x<BF16>(t, row * cols + e), base + kDeltas[i], false);
+        if (wave_and_u32(ok ? 1u : 0u)) return i;
+    }
+    return -1;
+}
+
+// One wave per row held in registers (rows of up to kWave * VPL vectors,
+// 16-byte aligned): |x|max, the base exponent, the candidates in the
+// reference's order, each one wave vote over the registers (the base
+// candidate is the only one a recipe round trip usually needs), then, when
+// q is given, the row's wire image from the same registers with the exponent
+// found: one read of t and one write of q per element.  A row with no exact
+// candidate counts as bad and keeps base + 2 (fp8.py:82-93).
+template <int FMT, bool BF16, int VPL>
+__global__ __launch_bounds__(kQBlock) void recover_rows_kernel(const void* __restrict__ t, int64_t rows, int64_t cols,
+                                                               int32_t* __restrict__ k, uint8_t* __restrict__ q,
+                                                               unsigned long long* __restrict__ bad) {
+    constexpr int EPV = BF16 ? 8 : 4;
+    constexpr int ESZ = BF16 ? 2 : 4;
+    constexpr int QB = (ELY_Q_BATCH <= 0 || ELY_Q_BATCH > VPL) ? VPL : ELY_Q_BATCH;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + wave_uniform(threadIdx.x / kWave);
+    if (row >= rows) return;  // whole waves leave; the kernel has no block barrier
+    const int64_t nvec = cols / EPV;
+    const uint4* tr = reinterpret_cast<const uint4*>(static_cast<const char*>(t) + row * cols * ESZ);
+    uint4 buf[VPL];
+    uint32_t amax = 0;
+#pragma unroll
+    for (int j0 = 0; j0 < VPL; j0 += QB) {
+#pragma unroll
+        for (int j = j0; j < j0 + QB && j < VPL; ++j) {
+            const int64_t vi = lane + (int64_t)kWave * j;
+            buf[j] = ld_vec(tr + (vi < nvec ? vi : nvec - 1));
+        }
+#pragma unroll
+        for (int j = j0; j < j0 + QB && j < VPL; ++j) {
+            const int64_t vi = lane + (int64_t)kWave * j;
+            if (vi >= nvec) buf[j] = make_uint4(0u, 0u, 0u, 0u);
+            amax = vec_absmax<BF16>(buf[j], amax);
+        }
+        if (QB < VPL) __builtin_amdgcn_sched_barrier(0);
+    }
+    amax = wave_max_u32(amax);
+    const int base = scale_exp_from_amax<FMT>(to_f32_bits<BF16>(amax));
+    int chosen = -1;
+    if (base - 2 >= -kFastK && base + 2 <= kFastK) {
+#pragma unroll 1
+        for (int i = 0; i < 5; ++i) {
+            const int c = base + kDeltas[i];
+            const float s_down = __uint_as_float((uint32_t)(127 - c) << 23);
+            const float s_up = __uint_as_float((uint32_t)(127 + c) << 23);
+            bool ok = true;
+#pragma unroll
+            for (int j = 0; j < VPL; ++j) {
+                float v[EPV];
+                unpack<BF16>(buf[j], v);  // lanes past the end hold zeros: exact at any c
+#pragma unroll
+                for (int e = 0; e < EPV; e += 2) {
+                    const uint32_t code = cvt_pk_fp8<FMT, false>(v[e] * s_down, v[e + 1] * s_down, 0u);
+                    float b0, b1;
+                    cvt_pk_f32<FMT, false>(code, b0, b1);
+                    const bool x0 = __builtin_isfinite(v[e]) ? b0 * s_up == v[e] : exact_nonfinite<FMT>(v[e]);
+                    const bool x1 = __builtin_isfinite(v[e + 1]) ? b1 * s_up == v[e + 1] : exact_nonfinite<FMT>(v[e + 1]);
+                    ok = ok && x0 && x1;
+                }
+            }
+            if (wave_and_u32(ok ? 1u : 0u)) {
+                chosen = i;
+                break;
+            }
+        }
+    } else {
+        chosen = recover_slow_row<FMT, BF16>(t, row, cols, base, lane);
+    }
+    const int kk = chosen >= 0 ? base + kDeltas[chosen] : base + 2;
+    if (lane == 0) {
+        k[row] = kk;
+        if (chosen < 0) atomicAdd(bad, 1ull);
+    }
+    if (!q) return;
+    // the image with the exponent found, as quant_k_kernel writes it
+    uint8_t* qr = q + row * cols;
+    if (kk >= -kFastK && kk <= kFastK) {
+        const float s_down = __uint_as_float((uint32_t)(127 - kk) << 23);
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) {
+            const int64_t vi = lane + (int64_t)kWave * j;
+            if (vi >= nvec) continue;
+            float f[EPV];
+            unpack<BF16>(buf[j], f);
+            uint32_t words[2];
+#pragma unroll
+            for (int h = 0; h < EPV; h += 4) {
+                uint32_t w = 0;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t c = __builtin_isfinite(f[h + e])
+                                           ? cvt_pk_fp8<FMT, false>(f[h + e] * s_down, 0.0f, 0u) & 0xFFu
+                                           : quant_sw<FMT, BF16>(f[h + e], s_down);
+                    w |= c << (8 * e);
+                }
+                words[h / 4] = w;
+            }
+            if (BF16) st_vec2(qr + vi * EPV, make_uint2(words[0], words[1]));
+            else st_u32(qr + vi * EPV, words[0]);
+        }
+    } else {
+        const float s_down = pow2_dtype(-kk, BF16);
+#pragma unroll 1
+        for (int64_t e = lane; e < cols; e += kWave) qr[e] = (uint8_t)quant_sw<FMT, BF16>(load_x<BF16>(t, row * cols + e), s_down);
+    }
+}
+
 // --------------------------------------------------------------- self-test
 
 template <int FMT>
@@ -980,6 +1113,115 @@ static void dequantize_impl(const uint8_t* q, const int32_t* k, int64_t rows, in
     check_launch("dequant_any_kernel");
 }
 
+// Register path of recover_exp / recover_image: vectors per lane (2, 4, 5,
+// 6, 8 or 16) for rows of `cols` elements, or 0 when the row does not fit it.
+static int recover_vpl(int64_t cols, bool bf16, const void* t, const uint8_t* q) {
+    const int64_t epv = bf16 ? 8 : 4;
+    if (cols == 0 || cols % epv != 0 || !aligned16(t)) return 0;
+    if (q && reinterpret_cast<uintptr_t>(q) % (uintptr_t)epv != 0) return 0;
+    const int64_t nvec = cols / epv;
+    for (int v : {2, 4, 5, 6, 8, 16})
+        if (nvec <= (int64_t)kWave * v) return v;
+    return 0;
+}
+
+template <int FMT, bool BF16>
+static void launch_recover_rows(int vpl, const void* t, int64_t rows, int64_t cols, int32_t* k, uint8_t* q,
+                                unsigned long long* bad, hipStream_t s) {
+    const dim3 g(blocks_for_waves(rows)), b(kQBlock);
+    switch (vpl) {
+        case 2: hipLaunchKernelGGL((recover_rows_kernel<FMT, BF16, 2>), g, b, 0, s, t, rows, cols, k, q, bad); break;
+        case 4: hipLaunchKernelGGL((recover_rows_kernel<FMT, BF16, 4>), g, b, 0, s, t, rows, cols, k, q, bad); break;
+        case 5: hipLaunchKernelGGL((recover_rows_kernel<FMT, BF16, 5>), g, b, 0, s, t, rows, cols, k, q, bad); break;
+        case 6: hipLaunchKernelGGL((recover_rows_kernel<FMT, BF16, 6>), g, b, 0, s, t, rows, cols, k, q, bad); break;
+        case 8: hipLaunchKernelGGL((recover_rows_kernel<FMT, BF16, 8>), g, b, 0, s, t, rows, cols, k, q, bad); break;
+        case 16: hipLaunchKernelGGL((recover_rows_kernel<FMT, BF16, 16>), g, b, 0, s, t, rows, cols, k, q, bad); break;
+        default: fail(ELY_EINVAL, "internal: no register path for this row length");
+    }
+    check_launch("recover_rows_kernel");
+}
+
+static void recover_rows(int vpl, const void* t, bool bf16, int64_t rows, int64_t cols, int32_t fmt, int32_t* k,
+                         uint8_t* q, unsigned long long* bad, hipStream_t s) {
+    if (fmt == ELY_E4M3) {
+        if (bf16) launch_recover_rows<kE4M3, true>(vpl, t, rows, cols, k, q, bad, s);
+        else launch_recover_rows<kE4M3, false>(vpl, t, rows, cols, k, q, bad, s);
+    } else {
+        if (bf16) launch_recover_rows<kE5M2, true>(vpl, t, rows, cols, k, q, bad, s);
+        else launch_recover_rows<kE5M2, false>(vpl, t, rows, cols, k, q, bad, s);
+    }
+}
+
+// The multi-launch recovery for any shape: row maxima, the candidates'
+// exactness per segment, then k per row.
+static void recover_multi(const void* t, bool bf16, int64_t rows, int64_t cols, int32_t fmt, int32_t* k,
+                          unsigned long long* bad_rows_dev, void* workspace, hipStream_t s) {
+    uint32_t* rowmax = static_cast<uint32_t*>(workspace);
+    uint32_t* rowmask = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + split_ws_bytes(rows));
+    const unsigned fb = (unsigned)std::min<int64_t>((rows + 255) / 256, 4096);
+    hipLaunchKernelGGL(fill_u32_kernel, dim3(fb), dim3(256), 0, s, rowmask, rows, 0x1Fu);
+    check_launch("fill_u32_kernel");
+    if (cols == 0) {
+        hipLaunchKernelGGL(fill_u32_kernel, dim3(fb), dim3(256), 0, s, rowmax, rows, 0u);
+        check_launch("fill_u32_kernel");
+    } else {
+        const int64_t segs = (cols + kSegElems - 1) / kSegElems;
+        if (rows > INT64_MAX / segs) fail(ELY_EINVAL, "too many segments");
+        const unsigned blocks = blocks_for_waves(rows * segs);
+        const int vec = (cols % (bf16 ? 8 : 4) == 0) && aligned16(t);
+        if (bf16) split_rowmax<true>(t, rows, cols, vec, workspace, rowmax, s);
+        else split_rowmax<false>(t, rows, cols, vec, workspace, rowmax, s);
+#define ELY_RECOVER_MASK(F, B)                                                                                    \
+    do {                                                                                                          \
+        hipLaunchKernelGGL((recover_mask_kernel<F, B, 0>), dim3(blocks), dim3(kQBlock), 0, s, t, rows, cols, segs, \
+                           vec, (const uint32_t*)rowmax, rowmask);                                                \
+        hipLaunchKernelGGL((recover_mask_kernel<F, B, 1>), dim3(blocks), dim3(kQBlock), 0, s, t, rows, cols, segs, \
+                           vec, (const uint32_t*)rowmax, rowmask);                                                \
+    } while (0)
+        if (fmt == ELY_E4M3) {
+            if (bf16) ELY_RECOVER_MASK(kE4M3, true);
+            else ELY_RECOVER_MASK(kE4M3, false);
+        } else {
+            if (bf16) ELY_RECOVER_MASK(kE5M2, true);
+            else ELY_RECOVER_MASK(kE5M2, false);
+        }
+#undef ELY_RECOVER_MASK
+        check_launch("recover_mask_kernel");
+    }
+#define ELY_RECOVER_FINAL(F, B)                                                                                   \
+    hipLaunchKernelGGL((recover_final_kernel<F, B>), dim3(fb), dim3(256), 0, s, rows, (const uint32_t*)rowmax,      \
+                       (const uint32_t*)rowmask, k, bad_rows_dev)
+    if (fmt == ELY_E4M3) {
+        if (bf16) ELY_RECOVER_FINAL(kE4M3, true);
+        else ELY_RECOVER_FINAL(kE4M3, false);
+    } else {
+        if (bf16) ELY_RECOVER_FINAL(kE5M2, true);
+        else ELY_RECOVER_FINAL(kE5M2, false);
+    }
+#undef ELY_RECOVER_FINAL
+    check_launch("recover_final_kernel");
+}
+
+static void quant_k_launch(const void* x, bool bf16, int64_t rows, int64_t cols, int32_t fmt, const int32_t* k,
+                           uint8_t* q, hipStream_t s) {
+    const int64_t segs = (cols + kSegElems - 1) / kSegElems;
+    if (rows > INT64_MAX / segs) fail(ELY_EINVAL, "too many segments");
+    const unsigned blocks = blocks_for_waves(rows * segs);
+    const int vec = (cols % (bf16 ? 8 : 4) == 0) && aligned16(x) &&
+                    (reinterpret_cast<uintptr_t>(q) % (bf16 ? 8 : 4) == 0);
+#define ELY_QK(F, B) \
+    hipLaunchKernelGGL((quant_k_kernel<F, B>), dim3(blocks), dim3(kQBlock), 0, s, x, rows, cols, segs, vec, k, q)
+    if (fmt == ELY_E4M3) {
+        if (bf16) ELY_QK(kE4M3, true);
+        else ELY_QK(kE4M3, false);
+    } else {
+        if (bf16) ELY_QK(kE5M2, true);
+        else ELY_QK(kE5M2, false);
+    }
+#undef ELY_QK
+    check_launch("quant_k_kernel");
+}
+
 }  // namespace ely
 
 using namespace ely;
@@ -1095,51 +1337,30 @@ int ely_fp8_recover_exp(const void* t, int32_t t_dtype, int64_t rows, int64_t co
         if (!workspace || ws_bytes < ely_fp8_recover_workspace_bytes(rows))
             fail(ELY_EWORKSPACE, "ely_fp8_recover_exp: workspace smaller than ely_fp8_recover_workspace_bytes");
         hipStream_t s = static_cast<hipStream_t>(stream);
-        uint32_t* rowmax = static_cast<uint32_t*>(workspace);
-        uint32_t* rowmask = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + split_ws_bytes(rows));
-        const unsigned fb = (unsigned)std::min<int64_t>((rows + 255) / 256, 4096);
-        hipLaunchKernelGGL(fill_u32_kernel, dim3(fb), dim3(256), 0, s, rowmask, rows, 0x1Fu);
-        check_launch("fill_u32_kernel");
         const bool bf16 = t_dtype == ELY_BF16;
-        if (cols == 0) {
-            hipLaunchKernelGGL(fill_u32_kernel, dim3(fb), dim3(256), 0, s, rowmax, rows, 0u);
-            check_launch("fill_u32_kernel");
-        } else {
-            const int64_t segs = (cols + kSegElems - 1) / kSegElems;
-            if (rows > INT64_MAX / segs) fail(ELY_EINVAL, "too many segments");
-            const unsigned blocks = blocks_for_waves(rows * segs);
-            const int vec = (cols % (bf16 ? 8 : 4) == 0) && aligned16(t);
-            if (bf16) split_rowmax<true>(t, rows, cols, vec, workspace, rowmax, s);
-            else split_rowmax<false>(t, rows, cols, vec, workspace, rowmax, s);
-#define ELY_RECOVER_MASK(F, B)                                                                                    \
-    do {                                                                                                          \
-        hipLaunchKernelGGL((recover_mask_kernel<F, B, 0>), dim3(blocks), dim3(kQBlock), 0, s, t, rows, cols, segs, \
-                           vec, (const uint32_t*)rowmax, rowmask);                                                \
-        hipLaunchKernelGGL((recover_mask_kernel<F, B, 1>), dim3(blocks), dim3(kQBlock), 0, s, t, rows, cols, segs, \
-                           vec, (const uint32_t*)rowmax, rowmask);                                                \
-    } while (0)
-            if (fmt == ELY_E4M3) {
-                if (bf16) ELY_RECOVER_MASK(kE4M3, true);
-                else ELY_RECOVER_MASK(kE4M3, false);
-            } else {
-                if (bf16) ELY_RECOVER_MASK(kE5M2, true);
-                else ELY_RECOVER_MASK(kE5M2, false);
-            }
-#undef ELY_RECOVER_MASK
-            check_launch("recover_mask_kernel");
-        }
-#define ELY_RECOVER_FINAL(F, B)                                                                                   \
-    hipLaunchKernelGGL((recover_final_kernel<F, B>), dim3(fb), dim3(256), 0, s, rows, (const uint32_t*)rowmax,      \
-                       (const uint32_t*)rowmask, k, bad_rows_dev)
-        if (fmt == ELY_E4M3) {
-            if (bf16) ELY_RECOVER_FINAL(kE4M3, true);
-            else ELY_RECOVER_FINAL(kE4M3, false);
-        } else {
-            if (bf16) ELY_RECOVER_FINAL(kE5M2, true);
-            else ELY_RECOVER_FINAL(kE5M2, false);
-        }
-#undef ELY_RECOVER_FINAL
-        check_launch("recover_final_kernel");
+        const int vpl = recover_vpl(cols, bf16, t, nullptr);
+        if (vpl) return recover_rows(vpl, t, bf16, rows, cols, fmt, k, nullptr, bad_rows_dev, s);
+        recover_multi(t, bf16, rows, cols, fmt, k, bad_rows_dev, workspace, s);
+    });
+}
+
+int ely_fp8_recover_image(const void* t, int32_t t_dtype, int64_t rows, int64_t cols, int32_t fmt, int32_t* k,
+                          uint8_t* q, unsigned long long* bad_rows_dev, void* workspace, int64_t ws_bytes,
+                          void* stream) {
+    return guarded([&] {
+        check_fmt(fmt);
+        check_dtype(t_dtype, "t_dtype");
+        check_shape(rows, cols);
+        if (rows == 0) return;
+        if (!k || !bad_rows_dev || (cols > 0 && (!t || !q))) fail(ELY_EINVAL, "ely_fp8_recover_image: null pointer");
+        if (!workspace || ws_bytes < ely_fp8_recover_workspace_bytes(rows))
+            fail(ELY_EWORKSPACE, "ely_fp8_recover_image: workspace smaller than ely_fp8_recover_workspace_bytes");
+        hipStream_t s = static_cast<hipStream_t>(stream);
+        const bool bf16 = t_dtype == ELY_BF16;
+        const int vpl = recover_vpl(cols, bf16, t, q);
+        if (vpl) return recover_rows(vpl, t, bf16, rows, cols, fmt, k, q, bad_rows_dev, s);
+        recover_multi(t, bf16, rows, cols, fmt, k, bad_rows_dev, workspace, s);
+        if (cols > 0) quant_k_launch(t, bf16, rows, cols, fmt, k, q, s);
     });
 }
 
@@ -1151,24 +1372,7 @@ int ely_fp8_quantize_k(const void* x, int32_t x_dtype, int64_t rows, int64_t col
         check_shape(rows, cols);
         if (rows * cols == 0) return;
         if (!x || !k || !q) fail(ELY_EINVAL, "ely_fp8_quantize_k: null pointer");
-        hipStream_t s = static_cast<hipStream_t>(stream);
-        const int64_t segs = (cols + kSegElems - 1) / kSegElems;
-        if (rows > INT64_MAX / segs) fail(ELY_EINVAL, "too many segments");
-        const unsigned blocks = blocks_for_waves(rows * segs);
-        const bool bf16 = x_dtype == ELY_BF16;
-        const int vec = (cols % (bf16 ? 8 : 4) == 0) && aligned16(x) &&
-                        (reinterpret_cast<uintptr_t>(q) % (bf16 ? 8 : 4) == 0);
-#define ELY_QK(F, B) \
-    hipLaunchKernelGGL((quant_k_kernel<F, B>), dim3(blocks), dim3(kQBlock), 0, s, x, rows, cols, segs, vec, k, q)
-        if (fmt == ELY_E4M3) {
-            if (bf16) ELY_QK(kE4M3, true);
-            else ELY_QK(kE4M3, false);
-        } else {
-            if (bf16) ELY_QK(kE5M2, true);
-            else ELY_QK(kE5M2, false);
-        }
-#undef ELY_QK
-        check_launch("quant_k_kernel");
+        quant_k_launch(x, x_dtype == ELY_BF16, rows, cols, fmt, k, q, static_cast<hipStream_t>(stream));
     });
 }
 

@@ -70,20 +70,23 @@ def encode_scaled_fp8(t: torch.Tensor, fmt: str = "e4m3"):
     _lib.require_gpu(t, "encode_scaled_fp8")
     t = t.detach().contiguous()
     flat = t.reshape(-1, t.shape[-1]) if t.dim() > 1 else t.reshape(1, -1)
-    try:
-        k = _fp8.recover_exp(flat, fmt)  # (rows, 1) int32
-    except ValueError:
-        raise ValueError(
-            "boundary is not scaled-FP8 representable: recipe mismatch. The tensor "
-            "reaching the wire must be the recipe's own fp8 round trip."
-        ) from None
     rows, cols = flat.shape
+    # recover_exp's k and the byte image in one device call (fp8.py:66-93, planes.py:110-111)
+    k = torch.empty(rows, dtype=torch.int32, device=flat.device)
     q = torch.empty(flat.shape, dtype=torch.uint8, device=flat.device)
+    bad = torch.zeros(1, dtype=torch.int64, device=flat.device)
     L = _lib.load()
+    ws = _lib.workspace(flat.device, L.ely_fp8_recover_workspace_bytes(rows))
     _lib.check(
-        L.ely_fp8_quantize_k(flat.data_ptr(), _lib.dtype_code(flat), rows, cols, _lib.FMT[fmt], k.data_ptr(), q.data_ptr(), _lib.stream_ptr(flat.device)),
+        L.ely_fp8_recover_image(flat.data_ptr(), _lib.dtype_code(flat), rows, cols, _lib.FMT[fmt], k.data_ptr(), q.data_ptr(),
+                                bad.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_ptr(flat.device)),
         "encode_scaled_fp8",
     )
+    if int(bad.item()):
+        # the reference's recover_exp raises first, with its own message
+        # (model/fp8.py:91-92); its later round-trip check (planes.py:104-109)
+        # cannot fail once every row has an exact k
+        raise ValueError("boundary tensor is not scaled-FP8 representable: recipe mismatch")
     raw = q.reshape(-1).cpu().numpy()
     exps = k.reshape(-1).cpu().numpy().astype(np.int8)  # torch's .to(int8): two's-complement wrap
     c_v = _compress(raw.tobytes())

@@ -158,6 +158,16 @@ int ely_fp8_recover_exp(const void* t, int32_t t_dtype, int64_t rows, int64_t co
                         int32_t* k, unsigned long long* bad_rows_dev, void* workspace, int64_t ws_bytes,
                         void* stream);
 
+/* encode_scaled_fp8's device half (codec/planes.py:85-117): recover_exp's k
+ * (model/fp8.py:66-93, as ely_fp8_recover_exp) and the byte image
+ * q = fp8(t * 2^-k[row]) (planes.py:110-111, as ely_fp8_quantize_k) in one
+ * call; rows that fit registers take one read of t and one write of q.
+ * q: [rows * cols] bytes; bad rows as in ely_fp8_recover_exp (their q is not
+ * meaningful).  Workspace: ely_fp8_recover_workspace_bytes(rows). */
+int ely_fp8_recover_image(const void* t, int32_t t_dtype, int64_t rows, int64_t cols, int32_t fmt,
+                          int32_t* k, uint8_t* q, unsigned long long* bad_rows_dev, void* workspace,
+                          int64_t ws_bytes, void* stream);
+
 /* q = fp8(x * 2^-k[row]) with the caller's exponents, the multiply in x's
  * dtype: the byte image of the scaled-fp8 wire (codec/planes.py:110-111). */
 int ely_fp8_quantize_k(const void* x, int32_t x_dtype, int64_t rows, int64_t cols, int32_t fmt,

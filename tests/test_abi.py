@@ -108,6 +108,13 @@ def test_argument_errors_of_the_fold_wire_and_recover_entry_points(lib):
     assert lib.ely_fp8_recover_exp(None, _lib.BF16, 2, 8, 9, None, None, None, 0, None) == _lib.EINVAL
     assert lib.ely_fp8_recover_exp(None, _lib.BF16, 2, 8, _lib.E4M3, None, None, None, 0, None) == _lib.EINVAL
     assert lib.ely_fp8_quantize_k(None, _lib.F32, 2, 8, _lib.E5M2, None, None, None) == _lib.EINVAL
+    fake = 1 << 20  # never dereferenced: every call below fails its checks first
+    assert lib.ely_fp8_recover_image(None, _lib.BF16, 2, 8, 9, None, None, None, None, 0, None) == _lib.EINVAL
+    assert lib.ely_fp8_recover_image(None, 3, 2, 8, _lib.E4M3, None, None, None, None, 0, None) == _lib.EINVAL
+    assert lib.ely_fp8_recover_image(fake, _lib.BF16, 2, 8, _lib.E4M3, fake, None, fake, fake, 1 << 20, None) == _lib.EINVAL
+    assert b"null pointer" in lib.ely_last_error()
+    assert lib.ely_fp8_recover_image(fake, _lib.BF16, 2, 8, _lib.E4M3, fake, fake, fake, fake, 1, None) == _lib.EWORKSPACE
+    assert lib.ely_fp8_recover_image(None, _lib.BF16, 0, 8, _lib.E4M3, None, None, None, None, 0, None) == _lib.OK
 
 
 def test_workspace_queries_are_host_arithmetic(lib):

@@ -119,3 +119,68 @@ def test_recover_exp_on_odd_and_long_rows_equals_the_oracle(oracle, fmt, shape):
     off[0, shape[1] // 2] = (1 + 2.0**-6) * 2.0 ** int(bits(k).reshape(-1)[0])
     with pytest.raises(ValueError, match="recipe mismatch"):
         fp8.recover_exp(off, fmt)
+
+
+def _oracle_image(oracle, t_bits, fmt):
+    """The reference's byte image and int8 exponents (codec/planes.py:85-117),
+    unpacked from the oracle's payload."""
+    import struct
+    import zlib
+
+    payload = oracle.wire_encode(t_bits, fmt)
+    off = struct.calcsize("<BBQ")
+    lv, lk = struct.unpack_from("<II", payload, off)
+    off += 8
+    q = np.frombuffer(zlib.decompress(payload[off : off + lv]), dtype=np.uint8)
+    k = np.frombuffer(zlib.decompress(payload[off + lv : off + lv + lk]), dtype=np.int8)
+    return q, k
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+@pytest.mark.parametrize("dname", ["bf16", "f32"])
+@pytest.mark.parametrize("cols", [32, 768, 2560, 8192, 1000])
+def test_recover_image_equals_the_oracle(oracle, fmt, dname, cols):
+    """ely_fp8_recover_image (k and the byte image in one call; one pass over
+    rows that fit registers, the multi-launch path otherwise) on rows taking
+    each branch: an ordinary round trip, a zero row, a tiny and a huge row
+    (base exponent off the instruction path), a row whose base exponent is
+    one too high (offset -1 wins), and for e5m2 a row holding +-Inf and an
+    all-Inf row (|x|max not finite).  k,
+    the bytes and the int8 exponents equal the oracle's wire_encode; a value
+    off the grid is refused with the reference's message."""
+    from elysium_wan_amd import _lib, fp8, planes
+
+    dt = {"bf16": torch.bfloat16, "f32": torch.float32}[dname]
+    g = torch.Generator().manual_seed(cols)
+    x = torch.randn(7, cols, generator=g)
+    x[1] = 0.0
+    # |base| > 108: the candidates leave the instruction path (restatement rows)
+    x[2] *= 2.0 ** (-118 if fmt == "e4m3" else -100)
+    x[3] *= 2.0 ** (115 if fmt == "e4m3" else 121)
+    x[4, 0] = 255.9  # rounds to 256 in fp8: the base exponent is one octave high
+    if fmt == "e5m2":
+        x[5, cols // 2] = float("inf")
+        x[5, cols - 1] = float("-inf")
+        x[6] *= 2.0**-118  # 2^-k overflows in the quantize: the round trip is all +-Inf
+    rt = fp8.roundtrip(x.to(dt).cuda(), fmt)
+    rows = rt.shape[0]
+    say("recover_image", fmt, dname, cols)
+    k = torch.empty(rows, dtype=torch.int32, device="cuda")
+    q = torch.empty(rt.shape, dtype=torch.uint8, device="cuda")
+    bad = torch.zeros(1, dtype=torch.int64, device="cuda")
+    L = _lib.load()
+    ws = _lib.workspace(rt.device, L.ely_fp8_recover_workspace_bytes(rows))
+    _lib.check(L.ely_fp8_recover_image(rt.data_ptr(), _lib.dtype_code(rt), rows, cols, _lib.FMT[fmt], k.data_ptr(), q.data_ptr(),
+                                       bad.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_ptr(rt.device)), "recover_image")
+    assert int(bad.item()) == 0
+    ok, obad = oracle.recover_exp(bits(rt), fmt)
+    assert obad == 0 and np.array_equal(bits(k), ok)
+    oq, ok8 = _oracle_image(oracle, bits(rt), fmt)
+    assert np.array_equal(q.cpu().numpy().reshape(-1), oq)
+    assert np.array_equal(bits(k).astype(np.int8), ok8)
+    # recover_exp (register path without the image) agrees
+    assert torch.equal(fp8.recover_exp(rt, fmt).reshape(-1), k)
+    off = rt.clone()
+    off[0, cols // 3] = (1 + 2.0**-6) * 2.0 ** int(bits(k)[0])
+    with pytest.raises(ValueError, match="^boundary tensor is not scaled-FP8 representable: recipe mismatch$"):
+        planes.encode_scaled_fp8(off, fmt)
