@@ -11,11 +11,12 @@ Modules mirror the reference's:
   planes  -- codec/planes.py    (encode, decode, encode_scaled_fp8: the
              byte-plane and scaled-fp8 wires)
   fp8_planes -- codec/fp8_planes.py (encode, decode: the e4m3 nibble wire)
+  f32_planes -- codec/f32_planes.py (encode, decode: the fp32 gradient wire)
   boundary -- model/gpt.py:284-317 (narrow, Boundary: the codec's caller)
 The kernels live in libelyhip.so (C ABI: include/ely.h), built by
 elysium_wan_amd.build for gfx950.
 """
 
-from . import boundary, fp8, fp8_planes, optim, pieces, planes  # noqa: F401
+from . import boundary, f32_planes, fp8, fp8_planes, optim, pieces, planes  # noqa: F401
 
-__all__ = ["boundary", "fp8", "fp8_planes", "optim", "pieces", "planes"]
+__all__ = ["boundary", "f32_planes", "fp8", "fp8_planes", "optim", "pieces", "planes"]

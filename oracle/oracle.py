@@ -374,6 +374,22 @@ def planes_decode(payload: bytes) -> tuple:
     return did, out.reshape(-1)
 
 
+def f32_planes_encode(raw: np.ndarray) -> bytes:
+    """codec/f32_planes.py:17-26: float32 elements (as raw bytes, 4 per
+    element) -> <Q> count + zlib-1 of the 4 byte planes, byte 0 (least
+    significant) first: planes.py's byte planes in the reverse order."""
+    b = np.ascontiguousarray(raw, dtype=np.uint8)
+    planes = byte_planes(b, 4)[::-1]
+    return struct.pack("<Q", b.size // 4) + zlib.compress(b"".join(p.tobytes() for p in planes), 1)
+
+
+def f32_planes_decode(payload: bytes) -> np.ndarray:
+    """codec/f32_planes.py:29-33 -> the elements' raw bytes."""
+    (n,) = struct.unpack_from("<Q", payload, 0)
+    planes = np.frombuffer(zlib.decompress(payload[8:]), dtype=np.uint8).reshape(4, n)
+    return np.ascontiguousarray(planes.T).reshape(-1)
+
+
 def nibble_planes(codes: np.ndarray):
     """codec/fp8_planes.py:27-30: each e4m3 code's high and low nibble, two
     nibbles per byte in element order (element 2i in the high half), the last

@@ -144,3 +144,34 @@ def test_empty_and_scalar_tensors():
         assert torch.equal(planes.decode(payload, shape), t)
         payload, shape = fp8_planes.encode(t)
         assert torch.equal(fp8_planes.decode(payload, shape), t.float())
+
+
+def test_f32_planes_wire_at_c1_gradient_size_and_refusals(oracle):
+    """codec/f32_planes.py:17-33 at the size of C1's boundary gradient
+    ([8, 2048, 2560] fp32, N(0, 1e-4)): payload bytes equal the oracle's,
+    decode is bit-exact on the GPU; a non-fp32 tensor is refused with the
+    reference's AssertionError and a wrong shape with numpy's ValueError."""
+    from elysium_wan_amd import f32_planes
+
+    t = torch.empty(8, 2048, 2560, device="cuda").normal_(0.0, 1e-4, generator=torch.Generator(device="cuda").manual_seed(4))
+    say("f32 planes C1 gradient")
+    payload, shape = f32_planes.encode(t)
+    assert payload == oracle.f32_planes_encode(_raw(t))
+    assert len(payload) < t.numel() * 4  # the exponent planes code below raw
+    back = f32_planes.decode(payload, shape)
+    assert torch.equal(back.view(torch.int32), t.view(torch.int32))
+    with pytest.raises(AssertionError):
+        f32_planes.encode(t.bfloat16())
+    with pytest.raises(ValueError):
+        f32_planes.decode(payload, (3, 5))
+
+
+def test_byte_planes_compress_trained_like_fp32():
+    """The reference's test_planes_compresses_trained_like_fp32
+    (tests/unit/test_codecs_identity.py:46-49): the exponent planes of
+    N(0, 0.02) weights code below the raw bytes."""
+    from elysium_wan_amd import planes
+
+    t = torch.empty(4, 64, 256, device="cuda").normal_(0.0, 0.02, generator=torch.Generator(device="cuda").manual_seed(0))
+    payload, _ = planes.encode(t)
+    assert len(payload) < t.numel() * 4

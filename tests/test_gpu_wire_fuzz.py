@@ -1,8 +1,9 @@
 """Property fuzzing of the wire codecs on the GPU, after the reference's
 tests/fuzz/test_wire_fuzz.py:57-80 (hypothesis): arbitrary bit patterns of
 every wire dtype (NaN payloads, infinities, -0.0 and subnormals included) and
-shapes from scalars to empty tensors go through the byte-plane wire bit for
-bit, with the oracle's payload bytes; arbitrary e4m3 codes (NaN replaced by
+shapes from scalars to empty tensors go through the byte-plane wire and,
+for float32, the f32 plane wire bit for bit, with the oracle's payload
+bytes; arbitrary e4m3 codes (NaN replaced by
 0, as the reference does) widened to fp32 or bf16 go through the nibble-plane
 wire bit for bit; and fp8 round trips of arbitrary shapes and scales go
 through the scaled-fp8 wire with the oracle's payload.  Examples are
@@ -57,6 +58,18 @@ def test_byte_planes_are_bit_exact_for_every_bit_pattern(oracle, t):
     assert payload == oracle.planes_encode(raw, NAMES[t.dtype])
     back = planes.decode(payload, shape)
     assert back.dtype == t.dtype and tuple(back.shape) == tuple(t.shape)
+    assert _bits(back) == _bits(t)
+
+
+@FUZZ
+@given(raw_tensors([torch.float32]))
+def test_f32_planes_are_bit_exact_for_every_bit_pattern(oracle, t):
+    from elysium_wan_amd import f32_planes
+
+    payload, shape = f32_planes.encode(t.cuda())
+    assert payload == oracle.f32_planes_encode(np.frombuffer(_bits(t), dtype=np.uint8))
+    back = f32_planes.decode(payload, shape)
+    assert back.dtype == torch.float32 and tuple(back.shape) == tuple(t.shape)
     assert _bits(back) == _bits(t)
 
 

@@ -387,6 +387,27 @@ def test_byte_planes_are_the_textbook_split(oracle):
         assert np.array_equal(planes[j], be[:, j])
 
 
+def test_f32_planes_are_the_transposed_little_endian_bytes(oracle):
+    """codec/f32_planes.py:17-33: the decompressed body is the elements'
+    little-endian bytes read column by column (numpy's transpose of the
+    (n, 4) byte matrix: byte 0 of every element first), behind an <Q>
+    count; decode inverts it for every bit pattern, including NaN payloads,
+    infinities, -0.0 and subnormals, and for no elements at all."""
+    import struct
+    import zlib
+
+    rng = np.random.default_rng(3)
+    for n in (0, 1, 7, 1001):
+        x = rng.integers(0, 2**32, n, dtype=np.uint64).astype(np.uint32)
+        x[: min(n, 5)] = np.array([0x7FC00001, 0xFF800000, 0x80000000, 0x00000001, 0x7F7FFFFF], dtype=np.uint32)[: min(n, 5)]
+        raw = x.view(np.uint8)
+        payload = oracle.f32_planes_encode(raw)
+        assert struct.unpack_from("<Q", payload, 0) == (n,)
+        body = np.frombuffer(zlib.decompress(payload[8:]), dtype=np.uint8)
+        assert np.array_equal(body, raw.reshape(-1, 4).T.reshape(-1))
+        assert np.array_equal(oracle.f32_planes_decode(payload), raw)
+
+
 def test_nibble_payloads_match_reference_golden(oracle):
     """codec/fp8_planes.py:19-52: payload bytes and decoded values equal the
     reference's; the inputs it refuses are refused."""
