@@ -13,7 +13,7 @@
 //     in flight per CU keep the memory latency, and the bandwidth, up.
 //   * longer rows (per-tensor scaling is rows = 1): the row is cut into
 //     2048-element segments.  A first launch reduces the row's |x|max into
-//     at most 8,192 partial maxima (each wave strides over its row's
+//     at most 2,048 partial maxima (each wave strides over its row's
 //     segments; integer max, so order-free), a small second launch folds the
 //     partials per row, a third converts one segment per wave.  Two reads
 //     of x, no atomics.
@@ -42,6 +42,12 @@
 #endif
 #ifndef ELY_DEQ_BATCH
 #define ELY_DEQ_BATCH 0  // dequantize: vectors per lane per load batch (0: the whole segment at once)
+#endif
+#ifndef ELY_SPLIT_WAVES
+#define ELY_SPLIT_WAVES 2048  // split path: waves of the partial-max launch (at most)
+#endif
+#ifndef ELY_SPLIT_BATCH
+#define ELY_SPLIT_BATCH 1  // split path: vectors per lane per load batch of the convert launch (0: all)
 #endif
 #ifndef ELY_Q_BATCH
 #define ELY_Q_BATCH 1  // register paths: vectors per lane per load batch (0: the whole row at once)
@@ -388,7 +394,7 @@ __global__ void fill_u32_kernel(uint32_t* p, int64_t n, uint32_t value) {
 // into partial[r * wpr + j]; rowmax_reduce_kernel folds a row's wpr partials
 // (wpr == 1: the partials are the row maxima).  Values are |x| bit patterns
 // (fp32 bits for fp32 input, bf16 bits for bf16), so max is an integer max.
-constexpr int64_t kSplitWaves = 8192;  // waves of the partial-max launch (at most)
+constexpr int64_t kSplitWaves = ELY_SPLIT_WAVES;  // waves of the partial-max launch (at most)
 
 static int64_t split_wpr(int64_t rows, int64_t segs) {
     return std::max<int64_t>(1, std::min<int64_t>(segs, kSplitWaves / std::max<int64_t>(rows, 1)));
@@ -483,23 +489,28 @@ __global__ __launch_bounds__(kQBlock) void quant_split_kernel(const void* __rest
     if (vec && rs.fast) {
         const uint4* xr = reinterpret_cast<const uint4*>(static_cast<const char*>(x) + (base + e0) * ESZ);
         const int64_t nv = (e1 - e0) / EPV;
+        constexpr int SB = (ELY_SPLIT_BATCH <= 0 || ELY_SPLIT_BATCH > VPL) ? VPL : ELY_SPLIT_BATCH;
         uint4 buf[VPL];
 #pragma unroll
-        for (int j = 0; j < VPL; ++j) {
-            const int64_t vi = lane + (int64_t)kWave * j;
-            buf[j] = ld_vec(xr + (vi < nv ? vi : nv - 1));
-        }
+        for (int j0 = 0; j0 < VPL; j0 += SB) {
 #pragma unroll
-        for (int j = 0; j < VPL; ++j) {
-            const int64_t vi = lane + (int64_t)kWave * j;
-            if (vi >= nv) continue;
-            uint32_t words[2];
-            const int64_t e = e0 + vi * EPV;
-            quant_vec_fast<FMT, BF16>(buf[j], rs, words, out ? static_cast<char*>(out) + (base + e) * ESZ : nullptr);
-            if (q) {
-                if (BF16) st_vec2(q + base + e, make_uint2(words[0], words[1]));
-                else st_u32(q + base + e, words[0]);
+            for (int j = j0; j < j0 + SB && j < VPL; ++j) {
+                const int64_t vi = lane + (int64_t)kWave * j;
+                buf[j] = ld_vec(xr + (vi < nv ? vi : nv - 1));
             }
+#pragma unroll
+            for (int j = j0; j < j0 + SB && j < VPL; ++j) {
+                const int64_t vi = lane + (int64_t)kWave * j;
+                if (vi >= nv) continue;
+                uint32_t words[2];
+                const int64_t e = e0 + vi * EPV;
+                quant_vec_fast<FMT, BF16>(buf[j], rs, words, out ? static_cast<char*>(out) + (base + e) * ESZ : nullptr);
+                if (q) {
+                    if (BF16) st_vec2(q + base + e, make_uint2(words[0], words[1]));
+                    else st_u32(q + base + e, words[0]);
+                }
+            }
+            if (SB < VPL) __builtin_amdgcn_sched_barrier(0);
         }
     } else {
         quant_slow<FMT, BF16>(x, base, e0, e1, rs, q, out, lane);
