@@ -44,8 +44,7 @@ int64_t mt_blocks(int per_cu);
 
 // Copy `bytes` of host data to device memory `dst` on `stream` through a
 // library-owned pinned ring buffer: returns once the bytes are staged; the
-// copy (a staging kernel) is ordered on `stream` before any later work there.
-// `dst` must be 16-byte aligned with room for `bytes` rounded up to 16.
+// copy is ordered on `stream` before any later work there.
 void upload(void* dst, const void* src, size_t bytes, hipStream_t stream);
 
 inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }

@@ -18,7 +18,6 @@
 // tile partials in a fixed order.  Neither the grid size nor pointer
 // alignment changes a bit of the result.
 #include <math.h>
-#include <string.h>
 
 #include <algorithm>
 #include <vector>
@@ -650,14 +649,10 @@ static void adamw_impl(const ely_tensor* params, const ely_tensor* accs, const e
     if (tiles == 0) return;
     hipStream_t s = static_cast<hipStream_t>(stream);
     char* ws = static_cast<char*>(workspace);
-    // the table and the constants go up as one image: [table | pad to 256 | constants]
-    const size_t cs_off = align_up((size_t)n * sizeof(AdamDesc), 256);
     AdamDesc* dtable = reinterpret_cast<AdamDesc*>(ws);
-    ely_adamw_consts* dconsts = reinterpret_cast<ely_adamw_consts*>(ws + cs_off);
-    std::vector<char> image(cs_off + cs.size() * sizeof(ely_adamw_consts), 0);
-    memcpy(image.data(), table.data(), table.size() * sizeof(AdamDesc));
-    memcpy(image.data() + cs_off, cs.data(), cs.size() * sizeof(ely_adamw_consts));
-    upload(ws, image.data(), image.size(), s);
+    ely_adamw_consts* dconsts = reinterpret_cast<ely_adamw_consts*>(ws + align_up((size_t)n * sizeof(AdamDesc), 256));
+    upload(dtable, table.data(), table.size() * sizeof(AdamDesc), s);
+    upload(dconsts, cs.data(), cs.size() * sizeof(ely_adamw_consts), s);
     const bool wd = weight_decay_nonzero != 0;
     const bool clip = coef_dev != nullptr;
     AdamKernel k;
