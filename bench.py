@@ -416,21 +416,29 @@ def bench_fold(device, stream, iters=5):
 
 def bench_host_moments(device, steps=3):
     """adamw-host with its moments in pinned host memory (the reference's
-    recipe), streamed through HBM in 2^24-element chunks over 3 slots: the
-    PCIe-inclusive rate of C1's step (m and v cross PCIe both ways, 16 B per
-    element), for comparison with the HBM-resident `value`."""
+    recipe), updated in place through the GPU's mapping of the pinned
+    buffers, and, for comparison, streamed through HBM in 2^24-element chunks
+    over 3 staging slots (the reference's scheme): the PCIe-inclusive rate of
+    C1's step (m and v cross PCIe both ways, 16 B per element), against the
+    HBM-resident `value`."""
     from elysium_wan_amd import optim
 
     params, grads = make_shard(device)
     n_elem = sum(p.numel() for p in params)
-    opt = optim.FusedAdamW(params, lr=LR, betas=BETAS, eps=EPS, weight_decay=WD, order="host", max_norm=MAX_NORM, working_copy=True, moments="host")
-    opt.step(grads=grads)
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        opt.step(grads=grads)  # synchronizes at its end, as the reference's does
-    dt = (time.perf_counter() - t0) / steps
-    del opt, params, grads
-    return {"step_s": dt, "params_per_s": n_elem / dt, "pcie_GBs": n_elem * 16 / dt / 1e9}
+    out = {}
+    for name, pipeline in (("in_place", None), ("staged", True)):
+        opt = optim.FusedAdamW(params, lr=LR, betas=BETAS, eps=EPS, weight_decay=WD, order="host", max_norm=MAX_NORM,
+                               working_copy=True, moments="host", pipeline=pipeline)
+        opt.step(grads=grads)
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            opt.step(grads=grads)  # synchronizes at its end, as the reference's does
+        dt = (time.perf_counter() - t0) / steps
+        out[name] = {"step_s": dt, "params_per_s": n_elem / dt, "pcie_GBs": n_elem * 16 / dt / 1e9}
+        del opt
+        torch.cuda.empty_cache()
+    del params, grads
+    return out
 
 
 def cpu_baseline(sample_elems: int, steps: int = 2):

@@ -45,6 +45,7 @@ EXPORTS = (
     "ely_fold_add",
     "ely_scale_inplace",
     "ely_set_max_blocks",
+    "ely_host_device_pointer",
     "ely_byteplanes_split",
     "ely_byteplanes_join",
     "ely_fp8_nibbles_encode",
@@ -110,6 +111,7 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
         L.ely_fold_add.argtypes = [P, P, I32, I64, P]
         L.ely_scale_inplace.argtypes = [TP, I32, P, P]
         L.ely_set_max_blocks.argtypes = [I32]
+        L.ely_host_device_pointer.argtypes = [P, ctypes.POINTER(ctypes.c_void_p)]
         L.ely_byteplanes_split.argtypes = [P, I64, I32, P, P]
         L.ely_byteplanes_join.argtypes = [P, I64, I32, P, P]
         L.ely_fp8_nibbles_encode.argtypes = [P, I32, I64, P, P, P, P]
@@ -175,6 +177,16 @@ def tensor_array(ts) -> ctypes.Array:
             table["ptr"][:n] = [t.data_ptr() for t in ts]
             table["numel"][:n] = [t.numel() for t in ts]
     return (ElyTensor * max(1, n)).from_buffer(table)
+
+
+def host_device_pointer(t: torch.Tensor) -> int | None:
+    """The address under which the GPU reaches the pinned host tensor `t`
+    in place (ely_host_device_pointer), or None when it cannot."""
+    L = load()
+    d = ctypes.c_void_p()
+    if L.ely_host_device_pointer(t.data_ptr(), ctypes.byref(d)) != OK or not d.value:
+        return None
+    return d.value
 
 
 def stream_ptr(device: torch.device) -> int:

@@ -95,6 +95,18 @@ int32_t ely_abi_version(void) { return 1; }
 
 const char* ely_last_error(void) { return ely::g_last_error.c_str(); }
 
+int ely_host_device_pointer(const void* host, void** device) {
+    return ely::guarded([&] {
+        if (!host || !device) ely::fail(ELY_EINVAL, "ely_host_device_pointer: null pointer");
+        void* d = nullptr;
+        if (hipHostGetDevicePointer(&d, const_cast<void*>(host), 0) != hipSuccess || !d) {
+            (void)hipGetLastError();  // the query's error is not sticky state for later calls
+            ely::fail(ELY_EINVAL, "ely_host_device_pointer: not pinned, mapped host memory");
+        }
+        *device = d;
+    });
+}
+
 int ely_set_max_blocks(int32_t max_blocks) {
     if (max_blocks < 0) {
         ely::set_last_error("ely_set_max_blocks: negative cap");

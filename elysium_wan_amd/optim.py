@@ -131,9 +131,13 @@ class FusedAdamW:
         parameter) or a list of bf16 tensors shaped like the parameters;
         refreshed with the RNE bf16 cast of the updated parameter
         (pieces.cast_piece) in the update's own pass.
-    moments: "device" (HBM) or "host" (pinned host memory streamed through
-        the GPU in `chunk`-element pieces over `slots` staging buffers,
-        pipelined unless pipeline=False: HostAdamW's memory contract).
+    moments: "device" (HBM) or "host" (pinned host memory: HostAdamW's
+        memory contract).  Host moments are updated in place: the fused
+        kernel reads and writes them through the GPU's mapping of the pinned
+        buffers, PCIe busy in both directions at once.  pipeline=True
+        instead streams them through the GPU in `chunk`-element pieces over
+        `slots` staging buffers (the reference's scheme), pipeline=False
+        with serial copies; the bits are the same either way.
     Gradients (p.grad, or step(grads=...)) may be float32 or bfloat16 (the
     bf16 fold start of runtime/pieces.py:198-203 happens in registers);
     step(acc=...) folds the last microbatch into fp32 accumulators inside the
@@ -169,6 +173,7 @@ class FusedAdamW:
         self.chunk, self.pipeline, self.slots = int(chunk), pipeline, int(slots)
         self.resident: set = set()  # host mode: indices whose moments were promoted to the GPU
         self._staging = None  # host mode: per-step streaming buffers, streams and events
+        self._mapped = None  # host mode: the GPU's addresses of the pinned moment buffers
         self.order = order
         self.recipe = "adamw-host" if order == "host" else "adamw"
         if order == "torch":
@@ -255,6 +260,16 @@ class FusedAdamW:
         if self.moments == "host":
             self._flat_m = torch.zeros(max(total, 1), dtype=torch.float32, pin_memory=True)
             self._flat_v = torch.zeros(max(total, 1), dtype=torch.float32, pin_memory=True)
+            # the GPU's own addresses of the pinned buffers: the update then
+            # reads and writes the moments in place over PCIe (both directions
+            # at once) instead of copying chunks through staging buffers;
+            # pipeline=True or False asks for the staged or the serial copies
+            self._mapped = None
+            if self.pipeline is None:
+                with torch.cuda.device(dev):
+                    dm, dvv = _lib.host_device_pointer(self._flat_m), _lib.host_device_pointer(self._flat_v)
+                if dm is not None and dvv is not None:
+                    self._mapped = (dm, dvv)
         else:
             self._flat_m = torch.zeros(max(total, 1), dtype=torch.float32, device=dev)
             self._flat_v = torch.zeros(max(total, 1), dtype=torch.float32, device=dev)
@@ -350,10 +365,14 @@ class FusedAdamW:
                                      [vs[j] for j in sel], [cs[j] for j in sel], [consts[j] for j in sel], coef_ptr,
                                      None if fold is None else [fold[j] for j in sel])
                 if streamed:
-                    self._stream_host_moments([idx[j] for j in streamed], [ps[j] for j in streamed], [gs[j] for j in streamed],
-                                              [cs[j] for j in streamed], [consts[j] for j in streamed], coef_ptr,
-                                              None if fold is None else [fold[j] for j in streamed])
-                    # the host copies are the state: they land before the step returns (runtime/optim.py:171-174)
+                    sub = lambda xs: [xs[j] for j in streamed]  # noqa: E731
+                    if self._mapped is not None:
+                        self._update_mapped(sub(ps), sub(gs), sub(ms), sub(vs), sub(cs), sub(consts), coef_ptr,
+                                            None if fold is None else sub(fold))
+                    else:
+                        self._stream_host_moments(sub(idx), sub(ps), sub(gs), sub(cs), sub(consts), coef_ptr,
+                                                  None if fold is None else sub(fold))
+                    # the host moments are the state: they land before the step returns (runtime/optim.py:171-174)
                     torch.cuda.synchronize(dev)
         if on_param is not None:
             for i in idx:
@@ -409,76 +428,102 @@ class FusedAdamW:
         self._launch_arrays(len(ps), t["p"], _lib.tensor_array(gs), t["m"], t["v"], t["c"], consts, coef_ptr,
                             None if accs is None else _lib.tensor_array(accs), ps[0].device)
 
+    def _update_mapped(self, ps, gs, ms, vs, cs, consts, coef_ptr, accs) -> None:
+        """The update of parameters whose moments live in pinned host memory,
+        in place: the fused kernel gets the moments' addresses as the GPU
+        sees the mapped buffers, and its loads and stores of m and v cross
+        PCIe in both directions at once (one launch per gradient dtype)."""
+        (dm, dv), hm, hv = self._mapped, self._flat_m.data_ptr(), self._flat_v.data_ptr()
+        mapped = lambda t, dbase, hbase: _lib.ElyTensor(dbase + (t.data_ptr() - hbase), t.numel(), _lib.F32, 0)  # noqa: E731
+        for gdt in (torch.bfloat16, torch.float32):
+            sel = [j for j in range(len(ps)) if gs[j].dtype == gdt]
+            if not sel:
+                continue
+            self._launch([ps[j] for j in sel], [gs[j] for j in sel], [mapped(ms[j], dm, hm) for j in sel],
+                         [mapped(vs[j], dv, hv) for j in sel], [cs[j] for j in sel], [consts[j] for j in sel], coef_ptr,
+                         None if accs is None else [accs[j] for j in sel])
+
     def _stream_host_moments(self, idx, ps, gs, cs, consts, coef_ptr, accs) -> None:
         """The update of parameters whose moments live in host memory
         (runtime/optim.py:176-204, 301-363): the flat moment buffers are cut
-        into chunks of at most `chunk` elements along parameter order (a
-        chunk may span several parameters); chunk k goes through staging
-        slot k % slots -- its copy in on the h2d stream, the fused update of
-        every parameter piece it holds on the current stream, its copy out on
-        the d2h stream, ordered by events, so copies in, updates and copies
-        out of neighbouring chunks overlap (PCIe is full duplex).  With
-        pipeline=False the copies run on the current stream."""
+        into equal chunks of `chunk` elements along parameter order (a chunk
+        spans as many parameters as it overlaps); chunk k goes through
+        staging slot k % slots.  Its copy in, its update (with the launch's small
+        table upload) and the release of the slot run in order on the upload
+        stream; its copy out runs on the download stream once the update is
+        done, so the next chunk's copy in and this one's copy out overlap
+        (PCIe is full duplex).  Keeping each chunk's table upload behind its
+        own copy in, on one stream, measured faster than updating on the
+        caller's stream, where the small uploads waited behind the bulk
+        copies.  With pipeline=False everything runs on the current stream."""
         dev = self.device
         chunk = self.chunk
-        pieces = []  # (j, s, e): elements [s, e) of stepped parameter j
-        for j, p in enumerate(ps):
-            n = p.numel()
-            for s0 in range(0, n, chunk):
-                pieces.append((j, s0, min(n, s0 + chunk)))
-        groups = []  # [flat start, flat end, pieces]
-        for j, s0, e0 in pieces:
-            a, b = self._offs[idx[j]] + s0, self._offs[idx[j]] + e0
-            if groups and b - groups[-1][0] <= chunk:
-                groups[-1][1] = b
-                groups[-1][2].append((j, s0, e0))
+        # runs of stepped parameters adjacent in the flat buffers (only the
+        # 256-byte alignment between them), each cut into equal chunks of the
+        # flat buffer: a chunk updates every parameter piece it overlaps, so
+        # the pipeline moves full chunks instead of one per tensor boundary
+        runs = []  # [flat start, flat end, stepped parameters]
+        for o, j in sorted((self._offs[idx[j]], j) for j in range(len(ps))):
+            n = ps[j].numel()
+            if runs and o - runs[-1][1] < _ALIGN:
+                runs[-1][1] = o + n
+                runs[-1][2].append(j)
             else:
-                groups.append([a, b, [(j, s0, e0)]])
+                runs.append([o, o + n, [j]])
+        groups = []  # [flat start, flat end, pieces (j, s, e): elements [s, e) of stepped parameter j]
+        for a0, b0, js in runs:
+            for a in range(a0, b0, chunk):
+                b = min(a + chunk, b0)
+                members = []
+                for j in js:
+                    o = self._offs[idx[j]]
+                    s0, e0 = max(a, o) - o, min(b, o + ps[j].numel()) - o
+                    if s0 < e0:
+                        members.append((j, s0, e0))
+                groups.append([a, b, members])
         staged = self.pipeline is not False
         st = self._staging_buffers(dev, max(b - a for a, b, _ in groups))
-        compute = torch.cuda.current_stream(dev)
+        caller = torch.cuda.current_stream(dev)
+        up, down = (st["h2d"], st["d2h"]) if staged else (caller, caller)
+        if staged:
+            # the gradients, the clip coefficient and earlier updates are the caller's
+            up.wait_stream(caller)
         mh, vh = self._flat_m, self._flat_v
         for k, (a, b, members) in enumerate(groups):
             slot = k % len(st["bufs"])
             md, vd = st["bufs"][slot][0][: b - a], st["bufs"][slot][1][: b - a]
-            if staged:
-                if st["used"][slot]:
-                    st["h2d"].wait_event(st["ev_back"][slot])
-                with torch.cuda.stream(st["h2d"]):
-                    md.copy_(mh[a:b], non_blocking=True)
-                    vd.copy_(vh[a:b], non_blocking=True)
-                    st["ev_in"][slot].record(st["h2d"])
-                compute.wait_event(st["ev_in"][slot])
-            else:
+            if staged and st["used"][slot]:
+                up.wait_event(st["ev_back"][slot])
+            with torch.cuda.stream(up):
                 md.copy_(mh[a:b], non_blocking=True)
                 vd.copy_(vh[a:b], non_blocking=True)
-            for gdt in (torch.bfloat16, torch.float32):
-                sel = [(j, s0, e0) for j, s0, e0 in members if gs[j].dtype == gdt]
-                if not sel:
-                    continue
-                views = lambda ts: [ts[j].view(-1)[s0:e0] for j, s0, e0 in sel]  # noqa: E731
-                off = [self._offs[idx[j]] - a for j, _, _ in sel]
-                self._launch(
-                    views(ps), views(gs),
-                    [md[o + s0 : o + e0] for o, (_, s0, e0) in zip(off, sel)],
-                    [vd[o + s0 : o + e0] for o, (_, s0, e0) in zip(off, sel)],
-                    [None if cs[j] is None else cs[j].view(-1)[s0:e0] for j, s0, e0 in sel],
-                    [consts[j] for j, _, _ in sel], coef_ptr,
-                    None if accs is None else views(accs),
-                )
+                for gdt in (torch.bfloat16, torch.float32):
+                    sel = [(j, s0, e0) for j, s0, e0 in members if gs[j].dtype == gdt]
+                    if not sel:
+                        continue
+                    views = lambda ts: [ts[j].view(-1)[s0:e0] for j, s0, e0 in sel]  # noqa: E731
+                    off = [self._offs[idx[j]] - a for j, _, _ in sel]
+                    self._launch(
+                        views(ps), views(gs),
+                        [md[o + s0 : o + e0] for o, (_, s0, e0) in zip(off, sel)],
+                        [vd[o + s0 : o + e0] for o, (_, s0, e0) in zip(off, sel)],
+                        [None if cs[j] is None else cs[j].view(-1)[s0:e0] for j, s0, e0 in sel],
+                        [consts[j] for j, _, _ in sel], coef_ptr,
+                        None if accs is None else views(accs),
+                    )
+                if staged:
+                    st["ev_done"][slot].record(up)
             if staged:
-                st["ev_done"][slot].record(compute)
-                st["d2h"].wait_event(st["ev_done"][slot])
-                with torch.cuda.stream(st["d2h"]):
-                    mh[a:b].copy_(md, non_blocking=True)
-                    vh[a:b].copy_(vd, non_blocking=True)
-                    st["ev_back"][slot].record(st["d2h"])
-                st["used"][slot] = True
-            else:
+                down.wait_event(st["ev_done"][slot])
+            with torch.cuda.stream(down):
                 mh[a:b].copy_(md, non_blocking=True)
                 vh[a:b].copy_(vd, non_blocking=True)
+                if staged:
+                    st["ev_back"][slot].record(down)
+            st["used"][slot] = staged
         if staged:
-            compute.wait_stream(st["d2h"])
+            caller.wait_stream(up)
+            caller.wait_stream(down)
             st["used"] = [False] * len(st["bufs"])
 
     def _staging_buffers(self, dev, need: int) -> dict:

@@ -189,6 +189,13 @@ int ely_fold_add(float* acc, const void* g, int32_t g_dtype, int64_t n, void* st
  * left on the device. */
 int ely_scale_inplace(const ely_tensor* tensors, int32_t n, const float* coef_dev, void* stream);
 
+/* No counterpart in the reference (its HostAdamW copies m and v through
+ * staging buffers, runtime/optim.py:176-204, 301-363): the address under
+ * which the GPU reaches pinned, mapped host memory (hipHostGetDevicePointer),
+ * so that the fused update reads and writes host-resident moments in place
+ * over PCIe.  ELY_EINVAL if `host` is not such memory. */
+int ely_host_device_pointer(const void* host, void** device);
+
 /* Cap on the blocks one multi-tensor launch (grad-norm, AdamW) may use; 0
  * restores the default (8 per compute unit).  For tuning and for the tests
  * that prove results do not depend on the grid.  Process-wide. */

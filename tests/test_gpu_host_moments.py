@@ -55,9 +55,10 @@ def _same(a, b) -> bool:
 
 @pytest.mark.parametrize("chunk,slots,pipeline", [(7, 2, True), (7, 3, False), (64, 3, None), (1 << 24, 3, None)])
 def test_streamed_moments_equal_resident_moments(chunk, slots, pipeline):
-    """test_host_adamw.py:50-55, 154-167: chunk k in slot k % slots,
-    refilled across parameter boundaries, staged or direct -- the parameters
-    and moments equal the HBM-resident run's, bit for bit."""
+    """test_host_adamw.py:50-55, 154-167: updated in place through the GPU's
+    mapping of the pinned buffers (the default), or chunk k in slot k %
+    slots, refilled across parameter boundaries, staged or serial -- the
+    parameters and moments equal the HBM-resident run's, bit for bit."""
     from elysium_wan_amd import optim
 
     hp = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, order="host", max_norm=1.0, working_copy=True)
@@ -65,21 +66,24 @@ def test_streamed_moments_equal_resident_moments(chunk, slots, pipeline):
     dev = _train(lambda ps: optim.FusedAdamW(ps, **hp), _params())
     host = _train(lambda ps: optim.FusedAdamW(ps, moments="host", chunk=chunk, slots=slots, pipeline=pipeline, **hp), _params())
     assert all(host.state[i]["exp_avg"].device.type == "cpu" for i in host.state)
+    assert (host._mapped is not None) == (pipeline is None)
     assert _same(dev, host)
 
 
+@pytest.mark.parametrize("pipeline", [None, True])
 @pytest.mark.parametrize("order", ["host", "torch"])
-def test_streamed_c0_shard_with_bf16_grads_and_fold(order):
-    """Config C0's layout (3 GPT blocks at d = 768, 21.3M elements) in chunks
-    of 2^20 through 3 slots, bf16 gradients folded into fp32 accumulators
-    inside the update: equal to the resident run."""
+def test_streamed_c0_shard_with_bf16_grads_and_fold(order, pipeline):
+    """Config C0's layout (3 GPT blocks at d = 768, 21.3M elements), in place
+    or in chunks of 2^20 through 3 slots, bf16 gradients folded into fp32
+    accumulators inside the update: equal to the resident run."""
     from elysium_wan_amd import optim
 
     shapes = tuple(gpt_block_shapes(768) * 3 + [(768,), (768,)])
     hp = dict(lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, order=order, max_norm=1.0, working_copy=True)
-    say("host moments C0", order)
+    say("host moments C0", order, pipeline)
     dev = _train(lambda ps: optim.FusedAdamW(ps, **hp), _params(7, shapes), steps=2, dtype=torch.bfloat16, fold=True)
-    host = _train(lambda ps: optim.FusedAdamW(ps, moments="host", chunk=1 << 20, **hp), _params(7, shapes), steps=2, dtype=torch.bfloat16, fold=True)
+    host = _train(lambda ps: optim.FusedAdamW(ps, moments="host", chunk=1 << 20, pipeline=pipeline, **hp), _params(7, shapes), steps=2,
+                  dtype=torch.bfloat16, fold=True)
     assert _same(dev, host)
 
 
