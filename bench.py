@@ -44,6 +44,7 @@ LR, BETAS, EPS, WD, MAX_NORM = 3e-4, (0.9, 0.95), 1e-8, 0.1, 1.0
 ADAM_BYTES_PER_ELEM = 28  # bf16 grads, bf16 copy out
 NORM_BYTES_PER_ELEM = 2
 CODEC_BYTES_PER_ELEM = 3  # bf16 in / fp8 out (quantize); fp8 in / bf16 out (dequantize)
+ROUNDTRIP_BYTES_PER_ELEM = 4  # bf16 in, bf16 out (fp8.roundtrip, nothing else written)
 CAL_ELEMS = 1 << 28  # calibration cast of the --pmc passes
 
 
@@ -294,8 +295,8 @@ def _c4_inputs(device, seed):
 
 
 def bench_codec(device, stream, rows, cols, copies, iters=20, per_tensor=False, xs=None, fmts=("e4m3", "e5m2"), stats=False):
-    """Quantize and dequantize (bf16 <-> fp8, per-row or per-tensor) of a
-    [rows, cols] activation, rotating through `copies` inputs so that
+    """Quantize, dequantize and the fused round trip (bf16 <-> fp8, per-row
+    or per-tensor) of a [rows, cols] activation, rotating through `copies` inputs so that
     launches stream from HBM rather than the 256 MB MALL. With `stats`, the
     round trip of the first input is also reported, outside the timed
     region: relative L2 error of dequantize(quantize(x)) against x, the
@@ -326,15 +327,23 @@ def bench_codec(device, stream, rows, cols, copies, iters=20, per_tensor=False, 
             j = i % copies
             _lib.check(L.ely_fp8_dequantize(qs[j].data_ptr(), ks[j].data_ptr(), qr, qc, f, outs[j].data_ptr(), _lib.BF16, sptr), "dq")
 
+        def rt(i, f=f):
+            # fp8.roundtrip (model/fp8.py:56-63): quantize and dequantize fused, bf16 in and out
+            j = i % copies
+            _lib.check(L.ely_fp8_roundtrip(xs[j].data_ptr(), _lib.BF16, qr, qc, f, outs[j].data_ptr(), None, None, ws.data_ptr(), ws.numel(), sptr), "rt")
+
         for i in range(copies):
             quant(i)
         q_ms = time_events(quant, iters, stream)
         d_ms = time_events(deq, iters, stream)
+        r_ms = time_events(rt, iters, stream)
         out[fmt] = {
             "quantize_ms": q_ms,
             "quantize_GBs": n * CODEC_BYTES_PER_ELEM / q_ms / 1e6,
             "dequantize_ms": d_ms,
             "dequantize_GBs": n * CODEC_BYTES_PER_ELEM / d_ms / 1e6,
+            "roundtrip_ms": r_ms,
+            "roundtrip_GBs": n * ROUNDTRIP_BYTES_PER_ELEM / r_ms / 1e6,
         }
         if stats:
             quant(0)
