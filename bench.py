@@ -48,8 +48,11 @@ ROUNDTRIP_BYTES_PER_ELEM = 4  # bf16 in, bf16 out (fp8.roundtrip, nothing else w
 CAL_ELEMS = 1 << 28  # calibration cast of the --pmc passes
 
 
+_T0 = time.perf_counter()
+
+
 def log(*a):
-    print(*a, file=sys.stderr, flush=True)
+    print(f"[{time.perf_counter() - _T0:6.1f}s]", *a, file=sys.stderr, flush=True)
 
 
 def block_shapes(d: int):
