@@ -335,12 +335,15 @@ class FusedAdamW:
         self._check_inputs(idx, ps, gs, accs)
         if idx:
             sts = [self._slot(i, p) for i, p in zip(idx, ps)]
+            ms = [st["exp_avg"] for st in sts]
+            vs = [st["exp_avg_sq"] for st in sts]
+            if self.moments == "host":
+                host = [j for j, m in enumerate(ms) if m.device.type != "cuda"]
+                self._check_host_moments([idx[j] for j in host], [ms[j] for j in host], [vs[j] for j in host])
             # the step counters are views of one flat tensor: one increment for all
             it = torch.tensor(idx, dtype=torch.int64)
             self._steps[it] += 1
             ts = self._steps[it].tolist()
-            ms = [st["exp_avg"] for st in sts]
-            vs = [st["exp_avg_sq"] for st in sts]
             cs = [self.working_copies[i] if self.working_copies is not None else None for i in idx]
             per_t = {t: self._consts(t) for t in set(ts)}
             consts = [per_t[t] for t in ts]
@@ -427,6 +430,18 @@ class FusedAdamW:
             }
         self._launch_arrays(len(ps), t["p"], _lib.tensor_array(gs), t["m"], t["v"], t["c"], consts, coef_ptr,
                             None if accs is None else _lib.tensor_array(accs), ps[0].device)
+
+    def _check_host_moments(self, idx, ms, vs) -> None:
+        """Host moments are views of the optimizer's two pinned buffers (the
+        update reads and writes them there, in place or through the staging
+        copies); a state tensor swapped for another host tensor is refused
+        before any launch."""
+        for name, flat, ts in (("exp_avg", self._flat_m, ms), ("exp_avg_sq", self._flat_v, vs)):
+            lo, hi = flat.data_ptr(), flat.data_ptr() + flat.numel() * 4
+            for i, t in zip(idx, ts):
+                a = t.data_ptr()
+                if not (t.dtype == torch.float32 and t.is_contiguous() and lo <= a and a + t.numel() * 4 <= hi):
+                    raise ValueError(f"{self.recipe}: state[{i}][{name!r}] is not a view of the optimizer's pinned moment buffer")
 
     def _update_mapped(self, ps, gs, ms, vs, cs, consts, coef_ptr, accs) -> None:
         """The update of parameters whose moments live in pinned host memory,

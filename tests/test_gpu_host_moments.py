@@ -119,3 +119,24 @@ def test_recipe_lives_in_host_memory_checkpoints_and_promotes():
     opt2.step(grads=_grads(params2, 6))
     torch.cuda.synchronize()
     assert all(torch.equal(a.detach().view(torch.int32), b.detach().view(torch.int32)) for a, b in zip(ref.params, params2))
+
+
+def test_a_swapped_host_moment_is_refused_before_any_launch():
+    """Host moments are views of the optimizer's pinned buffers, which the
+    update reaches in place; a state tensor replaced by another host tensor
+    is refused with ValueError before anything is launched, and the
+    parameters stay as they were."""
+    from elysium_wan_amd import optim
+
+    params = _params()
+    opt = optim.build("adamw-host", params, 1e-3)
+    opt.step(grads=_grads(params, 0))
+    torch.cuda.synchronize()
+    before = [p.detach().clone() for p in params]
+    opt.state[2]["exp_avg"] = torch.zeros_like(opt.state[2]["exp_avg"])
+    say("swapped host moment")
+    with pytest.raises(ValueError, match="pinned moment buffer"):
+        opt.step(grads=_grads(params, 1))
+    torch.cuda.synchronize()
+    assert all(torch.equal(a, b.detach()) for a, b in zip(before, params))
+    assert all(float(opt.state[i]["step"]) == 1.0 for i in range(len(params)))
