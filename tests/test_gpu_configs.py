@@ -10,7 +10,9 @@ through properties that do not need a CPU pass over billions of elements:
 * C3 (the 25.1B model's 4-stage shard: 1,000 vectors of 6,144 interleaved
   with 100 matrices of 6,144 x 10,240, bf16 Student-t gradients): five runs
   from the same seeded inputs give bitwise-identical norms, parameters and
-  moments, and a sampled oracle check.
+  moments, and a sampled oracle check;
+* maximum sizes: one tensor past 2^31 elements through the fused step, and
+  an activation past 2^32 codes through the codec (64-bit indexing).
 """
 
 from __future__ import annotations
@@ -133,3 +135,61 @@ def test_c3_ragged_shard_is_bitwise_reproducible(oracle):
         del opt, params, grads
         torch.cuda.empty_cache()
     assert all(s == sums[0] for s in sums), sums
+
+
+def test_one_tensor_past_two_to_the_31_elements(oracle):
+    """Maximum sizes: one fp32 parameter of 2^31 + 4099 elements (bf16 grads,
+    clip on) -- 64-bit element and tile indexing.  The norm equals an fp64
+    sum within 1e-6; elements at the start, around 2^31 and at the end equal
+    the oracle's step of their gathered inputs, bit for bit."""
+    from elysium_wan_amd import optim
+
+    n = (1 << 31) + 4099
+    gen = torch.Generator(device="cuda").manual_seed(31)
+    p = torch.empty(n, device="cuda").normal_(0.0, 0.02, generator=gen).requires_grad_(True)
+    g = torch.empty(n, device="cuda").normal_(0.0, 1e-3, generator=gen).to(torch.bfloat16)
+    sel = torch.cat([torch.arange(0, 4096), torch.arange((1 << 31) - 4096, (1 << 31) + 4096), torch.arange(n - 4096, n)]).cuda()
+    p_in, g_in = p.detach()[sel].clone(), g[sel].clone()
+    want = float(g.double().square().sum())
+    say("one tensor of", n, "elements")
+    opt = optim.FusedAdamW([p], lr=LR, betas=BETAS, eps=EPS, weight_decay=WD, order="host", max_norm=MAX_NORM, working_copy=True)
+    opt.step(grads=[g])
+    torch.cuda.synchronize()
+    norm = float(opt.grad_norm())
+    assert abs(norm - want**0.5) <= 1e-6 * want**0.5
+    coef = float(opt._norm[12:16].view(torch.float32))
+    pi = p_in.cpu().numpy()
+    gi = g_in.view(torch.int16).cpu().numpy().view(np.uint16)
+    m, v = np.zeros_like(pi), np.zeros_like(pi)
+    cp = np.zeros(pi.size, np.uint16)
+    oracle.adamw_host(pi, gi, m, v, np.array(optim.host_consts(LR, BETAS, EPS, WD, 1.0), dtype=np.float32), True, coef, cp)
+    assert np.array_equal(p.detach()[sel].cpu().numpy().view(np.uint32), pi.view(np.uint32))
+    assert np.array_equal(opt.state[0]["exp_avg"][sel].cpu().numpy().view(np.uint32), m.view(np.uint32))
+    assert np.array_equal(opt.state[0]["exp_avg_sq"][sel].cpu().numpy().view(np.uint32), v.view(np.uint32))
+    assert np.array_equal(opt.working_copies[0][sel].view(torch.int16).cpu().numpy().view(np.uint16), cp)
+    del opt, p, g
+    torch.cuda.empty_cache()
+
+
+def test_fp8_codes_past_two_to_the_32(oracle):
+    """Maximum sizes: a [524289, 8192] bf16 activation holds 2^32 + 8192
+    codes, so dequantize takes its 64-bit flat indexing; rows before and
+    after the 2^32 boundary quantize, dequantize and round-trip like the
+    oracle, bit for bit."""
+    from elysium_wan_amd import fp8
+
+    rows, cols = (1 << 19) + 1, 8192
+    gen = torch.Generator(device="cuda").manual_seed(32)
+    x = torch.empty(rows, cols, device="cuda", dtype=torch.bfloat16).normal_(generator=gen)
+    say("fp8 rows", rows, "x", cols)
+    q, k = fp8.quantize(x, "e4m3")
+    d = fp8.dequantize(q, k, torch.bfloat16)
+    torch.cuda.synchronize()
+    for r in (0, (1 << 19) - 1, 1 << 19):
+        xb = x[r : r + 1].view(torch.int16).cpu().numpy().view(np.uint16)
+        oq, ok = oracle.quantize(xb, "e4m3")
+        assert np.array_equal(q[r : r + 1].view(torch.uint8).cpu().numpy(), oq), r
+        assert int(k[r]) == int(ok[0]), r
+        assert np.array_equal(d[r : r + 1].view(torch.int16).cpu().numpy().view(np.uint16), oracle.dequantize(oq, ok, "e4m3", "bf16")), r
+    del x, q, k, d
+    torch.cuda.empty_cache()
