@@ -57,12 +57,15 @@ namespace ely {
 #ifndef ELY_ADAM_BPC
 #define ELY_ADAM_BPC 1           // AdamW blocks per compute unit
 #endif
+#ifndef ELY_NORM_TILE
+#define ELY_NORM_TILE 16384      // grad-norm elements per tile (one wave's share; fixes the summation order)
+#endif
 #ifndef ELY_NORM_BPC
 #define ELY_NORM_BPC 24          // grad-norm blocks (of 4 waves) per compute unit
 #endif
 
 constexpr int64_t kAdamTile = ELY_ADAM_TILE;
-constexpr int64_t kNormTile = 16384;    // elements per grad-norm tile (one wave): fixes the summation order
+constexpr int64_t kNormTile = ELY_NORM_TILE;  // elements per grad-norm tile (one wave): fixes the summation order
 constexpr int kNormUnroll = ELY_NORM_UNROLL;
 constexpr int kBlock = 256;
 constexpr int kFinalThreads = 1024;
