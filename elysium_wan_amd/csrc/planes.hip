@@ -22,9 +22,22 @@
 
 namespace ely {
 
+#ifndef ELY_PLANES_UNROLL
+#define ELY_PLANES_UNROLL 1  // byte planes: 16-byte vectors a lane keeps in flight
+#endif
+#ifndef ELY_PLANES_BPC
+#define ELY_PLANES_BPC 4  // byte planes: blocks per compute unit
+#endif
+#ifndef ELY_NIBBLES_UNROLL
+#define ELY_NIBBLES_UNROLL 4  // nibble planes: vectors a lane keeps in flight
+#endif
+#ifndef ELY_NIBBLES_BPC
+#define ELY_NIBBLES_BPC 8  // nibble planes: blocks per compute unit
+#endif
+
 constexpr int kPBlock = 256;
 
-static unsigned grid_for(int64_t work, int per_cu = 8) {
+static unsigned grid_for(int64_t work, int per_cu) {
     const int64_t cap = (int64_t)device_info().cus * per_cu;
     const int64_t b = std::max<int64_t>(1, std::min<int64_t>((work + kPBlock - 1) / kPBlock, cap));
     return (unsigned)b;
@@ -37,7 +50,8 @@ static unsigned grid_for(int64_t work, int per_cu = 8) {
 // every store instruction of a wave covers one contiguous run.  kPUnroll
 // vectors per lane are loaded before the first is used; all streams are
 // nontemporal.
-constexpr int kPUnroll = 4;
+constexpr int kPUnroll = ELY_PLANES_UNROLL;
+constexpr int kNUnroll = ELY_NIBBLES_UNROLL;
 
 typedef uint32_t pv4 __attribute__((ext_vector_type(4)));
 typedef uint32_t pv2 __attribute__((ext_vector_type(2)));
@@ -198,15 +212,15 @@ __global__ __launch_bounds__(kPBlock) void nibbles_encode_kernel(const void* __r
     if (vec) {
         const int64_t nvec = n / 16 * (16 / EPL);  // whole 16-element groups only
         const uint8_t* tb = static_cast<const uint8_t*>(t);
-        for (int64_t base = tid; base < nvec; base += T * kPUnroll) {
-            pv4 v[kPUnroll];
+        for (int64_t base = tid; base < nvec; base += T * kNUnroll) {
+            pv4 v[kNUnroll];
 #pragma unroll
-            for (int u = 0; u < kPUnroll; ++u) {
+            for (int u = 0; u < kNUnroll; ++u) {
                 const int64_t vi = base + u * T;
                 v[u] = ld16(tb + (vi < nvec ? vi : nvec - 1) * 16);
             }
 #pragma unroll
-            for (int u = 0; u < kPUnroll; ++u) {
+            for (int u = 0; u < kNUnroll; ++u) {
                 const int64_t vi = base + u * T;
                 if (vi >= nvec) continue;
                 float f[EPL];
@@ -271,17 +285,17 @@ __global__ __launch_bounds__(kPBlock) void nibbles_decode_kernel(const uint8_t* 
     int64_t done = 0;
     if (vec) {
         const int64_t nq = n / 4;
-        for (int64_t base = tid; base < nq; base += T * kPUnroll) {
-            uint32_t h[kPUnroll], l[kPUnroll];
+        for (int64_t base = tid; base < nq; base += T * kNUnroll) {
+            uint32_t h[kNUnroll], l[kNUnroll];
 #pragma unroll
-            for (int u = 0; u < kPUnroll; ++u) {
+            for (int u = 0; u < kNUnroll; ++u) {
                 const int64_t q = base + u * T;
                 const int64_t qc = q < nq ? q : nq - 1;
                 h[u] = __builtin_nontemporal_load((const PL_G1 uint16_t*)(hi + qc * 2));
                 l[u] = __builtin_nontemporal_load((const PL_G1 uint16_t*)(lo + qc * 2));
             }
 #pragma unroll
-            for (int u = 0; u < kPUnroll; ++u) {
+            for (int u = 0; u < kNUnroll; ++u) {
                 const int64_t q = base + u * T;
                 if (q >= nq) continue;
                 uint32_t word = 0;  // codes of elements 4q .. 4q+3, one per byte
@@ -327,7 +341,7 @@ int ely_byteplanes_split(const void* x, int64_t n, int32_t esz, uint8_t* planes,
         hipStream_t s = static_cast<hipStream_t>(stream);
         if (n % 16 == 0 && aligned16(x) && aligned16(planes)) {
             const int64_t nvec = n * esz / 16;
-            const unsigned g = grid_for((nvec + kPUnroll - 1) / kPUnroll);
+            const unsigned g = grid_for((nvec + kPUnroll - 1) / kPUnroll, ELY_PLANES_BPC);
             const uint8_t* xb = static_cast<const uint8_t*>(x);
             switch (esz) {
                 case 1: hipLaunchKernelGGL(split_vec_kernel<1>, dim3(g), dim3(kPBlock), 0, s, xb, nvec, planes, n); break;
@@ -337,7 +351,7 @@ int ely_byteplanes_split(const void* x, int64_t n, int32_t esz, uint8_t* planes,
             }
             check_launch("split_vec_kernel");
         } else {
-            hipLaunchKernelGGL(split_any_kernel, dim3(grid_for(n)), dim3(kPBlock), 0, s, static_cast<const uint8_t*>(x), n,
+            hipLaunchKernelGGL(split_any_kernel, dim3(grid_for(n, ELY_PLANES_BPC)), dim3(kPBlock), 0, s, static_cast<const uint8_t*>(x), n,
                                (int)esz, planes);
             check_launch("split_any_kernel");
         }
@@ -354,7 +368,7 @@ int ely_byteplanes_join(const uint8_t* planes, int64_t n, int32_t esz, void* out
         hipStream_t s = static_cast<hipStream_t>(stream);
         if (n % 16 == 0 && aligned16(out) && aligned16(planes)) {
             const int64_t nvec = n * esz / 16;
-            const unsigned g = grid_for((nvec + kPUnroll - 1) / kPUnroll);
+            const unsigned g = grid_for((nvec + kPUnroll - 1) / kPUnroll, ELY_PLANES_BPC);
             uint8_t* ob = static_cast<uint8_t*>(out);
             switch (esz) {
                 case 1: hipLaunchKernelGGL(join_vec_kernel<1>, dim3(g), dim3(kPBlock), 0, s, planes, nvec, n, ob); break;
@@ -364,7 +378,7 @@ int ely_byteplanes_join(const uint8_t* planes, int64_t n, int32_t esz, void* out
             }
             check_launch("join_vec_kernel");
         } else {
-            hipLaunchKernelGGL(join_any_kernel, dim3(grid_for(n)), dim3(kPBlock), 0, s, planes, n, (int)esz,
+            hipLaunchKernelGGL(join_any_kernel, dim3(grid_for(n, ELY_PLANES_BPC)), dim3(kPBlock), 0, s, planes, n, (int)esz,
                                static_cast<uint8_t*>(out));
             check_launch("join_any_kernel");
         }
@@ -380,7 +394,7 @@ int ely_fp8_nibbles_encode(const void* t, int32_t t_dtype, int64_t n, uint8_t* h
         if (!t || !hi || !lo || !bad_dev) fail(ELY_EINVAL, "ely_fp8_nibbles_encode: null pointer");
         hipStream_t s = static_cast<hipStream_t>(stream);
         const int vec = aligned16(t) && (reinterpret_cast<uintptr_t>(hi) % 4 == 0) && (reinterpret_cast<uintptr_t>(lo) % 4 == 0);
-        const unsigned g = grid_for(std::max<int64_t>(n / 8 / kPUnroll, 1));
+        const unsigned g = grid_for(std::max<int64_t>(n / 8 / kNUnroll, 1), ELY_NIBBLES_BPC);
         if (t_dtype == ELY_BF16)
             hipLaunchKernelGGL(nibbles_encode_kernel<true>, dim3(g), dim3(kPBlock), 0, s, t, n, vec, hi, lo, bad_dev);
         else
@@ -396,7 +410,7 @@ int ely_fp8_nibbles_decode(const uint8_t* hi, const uint8_t* lo, int64_t n, floa
         if (!out || !hi || !lo) fail(ELY_EINVAL, "ely_fp8_nibbles_decode: null pointer");
         hipStream_t s = static_cast<hipStream_t>(stream);
         const int vec = aligned16(out) && (reinterpret_cast<uintptr_t>(hi) % 2 == 0) && (reinterpret_cast<uintptr_t>(lo) % 2 == 0);
-        hipLaunchKernelGGL(nibbles_decode_kernel, dim3(grid_for(std::max<int64_t>(n / 4 / kPUnroll, 1))), dim3(kPBlock), 0, s,
+        hipLaunchKernelGGL(nibbles_decode_kernel, dim3(grid_for(std::max<int64_t>(n / 4 / kNUnroll, 1), ELY_NIBBLES_BPC)), dim3(kPBlock), 0, s,
                            hi, lo, n, vec, out);
         check_launch("nibbles_decode_kernel");
     });
