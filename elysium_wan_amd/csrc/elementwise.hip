@@ -3,8 +3,8 @@
 // runtime/pieces.py:192-195), the fp32 fold of a microbatch gradient
 // (pieces.fold_add, runtime/pieces.py:206-214) and the clip's in-place
 // scaling (clip_grad_norm_).  Each is one HBM pass over 4-element quads
-// (16-byte fp32, 8-byte bf16 vectors, nontemporal), four quads in flight per
-// thread, on a persistent grid.
+// (16-byte fp32, 8-byte bf16 vectors, nontemporal) on a persistent grid,
+// with a per-kernel number of quads in flight per thread.
 #include <algorithm>
 
 #include "ely_device.hpp"
@@ -12,10 +12,49 @@
 
 #pragma clang fp contract(off)
 
+// Tunables, per kernel: quads of 4 elements a thread has in flight (_UNROLL)
+// and the persistent grid's blocks per CU (_BPC).  Together they set the
+// bytes each CU has outstanding, which is what bounds a streaming pass on
+// this part; the passes reading 16-24 B per quad run fastest at about 16-25
+// KB of reads in flight per CU, the bf16 scale (8 B per quad) wants more
+// waves.
+#ifndef ELY_CAST_UNROLL
+#define ELY_CAST_UNROLL 1
+#endif
+#ifndef ELY_CAST_BPC
+#define ELY_CAST_BPC 4
+#endif
+#ifndef ELY_FOLD_UNROLL
+#define ELY_FOLD_UNROLL 1
+#endif
+#ifndef ELY_FOLD_BPC
+#define ELY_FOLD_BPC 3
+#endif
+#ifndef ELY_SCALE32_UNROLL
+#define ELY_SCALE32_UNROLL 1
+#endif
+#ifndef ELY_SCALE32_BPC
+#define ELY_SCALE32_BPC 4
+#endif
+#ifndef ELY_SCALE16_UNROLL
+#define ELY_SCALE16_UNROLL 2
+#endif
+#ifndef ELY_SCALE16_BPC
+#define ELY_SCALE16_BPC 8
+#endif
+
 namespace ely {
 
 constexpr int kEwBlock = 256;
-constexpr int kEwUnroll = 4;  // quads of 4 elements a thread has in flight
+
+// A launch shape: quads in flight per thread, blocks per CU.
+struct EwShape {
+    int unroll, bpc;
+};
+constexpr EwShape kCastShape{ELY_CAST_UNROLL, ELY_CAST_BPC};
+constexpr EwShape kFoldShape{ELY_FOLD_UNROLL, ELY_FOLD_BPC};
+constexpr EwShape kScale32Shape{ELY_SCALE32_UNROLL, ELY_SCALE32_BPC};
+constexpr EwShape kScale16Shape{ELY_SCALE16_UNROLL, ELY_SCALE16_BPC};
 
 typedef float ef4 __attribute__((ext_vector_type(4)));
 typedef uint32_t eu2 __attribute__((ext_vector_type(2)));
@@ -35,23 +74,23 @@ __device__ __forceinline__ eu2 narrow4(ef4 v) {
 }
 
 // The quad loop shared by the kernels below: thread t of T takes quads
-// t, t + T, ..., kEwUnroll of them loaded before the first is computed, so
-// each load or store instruction of a wave covers one contiguous run.
-// load(q) reads quad q into registers, store(q, regs) computes and writes it;
-// returns the elements covered.
-template <class Load, class Store>
+// t, t + T, ..., U of them loaded before the first is computed, so each load
+// or store instruction of a wave covers one contiguous run.  load(q) reads
+// quad q into registers, store(q, regs) computes and writes it; returns the
+// elements covered.
+template <int U, class Load, class Store>
 __device__ __forceinline__ int64_t quad_loop(int64_t nq, Load load, Store store) {
     const int64_t T = (int64_t)gridDim.x * kEwBlock;
     const int64_t t = (int64_t)blockIdx.x * kEwBlock + threadIdx.x;
-    for (int64_t base = t; base < nq; base += T * kEwUnroll) {
-        decltype(load(0)) r[kEwUnroll];
+    for (int64_t base = t; base < nq; base += T * U) {
+        decltype(load(0)) r[U];
 #pragma unroll
-        for (int u = 0; u < kEwUnroll; ++u) {
+        for (int u = 0; u < U; ++u) {
             const int64_t q = base + u * T;
             r[u] = load(q < nq ? q : nq - 1);
         }
 #pragma unroll
-        for (int u = 0; u < kEwUnroll; ++u) {
+        for (int u = 0; u < U; ++u) {
             const int64_t q = base + u * T;
             if (q < nq) store(q, r[u]);
         }
@@ -64,7 +103,7 @@ __global__ __launch_bounds__(kEwBlock) void cast_bf16_kernel(const float* __rest
                                                              int64_t n, int vec) {
     int64_t done = 0;
     if (vec)
-        done = quad_loop(
+        done = quad_loop<kCastShape.unroll>(
             n / 4, [&](int64_t q) { return ld4(x + 4 * q); }, [&](int64_t q, ef4 v) { sth4(out + 4 * q, narrow4(v)); });
     const int64_t T = (int64_t)gridDim.x * kEwBlock;
     for (int64_t i = done + (int64_t)blockIdx.x * kEwBlock + threadIdx.x; i < n; i += T) out[i] = (uint16_t)f32_to_bf16(x[i]);
@@ -80,7 +119,7 @@ __global__ __launch_bounds__(kEwBlock) void fold_add_kernel(float* __restrict__ 
                                                             int64_t n, int vec) {
     int64_t done = 0;
     if (vec)
-        done = quad_loop(
+        done = quad_loop<kFoldShape.unroll>(
             n / 4,
             [&](int64_t q) {
                 AccG r;
@@ -106,12 +145,12 @@ __global__ __launch_bounds__(kEwBlock) void scale_kernel(void* __restrict__ g, i
     if (vec) {
         if (BF16G) {
             uint16_t* p = static_cast<uint16_t*>(g);
-            done = quad_loop(
+            done = quad_loop<kScale16Shape.unroll>(
                 n / 4, [&](int64_t q) { return widen4(ldh4(p + 4 * q)); },
                 [&](int64_t q, ef4 v) { sth4(p + 4 * q, narrow4(ef4{v[0] * coef, v[1] * coef, v[2] * coef, v[3] * coef})); });
         } else {
             float* p = static_cast<float*>(g);
-            done = quad_loop(
+            done = quad_loop<kScale32Shape.unroll>(
                 n / 4, [&](int64_t q) { return ld4(p + 4 * q); },
                 [&](int64_t q, ef4 v) { st4(p + 4 * q, ef4{v[0] * coef, v[1] * coef, v[2] * coef, v[3] * coef}); });
         }
@@ -128,10 +167,13 @@ __global__ __launch_bounds__(kEwBlock) void scale_kernel(void* __restrict__ g, i
     }
 }
 
-static unsigned ew_blocks(int64_t n) {
+// Blocks for n elements: one quad per thread per unrolled slot, capped at
+// the shape's blocks per CU.
+static unsigned ew_blocks(int64_t n, EwShape sh) {
     const DeviceInfo& dev = device_info();
-    const int64_t want = (n + (int64_t)kEwBlock * 4 * kEwUnroll - 1) / ((int64_t)kEwBlock * 4 * kEwUnroll);
-    return (unsigned)std::max<int64_t>(1, std::min<int64_t>(want, (int64_t)dev.cus * 8));
+    const int64_t per_block = (int64_t)kEwBlock * 4 * sh.unroll;
+    const int64_t want = (n + per_block - 1) / per_block;
+    return (unsigned)std::max<int64_t>(1, std::min<int64_t>(want, (int64_t)dev.cus * sh.bpc));
 }
 
 }  // namespace ely
@@ -146,7 +188,7 @@ int ely_cast_bf16(const float* x, uint16_t* out, int64_t n, void* stream) {
         if (n == 0) return;
         if (!x || !out) fail(ELY_EINVAL, "ely_cast_bf16: null pointer");
         const int vec = aligned16(x) && (reinterpret_cast<uintptr_t>(out) % 8 == 0);
-        hipLaunchKernelGGL(cast_bf16_kernel, dim3(ew_blocks(n)), dim3(kEwBlock), 0, static_cast<hipStream_t>(stream),
+        hipLaunchKernelGGL(cast_bf16_kernel, dim3(ew_blocks(n, kCastShape)), dim3(kEwBlock), 0, static_cast<hipStream_t>(stream),
                            x, out, n, vec);
         check_launch("cast_bf16_kernel");
     });
@@ -161,9 +203,9 @@ int ely_fold_add(float* acc, const void* g, int32_t g_dtype, int64_t n, void* st
         const int vec = aligned16(acc) && (reinterpret_cast<uintptr_t>(g) % (g_dtype == ELY_BF16 ? 8 : 16) == 0);
         hipStream_t s = static_cast<hipStream_t>(stream);
         if (g_dtype == ELY_BF16)
-            hipLaunchKernelGGL(fold_add_kernel<true>, dim3(ew_blocks(n)), dim3(kEwBlock), 0, s, acc, g, n, vec);
+            hipLaunchKernelGGL(fold_add_kernel<true>, dim3(ew_blocks(n, kFoldShape)), dim3(kEwBlock), 0, s, acc, g, n, vec);
         else
-            hipLaunchKernelGGL(fold_add_kernel<false>, dim3(ew_blocks(n)), dim3(kEwBlock), 0, s, acc, g, n, vec);
+            hipLaunchKernelGGL(fold_add_kernel<false>, dim3(ew_blocks(n, kFoldShape)), dim3(kEwBlock), 0, s, acc, g, n, vec);
         check_launch("fold_add_kernel");
     });
 }
@@ -179,10 +221,10 @@ int ely_scale_inplace(const ely_tensor* ts, int32_t n, const float* coef_dev, vo
             if (t.numel == 0) continue;
             const int vec = reinterpret_cast<uintptr_t>(t.ptr) % (t.dtype == ELY_BF16 ? 8 : 16) == 0;
             if (t.dtype == ELY_BF16)
-                hipLaunchKernelGGL(scale_kernel<true>, dim3(ew_blocks(t.numel)), dim3(kEwBlock), 0, s, t.ptr, t.numel,
+                hipLaunchKernelGGL(scale_kernel<true>, dim3(ew_blocks(t.numel, kScale16Shape)), dim3(kEwBlock), 0, s, t.ptr, t.numel,
                                    vec, coef_dev);
             else if (t.dtype == ELY_F32)
-                hipLaunchKernelGGL(scale_kernel<false>, dim3(ew_blocks(t.numel)), dim3(kEwBlock), 0, s, t.ptr, t.numel,
+                hipLaunchKernelGGL(scale_kernel<false>, dim3(ew_blocks(t.numel, kScale32Shape)), dim3(kEwBlock), 0, s, t.ptr, t.numel,
                                    vec, coef_dev);
             else
                 fail(ELY_EINVAL, "ely_scale_inplace: dtype");

@@ -74,3 +74,36 @@ def test_step_unit_steps_only_its_unit():
     assert all(p.grad is None for p in ps)
     with pytest.raises(ValueError, match="outside"):
         pieces.step_unit(opt, [torch.zeros(3, device="cuda", requires_grad=True)], [torch.zeros(3, device="cuda")])
+
+
+def test_elementwise_passes_over_several_grid_strides():
+    """fold_add and the clip's in-place scale over 9M elements, several
+    strides of every kernel's persistent grid, on aligned views and views one
+    element off (the scalar path), bit for bit against torch on the GPU:
+    a + widen(g) and g * coef are each one fp32 rounding (then one bf16
+    rounding for a bf16 g)."""
+    from elysium_wan_amd import _lib, pieces
+
+    L = _lib.load()
+    n = 9_000_003
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    acc0 = torch.randn(n + 1, device="cuda", generator=gen)
+    gf = torch.randn(n + 1, device="cuda", generator=gen)
+    gb = torch.randn(n + 1, device="cuda", generator=gen).bfloat16()
+    coef = torch.tensor([0.3712], device="cuda")
+    for off in (0, 1):
+        for g in (gb, gf):
+            say("fold_add", g.dtype, "offset", off)
+            a = acc0[off:].clone() if off == 0 else acc0.clone()[off:]
+            want = a + g[off:].float()
+            pieces.fold_add(a, g[off:])
+            assert torch.equal(a, want)
+            say("scale_inplace", g.dtype, "offset", off)
+            h = g.clone()[off:]
+            want = (h.float() * coef).to(g.dtype)
+            _lib.check(L.ely_scale_inplace(_lib.tensor_array([h]), 1, coef.data_ptr(), _lib.stream_ptr(h.device)), "scale")
+            assert torch.equal(bits_t(h), bits_t(want))
+
+
+def bits_t(t: torch.Tensor) -> torch.Tensor:
+    return t.view(torch.int16) if t.dtype == torch.bfloat16 else t.view(torch.int32)
