@@ -31,6 +31,7 @@ import json
 import os
 import sys
 import time
+from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
 import torch
@@ -685,11 +686,28 @@ def cpu_context(sample_elems: int = 1 << 25):
         torch.set_num_threads(threads0)
     x = (np.random.default_rng(1).standard_normal((4096, D_MODEL)) ).astype(np.float32)
     xb = O.f32_to_bf16_bits(x).reshape(x.shape)
-    t0 = time.perf_counter()
-    O.quantize(xb, "e4m3")
-    dt = time.perf_counter() - t0
-    out["oracle_fp8_quantize_GBs_1t"] = xb.size * CODEC_BYTES_PER_ELEM / dt / 1e9
-    out["sample"] = f"torch AdamW over {sample_elems} fp32 elements (threads: 1 and {threads0}); oracle quantize of [4096, {D_MODEL}] bf16"
+    rng = np.random.default_rng(2)
+    p = (rng.standard_normal(sample_elems) * 0.02).astype(np.float32)
+    g = O.f32_to_bf16_bits((rng.standard_normal(sample_elems) * 1e-4).astype(np.float32))
+    m = np.zeros(sample_elems, np.float32)
+    v = np.zeros(sample_elems, np.float32)
+    cp = np.zeros(sample_elems, np.uint16)
+    consts = O.host_adamw_consts(LR, BETAS, EPS, WD, 1)
+    for threads in sorted({1, threads0}):
+        # the oracle's C calls release the GIL: `threads` Python threads on
+        # disjoint slices run on that many cores
+        cuts = np.linspace(0, sample_elems, threads + 1).astype(np.int64)
+        spans = list(zip(cuts[:-1], cuts[1:]))
+        rows = np.linspace(0, xb.shape[0], threads + 1).astype(np.int64)
+        with ThreadPoolExecutor(threads) as ex:
+            t0 = time.perf_counter()
+            list(ex.map(lambda s: O.adamw_host(p[s[0]:s[1]], g[s[0]:s[1]], m[s[0]:s[1]], v[s[0]:s[1]], consts, True, 1.0, cp[s[0]:s[1]]), spans))
+            out[f"oracle_adamw_params_per_s_{threads}t"] = sample_elems / (time.perf_counter() - t0)
+            t0 = time.perf_counter()
+            list(ex.map(lambda r: O.quantize(xb[r[0]:r[1]], "e4m3"), zip(rows[:-1], rows[1:])))
+            out[f"oracle_fp8_quantize_GBs_{threads}t"] = xb.size * CODEC_BYTES_PER_ELEM / (time.perf_counter() - t0) / 1e9
+    out["sample"] = (f"torch AdamW and the oracle's HostAdamW (bf16 grads + bf16 copy) over {sample_elems} fp32 elements, "
+                     f"oracle quantize of [4096, {D_MODEL}] bf16; threads 1 and {threads0} (torch's count)")
     return out
 
 
