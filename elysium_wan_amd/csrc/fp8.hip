@@ -52,6 +52,15 @@
 #ifndef ELY_Q_BATCH
 #define ELY_Q_BATCH 1  // register paths: vectors per lane per load batch (0: the whole row at once)
 #endif
+#ifndef ELY_RECOVER_KEEP_VPL
+#define ELY_RECOVER_KEEP_VPL 16  // longest rows (vectors per lane) whose image reuses the test's codes
+#endif
+#ifndef ELY_RECOVER_BATCH
+#define ELY_RECOVER_BATCH ELY_Q_BATCH  // recover register path: vectors per lane per load batch (0: all)
+#endif
+#ifndef ELY_RECOVER_WHOLE_VPL
+#define ELY_RECOVER_WHOLE_VPL 8  // recover register path: rows of this many vectors per lane or more load at once
+#endif
 
 namespace ely {
 
@@ -59,6 +68,7 @@ constexpr int kQBlock = 256;                   // 4 waves, one row (or segment) 
 constexpr int kWavesPerBlock = kQBlock / kWave;
 constexpr int64_t kSegElems = 2048;            // split-path segment, elements
 constexpr int64_t kDeqSegCodes = ELY_DEQ_SEG;  // dequantize segment, codes
+constexpr int kRecoverKeepVpl = ELY_RECOVER_KEEP_VPL;
 constexpr int kFastK = 110;                    // |k| bound of the instruction path
 
 // ----------------------------------------------------------- element helpers
@@ -797,17 +807,9 @@ __global__ __launch_bounds__(kQBlock) void quant_k_kernel(const void* __restrict
 
 // ---------------------------------------------- recover + image, registers
 
-// exact_at for a non-finite element of a row whose candidates are all on the
-// instruction path (|c| <= 112, so 2^+-c is finite and nonzero in either
-// dtype): the restatement turns NaN into a NaN code (never equal) and Inf
-// into a NaN code for e4m3 (no Inf there) or back into the same Inf for e5m2.
-template <int FMT>
-__device__ __forceinline__ bool exact_nonfinite(float v) {
-    return FMT == kE5M2 && __builtin_isinf(v);
-}
-
-// The first exact candidate of a row outside the instruction path, element
-// by element through the restatement, or -1 (the recover_mask_kernel test).
+// The first exact candidate of a row outside the register test (a NaN or Inf
+// in the row, or candidates outside the instruction path), element by
+// element through the restatement, or -1 (the recover_mask_kernel test).
 template <int FMT, bool BF16>
 __device__ __forceinline__ int recover_slow_row(const void* t, int64_t row, int64_t cols, int base, int lane) {
 #pragma unroll 1
@@ -821,20 +823,56 @@ __device__ __forceinline__ int recover_slow_row(const void* t, int64_t row, int6
     return -1;
 }
 
+// One candidate exponent c over a row of finite elements held in registers:
+// every element's code at 2^-c (packed four to a word, as quant_vec_fast
+// packs them) into `codes`, and whether every element of this lane decodes
+// back to itself.
+template <int FMT, bool BF16, int VPL>
+__device__ __forceinline__ bool recover_candidate(const uint4 (&buf)[VPL], int c, uint32_t (&codes)[VPL][BF16 ? 2 : 1]) {
+    constexpr int EPV = BF16 ? 8 : 4;
+    const float s_down = __uint_as_float((uint32_t)(127 - c) << 23);
+    const float s_up = __uint_as_float((uint32_t)(127 + c) << 23);
+    bool ok = true;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+        float v[EPV];
+        unpack<BF16>(buf[j], v);  // lanes past the end hold zeros: exact at any c
+#pragma unroll
+        for (int h = 0; h < EPV; h += 4) {
+            uint32_t w = cvt_pk_fp8<FMT, false>(v[h] * s_down, v[h + 1] * s_down, 0u);
+            w = cvt_pk_fp8<FMT, true>(v[h + 2] * s_down, v[h + 3] * s_down, w);
+            codes[j][h / 4] = w;
+            float b[4];
+            cvt_pk_f32<FMT, false>(w, b[0], b[1]);
+            cvt_pk_f32<FMT, true>(w, b[2], b[3]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                ok = ok & (b[e] * s_up == v[h + e]);
+            }
+        }
+    }
+    return ok;
+}
+
 // One wave per row held in registers (rows of up to kWave * VPL vectors,
 // 16-byte aligned): |x|max, the base exponent, the candidates in the
 // reference's order, each one wave vote over the registers (the base
 // candidate is the only one a recipe round trip usually needs), then, when
-// q is given, the row's wire image from the same registers with the exponent
-// found: one read of t and one write of q per element.  A row with no exact
-// candidate counts as bad and keeps base + 2 (fp8.py:82-93).
+// q is given, the row's wire image with the exponent found: one read of t
+// and one write of q per element.  A row with no exact candidate counts as
+// bad and keeps base + 2 (fp8.py:82-93), the last candidate tested, so in
+// either case the codes the last test computed are the image of a row
+// without NaN or Inf (the instruction equals the restatement there).
 template <int FMT, bool BF16, int VPL>
 __global__ __launch_bounds__(kQBlock) void recover_rows_kernel(const void* __restrict__ t, int64_t rows, int64_t cols,
                                                                int32_t* __restrict__ k, uint8_t* __restrict__ q,
                                                                unsigned long long* __restrict__ bad) {
     constexpr int EPV = BF16 ? 8 : 4;
     constexpr int ESZ = BF16 ? 2 : 4;
-    constexpr int QB = (ELY_Q_BATCH <= 0 || ELY_Q_BATCH > VPL) ? VPL : ELY_Q_BATCH;
+    // long rows leave few waves per SIMD (registers), so each wave keeps its
+    // whole row in flight; short rows batch their loads
+    constexpr int QB =
+        (VPL >= ELY_RECOVER_WHOLE_VPL || ELY_RECOVER_BATCH <= 0 || ELY_RECOVER_BATCH > VPL) ? VPL : ELY_RECOVER_BATCH;
     const int lane = threadIdx.x & (kWave - 1);
     const int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + wave_uniform(threadIdx.x / kWave);
     if (row >= rows) return;  // whole waves leave; the kernel has no block barrier
@@ -858,35 +896,23 @@ __global__ __launch_bounds__(kQBlock) void recover_rows_kernel(const void* __res
         if (QB < VPL) __builtin_amdgcn_sched_barrier(0);
     }
     amax = wave_max_u32(amax);
-    const int base = scale_exp_from_amax<FMT>(to_f32_bits<BF16>(amax));
+    const uint32_t amax_bits = to_f32_bits<BF16>(amax);
+    const bool finite_row = amax_bits < 0x7F800000u;  // NaN bits sort above Inf's
+    const int base = scale_exp_from_amax<FMT>(amax_bits);
     int chosen = -1;
-    if (base - 2 >= -kFastK && base + 2 <= kFastK) {
+    bool have_codes = false;
+    uint32_t codes[VPL][BF16 ? 2 : 1];
+    if (finite_row && base - 2 >= -kFastK && base + 2 <= kFastK) {
 #pragma unroll 1
         for (int i = 0; i < 5; ++i) {
-            const int c = base + kDeltas[i];
-            const float s_down = __uint_as_float((uint32_t)(127 - c) << 23);
-            const float s_up = __uint_as_float((uint32_t)(127 + c) << 23);
-            bool ok = true;
-#pragma unroll
-            for (int j = 0; j < VPL; ++j) {
-                float v[EPV];
-                unpack<BF16>(buf[j], v);  // lanes past the end hold zeros: exact at any c
-#pragma unroll
-                for (int e = 0; e < EPV; e += 2) {
-                    const uint32_t code = cvt_pk_fp8<FMT, false>(v[e] * s_down, v[e + 1] * s_down, 0u);
-                    float b0, b1;
-                    cvt_pk_f32<FMT, false>(code, b0, b1);
-                    const bool x0 = __builtin_isfinite(v[e]) ? b0 * s_up == v[e] : exact_nonfinite<FMT>(v[e]);
-                    const bool x1 = __builtin_isfinite(v[e + 1]) ? b1 * s_up == v[e + 1] : exact_nonfinite<FMT>(v[e + 1]);
-                    ok = ok && x0 && x1;
-                }
-            }
-            if (wave_and_u32(ok ? 1u : 0u)) {
+            if (wave_and_u32(recover_candidate<FMT, BF16, VPL>(buf, base + kDeltas[i], codes) ? 1u : 0u)) {
                 chosen = i;
                 break;
             }
         }
+        have_codes = VPL <= kRecoverKeepVpl;  // a compile-time false drops the codes
     } else {
+        // rows holding NaN or Inf, or outside the instruction's exponent range
         chosen = recover_slow_row<FMT, BF16>(t, row, cols, base, lane);
     }
     const int kk = chosen >= 0 ? base + kDeltas[chosen] : base + 2;
@@ -897,7 +923,15 @@ __global__ __launch_bounds__(kQBlock) void recover_rows_kernel(const void* __res
     if (!q) return;
     // the image with the exponent found, as quant_k_kernel writes it
     uint8_t* qr = q + row * cols;
-    if (kk >= -kFastK && kk <= kFastK) {
+    if (have_codes) {
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) {
+            const int64_t vi = lane + (int64_t)kWave * j;
+            if (vi >= nvec) continue;
+            if (BF16) st_vec2(qr + vi * EPV, make_uint2(codes[j][0], codes[j][BF16 ? 1 : 0]));
+            else st_u32(qr + vi * EPV, codes[j][0]);
+        }
+    } else if (kk >= -kFastK && kk <= kFastK) {
         const float s_down = __uint_as_float((uint32_t)(127 - kk) << 23);
 #pragma unroll
         for (int j = 0; j < VPL; ++j) {
