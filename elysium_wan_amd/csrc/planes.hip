@@ -29,7 +29,7 @@ namespace ely {
 #define ELY_PLANES_BPC 4  // byte planes: blocks per compute unit
 #endif
 #ifndef ELY_NIBBLES_UNROLL
-#define ELY_NIBBLES_UNROLL 4  // nibble planes: vectors a lane keeps in flight
+#define ELY_NIBBLES_UNROLL 2  // nibble planes: vectors a lane keeps in flight
 #endif
 #ifndef ELY_NIBBLES_BPC
 #define ELY_NIBBLES_BPC 8  // nibble planes: blocks per compute unit
@@ -194,8 +194,45 @@ __device__ __forceinline__ float load_elem(const void* t, int64_t i) {
     return static_cast<const float*>(t)[i];
 }
 
-// Nibble index of element e within its byte: element 2i is the high half.
-__device__ __forceinline__ int nib_shift(int e) { return 8 * ((e / 2) % 4) + ((e & 1) ? 0 : 4); }
+// Four codes (element k in byte k of w) -> their nibble pairs as the planes
+// hold them, in the low 16 bits: hi byte 0 = c0 >> 4 << 4 | c1 >> 4, byte 1
+// the same of c2, c3; lo likewise with the low nibbles.
+__device__ __forceinline__ uint32_t hi_pairs(uint32_t w) {
+    const uint32_t t = w & 0xF0F0F0F0u;
+    const uint32_t u = t | (t >> 12);  // bytes 0 and 2 hold the pairs
+    return (u & 0xFFu) | ((u >> 8) & 0xFF00u);
+}
+__device__ __forceinline__ uint32_t lo_pairs(uint32_t w) {
+    const uint32_t t = w & 0x0F0F0F0Fu;
+    const uint32_t u = (t << 4) | (t >> 8);  // bytes 0 and 2 hold the pairs
+    return (u & 0xFFu) | ((u >> 8) & 0xFF00u);
+}
+
+// The inverse: two bytes of each plane (h, l, low 16 bits) -> the four
+// codes, element k in byte k.
+__device__ __forceinline__ uint32_t join_pairs(uint32_t h, uint32_t l) {
+    const uint32_t hx = (h & 0xFFu) | ((h & 0xFF00u) << 8);
+    const uint32_t hs = hx | (hx << 8);  // bytes h0, h0, h1, h1
+    const uint32_t lx = (l & 0xFFu) | ((l & 0xFF00u) << 8);
+    const uint32_t ls = lx | (lx << 8);
+    return (hs & 0x00F000F0u) | ((hs << 4) & 0xF000F000u) | ((ls >> 4) & 0x000F000Fu) | (ls & 0x0F000F00u);
+}
+
+// e4m3 codes of four floats, element k in byte k, and how many of them do
+// not convert back to themselves.  That test alone decides
+// representability: a NaN never equals, and no code decodes to Inf or to a
+// value beyond 448, so only the grid values of the instruction's exact
+// domain pass (where it is torch's rounding); the codes of the others are
+// never used (the encode is refused).
+__device__ __forceinline__ uint32_t e4m3_quad(float a, float b, float c, float d, uint32_t& nbad) {
+    uint32_t w = cvt_pk_fp8<kE4M3, false>(a, b, 0u);
+    w = cvt_pk_fp8<kE4M3, true>(c, d, w);
+    float ra, rb, rc, rd;
+    cvt_pk_f32<kE4M3, false>(w, ra, rb);
+    cvt_pk_f32<kE4M3, true>(w, rc, rd);
+    nbad += (ra != a) + (rb != b) + (rc != c) + (rd != d);
+    return w;
+}
 
 // Encode: a lane converts one 16-byte vector of t (8 bf16 or 4 fp32), so its
 // share of each nibble plane is EPL/2 bytes (4 or 2) and every load and
@@ -235,12 +272,10 @@ __global__ __launch_bounds__(kPBlock) void nibbles_encode_kernel(const void* __r
                 }
                 uint32_t hw = 0u, lw = 0u;
 #pragma unroll
-                for (int e = 0; e < EPL; ++e) {
-                    bool ok;
-                    const uint32_t code = e4m3_exact(f[e], ok);
-                    nbad += ok ? 0u : 1u;
-                    hw |= (code >> 4) << nib_shift(e);
-                    lw |= (code & 0xFu) << nib_shift(e);
+                for (int e = 0; e < EPL; e += 4) {
+                    const uint32_t w = e4m3_quad(f[e], f[e + 1], f[e + 2], f[e + 3], nbad);
+                    hw |= hi_pairs(w) << (4 * e);
+                    lw |= lo_pairs(w) << (4 * e);
                 }
                 if (BF16) {
                     __builtin_nontemporal_store(hw, (PL_G1 uint32_t*)(hi + vi * 4));
@@ -298,12 +333,7 @@ __global__ __launch_bounds__(kPBlock) void nibbles_decode_kernel(const uint8_t* 
             for (int u = 0; u < kNUnroll; ++u) {
                 const int64_t q = base + u * T;
                 if (q >= nq) continue;
-                uint32_t word = 0;  // codes of elements 4q .. 4q+3, one per byte
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    const int sh = nib_shift(k);
-                    word |= ((((h[u] >> sh) & 0xFu) << 4) | ((l[u] >> sh) & 0xFu)) << (8 * k);
-                }
+                const uint32_t word = join_pairs(h[u], l[u]);  // codes of elements 4q .. 4q+3, one per byte
                 float a, b, c, d;
                 cvt_pk_f32<kE4M3, false>(word, a, b);
                 cvt_pk_f32<kE4M3, true>(word, c, d);

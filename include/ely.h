@@ -220,7 +220,8 @@ int ely_byteplanes_join(const uint8_t* planes, int64_t n, int32_t esz, void* out
  * element as 0.  Every element whose code does not convert back to it
  * exactly (NaN, Inf, beyond 448, off the e4m3 grid; -0 == 0 as in
  * torch.equal) adds 1 to *bad_dev (the caller zeroes it; the reference
- * asserts, which the Python layer does when the count is non-zero). */
+ * asserts, which the Python layer does when the count is non-zero).  The
+ * planes' nibbles for such elements are unspecified. */
 int ely_fp8_nibbles_encode(const void* t, int32_t t_dtype, int64_t n, uint8_t* hi, uint8_t* lo,
                            unsigned long long* bad_dev, void* stream);
 
