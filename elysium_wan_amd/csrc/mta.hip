@@ -3,7 +3,8 @@
 //   (b) the fused clip + AdamW step with the bf16 working copy.
 //
 // Work decomposition.  Every tensor is cut into fixed tiles (kAdamTile /
-// kNormTile elements; a tensor's last tile may be short) numbered
+// the norm tile of the call, kNormTile or, for lists under 2^29 elements,
+// kNormSmallTile; a tensor's last tile may be short) numbered
 // consecutively across the list, so the ragged list costs one launch on a
 // persistent grid.  AdamW: in round r block b takes tile r*G + b, so at any
 // moment the whole chip streams one small window of the shard (4,096-element
@@ -63,9 +64,18 @@ namespace ely {
 #ifndef ELY_NORM_BPC
 #define ELY_NORM_BPC 24          // grad-norm blocks (of 4 waves) per compute unit
 #endif
+#ifndef ELY_NORM_SMALL_TILE
+#define ELY_NORM_SMALL_TILE 4096  // grad-norm tile of a small list (more waves than its large tiles)
+#endif
+#ifndef ELY_NORM_SMALL_LIMIT
+#define ELY_NORM_SMALL_LIMIT (1LL << 29)  // lists of fewer elements take the small tile
+#endif
 
 constexpr int64_t kAdamTile = ELY_ADAM_TILE;
 constexpr int64_t kNormTile = ELY_NORM_TILE;  // elements per grad-norm tile (one wave): fixes the summation order
+constexpr int64_t kNormSmallTile = ELY_NORM_SMALL_TILE;
+static_assert(kNormTile % (64 * 8 * ELY_NORM_UNROLL) == 0 && kNormSmallTile % (64 * 8 * ELY_NORM_UNROLL) == 0,
+              "a grad-norm tile is whole unrolled rounds of 8-element groups");
 constexpr int kNormUnroll = ELY_NORM_UNROLL;
 constexpr int kBlock = 256;
 constexpr int kFinalThreads = 1024;
@@ -174,11 +184,11 @@ __device__ __forceinline__ float raw8_sumsq(const Raw8<BF16, FOLD>& r) {
 }
 
 // Sum of squares of one full, aligned tile: lane l owns the 8-element groups
-// j*64 + l, j = 0..31, added in order; kNormUnroll groups' raw vectors are
+// j*64 + l, j = 0..TILE/512-1, added in order; kNormUnroll groups' raw vectors are
 // loaded before the first of them is summed.
-template <bool BF16, bool FOLD>
+template <bool BF16, bool FOLD, int64_t TILE>
 __device__ __forceinline__ double tile_sumsq_vec(const NormDesc& d, int64_t e0, int lane) {
-    constexpr int G = (int)(kNormTile / (kWave * 8));
+    constexpr int G = (int)(TILE / (kWave * 8));
     constexpr int U = kNormUnroll;
     static_assert(G % U == 0, "unroll divides the groups of a tile");
     double acc = 0.0;
@@ -212,7 +222,7 @@ __device__ __forceinline__ void load8_any(const NormDesc& d, int64_t i, int64_t 
 // (the tile loop is then compiled for that dtype only, which keeps the
 // kernel's registers, and so its occupancy, to what that dtype needs), or -1
 // for a mixed list, dispatched per tile.
-template <bool FOLD, int DT>
+template <bool FOLD, int DT, int64_t TILE>
 __global__ __launch_bounds__(kBlock) void norm_partials_kernel(const NormDesc* __restrict__ desc, int32_t n,
                                                                int64_t total_tiles, double* __restrict__ partials) {
     const int lane = threadIdx.x & (kWave - 1);
@@ -228,15 +238,15 @@ __global__ __launch_bounds__(kBlock) void norm_partials_kernel(const NormDesc* _
     for (int64_t tile = t0; tile < t1; tile += tstep) {
         while (ti + 1 < n && desc[ti + 1].tile_begin <= tile) ++ti;
         const NormDesc d = desc[ti];
-        const int64_t e0 = (tile - d.tile_begin) * kNormTile;
-        const int64_t e1 = min(e0 + kNormTile, d.numel);
+        const int64_t e0 = (tile - d.tile_begin) * TILE;
+        const int64_t e1 = min(e0 + TILE, d.numel);
         double acc = 0.0;
         // lane l owns groups j*64 + l of 8 elements, in the same order on both paths
-        if (d.aligned && e1 - e0 == kNormTile) {
-            if (DT == ELY_BF16 || (DT < 0 && d.dtype == ELY_BF16)) acc = tile_sumsq_vec<true, FOLD>(d, e0, lane);
-            else acc = tile_sumsq_vec<false, FOLD>(d, e0, lane);
+        if (d.aligned && e1 - e0 == TILE) {
+            if (DT == ELY_BF16 || (DT < 0 && d.dtype == ELY_BF16)) acc = tile_sumsq_vec<true, FOLD, TILE>(d, e0, lane);
+            else acc = tile_sumsq_vec<false, FOLD, TILE>(d, e0, lane);
         } else {
-            for (int j = 0; j < (int)(kNormTile / (kWave * 8)); ++j) {
+            for (int j = 0; j < (int)(TILE / (kWave * 8)); ++j) {
                 float x[8];
                 load8_any<FOLD>(d, e0 + ((int64_t)j * kWave + lane) * 8, e1, x);
                 acc += (double)sq8(x);
@@ -283,13 +293,34 @@ __global__ __launch_bounds__(kFinalThreads) void norm_final_kernel(const double*
     }
 }
 
-static int64_t norm_tiles(const ely_tensor* grads, int32_t n) {
+// The tile of one call, a function of the list alone (never of the grid, so
+// the result stays bitwise reproducible): lists under ELY_NORM_SMALL_LIMIT
+// elements take the small tile, which gives them enough waves to fill the
+// chip.
+static int64_t norm_tile(const ely_tensor* grads, int32_t n) {
+    int64_t total = 0;
+    for (int32_t i = 0; i < n; ++i) total += std::max<int64_t>(grads[i].numel, 0);
+    return total < ELY_NORM_SMALL_LIMIT ? kNormSmallTile : kNormTile;
+}
+
+static int64_t norm_tiles(const ely_tensor* grads, int32_t n, int64_t tile) {
     int64_t t = 0;
-    for (int32_t i = 0; i < n; ++i) t += (grads[i].numel + kNormTile - 1) / kNormTile;
+    for (int32_t i = 0; i < n; ++i) t += (std::max<int64_t>(grads[i].numel, 0) + tile - 1) / tile;
     return t;
 }
 
 static size_t norm_table_bytes(int32_t n) { return align_up((size_t)n * sizeof(NormDesc), 256); }
+
+typedef void (*NormKernel)(const NormDesc*, int32_t, int64_t, double*);
+
+template <int64_t TILE>
+static NormKernel pick_norm(bool fold, int dt) {
+    if (fold)
+        return dt == ELY_BF16 ? norm_partials_kernel<true, ELY_BF16, TILE>
+                              : dt == ELY_F32 ? norm_partials_kernel<true, ELY_F32, TILE> : norm_partials_kernel<true, -1, TILE>;
+    return dt == ELY_BF16 ? norm_partials_kernel<false, ELY_BF16, TILE>
+                          : dt == ELY_F32 ? norm_partials_kernel<false, ELY_F32, TILE> : norm_partials_kernel<false, -1, TILE>;
+}
 
 // ------------------------------------------------------------- (b) AdamW
 
@@ -555,6 +586,7 @@ static void grad_norm_impl(const ely_tensor* accs, const ely_tensor* grads, int3
     hipStream_t s = static_cast<hipStream_t>(stream);
     std::vector<NormDesc> table;
     table.reserve(n);
+    const int64_t tile = norm_tile(grads, n);
     int64_t tiles = 0;
     for (int32_t i = 0; i < n; ++i) {
         if (grads[i].numel == 0) continue;
@@ -566,7 +598,7 @@ static void grad_norm_impl(const ely_tensor* accs, const ely_tensor* grads, int3
         d.dtype = grads[i].dtype;
         d.aligned = aligned16(grads[i].ptr) && (!accs || aligned16(accs[i].ptr)) ? 1 : 0;
         table.push_back(d);
-        tiles += (d.numel + kNormTile - 1) / kNormTile;
+        tiles += (d.numel + tile - 1) / tile;
     }
     char* ws = static_cast<char*>(workspace);
     NormDesc* dtable = reinterpret_cast<NormDesc*>(ws);
@@ -578,14 +610,8 @@ static void grad_norm_impl(const ely_tensor* accs, const ely_tensor* grads, int3
         int dt = table[0].dtype;
         for (const NormDesc& d : table)
             if (d.dtype != dt) dt = -1;
-        typedef void (*NormKernel)(const NormDesc*, int32_t, int64_t, double*);
-        NormKernel kern;
-        if (accs)
-            kern = dt == ELY_BF16 ? norm_partials_kernel<true, ELY_BF16>
-                                  : dt == ELY_F32 ? norm_partials_kernel<true, ELY_F32> : norm_partials_kernel<true, -1>;
-        else
-            kern = dt == ELY_BF16 ? norm_partials_kernel<false, ELY_BF16>
-                                  : dt == ELY_F32 ? norm_partials_kernel<false, ELY_F32> : norm_partials_kernel<false, -1>;
+        const NormKernel kern = tile == kNormTile ? pick_norm<kNormTile>(accs != nullptr, dt)
+                                                  : pick_norm<kNormSmallTile>(accs != nullptr, dt);
         hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(kBlock), 0, s, dtable, (int32_t)table.size(), tiles,
                            partials);
         check_launch("norm_partials_kernel");
@@ -673,7 +699,8 @@ extern "C" {
 
 int64_t ely_grad_norm_workspace_bytes(const ely_tensor* grads, int32_t n) {
     if (n < 0 || (n > 0 && !grads)) return -1;
-    return (int64_t)(norm_table_bytes(n) + align_up((size_t)std::max<int64_t>(norm_tiles(grads, n), 1) * 8, 256));
+    return (int64_t)(norm_table_bytes(n) +
+                     align_up((size_t)std::max<int64_t>(norm_tiles(grads, n, norm_tile(grads, n)), 1) * 8, 256));
 }
 
 int ely_grad_norm(const ely_tensor* grads, int32_t n, float max_norm, ely_norm_result* out_dev, void* workspace,

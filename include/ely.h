@@ -74,9 +74,10 @@ int64_t ely_grad_norm_workspace_bytes(const ely_tensor* grads, int32_t n);
  * coefficient clip_grad_norm_ derives from it.  Replaces the norm of
  * TORCH/nn/utils/clip_grad.py:50-108 and the coefficient of :160-169 (the
  * reference itself never clips; its optimizer is runtime/optim.py:45-54).
- * Each fixed 16,384-element tile is reduced in a fixed lane order (fp32
- * squares of at most 8 elements, fp64 above), tiles in index order: the
- * result is bitwise identical across runs and grid sizes.  coef =
+ * Each fixed tile (16,384 elements; 4,096 when the list holds fewer than
+ * 2^29 elements) is reduced in a fixed lane order (fp32 squares of at most 8
+ * elements, fp64 above), tiles in index order: the result is a function of
+ * the list alone, bitwise identical across runs and grid sizes.  coef =
  * min(max_norm * (1/(norm + 1e-6)), 1) in fp32 when max_norm > 0, else 1. */
 int ely_grad_norm(const ely_tensor* grads, int32_t n, float max_norm,
                   ely_norm_result* out_dev, void* workspace, int64_t ws_bytes, void* stream);
