@@ -592,6 +592,135 @@ def traffic_summary(fetch_dir: str, write_dir: str, command: str) -> None:
     print("\n".join(lines))
 
 
+def _dispatches(trace_dir: str):
+    """(kernel name, duration ns) of every dispatch in a rocprofv3
+    --kernel-trace csv directory, in dispatch order."""
+    import csv
+    import glob
+
+    rows = []
+    for path in glob.glob(os.path.join(trace_dir, "**", "*kernel_trace.csv"), recursive=True):
+        with open(path) as f:
+            rows += list(csv.DictReader(f))
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    return [(r["Kernel_Name"], int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) for r in rows]
+
+
+def _runs(disp, names):
+    """Maximal runs of consecutive dispatches of one of `names` (other kernels
+    in between end a run) -> [(name, [durations])]."""
+    runs = []
+    for name, ns in disp:
+        if name not in names:
+            if runs and runs[-1][0] is not None:
+                runs.append((None, []))
+            continue
+        if runs and runs[-1][0] == name:
+            runs[-1][1].append(ns)
+        else:
+            runs.append((name, [ns]))
+    return [r for r in runs if r[0] is not None]
+
+
+def _row(label, ds):
+    return f"| {label} | {len(ds)} | {sum(ds) / len(ds):,.0f} | {min(ds):,} | {max(ds):,} |"
+
+
+def trace_summary(step_dir: str, codec_dir: str, bench_json: str | None) -> None:
+    """Kernel durations from two rocprofv3 --kernel-trace runs: the C1
+    optimizer step (`bench.py --no-cpu --no-codec --no-extra`) and the C1
+    codec (`bench.py --no-optimizer --codec c1`).  The codec's quantize and
+    fused round trip are one kernel (quant_rows_kernel, with or without the
+    dequantized output), told apart by bench_codec's launch order: per
+    format, quantize launches, dequantize launches, then as many round trips
+    as dequantizes.  Writes profiles/c1_step_kernel_trace.md and
+    profiles/codec_c1_kernel_trace.md; with `bench_json` (the line of a
+    bench.py run on the same box) the HIP-event figures are set beside."""
+    b = None
+    if bench_json:
+        with open(bench_json) as f:
+            b = json.loads(f.read().strip().splitlines()[-1])
+    n = N_BLOCKS * (12 * D_MODEL * D_MODEL + 13 * D_MODEL)
+    step = _dispatches(step_dir)
+    by = {}
+    for name, ns in step:
+        by.setdefault(name, []).append(ns)
+    lines = [
+        "# Kernel durations, C1 optimizer step (the roofline kernel)",
+        "",
+        "Commands (on one MI355X, from the repository root):",
+        "",
+        "    rocprofv3 --kernel-trace --stats -T -d <step dir> -o kt --output-format csv -- python3 bench.py --no-cpu --no-codec --no-extra",
+        "    python bench.py --trace-summary <step dir> <codec dir> [--bench-json <bench.py line>]",
+        "",
+        "Workload: config C1's shard (16 GPT blocks at d = 2560, 192 tensors,",
+        f"{n:,} fp32 params, bf16 grads N(0, 1e-4), bf16 working copy, AdamW",
+        "lr 3e-4, betas 0.9/0.95, eps 1e-8, weight decay 0.1, clip 1.0): warmup and",
+        "timed optimizer steps, then event-timed launches of each kernel.",
+        "",
+        "| kernel | calls | average (ns) | min (ns) | max (ns) |",
+        "|---|---|---|---|---|",
+    ]
+    lines += [_row(k, by[k]) for k in ("adamw_kernel", "norm_partials_kernel", "norm_final_kernel") if k in by]
+    if "adamw_kernel" in by:
+        avg = sum(by["adamw_kernel"]) / len(by["adamw_kernel"]) / 1e6
+        lines += ["", f"adamw_kernel: {n * ADAM_BYTES_PER_ELEM / 1e9:.2f} GB ({ADAM_BYTES_PER_ELEM} B/elem) / {avg:.3f} ms = "
+                  f"{n * ADAM_BYTES_PER_ELEM / avg / 1e6:,.0f} GB/s, {n * ADAM_BYTES_PER_ELEM / avg / 1e6 / HBM_PEAK_GBS:.3f} of 8 TB/s."]
+        if b:
+            ev = b["kernels"]["adamw_ms"]
+            lines += [f"bench.py's HIP-event average on the same box: {ev:.3f} ms ({abs(avg - ev) / ev * 100:.1f} % apart)."]
+    with open(os.path.join(HERE, "profiles", "c1_step_kernel_trace.md"), "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+    runs = _runs(_dispatches(codec_dir), ("quant_rows_kernel", "dequant_flat_kernel"))
+    kinds = {"quantize": [], "dequantize": [], "roundtrip": []}
+    rt_left = 0  # quant_rows_kernel launches still due as round trips
+    for name, ds in runs:
+        if name == "dequant_flat_kernel":
+            kinds["dequantize"] += ds
+            rt_left = len(ds)  # the round trips follow, as many as the dequantizes
+        else:
+            kinds["roundtrip"] += ds[:rt_left]
+            kinds["quantize"] += ds[rt_left:]
+            rt_left = max(0, rt_left - len(ds))
+    na = 8 * 2048 * D_MODEL
+    lines = [
+        "# Kernel durations, fp8 codec on C1's activation",
+        "",
+        "Commands (on one MI355X, from the repository root):",
+        "",
+        "    rocprofv3 --kernel-trace --stats -T -d <codec dir> -o kc --output-format csv -- python3 bench.py --no-optimizer --codec c1",
+        "    python bench.py --trace-summary <step dir> <codec dir> [--bench-json <bench.py line>]",
+        "",
+        "Workload: config C1's boundary activation [8, 2048, 2560] bf16 (N(0, 1) with",
+        "0.1% of the elements x50), per-row scaling (one exponent per 2,560-element",
+        "row), e4m3 and e5m2, rotating through 8 copies so that no launch reads from",
+        f"the 256 MB MALL.  Algorithmic traffic per launch: {na:,} x 3 B = {na * 3 / 1e6:.1f} MB",
+        f"for quantize and dequantize, x 4 B = {na * 4 / 1e6:.1f} MB for the fused round trip.",
+        "quant_rows_kernel serves quantize and the round trip; the launches are",
+        "split by bench.py's order (per format: quantize, dequantize, then as many",
+        "round trips as dequantizes).",
+        "",
+        "| launches | calls | average (ns) | min (ns) | max (ns) | kernel-time rate |",
+        "|---|---|---|---|---|---|",
+    ]
+    per = {"quantize": 3, "dequantize": 3, "roundtrip": 4}
+    for kind, ds in kinds.items():
+        if ds:
+            avg = sum(ds) / len(ds)
+            lines.append(_row(kind, ds)[:-2] + f" | {na * per[kind] / avg / 1e3:.2f} TB/s |")
+    if b:
+        c = b["fp8_codec"]["c1_per_row"]["e4m3"]
+        lines += ["", "bench.py's HIP-event averages (one launch between two events, so each also",
+                  f"holds the launch's dispatch latency): quantize {c['quantize_ms'] * 1e3:.1f} us ({c['quantize_GBs'] / 1e3:.2f} TB/s),",
+                  f"dequantize {c['dequantize_ms'] * 1e3:.1f} us ({c['dequantize_GBs'] / 1e3:.2f} TB/s), round trip "
+                  f"{c['roundtrip_ms'] * 1e3:.1f} us ({c['roundtrip_GBs'] / 1e3:.2f} TB/s)."]
+    with open(os.path.join(HERE, "profiles", "codec_c1_kernel_trace.md"), "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
 def bench_wire(device, stream, iters: int = 10):
     """The GPU half of the lossless boundary wires on C1's activation
     [8, 2048, 2560] bf16 (the host half, zlib, is not timed): the byte-plane
@@ -738,9 +867,14 @@ def main():
     ap.add_argument("--profile-pass", action="store_true", help="launch each measured kernel a few times, untimed, for rocprofv3 --pmc runs")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"), help="summarize two --pmc runs of --profile-pass into profiles/")
     ap.add_argument("--traffic-command", default="", help="the command line recorded in the traffic summary")
+    ap.add_argument("--trace-summary", nargs=2, metavar=("STEP_DIR", "CODEC_DIR"), help="summarize two rocprofv3 --kernel-trace runs into profiles/")
+    ap.add_argument("--bench-json", help="a bench.py output line from the same box, quoted beside the trace summary")
     args = ap.parse_args()
     if args.traffic_summary:
         traffic_summary(*args.traffic_summary, args.traffic_command)
+        return
+    if args.trace_summary:
+        trace_summary(*args.trace_summary, args.bench_json)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); run with --gpus 1", file=sys.stderr)
