@@ -92,6 +92,22 @@ def time_events(fn, iters, stream):
     return sum(s.elapsed_time(e) for s, e in zip(starts, ends)) / iters
 
 
+def time_back_to_back(fn, iters, stream):
+    """Average period (ms) of iters back-to-back launches of fn() between one
+    pair of HIP events on `stream`, after one untimed call: the launches
+    queue behind each other, so their dispatch latency overlaps the previous
+    launch's tail."""
+    fn(0)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i in range(iters):
+        fn(i)
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / iters
+
+
 def bench_optimizer(args, device, stream):
     params, grads = make_shard(device)
     log(f"C1 shard: {len(params)} tensors, {sum(p.numel() for p in params)} elements")
@@ -298,13 +314,15 @@ def _c4_inputs(device, seed):
     return {"activation": act, "gradient": grad}
 
 
-def bench_codec(device, stream, rows, cols, copies, iters=20, per_tensor=False, xs=None, fmts=("e4m3", "e5m2"), stats=False):
+def bench_codec(device, stream, rows, cols, copies, iters=20, per_tensor=False, xs=None, fmts=("e4m3", "e5m2"), stats=False,
+                back_to_back=False):
     """Quantize, dequantize and the fused round trip (bf16 <-> fp8, per-row
     or per-tensor) of a [rows, cols] activation, rotating through `copies` inputs so that
     launches stream from HBM rather than the 256 MB MALL. With `stats`, the
     round trip of the first input is also reported, outside the timed
     region: relative L2 error of dequantize(quantize(x)) against x, the
-    range of the exponents k, and SHA-256 digests of the fp8 bytes and k."""
+    range of the exponents k, and SHA-256 digests of the fp8 bytes and k.
+    With `back_to_back`, each leg is also timed as one queue of launches."""
     import hashlib
 
     from elysium_wan_amd import _lib
@@ -349,6 +367,13 @@ def bench_codec(device, stream, rows, cols, copies, iters=20, per_tensor=False, 
             "roundtrip_ms": r_ms,
             "roundtrip_GBs": n * ROUNDTRIP_BYTES_PER_ELEM / r_ms / 1e6,
         }
+        if back_to_back:
+            # the same launches queued back to back (one event pair around all)
+            out[fmt]["back_to_back_GBs"] = {
+                "quantize": n * CODEC_BYTES_PER_ELEM / time_back_to_back(quant, iters, stream) / 1e6,
+                "dequantize": n * CODEC_BYTES_PER_ELEM / time_back_to_back(deq, iters, stream) / 1e6,
+                "roundtrip": n * ROUNDTRIP_BYTES_PER_ELEM / time_back_to_back(rt, iters, stream) / 1e6,
+            }
         if stats:
             quant(0)
             deq(0)
@@ -908,7 +933,7 @@ def main():
             log("codec leg")
             codec = {}
             if args.codec in ("c1", "all"):
-                codec["c1_per_row"] = bench_codec(device, stream, 8 * 2048, D_MODEL, 8)
+                codec["c1_per_row"] = bench_codec(device, stream, 8 * 2048, D_MODEL, 8, back_to_back=True)
                 torch.cuda.empty_cache()
             if args.codec in ("c4", "all"):
                 codec["c4"] = bench_c4(device, stream)
