@@ -217,3 +217,51 @@ def test_a_missing_library_fails_loudly():
     ) % ROOT
     r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
     assert r.stdout.strip() == "raised True", r.stdout + r.stderr
+
+
+C_CALLER = r"""
+#include <stdio.h>
+#include <string.h>
+#include "ely.h"
+
+int main(void) {
+    ely_tensor g[2];
+    memset(g, 0, sizeof g);
+    g[0].numel = 16384 * 3 + 1;
+    g[0].dtype = ELY_BF16;
+    g[1].numel = 7;
+    g[1].dtype = ELY_F32;
+    int64_t ws = ely_grad_norm_workspace_bytes(g, 2);
+    int rc = ely_cast_bf16(NULL, NULL, -1, NULL);
+    printf("%d %d %lld %d %s\n", (int)ely_abi_version(), rc, (long long)(ws > 0 && ws % 256 == 0),
+           (int)(ely_adamw_workspace_bytes(-1) == -1), ely_last_error());
+    return 0;
+}
+"""
+
+
+def test_header_is_c_and_links_from_c(tmp_path):
+    """include/ely.h is a C header: a C11 program (gcc -std=c11 -pedantic
+    -Werror) includes it, links libelyhip.so and calls entry points that
+    need no GPU -- the binding a C, cgo or JNI caller would start from."""
+    import shutil
+    import subprocess
+
+    from elysium_wan_amd import _lib
+
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("no gcc")
+    so = _lib.LIB_PATH
+    src = tmp_path / "caller.c"
+    src.write_text(C_CALLER)
+    exe = tmp_path / "caller"
+    cmd = [gcc, "-std=c11", "-Wall", "-Wextra", "-pedantic", "-Werror", "-I", os.path.join(ROOT, "include"), str(src),
+           "-o", str(exe), so, f"-Wl,-rpath,{os.path.dirname(so)}"]
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    version, rc, ws_ok, neg_ok, msg = r.stdout.split(" ", 4)
+    assert (int(version), int(rc), int(ws_ok), int(neg_ok)) == (1, _lib.EINVAL, 1, 1)
+    assert "negative n" in msg
