@@ -858,10 +858,13 @@ def cpu_context(sample_elems: int = 1 << 25):
             list(ex.map(lambda s: O.adamw_host(p[s[0]:s[1]], g[s[0]:s[1]], m[s[0]:s[1]], v[s[0]:s[1]], consts, True, 1.0, cp[s[0]:s[1]]), spans))
             out[f"oracle_adamw_params_per_s_{threads}t"] = sample_elems / (time.perf_counter() - t0)
             t0 = time.perf_counter()
-            list(ex.map(lambda r: O.quantize(xb[r[0]:r[1]], "e4m3"), zip(rows[:-1], rows[1:])))
+            qk = list(ex.map(lambda r: O.quantize(xb[r[0]:r[1]], "e4m3"), zip(rows[:-1], rows[1:])))
             out[f"oracle_fp8_quantize_GBs_{threads}t"] = xb.size * CODEC_BYTES_PER_ELEM / (time.perf_counter() - t0) / 1e9
+            t0 = time.perf_counter()
+            list(ex.map(lambda c: O.dequantize(c[0], c[1], "e4m3", "bf16"), qk))
+            out[f"oracle_fp8_dequantize_GBs_{threads}t"] = xb.size * CODEC_BYTES_PER_ELEM / (time.perf_counter() - t0) / 1e9
     out["sample"] = (f"torch AdamW and the oracle's HostAdamW (bf16 grads + bf16 copy) over {sample_elems} fp32 elements, "
-                     f"oracle quantize of [4096, {D_MODEL}] bf16; threads 1 and {threads0} (torch's count)")
+                     f"oracle quantize and dequantize (-> bf16) of [4096, {D_MODEL}] bf16; threads 1 and {threads0} (torch's count)")
     return out
 
 
