@@ -64,6 +64,9 @@ namespace ely {
 #ifndef ELY_NORM_BPC
 #define ELY_NORM_BPC 24          // grad-norm blocks (of 4 waves) per compute unit
 #endif
+#ifndef ELY_FINAL_UNROLL
+#define ELY_FINAL_UNROLL 8       // tile partials a thread of the final norm kernel loads before adding (16, 32: slower)
+#endif
 #ifndef ELY_NORM_SMALL_TILE
 #define ELY_NORM_SMALL_TILE 4096  // grad-norm tile of a small list (more waves than its large tiles)
 #endif
@@ -77,6 +80,7 @@ constexpr int64_t kNormSmallTile = ELY_NORM_SMALL_TILE;
 static_assert(kNormTile % (64 * 8 * ELY_NORM_UNROLL) == 0 && kNormSmallTile % (64 * 8 * ELY_NORM_UNROLL) == 0,
               "a grad-norm tile is whole unrolled rounds of 8-element groups");
 constexpr int kNormUnroll = ELY_NORM_UNROLL;
+constexpr int kFinalUnroll = ELY_FINAL_UNROLL;
 constexpr int kBlock = 256;
 constexpr int kFinalThreads = 1024;
 
@@ -262,13 +266,13 @@ __global__ __launch_bounds__(kFinalThreads) void norm_final_kernel(const double*
     __shared__ double red[kFinalThreads];
     double s = 0.0;
     int64_t i = threadIdx.x;
-    // partials i, i + 1024, ... added in that order; 8 loads in flight
-    for (; i + 7 * kFinalThreads < tiles; i += 8 * kFinalThreads) {
-        double v[8];
+    // partials i, i + 1024, ... added in that order; kFinalUnroll loads in flight
+    for (; i + (kFinalUnroll - 1) * kFinalThreads < tiles; i += kFinalUnroll * kFinalThreads) {
+        double v[kFinalUnroll];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = partials[i + u * kFinalThreads];
+        for (int u = 0; u < kFinalUnroll; ++u) v[u] = partials[i + u * kFinalThreads];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) s += v[u];
+        for (int u = 0; u < kFinalUnroll; ++u) s += v[u];
     }
     for (; i < tiles; i += kFinalThreads) s += partials[i];
     red[threadIdx.x] = s;
