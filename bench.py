@@ -452,6 +452,42 @@ def bench_fold(device, stream, iters=5):
     }
 
 
+def bench_elementwise(device, stream, iters=5):
+    """The stand-alone passes of the unfused path over C1's 192-tensor shard,
+    one launch per tensor as the reference's callers make them: the fp32 ->
+    bf16 working-copy cast (pieces.cast_piece, 6 B/elem), the fold of a bf16
+    microbatch gradient into its fp32 sum (pieces.fold_add, 10 B/elem) and
+    the clip's in-place scale of bf16 gradients (clip_grad_norm_, 4 B/elem)."""
+    from elysium_wan_amd import _lib
+
+    L = _lib.load()
+    sptr = _lib.stream_ptr(device)
+    params, grads = make_shard(device)
+    n = sum(p.numel() for p in params)
+    copies = [torch.empty(p.shape, dtype=torch.bfloat16, device=device) for p in params]
+    accs = [torch.zeros_like(p) for p in params]
+    garr = _lib.tensor_array(grads)
+    one = torch.ones(1, dtype=torch.float32, device=device)
+
+    def cast(_):
+        for p, c in zip(params, copies):
+            _lib.check(L.ely_cast_bf16(p.data_ptr(), c.data_ptr(), p.numel(), sptr), "cast")
+
+    def fold(_):
+        for a, g in zip(accs, grads):
+            _lib.check(L.ely_fold_add(a.data_ptr(), g.data_ptr(), _lib.BF16, a.numel(), sptr), "fold")
+
+    def scale(_):
+        _lib.check(L.ely_scale_inplace(garr, len(grads), one.data_ptr(), sptr), "scale")
+
+    out = {}
+    for name, fn, b in (("cast_bf16", cast, 6), ("fold_add_bf16", fold, 10), ("scale_bf16", scale, 4)):
+        ms = time_events(fn, iters, stream)
+        out[name] = {"ms": ms, "GBs": n * b / ms / 1e6}
+    del params, grads, copies, accs
+    return out
+
+
 def bench_host_moments(device, steps=3):
     """adamw-host with its moments in pinned host memory (the reference's
     recipe), updated in place through the GPU's mapping of the pinned
@@ -886,7 +922,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-codec", action="store_true", help="skip the fp8 codec leg")
-    ap.add_argument("--no-extra", action="store_true", help="skip the fused-fold, host-moment, wire, vendor-reference and C0/C2/C3 legs")
+    ap.add_argument("--no-extra", action="store_true", help="skip the fused-fold, elementwise, host-moment, wire, vendor-reference and C0/C2/C3 legs")
     ap.add_argument("--codec", choices=("c1", "c4", "all"), default="all", help="activation sizes of the codec leg")
     ap.add_argument("--no-optimizer", action="store_true", help="skip the optimizer leg (profiling the other legs alone)")
     ap.add_argument("--no-configs", action="store_true", help="skip the C0/C2/C3 optimizer leg (--no-extra skips it too)")
@@ -945,6 +981,7 @@ def main():
             extra = {}
             legs = [
                 ("fold", "fold leg", lambda: bench_fold(device, stream)),
+                ("elementwise", "elementwise leg", lambda: bench_elementwise(device, stream)),
                 ("host_moments", "host-moments leg", lambda: bench_host_moments(device)),
                 ("wire", "wire leg", lambda: bench_wire(device, stream)),
                 ("hbm_reference", "vendor-kernel reference leg", lambda: hbm_reference(device, stream)),
