@@ -456,8 +456,10 @@ def bench_elementwise(device, stream, iters=5):
     """The stand-alone passes of the unfused path over C1's 192-tensor shard,
     one launch per tensor as the reference's callers make them: the fp32 ->
     bf16 working-copy cast (pieces.cast_piece, 6 B/elem), the fold of a bf16
-    microbatch gradient into its fp32 sum (pieces.fold_add, 10 B/elem) and
-    the clip's in-place scale of bf16 gradients (clip_grad_norm_, 4 B/elem)."""
+    microbatch gradient into its fp32 sum (pieces.fold_add, 10 B/elem),
+    the in-place scale of bf16 gradients by a device coefficient (one launch
+    per tensor, 4 B/elem) and clip_grad_norm_ in one call (the norm, then one
+    launch scaling every gradient: 6 B/elem)."""
     from elysium_wan_amd import _lib
 
     L = _lib.load()
@@ -480,8 +482,15 @@ def bench_elementwise(device, stream, iters=5):
     def scale(_):
         _lib.check(L.ely_scale_inplace(garr, len(grads), one.data_ptr(), sptr), "scale")
 
+    res = torch.zeros(16, dtype=torch.uint8, device=device)
+    nws = _lib.workspace(device, L.ely_grad_norm_workspace_bytes(garr, len(grads)))
+
+    def clip(_):
+        # clip_grad_norm_ in one call: the norm (2 B/elem) and one launch scaling every gradient (4 B/elem)
+        _lib.check(L.ely_grad_norm_clip(garr, len(grads), MAX_NORM, res.data_ptr(), nws.data_ptr(), nws.numel(), sptr), "clip")
+
     out = {}
-    for name, fn, b in (("cast_bf16", cast, 6), ("fold_add_bf16", fold, 10), ("scale_bf16", scale, 4)):
+    for name, fn, b in (("cast_bf16", cast, 6), ("fold_add_bf16", fold, 10), ("scale_bf16", scale, 4), ("clip_grad_norm_bf16", clip, 6)):
         ms = time_events(fn, iters, stream)
         out[name] = {"ms": ms, "GBs": n * b / ms / 1e6}
     del params, grads, copies, accs

@@ -28,6 +28,7 @@ EXPORTS = (
     "ely_abi_version",
     "ely_last_error",
     "ely_grad_norm_workspace_bytes",
+    "ely_grad_norm_clip",
     "ely_grad_norm",
     "ely_grad_norm_fold",
     "ely_adamw_workspace_bytes",
@@ -92,6 +93,7 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
         L.ely_grad_norm_workspace_bytes.restype = I64
         L.ely_grad_norm_workspace_bytes.argtypes = [TP, I32]
         L.ely_grad_norm.argtypes = [TP, I32, F, P, P, I64, P]
+        L.ely_grad_norm_clip.argtypes = [TP, I32, F, P, P, I64, P]
         L.ely_grad_norm_fold.argtypes = [TP, TP, I32, F, P, P, I64, P]
         L.ely_adamw_workspace_bytes.restype = I64
         L.ely_adamw_workspace_bytes.argtypes = [I32]

@@ -283,19 +283,81 @@ __global__ __launch_bounds__(kFinalThreads) void norm_final_kernel(const double*
     if (threadIdx.x == 0) {
         const double sumsq = red[0];
         const float norm = (float)sqrt(sumsq);
-        float coef = 1.0f;
-        if (max_norm > 0.0f) {
-            // clip_grad.py:165-169: (norm + 1e-6).reciprocal() * max_norm, clamp(max=1) keeping NaN
-            const float denom = norm + 1e-6f;
-            const float r = 1.0f / denom;
-            coef = r * max_norm;
-            coef = coef > 1.0f ? 1.0f : coef;
-        }
+        // clip_grad.py:165-169: max_norm / (norm + 1e-6) is torch's scalar
+        // __rdiv__, (norm + 1e-6).reciprocal() * max_norm, then clamp(max=1)
+        // keeping NaN; for any max_norm, as torch (0 zeroes the gradients)
+        const float denom = norm + 1e-6f;
+        const float r = 1.0f / denom;
+        float coef = r * max_norm;
+        coef = coef > 1.0f ? 1.0f : coef;
         out->sumsq = sumsq;
         out->norm = norm;
         out->coef = coef;
     }
 }
+
+#ifndef ELY_CLIP_BPC
+#define ELY_CLIP_BPC 4       // clip scale: blocks (of 4 waves) per compute unit
+#endif
+#ifndef ELY_CLIP_UNROLL
+#define ELY_CLIP_UNROLL 2    // clip scale: 16-byte vectors a lane loads before storing
+#endif
+
+// g <- g * coef in place, rounded once to g's dtype (torch's
+// _foreach_mul_(grads, clip_coef), clip_grad.py:170-177), over the norm's
+// own tile table: wave w scales tiles w, w + W, ...  A full, aligned tile
+// moves 16-byte vectors, lane l taking vectors l, l + 64, ...; others go
+// element by element.  DT as norm_partials_kernel.
+template <int DT, int64_t TILE>
+__global__ __launch_bounds__(kBlock) void clip_scale_kernel(const NormDesc* __restrict__ desc, int32_t n,
+                                                            int64_t total_tiles, const float* __restrict__ coef_ptr) {
+    constexpr int U = ELY_CLIP_UNROLL;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t waves = (int64_t)gridDim.x * (kBlock / kWave);
+    const int64_t w = (int64_t)blockIdx.x * (kBlock / kWave) + wave_uniform(threadIdx.x / kWave);
+    if (w >= total_tiles) return;
+    const float coef = *coef_ptr;
+    int ti = find_tensor(desc, n, w);
+    for (int64_t tile = w; tile < total_tiles; tile += waves) {
+        while (ti + 1 < n && desc[ti + 1].tile_begin <= tile) ++ti;
+        const NormDesc d = desc[ti];
+        const bool bf16 = DT == ELY_BF16 || (DT < 0 && d.dtype == ELY_BF16);
+        const int64_t e0 = (tile - d.tile_begin) * TILE;
+        const int64_t e1 = min(e0 + TILE, d.numel);
+        if (d.aligned && e1 - e0 == TILE) {
+            nu32x4* base = reinterpret_cast<nu32x4*>(static_cast<char*>(const_cast<void*>(d.g)) + e0 * (bf16 ? 2 : 4));
+            const int nvec = (int)(TILE * (bf16 ? 2 : 4) / 16);
+            for (int j0 = 0; j0 < nvec; j0 += kWave * U) {
+                nu32x4 r[U];
+#pragma unroll
+                for (int u = 0; u < U; ++u) r[u] = ld_norm(gp(base + j0 + u * kWave + lane));
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    nu32x4 o;
+                    if (bf16) {
+#pragma unroll
+                        for (int k = 0; k < 4; ++k)
+                            o[k] = f32_to_bf16(bf16_to_f32(r[u][k] & 0xFFFFu) * coef) |
+                                   (f32_to_bf16(bf16_to_f32(r[u][k] >> 16) * coef) << 16);
+                    } else {
+#pragma unroll
+                        for (int k = 0; k < 4; ++k) o[k] = __float_as_uint(__uint_as_float(r[u][k]) * coef);
+                    }
+                    __builtin_nontemporal_store(o, gp(base + j0 + u * kWave + lane));
+                }
+            }
+        } else if (bf16) {
+            uint16_t* g = static_cast<uint16_t*>(const_cast<void*>(d.g));
+            for (int64_t e = e0 + lane; e < e1; e += kWave) g[e] = (uint16_t)f32_to_bf16(bf16_to_f32(g[e]) * coef);
+        } else {
+            float* g = static_cast<float*>(const_cast<void*>(d.g));
+            for (int64_t e = e0 + lane; e < e1; e += kWave) g[e] = g[e] * coef;
+        }
+    }
+}
+
+static_assert((kNormSmallTile * 2 / 16) % (64 * ELY_CLIP_UNROLL) == 0,
+              "a full clip tile is whole unrolled rounds of 16-byte vectors");
 
 // The tile of one call, a function of the list alone (never of the grid, so
 // the result stays bitwise reproducible): lists under ELY_NORM_SMALL_LIMIT
@@ -577,9 +639,17 @@ extern "C" int64_t ely_adamw_workspace_bytes(int32_t n);
 
 namespace ely {
 
+// What a norm call left in the workspace for a clip scale to reuse.
+struct NormLaunch {
+    const NormDesc* dtable = nullptr;
+    int32_t entries = 0;
+    int64_t tiles = 0, tile = 0;
+    int dt = -1;
+};
+
 // The norm of grads (FOLD: of accs[i] + widen(grads[i])): see ely_grad_norm.
-static void grad_norm_impl(const ely_tensor* accs, const ely_tensor* grads, int32_t n, float max_norm,
-                           ely_norm_result* out_dev, void* workspace, int64_t ws_bytes, void* stream) {
+static NormLaunch grad_norm_impl(const ely_tensor* accs, const ely_tensor* grads, int32_t n, float max_norm,
+                                 ely_norm_result* out_dev, void* workspace, int64_t ws_bytes, void* stream) {
     check_list(grads, n, "ely_grad_norm grads");
     if (accs) check_folds(accs, grads, n, "ely_grad_norm_fold");
     if (!out_dev) fail(ELY_EINVAL, "ely_grad_norm: null result pointer");
@@ -607,6 +677,11 @@ static void grad_norm_impl(const ely_tensor* accs, const ely_tensor* grads, int3
     char* ws = static_cast<char*>(workspace);
     NormDesc* dtable = reinterpret_cast<NormDesc*>(ws);
     double* partials = reinterpret_cast<double*>(ws + norm_table_bytes(n));
+    NormLaunch out;
+    out.dtable = dtable;
+    out.entries = (int32_t)table.size();
+    out.tiles = tiles;
+    out.tile = tile;
     if (tiles > 0) {
         upload(dtable, table.data(), table.size() * sizeof(NormDesc), s);
         const int64_t waves = std::min<int64_t>(tiles, mt_blocks(ELY_NORM_BPC) * (kBlock / kWave));
@@ -614,6 +689,7 @@ static void grad_norm_impl(const ely_tensor* accs, const ely_tensor* grads, int3
         int dt = table[0].dtype;
         for (const NormDesc& d : table)
             if (d.dtype != dt) dt = -1;
+        out.dt = dt;
         const NormKernel kern = tile == kNormTile ? pick_norm<kNormTile>(accs != nullptr, dt)
                                                   : pick_norm<kNormSmallTile>(accs != nullptr, dt);
         hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(kBlock), 0, s, dtable, (int32_t)table.size(), tiles,
@@ -623,6 +699,28 @@ static void grad_norm_impl(const ely_tensor* accs, const ely_tensor* grads, int3
     hipLaunchKernelGGL(norm_final_kernel, dim3(1), dim3(kFinalThreads), 0, s, partials, tiles, max_norm,
                        out_dev);
     check_launch("norm_final_kernel");
+    return out;
+}
+
+typedef void (*ClipKernel)(const NormDesc*, int32_t, int64_t, const float*);
+
+template <int64_t TILE>
+static ClipKernel pick_clip(int dt) {
+    return dt == ELY_BF16 ? clip_scale_kernel<ELY_BF16, TILE>
+                          : dt == ELY_F32 ? clip_scale_kernel<ELY_F32, TILE> : clip_scale_kernel<-1, TILE>;
+}
+
+// Scale every gradient of a finished norm call by its clip coefficient, from
+// the tile table that call uploaded (same stream, so the table and the
+// coefficient are in place when this runs).
+static void clip_scale(const NormLaunch& nl, ely_norm_result* out_dev, void* stream) {
+    if (nl.tiles == 0) return;
+    const int64_t waves = std::min<int64_t>(nl.tiles, mt_blocks(ELY_CLIP_BPC) * (kBlock / kWave));
+    const int64_t blocks = (waves + 3) / 4;
+    const ClipKernel k = nl.tile == kNormTile ? pick_clip<kNormTile>(nl.dt) : pick_clip<kNormSmallTile>(nl.dt);
+    hipLaunchKernelGGL(k, dim3((unsigned)blocks), dim3(kBlock), 0, static_cast<hipStream_t>(stream), nl.dtable,
+                       nl.entries, nl.tiles, &out_dev->coef);
+    check_launch("clip_scale_kernel");
 }
 
 // One fused step (FOLD: the gradient of tensor i is accs[i] + widen(grads[i])).
@@ -710,6 +808,14 @@ int64_t ely_grad_norm_workspace_bytes(const ely_tensor* grads, int32_t n) {
 int ely_grad_norm(const ely_tensor* grads, int32_t n, float max_norm, ely_norm_result* out_dev, void* workspace,
                   int64_t ws_bytes, void* stream) {
     return guarded([&] { grad_norm_impl(nullptr, grads, n, max_norm, out_dev, workspace, ws_bytes, stream); });
+}
+
+int ely_grad_norm_clip(const ely_tensor* grads, int32_t n, float max_norm, ely_norm_result* out_dev, void* workspace,
+                       int64_t ws_bytes, void* stream) {
+    return guarded([&] {
+        const NormLaunch nl = grad_norm_impl(nullptr, grads, n, max_norm, out_dev, workspace, ws_bytes, stream);
+        clip_scale(nl, out_dev, stream);
+    });
 }
 
 int ely_grad_norm_fold(const ely_tensor* accs, const ely_tensor* grads, int32_t n, float max_norm,

@@ -706,10 +706,15 @@ def clip_grad_norm_(parameters, max_norm: float, norm_type: float = 2.0, error_i
         res = torch.empty(16, dtype=torch.uint8, device=dev)
         garr = _lib.tensor_array(grads)
         ws = _lib.workspace(dev, L.ely_grad_norm_workspace_bytes(garr, len(grads)))
-        _lib.check(L.ely_grad_norm(garr, len(grads), float(max_norm), res.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_ptr(dev)), "clip_grad_norm_")
+        sp = _lib.stream_ptr(dev)
+        if not error_if_nonfinite:
+            # the norm, then g <- g * coef in g's dtype over every gradient in one launch
+            _lib.check(L.ely_grad_norm_clip(garr, len(grads), float(max_norm), res.data_ptr(), ws.data_ptr(), ws.numel(), sp), "clip_grad_norm_")
+            return res[8:12].view(torch.float32).reshape(()).clone()
+        _lib.check(L.ely_grad_norm(garr, len(grads), float(max_norm), res.data_ptr(), ws.data_ptr(), ws.numel(), sp), "clip_grad_norm_")
         total = res[8:12].view(torch.float32).reshape(()).clone()
-        if error_if_nonfinite and bool(~torch.isfinite(total)):
+        if bool(~torch.isfinite(total)):
             raise RuntimeError(f"The total norm of order {norm_type} for gradients from `parameters` is non-finite, so it cannot be clipped.")
         # g <- g * coef in g's dtype, torch's _foreach_mul_ by the clamped coefficient
-        _lib.check(L.ely_scale_inplace(garr, len(grads), res.data_ptr() + 12, _lib.stream_ptr(dev)), "clip_grad_norm_ scale")
+        _lib.check(L.ely_scale_inplace(garr, len(grads), res.data_ptr() + 12, sp), "clip_grad_norm_ scale")
     return total

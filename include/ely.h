@@ -48,7 +48,7 @@ typedef struct ely_tensor {
 typedef struct ely_norm_result {
     double sumsq;         /* sum of g^2 over every element, fp64 */
     float norm;           /* (float)sqrt(sumsq) */
-    float coef;           /* clip coefficient, 1 when max_norm <= 0 */
+    float coef;           /* clip coefficient min(max_norm / (norm + 1e-6), 1), as torch */
 } ely_norm_result;
 
 /* AdamW per-step fp32 constants, one block per tensor.
@@ -78,9 +78,20 @@ int64_t ely_grad_norm_workspace_bytes(const ely_tensor* grads, int32_t n);
  * 2^29 elements) is reduced in a fixed lane order (fp32 squares of at most 8
  * elements, fp64 above), tiles in index order: the result is a function of
  * the list alone, bitwise identical across runs and grid sizes.  coef =
- * min(max_norm * (1/(norm + 1e-6)), 1) in fp32 when max_norm > 0, else 1. */
+ * min(max_norm * (1/(norm + 1e-6)), 1) in fp32 for any max_norm, as torch
+ * computes it (0 gives 0; a NaN norm gives NaN). */
 int ely_grad_norm(const ely_tensor* grads, int32_t n, float max_norm,
                   ely_norm_result* out_dev, void* workspace, int64_t ws_bytes, void* stream);
+
+/* torch's clip_grad_norm_ (TORCH/nn/utils/clip_grad.py:50-183) in one call:
+ * ely_grad_norm of grads, then every gradient scaled in place by the clip
+ * coefficient, g <- g * coef rounded once to g's dtype (the
+ * _foreach_mul_(grads, clip_coef) of :170-177), in one launch over the tile
+ * table the norm uploaded.  Same workspace as ely_grad_norm.  torch's
+ * error_if_nonfinite check needs the norm before the scale: a caller that
+ * wants it uses ely_grad_norm and ely_scale_inplace instead. */
+int ely_grad_norm_clip(const ely_tensor* grads, int32_t n, float max_norm, ely_norm_result* out_dev,
+                       void* workspace, int64_t ws_bytes, void* stream);
 
 /* ely_grad_norm of the folded gradients accs[i] + widen(grads[i]) (each sum
  * rounded once to fp32, pieces.fold_add, runtime/pieces.py:206-214): the

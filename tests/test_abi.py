@@ -125,6 +125,11 @@ def test_workspace_queries_are_host_arithmetic(lib):
     need = lib.ely_grad_norm_workspace_bytes(arr, 2)
     assert need >= 5 * 8 and need % 256 == 0
     assert lib.ely_grad_norm_workspace_bytes(arr, -1) == -1
+    # the one-call clip refuses what the norm refuses
+    res = ctypes.c_void_p(1)
+    assert lib.ely_grad_norm_clip(None, 2, 1.0, res, None, 0, None) == _lib.EINVAL
+    fake = _lib.tensor_array([_lib.ElyTensor(16, 16384 * 3 + 1, _lib.BF16, 0), _lib.ElyTensor(16, 7, _lib.F32, 0)])
+    assert lib.ely_grad_norm_clip(fake, 2, 1.0, res, res, need - 1, None) == _lib.EWORKSPACE  # refused before any access
     assert lib.ely_adamw_workspace_bytes(192) >= 192 * (64 + 32)
     assert lib.ely_fp8_workspace_bytes(16384, 2560, _lib.BF16) >= 16384 * 4
     # row maxima plus at most 2,048 partial maxima, whatever the row length

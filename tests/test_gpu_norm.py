@@ -119,3 +119,56 @@ def test_clip_grad_norm_matches_torch(oracle):
     c = oracle.clip_coef(float(total), 1.0)
     want = oracle.f32_to_bf16_bits(oracle.bf16_bits_to_f32(bits(h[0])) * np.float32(c))
     assert np.array_equal(bits(hp[0].grad), want)
+
+
+def test_clip_grad_norm_in_one_call_scales_every_gradient(oracle):
+    """optim.clip_grad_norm_ through ely_grad_norm_clip (the norm, then one
+    launch scaling every gradient in place) on a ragged list of bf16 and
+    fp32 gradients, unaligned views included, with small-list tiles and, past
+    2^29 elements, the large tiles: each gradient equals g * coef rounded once
+    to its dtype, with coef the oracle's from the same norm; max_norm 0 zeroes
+    the gradients and a negative max_norm flips them, as torch's formula
+    does; error_if_nonfinite raises on an Inf before touching anything."""
+    from elysium_wan_amd import optim
+
+    gen = torch.Generator(device="cuda").manual_seed(9)
+
+    def grads(big):
+        gs = [torch.randn(1_000_003, device="cuda", generator=gen) * 1e-2,
+              (torch.randn(4_097, device="cuda", generator=gen) * 3).bfloat16(),
+              torch.randn(70_001, device="cuda", generator=gen)[1:],
+              (torch.randn(300_001, device="cuda", generator=gen)).bfloat16()[1:]]
+        if big:
+            gs.append((torch.randn((1 << 29) + 4_099, device="cuda", generator=gen) * 1e-3).bfloat16())
+        return gs
+
+    for big, max_norm in ((False, 1.0), (False, 0.0), (False, -2.0), (True, 1.0)):
+        gs = grads(big)
+        ps = [torch.zeros(g.shape, dtype=g.dtype, device="cuda", requires_grad=True) for g in gs]
+        for p, g in zip(ps, gs):
+            if g.storage_offset():
+                # keep an unaligned view unaligned: a copy one element into a buffer
+                buf = torch.empty(g.numel() + 1, dtype=g.dtype, device="cuda")
+                buf[1:] = g
+                p.grad = buf[1:]
+            else:
+                p.grad = g.clone()
+        say("clip_grad_norm_ one call", "big" if big else "small", max_norm, sum(g.numel() for g in gs))
+        total = optim.clip_grad_norm_(ps, max_norm)
+        coef = oracle.clip_coef(float(total), max_norm)
+        for p, g in zip(ps, gs):
+            want = (g.float() * np.float32(coef)).to(g.dtype)
+            assert torch.equal(p.grad.view(torch.int16 if g.dtype == torch.bfloat16 else torch.int32),
+                               want.view(torch.int16 if g.dtype == torch.bfloat16 else torch.int32))
+        if max_norm == 0.0:
+            assert coef == 0.0
+        del gs, ps
+        torch.cuda.empty_cache()
+    # error_if_nonfinite: the norm is read first, and an Inf leaves the gradients as they were
+    g = torch.randn(10_000, device="cuda")
+    g[17] = float("inf")
+    p = torch.zeros(10_000, device="cuda", requires_grad=True)
+    p.grad = g.clone()
+    with pytest.raises(RuntimeError, match="non-finite"):
+        optim.clip_grad_norm_([p], 1.0, error_if_nonfinite=True)
+    assert torch.equal(p.grad, g)
