@@ -321,18 +321,21 @@ def test_sumsq_equals_exact_rational_sum(oracle):
 
 
 def test_clip_coefficient_equals_torch_clip_grad_norm(oracle):
+    """For every max_norm torch's formula covers: 0 zeroes the gradients, a
+    negative one flips them (the clamp is max=1 only)."""
     rng = np.random.default_rng(7)
-    for scale in (1e-3, 0.3, 10.0, 1e3):
-        ps = []
-        for n in (100, 1, 333):
-            p = torch.zeros(n, requires_grad=True)
-            g = torch.from_numpy((rng.standard_normal(n) * scale).astype(np.float32))
-            g[0] = 1.0  # after clipping this element is the coefficient itself
-            p.grad = g
-            ps.append(p)
-        total = torch.nn.utils.clip_grad_norm_(ps, max_norm=1.0, foreach=False)
-        coef_torch = float(ps[0].grad[0])
-        assert np.float32(oracle.clip_coef(float(total), 1.0)) == np.float32(coef_torch), scale
+    for max_norm in (1.0, 0.5, 0.0, -2.0):
+        for scale in (1e-3, 0.3, 10.0, 1e3):
+            ps = []
+            for n in (100, 1, 333):
+                p = torch.zeros(n, requires_grad=True)
+                g = torch.from_numpy((rng.standard_normal(n) * scale).astype(np.float32))
+                g[0] = 1.0  # after clipping this element is the coefficient itself
+                p.grad = g
+                ps.append(p)
+            total = torch.nn.utils.clip_grad_norm_(ps, max_norm=max_norm, foreach=False)
+            coef_torch = float(ps[0].grad[0])
+            assert np.float32(oracle.clip_coef(float(total), max_norm)) == np.float32(coef_torch), (max_norm, scale)
 
 
 # ---------------------------------------------------------------- mutations
