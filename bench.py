@@ -860,6 +860,18 @@ def hbm_reference(device, stream, n: int = 1 << 28, iters: int = 10):
     return {"torch_copy_GBs": 8 * n / copy_ms / 1e6, "torch_add_GBs": 12 * n / add_ms / 1e6, "elements": n}
 
 
+def _cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), or "unknown"."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_context(sample_elems: int = 1 << 25):
     """More CPU reference points on the same host: torch.optim.AdamW
     (foreach=False, the reference's "adamw" CPU path) over a 32M-element
@@ -908,6 +920,8 @@ def cpu_context(sample_elems: int = 1 << 25):
             t0 = time.perf_counter()
             list(ex.map(lambda c: O.dequantize(c[0], c[1], "e4m3", "bf16"), qk))
             out[f"oracle_fp8_dequantize_GBs_{threads}t"] = xb.size * CODEC_BYTES_PER_ELEM / (time.perf_counter() - t0) / 1e9
+    out["host_cpus"] = os.cpu_count()
+    out["cpu_model"] = _cpu_model()
     out["sample"] = (f"torch AdamW and the oracle's HostAdamW (bf16 grads + bf16 copy) over {sample_elems} fp32 elements, "
                      f"oracle quantize and dequantize (-> bf16) of [4096, {D_MODEL}] bf16; threads 1 and {threads0} (torch's count)")
     return out
