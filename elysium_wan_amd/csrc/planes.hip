@@ -31,6 +31,9 @@ namespace ely {
 #ifndef ELY_NIBBLES_UNROLL
 #define ELY_NIBBLES_UNROLL 2  // nibble planes: vectors a lane keeps in flight
 #endif
+#ifndef ELY_NIB_BALLOT
+#define ELY_NIB_BALLOT 1  // nibble encode: count mismatches per wave on the scalar unit
+#endif
 #ifndef ELY_NIBBLES_BPC
 #define ELY_NIBBLES_BPC 8  // nibble planes: blocks per compute unit
 #endif
@@ -219,18 +222,27 @@ __device__ __forceinline__ uint32_t join_pairs(uint32_t h, uint32_t l) {
 }
 
 // e4m3 codes of four floats, element k in byte k, and how many of them do
-// not convert back to themselves.  That test alone decides
+// not convert back to themselves, added to `bad`: with ELY_NIB_BALLOT the
+// count of the whole wave's active lanes (each comparison's lane mask,
+// popcounted on the scalar unit), else this lane's.  That test alone decides
 // representability: a NaN never equals, and no code decodes to Inf or to a
 // value beyond 448, so only the grid values of the instruction's exact
 // domain pass (where it is torch's rounding); the codes of the others are
 // never used (the encode is refused).
-__device__ __forceinline__ uint32_t e4m3_quad(float a, float b, float c, float d, uint32_t& nbad) {
+__device__ __forceinline__ uint32_t e4m3_quad(float a, float b, float c, float d, uint32_t& bad) {
     uint32_t w = cvt_pk_fp8<kE4M3, false>(a, b, 0u);
     w = cvt_pk_fp8<kE4M3, true>(c, d, w);
     float ra, rb, rc, rd;
     cvt_pk_f32<kE4M3, false>(w, ra, rb);
     cvt_pk_f32<kE4M3, true>(w, rc, rd);
-    nbad += (ra != a) + (rb != b) + (rc != c) + (rd != d);
+#if ELY_NIB_BALLOT
+    bad += (uint32_t)(__builtin_popcountll(__builtin_amdgcn_ballot_w64(ra != a)) +
+                      __builtin_popcountll(__builtin_amdgcn_ballot_w64(rb != b)) +
+                      __builtin_popcountll(__builtin_amdgcn_ballot_w64(rc != c)) +
+                      __builtin_popcountll(__builtin_amdgcn_ballot_w64(rd != d)));
+#else
+    bad += (ra != a) + (rb != b) + (rc != c) + (rd != d);
+#endif
     return w;
 }
 
@@ -244,7 +256,8 @@ __global__ __launch_bounds__(kPBlock) void nibbles_encode_kernel(const void* __r
     constexpr int EPL = BF16 ? 8 : 4;
     const int64_t T = (int64_t)gridDim.x * kPBlock;
     const int64_t tid = (int64_t)blockIdx.x * kPBlock + threadIdx.x;
-    uint32_t nbad = 0;
+    uint32_t nbad = 0;  // this lane's mismatches
+    uint32_t qbad = 0;  // the vector path's (the wave's, with ELY_NIB_BALLOT)
     int64_t done = 0;  // elements covered by the vector path
     if (vec) {
         const int64_t nvec = n / 16 * (16 / EPL);  // whole 16-element groups only
@@ -273,7 +286,7 @@ __global__ __launch_bounds__(kPBlock) void nibbles_encode_kernel(const void* __r
                 uint32_t hw = 0u, lw = 0u;
 #pragma unroll
                 for (int e = 0; e < EPL; e += 4) {
-                    const uint32_t w = e4m3_quad(f[e], f[e + 1], f[e + 2], f[e + 3], nbad);
+                    const uint32_t w = e4m3_quad(f[e], f[e + 1], f[e + 2], f[e + 3], qbad);
                     hw |= hi_pairs(w) << (4 * e);
                     lw |= lo_pairs(w) << (4 * e);
                 }
@@ -305,8 +318,15 @@ __global__ __launch_bounds__(kPBlock) void nibbles_encode_kernel(const void* __r
         hi[b] = (uint8_t)h;
         lo[b] = (uint8_t)l;
     }
-    // one atomic per wave that saw a mismatch
-    const uint32_t wave_bad = wave_sum_u32(nbad);
+    // one atomic per wave that saw a mismatch.  The wave counts of the vector
+    // path are complete in lane 0: a lane past the end has no elements, and
+    // lane 0 holds the wave's lowest vector, so it is active whenever any
+    // lane is; every lane is active again here.
+#if ELY_NIB_BALLOT
+    const uint32_t wave_bad = __builtin_amdgcn_readfirstlane(qbad) + wave_sum_u32(nbad);
+#else
+    const uint32_t wave_bad = wave_sum_u32(nbad + qbad);
+#endif
     if ((threadIdx.x & (kWave - 1)) == 0 && wave_bad) atomicAdd(bad, (unsigned long long)wave_bad);
 }
 
