@@ -175,3 +175,32 @@ def test_byte_planes_compress_trained_like_fp32():
     t = torch.empty(4, 64, 256, device="cuda").normal_(0.0, 0.02, generator=torch.Generator(device="cuda").manual_seed(0))
     payload, _ = planes.encode(t)
     assert len(payload) < t.numel() * 4
+
+
+def test_nibble_encode_counts_every_unrepresentable_element():
+    """ely_fp8_nibbles_encode adds one to the bad count per element that is
+    not exactly an e4m3 value (ely.h), whichever path takes it: planted
+    NaN, Inf, beyond-448 and off-grid elements in the vector path, in the
+    element-wise tail and in an unaligned view, against their exact number."""
+    from elysium_wan_amd import _lib
+
+    L = _lib.load()
+    gen = torch.Generator().manual_seed(21)
+    for dtype in (torch.bfloat16, torch.float32):
+        for n, off in ((1_000_003, 0), (4_099, 0), (70_001, 1)):
+            codes = torch.randint(0, 256, (n,), generator=gen, dtype=torch.int64).to(torch.uint8)
+            x = codes.view(torch.float8_e4m3fn).float()
+            x = torch.where(torch.isnan(x), torch.zeros_like(x), x)
+            idx = torch.randperm(n, generator=gen)[:37]
+            planted = torch.tensor([float("nan"), float("inf"), -500.0, 1.0 + 2.0**-6])[torch.arange(37) % 4]
+            x[idx] = planted
+            buf = torch.zeros(n + off, dtype=dtype, device="cuda")
+            t = buf[off:]
+            t.copy_(x.to(dtype))
+            hi = torch.empty((n + 1) // 2, dtype=torch.uint8, device="cuda")
+            lo = torch.empty_like(hi)
+            bad = torch.zeros(1, dtype=torch.int64, device="cuda")
+            say("nibble bad count", dtype, n, off)
+            _lib.check(L.ely_fp8_nibbles_encode(t.data_ptr(), _lib.dtype_code(t), n, hi.data_ptr(), lo.data_ptr(), bad.data_ptr(),
+                                                _lib.stream_ptr(t.device)), "nibbles")
+            assert int(bad.item()) == 37
