@@ -52,6 +52,9 @@
 #ifndef ELY_Q_BATCH
 #define ELY_Q_BATCH 1  // register paths: vectors per lane per load batch (0: the whole row at once)
 #endif
+#ifndef ELY_Q_LDS
+#define ELY_Q_LDS 40960  // wave-per-row quantize: unused dynamic LDS per block, capping it at 4 blocks (16 waves) per CU
+#endif
 #ifndef ELY_RECOVER_KEEP_VPL
 #define ELY_RECOVER_KEEP_VPL 16  // longest rows (vectors per lane) whose image reuses the test's codes
 #endif
@@ -1035,7 +1038,7 @@ constexpr int kMaxWaveVpl = 6;
 
 template <int FMT, bool BF16, int VPL>
 static void launch_rows(const void* x, int64_t rows, int64_t cols, uint8_t* q, int32_t* k, void* out, hipStream_t s) {
-    hipLaunchKernelGGL((quant_rows_kernel<FMT, BF16, VPL>), dim3(blocks_for_waves(rows)), dim3(kQBlock), 0, s, x,
+    hipLaunchKernelGGL((quant_rows_kernel<FMT, BF16, VPL>), dim3(blocks_for_waves(rows)), dim3(kQBlock), ELY_Q_LDS, s, x,
                        rows, cols, q, k, out);
     check_launch("quant_rows_kernel");
 }
