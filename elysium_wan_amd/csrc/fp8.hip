@@ -55,6 +55,9 @@
 #ifndef ELY_Q_LDS
 #define ELY_Q_LDS 40960  // wave-per-row quantize: unused dynamic LDS per block, capping it at 4 blocks (16 waves) per CU
 #endif
+#ifndef ELY_DEQ_LDS
+#define ELY_DEQ_LDS 0  // dequantize: unused dynamic LDS per block capping its blocks per CU (caps measured slower)
+#endif
 #ifndef ELY_RECOVER_KEEP_VPL
 #define ELY_RECOVER_KEEP_VPL 16  // longest rows (vectors per lane) whose image reuses the test's codes
 #endif
@@ -1146,10 +1149,10 @@ static void dequantize_impl(const uint8_t* q, const int32_t* k, int64_t rows, in
         const int64_t n = rows * cols;
         const unsigned blocks = blocks_for_waves((n + kDeqSegCodes - 1) / kDeqSegCodes);
         if (n < ((int64_t)1 << 32))
-            hipLaunchKernelGGL((dequant_flat_kernel<FMT, BF16OUT, true>), dim3(blocks), dim3(kQBlock), 0, s, q, k, n,
+            hipLaunchKernelGGL((dequant_flat_kernel<FMT, BF16OUT, true>), dim3(blocks), dim3(kQBlock), ELY_DEQ_LDS, s, q, k, n,
                                cols, out);
         else
-            hipLaunchKernelGGL((dequant_flat_kernel<FMT, BF16OUT, false>), dim3(blocks), dim3(kQBlock), 0, s, q, k, n,
+            hipLaunchKernelGGL((dequant_flat_kernel<FMT, BF16OUT, false>), dim3(blocks), dim3(kQBlock), ELY_DEQ_LDS, s, q, k, n,
                                cols, out);
         check_launch("dequant_flat_kernel");
         return;
