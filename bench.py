@@ -114,7 +114,7 @@ def bench_optimizer(args, device, stream):
     return measure_shard(params, grads, device, stream, args.steps, args.warmup)
 
 
-def measure_shard(params, grads, device, stream, steps, warmup):
+def measure_shard(params, grads, device, stream, steps, warmup, order="host"):
     """Times optimizer steps of one shard (grad-norm launch + fused clip +
     AdamW launch, bf16 working copy out) by wall clock around `steps` whole
     steps, then each of the two launches alone with HIP events on the
@@ -122,7 +122,7 @@ def measure_shard(params, grads, device, stream, steps, warmup):
     from elysium_wan_amd import _lib, optim
 
     n_elem = sum(p.numel() for p in params)
-    opt = optim.FusedAdamW(params, lr=LR, betas=BETAS, eps=EPS, weight_decay=WD, order="host", max_norm=MAX_NORM, working_copy=True)
+    opt = optim.FusedAdamW(params, lr=LR, betas=BETAS, eps=EPS, weight_decay=WD, order=order, max_norm=MAX_NORM, working_copy=True)
     for _ in range(warmup):
         opt.step(grads=grads)
     torch.cuda.synchronize()
@@ -152,12 +152,14 @@ def measure_shard(params, grads, device, stream, steps, warmup):
         _lib.check(L.ely_grad_norm(garr, n, MAX_NORM, res.data_ptr(), nws.data_ptr(), nws.numel(), sptr), "norm")
 
     iters = max(steps, 5)
-    per_step = [optim.host_consts(LR, BETAS, EPS, WD, base_step + 1 + i) for i in range(iters)]
+    cfn = optim.host_consts if order == "host" else optim.torch_consts
+    per_step = [cfn(LR, BETAS, EPS, WD, base_step + 1 + i) for i in range(iters)]
+    code = _lib.ORDER_HOST if order == "host" else _lib.ORDER_TORCH
 
     def adam(i):
         for j in range(n):
             consts[j].c[:] = per_step[i]
-        _lib.check(L.ely_adamw_step(parr, garr, marr, varr, carr, n, consts, _lib.ORDER_HOST, 1, res.data_ptr() + 12, aws.data_ptr(), aws.numel(), sptr), "adamw")
+        _lib.check(L.ely_adamw_step(parr, garr, marr, varr, carr, n, consts, code, 1, res.data_ptr() + 12, aws.data_ptr(), aws.numel(), sptr), "adamw")
 
     norm_ms = time_events(norm, iters, stream)
     adam_ms = time_events(adam, iters, stream)
@@ -243,6 +245,16 @@ def bench_configs(device, stream, names=("c0", "c2", "c3"), steps=3, warmup=1):
         del params, grads
         torch.cuda.empty_cache()
     return out
+
+
+def bench_torch_order(device, stream, steps=5, warmup=2):
+    """C1's step with the "adamw" recipe (build("adamw"): torch.optim.AdamW's
+    op order, TORCH/optim/adam.py:688-800) instead of "adamw-host"'s: the
+    same bytes, other arithmetic."""
+    params, grads = make_shard(device)
+    o = measure_shard(params, grads, device, stream, steps, warmup, order="torch")
+    del params, grads
+    return _shard_rates(o, 2, 192)
 
 
 def bench_placement(device, stream, hold_gib=150):
@@ -1005,6 +1017,7 @@ def main():
             legs = [
                 ("fold", "fold leg", lambda: bench_fold(device, stream)),
                 ("elementwise", "elementwise leg", lambda: bench_elementwise(device, stream)),
+                ("c1_torch_order", "torch-order leg", lambda: bench_torch_order(device, stream)),
                 ("host_moments", "host-moments leg", lambda: bench_host_moments(device)),
                 ("wire", "wire leg", lambda: bench_wire(device, stream)),
                 ("hbm_reference", "vendor-kernel reference leg", lambda: hbm_reference(device, stream)),
