@@ -1,5 +1,6 @@
 // mta.hip -- multi-tensor kernels over a stage's ragged parameter shard:
-//   (a) the deterministic global grad-norm (sum of squares -> norm -> clip coef)
+//   (a) the deterministic global grad-norm (sum of squares -> norm -> clip
+//       coef), and clip_grad_norm_'s in-place scale over the same tile table
 //   (b) the fused clip + AdamW step with the bf16 working copy.
 //
 // Work decomposition.  Every tensor is cut into fixed tiles (kAdamTile /
