@@ -1032,6 +1032,9 @@ def main():
                 except torch.OutOfMemoryError as e:
                     # a box with less free HBM skips the leg; the headline stands
                     extra[key] = {"skipped": f"out of device memory: {str(e)[:160]}"}
+                except Exception as e:  # noqa: BLE001 -- recorded in the line, the headline stands
+                    log(f"{what} failed: {e!r}")
+                    extra[key] = {"error": repr(e)[:300]}
                 torch.cuda.synchronize()
                 torch.cuda.empty_cache()
     n = o["n_elem"]
