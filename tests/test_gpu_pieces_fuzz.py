@@ -1,0 +1,56 @@
+"""Property-based fuzz of the stand-alone elementwise passes on the GPU:
+pieces.cast_piece, pieces.fold_add and the in-place scale over random sizes
+(quad tails, several grid strides) and element offsets (the vector and the
+scalar paths), bit for bit against torch on the GPU -- each is one IEEE
+rounding per element (runtime/pieces.py:192-214, clip_grad.py:170-177).
+Derandomized."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+from hypothesis import HealthCheck, given, settings
+from hypothesis import strategies as st
+
+from gpu_util import say
+
+pytestmark = pytest.mark.gpu
+
+FUZZ = settings(max_examples=40, deadline=None, derandomize=True, suppress_health_check=[HealthCheck.too_slow])
+
+
+def _at(x: torch.Tensor, off: int) -> torch.Tensor:
+    buf = torch.empty(x.numel() + off, dtype=x.dtype, device="cuda")
+    buf[off:] = x
+    return buf[off:]
+
+
+def _same(a: torch.Tensor, b: torch.Tensor) -> bool:
+    it = torch.int16 if a.dtype == torch.bfloat16 else torch.int32
+    return torch.equal(a.view(it), b.view(it))
+
+
+@FUZZ
+@given(n=st.integers(0, 3_000_000), offs=st.tuples(st.integers(0, 3), st.integers(0, 3)), bf16g=st.booleans(),
+       coef=st.sampled_from([1.0, 0.5, 0.3712, 0.0, -1.25]), seed=st.integers(0, 2**16))
+def test_elementwise_passes_match_torch(n, offs, bf16g, coef, seed):
+    from elysium_wan_amd import _lib, pieces
+
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    say("pieces fuzz", n, offs, "bf16" if bf16g else "f32", coef)
+    x = _at(torch.randn(n, device="cuda", generator=gen) * 3, offs[0])
+    got = pieces.cast_piece(x, torch.bfloat16)
+    assert _same(got, x.to(torch.bfloat16))
+    gdt = torch.bfloat16 if bf16g else torch.float32
+    g = _at(torch.randn(n, device="cuda", generator=gen).to(gdt), offs[1])
+    acc = _at(torch.randn(n, device="cuda", generator=gen), offs[0])
+    want = acc + g.float()
+    pieces.fold_add(acc, g)
+    assert _same(acc, want)
+    if n:
+        L = _lib.load()
+        c = torch.tensor([coef], dtype=torch.float32, device="cuda")
+        h = g.clone() if offs[1] == 0 else _at(g.clone(), offs[1])
+        want = (h.float() * c).to(gdt)
+        _lib.check(L.ely_scale_inplace(_lib.tensor_array([h]), 1, c.data_ptr(), _lib.stream_ptr(h.device)), "scale")
+        assert _same(h, want)
