@@ -19,9 +19,11 @@ Prints one JSON line (rank 0):
   roofline      -- the fused AdamW kernel: algorithmic bytes per launch
                    (28 B/elem: read p, g(bf16), m, v; write p, m, v, copy)
                    over its average duration from HIP events on its stream;
-  cpu_baseline  -- the oracle's HostAdamW arithmetic (oracle/ely_oracle.c,
-                   one thread) timed on this host on a bounded prefix of the
-                   same shard.
+  cpu_baseline  -- the reference's own CPU path for the step (torch's
+                   clip_grad_norm_ + AdamW(foreach=False) + the bf16 cast)
+                   on every core torch is given on this host, over a
+                   bounded prefix of the same shard; the 1-thread figure and
+                   the oracle's C port sit in extra.cpu_context.
 """
 
 from __future__ import annotations
@@ -464,6 +466,93 @@ def bench_fold(device, stream, iters=5):
     }
 
 
+def bench_release(device, stream, tokens: int = 2048, iters: int = 3):
+    """Per-layer release (runtime/stage.py:3080-3099, RUNTIME-I23): the C1
+    step runs on a side stream with on_param recording one event per block
+    (12 tensors) as its update group is issued, while a forward-style
+    consumer on the caller's stream waits on each block's event and then
+    multiplies a [tokens, d] bf16 activation by that block's four bf16
+    working-copy matrices.  Against: the single-launch step, then the same
+    forward after it.  Reported: time from the step's start to block 0's
+    release and to the last block's, and the wall time of step + forward
+    both ways (HIP events)."""
+    from elysium_wan_amd import optim
+
+    params, grads = make_shard(device)
+    per_block = len(block_shapes(D_MODEL))
+    opt = optim.FusedAdamW(params, lr=LR, betas=BETAS, eps=EPS, weight_decay=WD, order="host", max_norm=MAX_NORM,
+                           working_copy=True, release_elems=12 * D_MODEL * D_MODEL + 13 * D_MODEL)  # one group per block
+    copies = opt.working_copies
+    x = torch.randn(tokens, D_MODEL, device=device).bfloat16()
+    side = torch.cuda.Stream(device)
+    linear = torch.nn.functional.linear
+
+    def forward(block, s):
+        """One block's four GEMMs on its bf16 working copies (qkv, proj,
+        fc1, fc2 at positions 2, 4, 8, 10 of the block's tensors)."""
+        w = lambda j: copies[block * per_block + j]  # noqa: E731
+        with torch.cuda.stream(s):
+            h = linear(x, w(2))[:, :D_MODEL].contiguous()
+            h = linear(h, w(4))
+            h = linear(h, w(8))
+            return linear(h, w(10))
+
+    def serial():
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        opt.step(grads=grads)
+        for b in range(N_BLOCKS):
+            forward(b, stream)
+        end.record(stream)
+        torch.cuda.synchronize()
+        return start.elapsed_time(end)
+
+    def overlapped():
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        events = [None] * N_BLOCKS
+        left = [per_block] * N_BLOCKS
+        start.record(stream)
+        side.wait_stream(stream)
+
+        def release(i):
+            b = i // per_block
+            left[b] -= 1
+            if left[b] == 0:
+                ev = torch.cuda.Event(enable_timing=True)
+                ev.record(side)
+                events[b] = ev
+
+        with torch.cuda.stream(side):
+            opt.step(grads=grads, on_param=release)
+        for b in range(N_BLOCKS):
+            stream.wait_event(events[b])
+            forward(b, stream)
+        end.record(stream)
+        stream.wait_stream(side)
+        torch.cuda.synchronize()
+        return start.elapsed_time(end), start.elapsed_time(events[0]), start.elapsed_time(events[-1])
+
+    serial()
+    overlapped()
+    ser = [serial() for _ in range(iters)]
+    ovl = [overlapped() for _ in range(iters)]
+    fwd_start, fwd_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    fwd_start.record(stream)
+    for b in range(N_BLOCKS):
+        forward(b, stream)
+    fwd_end.record(stream)
+    torch.cuda.synchronize()
+    del opt, params, grads, copies
+    return {
+        "forward_tokens": tokens,
+        "forward_alone_ms": fwd_start.elapsed_time(fwd_end),
+        "serial_step_then_forward_ms": min(ser),
+        "per_layer_release_ms": min(o[0] for o in ovl),
+        "first_block_released_ms": min(o[1] for o in ovl),
+        "last_block_released_ms": min(o[2] for o in ovl),
+    }
+
+
 def bench_elementwise(device, stream, iters=5):
     """The stand-alone passes of the unfused path over C1's 192-tensor shard,
     one launch per tensor as the reference's callers make them: the fp32 ->
@@ -536,7 +625,85 @@ def bench_host_moments(device, steps=3):
     return out
 
 
-def cpu_baseline(sample_elems: int, steps: int = 2):
+# benchmarks/wan/runs/2026-10-12-sxm4/REPORT.md:23-29: check_host_adamw.py's
+# seconds per step at 200M parameters on an H100 80GB SXM host (the only
+# published figures for this path)
+REF_HOST_ADAMW_200M_S = {"serial": 0.074, "staged": 0.045, "staged_half_resident": 0.024}
+
+
+def bench_check_host_adamw(device, params_m: float = 200.0, steps: int = 3):
+    """benchmarks/wan/check_host_adamw.py:58-80 on this build: "adamw-host"
+    (the reference's memory contract, moments in pinned host memory) over
+    params_m million fp32 parameters in four tensors, fp32 grads N(0, 1),
+    seconds per step of each arm -- serial copies, staged copies (the
+    reference's default), staged with half the moments promoted to the GPU,
+    and this build's default, the in-place update through the GPU's mapping
+    (alone and with half resident) -- beside the reference's published
+    figures."""
+    from elysium_wan_amd import optim
+
+    n = int(params_m * 1e6)
+    out = {"params_m": params_m, "reference_h100_sxm_s": REF_HOST_ADAMW_200M_S if params_m == 200.0 else None}
+    arms = (("serial", False, 0.0), ("staged", True, 0.0), ("staged_half_resident", True, 0.5),
+            ("in_place", None, 0.0), ("in_place_half_resident", None, 0.5))
+    for name, pipeline, resident in arms:
+        gen = torch.Generator(device=device).manual_seed(2)
+        params = [torch.empty(s, device=device).normal_(generator=gen).requires_grad_(True)
+                  for s in (n // 4, n // 4, n // 2 - 7, 7)]
+        for p in params:
+            p.grad = torch.randn_like(p)
+        opt = optim.build("adamw-host", params, 3e-4, pipeline=pipeline)
+        opt.step()  # allocates the host moments
+        if resident:
+            opt.promote(int(resident * 8 * n))
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            opt.step()
+        torch.cuda.synchronize()
+        dt = (time.perf_counter() - t0) / steps
+        out[name] = {"step_s": dt, "pcie_GBs": 16 * n * (1.0 - resident) / dt / 1e9}
+        del params, opt
+        torch.cuda.empty_cache()
+    return out
+
+
+def cpu_baseline(sample_elems: int, threads: int, target_s: float = 10.0, max_steps: int = 50):
+    """The reference's CPU path for the same step, timed on this host's cores:
+    torch.nn.utils.clip_grad_norm_ (foreach=False), torch.optim.AdamW
+    (foreach=False; the "adamw" recipe, runtime/optim.py:50-51, on the CPU)
+    and the bf16 working copy (pieces.cast_piece, runtime/pieces.py:192-195)
+    over a prefix of C1's shard: fp32 params N(0, 0.02), the bf16 grads
+    N(0, 1e-4) widened to fp32 beforehand (pieces.fold_start), as many steps
+    as fit `target_s` seconds.  -> (params/s, seconds, steps)."""
+    threads0 = torch.get_num_threads()
+    try:
+        gen = torch.Generator().manual_seed(0)
+        p = (torch.randn(sample_elems, generator=gen) * 0.02).requires_grad_(True)
+        p.grad = (torch.randn(sample_elems, generator=gen) * 1e-4).bfloat16().float()
+        copy = torch.empty(sample_elems, dtype=torch.bfloat16)
+        torch.set_num_threads(threads)
+        opt = torch.optim.AdamW([p], lr=LR, betas=BETAS, eps=EPS, weight_decay=WD, foreach=False)
+
+        def step():
+            torch.nn.utils.clip_grad_norm_([p], MAX_NORM, foreach=False)
+            opt.step()
+            copy.copy_(p.detach())
+
+        step()  # moments allocated; first-touch page faults outside the timed steps
+        t0 = time.perf_counter()
+        k = 0
+        while k < max_steps and (k < 2 or time.perf_counter() - t0 < target_s):
+            step()
+            k += 1
+        dt = time.perf_counter() - t0
+        del opt, p, copy
+        return sample_elems * k / dt, dt, k
+    finally:
+        torch.set_num_threads(threads0)
+
+
+def cpu_port_baseline(sample_elems: int, steps: int = 2):
     """The oracle's HostAdamW (one thread of C) over a prefix of C1's shard."""
     from oracle import oracle as O
 
@@ -1016,9 +1183,11 @@ def main():
             extra = {}
             legs = [
                 ("fold", "fold leg", lambda: bench_fold(device, stream)),
+                ("release", "per-layer release leg", lambda: bench_release(device, stream)),
                 ("elementwise", "elementwise leg", lambda: bench_elementwise(device, stream)),
                 ("c1_torch_order", "torch-order leg", lambda: bench_torch_order(device, stream)),
                 ("host_moments", "host-moments leg", lambda: bench_host_moments(device)),
+                ("check_host_adamw", "check_host_adamw leg (200M parameters)", lambda: bench_check_host_adamw(device)),
                 ("wire", "wire leg", lambda: bench_wire(device, stream)),
                 ("hbm_reference", "vendor-kernel reference leg", lambda: hbm_reference(device, stream)),
             ]
@@ -1043,15 +1212,28 @@ def main():
     cpu = None
     if not args.no_cpu:
         log("cpu baseline leg")
-        rate, secs = cpu_baseline(args.cpu_sample)
+        # every core torch runs on: the thread count the box grants one GPU's
+        # process (OMP_NUM_THREADS), which may be fewer than os.cpu_count()
+        threads = torch.get_num_threads()
+        rate, secs, k = cpu_baseline(args.cpu_sample, threads)
+        rate1, secs1, k1 = cpu_baseline(args.cpu_sample // 4, 1, target_s=5.0)
+        prate, psecs = cpu_port_baseline(args.cpu_sample // 4)
         extra = extra or {}
         extra["cpu_context"] = cpu_context()
+        extra["cpu_context"]["torch_step_params_per_s_1t"] = rate1
+        extra["cpu_context"]["torch_step_1t_sample"] = f"{args.cpu_sample // 4} elements, {k1} steps, {secs1:.1f} s"
+        extra["cpu_context"]["oracle_port_params_per_s_1t"] = prate
+        extra["cpu_context"]["oracle_port_sample"] = (f"oracle HostAdamW (C, 1 thread) over {args.cpu_sample // 4} elements, "
+                                                      f"2 steps, bf16 grads + bf16 copy ({psecs:.1f} s)")
         cpu = {
             "value": rate,
             "unit": "params/s",
-            "cores": 1,
-            "kind": "port",
-            "sample": f"oracle HostAdamW (C, 1 thread) over a {args.cpu_sample}-element prefix of the C1 shard, 2 steps, bf16 grads + bf16 copy ({secs:.1f} s)",
+            "cores": threads,
+            "kind": "reference",
+            "sample": (f"the reference's CPU path in torch {torch.__version__}: clip_grad_norm_(foreach=False) + "
+                       f"torch.optim.AdamW(foreach=False).step() + bf16 working-copy cast, {threads} threads "
+                       f"(host shows {os.cpu_count()} CPUs), over a {args.cpu_sample}-element prefix of the C1 shard, "
+                       f"{k} steps ({secs:.1f} s)"),
         }
     result = {
         "metric": "fused AdamW params/s & GB/s (% HBM peak); fp8 codec GB/s; 2.8B stage",

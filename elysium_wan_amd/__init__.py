@@ -8,6 +8,9 @@ Modules mirror the reference's:
   fp8     -- model/fp8.py       (scale_exp, quantize, dequantize, roundtrip,
              recover_exp)
   pieces  -- runtime/pieces.py  (cast_piece, fold_start, fold_add, fold)
+  accumulate -- runtime/accumulate.py (OrderedAccumulator: the ordered
+             microbatch fold, with the last part optionally left for the
+             fused update)
   planes  -- codec/planes.py    (encode, decode, encode_scaled_fp8: the
              byte-plane and scaled-fp8 wires)
   fp8_planes -- codec/fp8_planes.py (encode, decode: the e4m3 nibble wire)
@@ -17,6 +20,6 @@ The kernels live in libelyhip.so (C ABI: include/ely.h), built by
 elysium_wan_amd.build for gfx950.
 """
 
-from . import boundary, f32_planes, fp8, fp8_planes, optim, pieces, planes  # noqa: F401
+from . import accumulate, boundary, f32_planes, fp8, fp8_planes, optim, pieces, planes  # noqa: F401
 
-__all__ = ["boundary", "f32_planes", "fp8", "fp8_planes", "optim", "pieces", "planes"]
+__all__ = ["accumulate", "boundary", "f32_planes", "fp8", "fp8_planes", "optim", "pieces", "planes"]

@@ -15,18 +15,22 @@
 
 Either way one step is at most two launches over the whole parameter list:
 the deterministic grad-norm (when max_norm is set) and the fused
-clip + AdamW + bf16-working-copy kernel, one HBM pass per element.
+clip + AdamW + bf16-working-copy kernel, one HBM pass per element.  With
+step(on_param=...) the update goes out in parameter-ordered groups instead,
+each followed by on_param of its parameters, so a caller can release layers
+as they land.
 
 The torch.optim surface the runtime uses is kept: step(on_param=None),
 zero_grad, state_dict, load_state_dict (torch's AdamW layout: state[i] =
 {step, exp_avg, exp_avg_sq}, one param group; "moments": "host" for
-adamw-host), param_groups and state.
+adamw-host), param_groups and state (keyed by parameter index for
+adamw-host, as HostAdamW, and by parameter tensor for adamw, as torch).
 """
 
 from __future__ import annotations
 
 import math
-from collections.abc import Iterable
+from collections.abc import Iterable, MutableMapping
 
 import numpy as np
 import torch
@@ -119,6 +123,60 @@ def torch_consts(lr: float, betas, eps: float, weight_decay: float, t: float) ->
     ]
 
 
+class _State(MutableMapping):
+    """`opt.state`, keyed as each recipe's reference keys it:
+    parameter indices for "adamw-host" (HostAdamW, runtime/optim.py:106) and
+    the parameter tensors themselves for "adamw" (torch.optim.AdamW, whose
+    state runtime/stage.py:2265-2271 reads and :2642-2646 assigns per master
+    tensor).  Either kind of key is accepted for lookup.  An entry is
+    {step, exp_avg, exp_avg_sq}; the moments are views of the optimizer's own
+    storage, so assigning an entry copies the given values into it (the
+    optimizer never adopts the caller's tensors), and deleting one makes the
+    parameter start again from zero moments at step 0."""
+
+    def __init__(self, opt: FusedAdamW):
+        self._opt = opt
+
+    def _index(self, key) -> int:
+        opt = self._opt
+        if isinstance(key, torch.Tensor):
+            i = opt._pindex.get(id(key))
+            if i is None or opt.params[i] is not key:
+                raise KeyError("a tensor that is not a parameter of this optimizer")
+            return i
+        if isinstance(key, (int, np.integer)) and not isinstance(key, bool) and 0 <= int(key) < len(opt.params):
+            return int(key)
+        raise KeyError(key)
+
+    def __getitem__(self, key) -> dict:
+        return self._opt._st[self._index(key)]
+
+    def __setitem__(self, key, value) -> None:
+        i = self._index(key)
+        self._opt._assign(i, value)
+
+    def __delitem__(self, key) -> None:
+        i = self._index(key)
+        del self._opt._st[i]
+
+    def __contains__(self, key) -> bool:
+        try:
+            return self._index(key) in self._opt._st
+        except KeyError:
+            return False
+
+    def __iter__(self):
+        opt = self._opt
+        for i in sorted(opt._st):
+            yield opt.params[i] if opt.order == "torch" else i
+
+    def __len__(self) -> int:
+        return len(self._opt._st)
+
+    def __repr__(self) -> str:
+        return f"{type(self).__name__}({len(self)} entries, keyed by {'parameter' if self._opt.order == 'torch' else 'index'})"
+
+
 class FusedAdamW:
     """AdamW (decoupled weight decay, no amsgrad) over a ragged list of fp32
     CUDA parameters, one fused launch per step.
@@ -144,6 +202,13 @@ class FusedAdamW:
     update.  Moments exist for trainable (requires_grad) parameters only,
     allocated at the first step, as the reference allocates them per stepped
     parameter.
+    release_elems: with step(on_param=...), the update is issued in
+        parameter-ordered groups of at least this many elements, and
+        on_param(i) runs as soon as the group holding parameter i is issued,
+        so a caller can release each layer while later ones still update
+        (runtime/optim.py:164-170, runtime/stage.py:3080-3099).  Without
+        on_param the step is one launch per gradient dtype.  The bits are the
+        same either way.
     """
 
     def __init__(
@@ -161,8 +226,11 @@ class FusedAdamW:
         chunk: int = CHUNK,
         pipeline: bool | None = None,
         slots: int = 3,
+        release_elems: int = 1 << 26,
     ):
         self.params = list(params)
+        self._pindex = {id(p): i for i, p in enumerate(self.params)}
+        self.release_elems = max(1, int(release_elems))
         if order not in ("host", "torch"):
             raise ValueError(f"order {order!r} is not 'host' or 'torch'")
         if moments not in ("device", "host"):
@@ -216,10 +284,12 @@ class FusedAdamW:
         group.update(lr=lr, betas=self.betas, eps=eps, weight_decay=weight_decay)
         self._group = group
         self.param_groups = [{**group, "params": self.params}]
-        self.state: dict = {}
+        self._st: dict = {}  # parameter index -> {"step", "exp_avg", "exp_avg_sq"}
+        self.state = _State(self)
         self._flat_m = self._flat_v = None
+        self._fresh: set = set()  # indices whose flat moment slices still hold the allocation's zeros
         self._steps = None  # flat fp32 step counters; state[i]["step"] are 0-d views of it
-        self._tables = None  # descriptor arrays kept between steps (_launch_cached)
+        self._tables: dict = {}  # descriptor arrays kept between steps, per launch group (_launch_cached)
         self._norm = None  # device ely_norm_result of the last clipped step
         self.working_copies = self._init_copies(working_copy)
 
@@ -275,10 +345,15 @@ class FusedAdamW:
             self._flat_v = torch.zeros(max(total, 1), dtype=torch.float32, device=dev)
         self._offs = offs
         self._steps = torch.zeros(max(len(self.params), 1), dtype=torch.float32)
-        self._tables = None
+        self._fresh = {i for i, o in enumerate(offs) if o is not None}
+        self._tables = {}
 
-    def _slot(self, i: int, p: torch.Tensor) -> dict:
-        st = self.state.get(i)
+    def _slot(self, i: int, p: torch.Tensor, clear: bool = True) -> dict:
+        """State entry i, made on first use: zero moments at step 0.  A slice
+        of the flat buffers that an earlier entry used (one that
+        load_state_dict or `del state[p]` dropped) is zeroed again, unless the
+        caller is about to overwrite it (clear=False)."""
+        st = self._st.get(i)
         if st is None:
             if self._flat_m is None:
                 self._alloc_state()
@@ -294,25 +369,48 @@ class FusedAdamW:
             else:
                 m = self._flat_m[o : o + n].view(p.shape)
                 v = self._flat_v[o : o + n].view(p.shape)
-            st = self.state[i] = {
+                if clear and i not in self._fresh:
+                    m.zero_()
+                    v.zero_()
+                self._fresh.discard(i)
+            self._steps[i] = 0.0
+            st = self._st[i] = {
                 "step": self._steps[i],  # a 0-d view of the flat counters
                 "exp_avg": m,
                 "exp_avg_sq": v,
             }
         return st
 
+    def _assign(self, i: int, st: dict) -> None:
+        """Entry i set to the given {step, exp_avg, exp_avg_sq}: the values are
+        copied into the optimizer's storage (a resume, runtime/stage.py:
+        2642-2646, and load_state_dict)."""
+        p = self.params[i]
+        for k in ("exp_avg", "exp_avg_sq"):
+            if tuple(st[k].shape) != tuple(p.shape):
+                raise ValueError(f"optimizer state {i}.{k} has shape {tuple(st[k].shape)}")
+        self._st.pop(i, None)
+        slot = self._slot(i, p, clear=False)
+        slot["step"].copy_(torch.as_tensor(st["step"], dtype=torch.float32).detach().cpu())
+        slot["exp_avg"].copy_(st["exp_avg"])
+        slot["exp_avg_sq"].copy_(st["exp_avg_sq"])
+
     # --------------------------------------------------------------- step
 
-    def _consts(self, t: float) -> list:
+    def _consts(self, t: float, lr: float, betas, eps: float, weight_decay: float) -> list:
         if self.order == "host":
-            return host_consts(self.lr, self.betas, self.eps, self.weight_decay, t)
-        return torch_consts(self.lr, self.betas, self.eps, self.weight_decay, t)
+            return host_consts(lr, betas, eps, weight_decay, t)
+        return torch_consts(lr, betas, eps, weight_decay, t)
 
     @torch.no_grad()
     def step(self, on_param=None, grads=None, acc=None) -> None:
         """One AdamW step over every parameter with a gradient, in order;
-        `on_param(i)` runs after parameter i's update is issued
-        (runtime/optim.py:145-170).  Nothing here waits for the GPU.
+        `on_param(i)` runs right after parameter i's update is issued
+        (runtime/optim.py:145-170): the update then goes out in
+        parameter-ordered groups of `release_elems` elements, so a layer can
+        be released while later ones still update.  Nothing here waits for
+        the GPU, except that host moments land before the step returns, as
+        HostAdamW's do (runtime/optim.py:171-174).
 
         grads: optional list aligned with the parameters (None entries skip
         a parameter) used instead of p.grad -- the way to hand in bf16
@@ -333,53 +431,79 @@ class FusedAdamW:
         gs = [gl[i] for i in idx]
         accs = None if acc is None else [acc[i] for i in idx]
         self._check_inputs(idx, ps, gs, accs)
-        if idx:
-            sts = [self._slot(i, p) for i, p in zip(idx, ps)]
-            ms = [st["exp_avg"] for st in sts]
-            vs = [st["exp_avg_sq"] for st in sts]
-            if self.moments == "host":
-                host = [j for j, m in enumerate(ms) if m.device.type != "cuda"]
-                self._check_host_moments([idx[j] for j in host], [ms[j] for j in host], [vs[j] for j in host])
-            # the step counters are views of one flat tensor: one increment for all
-            it = torch.tensor(idx, dtype=torch.int64)
-            self._steps[it] += 1
-            ts = self._steps[it].tolist()
-            cs = [self.working_copies[i] if self.working_copies is not None else None for i in idx]
-            per_t = {t: self._consts(t) for t in set(ts)}
-            consts = [per_t[t] for t in ts]
-            dev = ps[0].device
-            fold = accs
-            if self.moments == "host":
-                streamed = [j for j, m in enumerate(ms) if m.device.type != "cuda"]
-                direct = [j for j, m in enumerate(ms) if m.device.type == "cuda"]
+        if not idx:
+            return
+        sts = [self._slot(i, p) for i, p in zip(idx, ps)]
+        ms = [st["exp_avg"] for st in sts]
+        vs = [st["exp_avg_sq"] for st in sts]
+        host = [j for j, m in enumerate(ms) if m.device.type != "cuda"]
+        if host:
+            self._check_host_moments([idx[j] for j in host], [ms[j] for j in host], [vs[j] for j in host])
+        # the step counters are views of one flat tensor: one increment for all
+        it = torch.tensor(idx, dtype=torch.int64)
+        self._steps[it] += 1
+        ts = self._steps[it].tolist()
+        cs = [self.working_copies[i] if self.working_copies is not None else None for i in idx]
+        lr, betas, eps, wd = self._hyper()
+        per_t = {t: self._consts(t, lr, betas, eps, wd) for t in set(ts)}
+        consts = [per_t[t] for t in ts]
+        dev = ps[0].device
+        groups = [list(range(len(idx)))] if on_param is None else self._release_groups(ps)
+        with torch.cuda.device(dev):
+            # the norm covers every gradient of the step, before any group updates
+            coef_ptr = self._clip_coef(gs, accs) if self.max_norm is not None else None
+            for grp in groups:
+                self._issue(grp, idx, ps, gs, ms, vs, cs, consts, coef_ptr, accs, wd != 0)
+                if on_param is not None:
+                    for j in grp:
+                        on_param(idx[j])
+            if host:
+                # the host moments are the state: they land before the step returns (runtime/optim.py:171-174)
+                torch.cuda.synchronize(dev)
+
+    def _hyper(self) -> tuple:
+        """(lr, betas, eps, weight_decay) of this step: torch.optim.AdamW reads
+        them from its param group at every step (so a scheduler's lr takes
+        effect); HostAdamW keeps its constructor's (runtime/optim.py:100)."""
+        if self.order == "torch":
+            g = self.param_groups[0]
+            b1, b2 = g["betas"]
+            return float(g["lr"]), (float(b1), float(b2)), float(g["eps"]), float(g["weight_decay"])
+        return self.lr, self.betas, self.eps, self.weight_decay
+
+    def _release_groups(self, ps) -> list:
+        """Consecutive runs of stepped parameters, each closed once it holds
+        release_elems elements (the last may hold fewer)."""
+        groups, cur, n = [], [], 0
+        for j, p in enumerate(ps):
+            cur.append(j)
+            n += p.numel()
+            if n >= self.release_elems:
+                groups.append(cur)
+                cur, n = [], 0
+        if cur:
+            groups.append(cur)
+        return groups
+
+    def _issue(self, grp, idx, ps, gs, ms, vs, cs, consts, coef_ptr, accs, wd: bool) -> None:
+        """The update of the stepped parameters at positions `grp`: one launch
+        per gradient dtype for HBM moments (torch groups by dtype the same
+        way), then the host moments' update (in place through the mapping,
+        or staged)."""
+        direct = [j for j in grp if ms[j].device.type == "cuda"]
+        streamed = [j for j in grp if ms[j].device.type != "cuda"]
+        for gdt in (torch.bfloat16, torch.float32):
+            sel = [j for j in direct if gs[j].dtype == gdt]
+            if sel:
+                self._launch_cached(sel, idx, ps, gs, ms, vs, cs, consts, coef_ptr, accs, wd)
+        if streamed:
+            sub = lambda xs: [xs[j] for j in streamed]  # noqa: E731
+            if self._mapped is not None:
+                self._update_mapped(sub(ps), sub(gs), sub(ms), sub(vs), sub(cs), sub(consts), coef_ptr,
+                                    None if accs is None else sub(accs), wd)
             else:
-                streamed, direct = [], list(range(len(idx)))
-            with torch.cuda.device(dev):
-                coef_ptr = self._clip_coef(gs, fold) if self.max_norm is not None else None
-                # one launch per gradient dtype (torch groups by dtype the same way)
-                for gdt in (torch.bfloat16, torch.float32):
-                    sel = [j for j in direct if gs[j].dtype == gdt]
-                    if not sel:
-                        continue
-                    if len(sel) == len(idx):
-                        self._launch_cached(idx, ps, gs, ms, vs, cs, consts, coef_ptr, fold)
-                    else:
-                        self._launch([ps[j] for j in sel], [gs[j] for j in sel], [ms[j] for j in sel],
-                                     [vs[j] for j in sel], [cs[j] for j in sel], [consts[j] for j in sel], coef_ptr,
-                                     None if fold is None else [fold[j] for j in sel])
-                if streamed:
-                    sub = lambda xs: [xs[j] for j in streamed]  # noqa: E731
-                    if self._mapped is not None:
-                        self._update_mapped(sub(ps), sub(gs), sub(ms), sub(vs), sub(cs), sub(consts), coef_ptr,
-                                            None if fold is None else sub(fold))
-                    else:
-                        self._stream_host_moments(sub(idx), sub(ps), sub(gs), sub(cs), sub(consts), coef_ptr,
-                                                  None if fold is None else sub(fold))
-                    # the host moments are the state: they land before the step returns (runtime/optim.py:171-174)
-                    torch.cuda.synchronize(dev)
-        if on_param is not None:
-            for i in idx:
-                on_param(i)
+                self._stream_host_moments(sub(idx), sub(ps), sub(gs), sub(cs), sub(consts), coef_ptr,
+                                          None if accs is None else sub(accs), wd)
 
     _GRAD_DTYPES = (torch.float32, torch.bfloat16)
 
@@ -408,28 +532,33 @@ class FusedAdamW:
                 if a is None or a.dtype != f32 or a.shape != p.shape or not a.is_contiguous() or a.device != pd:
                     raise ValueError(f"{self.recipe}: the fold accumulator of parameter {i} must be a contiguous float32 tensor shaped like it, on its device")
 
-    def _launch_cached(self, idx, ps, gs, ms, vs, cs, consts, coef_ptr, accs) -> None:
-        """_launch over every stepped parameter, with the descriptor arrays
-        of the tensors the optimizer owns (moments, working copies) and of
-        the parameters kept from the last step with the same parameters: the
-        parameters' data pointers are compared each step, the moments' and
-        copies' change only through _alloc_state and promote (which drop the
-        cache).  Gradients and accumulators are new every step."""
-        key = tuple(idx)
-        pptrs = [p.data_ptr() for p in ps]
-        t = self._tables
-        if t is None or t["key"] != key or t["pptrs"] != pptrs:
-            copies = [(_lib.ely_tensor(c) if c is not None else _lib.ElyTensor(None, 0, _lib.BF16, 0)) for c in cs]
-            t = self._tables = {
-                "key": key,
-                "pptrs": pptrs,
-                "p": _lib.tensor_array(ps),
-                "m": _lib.tensor_array(ms),
-                "v": _lib.tensor_array(vs),
+    def _launch_cached(self, sel, idx, ps, gs, ms, vs, cs, consts, coef_ptr, accs, wd: bool) -> None:
+        """_launch over the stepped parameters at positions `sel`, with the
+        descriptor arrays of the parameters, moments and working copies kept
+        from the last launch of the same parameters while every one of their
+        data pointers is unchanged (a state entry replaced, a promote or a
+        load_state_dict moves the moments, and the arrays are rebuilt).
+        Gradients and accumulators are new every step."""
+        key = tuple(idx[j] for j in sel)
+        ptrs = [ps[j].data_ptr() for j in sel]
+        ptrs += [ms[j].data_ptr() for j in sel]
+        ptrs += [vs[j].data_ptr() for j in sel]
+        ptrs += [0 if cs[j] is None else cs[j].data_ptr() for j in sel]
+        t = self._tables.get(key)
+        if t is None or t["ptrs"] != ptrs:
+            if len(self._tables) >= 64:
+                self._tables.clear()
+            copies = [(_lib.ely_tensor(cs[j]) if cs[j] is not None else _lib.ElyTensor(None, 0, _lib.BF16, 0)) for j in sel]
+            t = self._tables[key] = {
+                "ptrs": ptrs,
+                "p": _lib.tensor_array([ps[j] for j in sel]),
+                "m": _lib.tensor_array([ms[j] for j in sel]),
+                "v": _lib.tensor_array([vs[j] for j in sel]),
                 "c": _lib.tensor_array(copies),
             }
-        self._launch_arrays(len(ps), t["p"], _lib.tensor_array(gs), t["m"], t["v"], t["c"], consts, coef_ptr,
-                            None if accs is None else _lib.tensor_array(accs), ps[0].device)
+        self._launch_arrays(len(sel), t["p"], _lib.tensor_array([gs[j] for j in sel]), t["m"], t["v"], t["c"],
+                            [consts[j] for j in sel], coef_ptr,
+                            None if accs is None else _lib.tensor_array([accs[j] for j in sel]), ps[sel[0]].device, wd)
 
     def _check_host_moments(self, idx, ms, vs) -> None:
         """Host moments are views of the optimizer's two pinned buffers (the
@@ -443,7 +572,7 @@ class FusedAdamW:
                 if not (t.dtype == torch.float32 and t.is_contiguous() and lo <= a and a + t.numel() * 4 <= hi):
                     raise ValueError(f"{self.recipe}: state[{i}][{name!r}] is not a view of the optimizer's pinned moment buffer")
 
-    def _update_mapped(self, ps, gs, ms, vs, cs, consts, coef_ptr, accs) -> None:
+    def _update_mapped(self, ps, gs, ms, vs, cs, consts, coef_ptr, accs, wd: bool) -> None:
         """The update of parameters whose moments live in pinned host memory,
         in place: the fused kernel gets the moments' addresses as the GPU
         sees the mapped buffers, and its loads and stores of m and v cross
@@ -456,9 +585,9 @@ class FusedAdamW:
                 continue
             self._launch([ps[j] for j in sel], [gs[j] for j in sel], [mapped(ms[j], dm, hm) for j in sel],
                          [mapped(vs[j], dv, hv) for j in sel], [cs[j] for j in sel], [consts[j] for j in sel], coef_ptr,
-                         None if accs is None else [accs[j] for j in sel])
+                         None if accs is None else [accs[j] for j in sel], wd)
 
-    def _stream_host_moments(self, idx, ps, gs, cs, consts, coef_ptr, accs) -> None:
+    def _stream_host_moments(self, idx, ps, gs, cs, consts, coef_ptr, accs, wd: bool) -> None:
         """The update of parameters whose moments live in host memory
         (runtime/optim.py:176-204, 301-363): the flat moment buffers are cut
         into equal chunks of `chunk` elements along parameter order (a chunk
@@ -524,7 +653,7 @@ class FusedAdamW:
                         [vd[o + s0 : o + e0] for o, (_, s0, e0) in zip(off, sel)],
                         [None if cs[j] is None else cs[j].view(-1)[s0:e0] for j, s0, e0 in sel],
                         [consts[j] for j, _, _ in sel], coef_ptr,
-                        None if accs is None else views(accs),
+                        None if accs is None else views(accs), wd,
                     )
                 if staged:
                     st["ev_done"][slot].record(up)
@@ -575,7 +704,6 @@ class FusedAdamW:
             st = self._slot(i, p)
             st["exp_avg"] = st["exp_avg"].to(p.device)
             st["exp_avg_sq"] = st["exp_avg_sq"].to(p.device)
-            self._tables = None
             self.resident.add(i)
             moved += need
         if moved:
@@ -599,13 +727,13 @@ class FusedAdamW:
         _lib.check(rc, "grad norm")
         return self._norm.data_ptr() + 12
 
-    def _launch(self, ps, gs, ms, vs, cs, consts, coef_ptr, accs=None) -> None:
+    def _launch(self, ps, gs, ms, vs, cs, consts, coef_ptr, accs, wd: bool) -> None:
         copies = [(_lib.ely_tensor(c) if c is not None else _lib.ElyTensor(None, 0, _lib.BF16, 0)) for c in cs]
         self._launch_arrays(len(ps), _lib.tensor_array(ps), _lib.tensor_array(gs), _lib.tensor_array(ms),
                             _lib.tensor_array(vs), _lib.tensor_array(copies), consts, coef_ptr,
-                            None if accs is None else _lib.tensor_array(accs), ps[0].device)
+                            None if accs is None else _lib.tensor_array(accs), ps[0].device, wd)
 
-    def _launch_arrays(self, n, parr, garr, marr, varr, carr, consts, coef_ptr, aarr, dev) -> None:
+    def _launch_arrays(self, n, parr, garr, marr, varr, carr, consts, coef_ptr, aarr, dev, wd: bool) -> None:
         L = _lib.load()
         stream = _lib.stream_ptr(dev)
         ctab = np.asarray(consts, dtype=np.float32).reshape(n, -1)
@@ -615,7 +743,7 @@ class FusedAdamW:
         carr_c = (_lib.ElyConsts * n).from_buffer(ctab)
         ws = _lib.workspace(dev, L.ely_adamw_workspace_bytes(n))
         order = _lib.ORDER_HOST if self.order == "host" else _lib.ORDER_TORCH
-        wd = int(self.weight_decay != 0)
+        wd = int(wd)
         if aarr is None:
             rc = L.ely_adamw_step(parr, garr, marr, varr, carr, n, carr_c, order, wd, coef_ptr, ws.data_ptr(), ws.numel(), stream)
         else:
@@ -640,9 +768,13 @@ class FusedAdamW:
     # --------------------------------------------------------- checkpoint
 
     def state_dict(self) -> dict:
-        """torch's AdamW layout; adamw-host returns host copies of the moments
-        as the reference does (runtime/optim.py:238-250)."""
+        """torch's AdamW layout, keyed by parameter index; adamw-host returns
+        host copies of the moments as the reference does
+        (runtime/optim.py:238-250), "adamw" the moment tensors themselves as
+        torch does.  The group is the live param group (a scheduler's lr
+        included)."""
         host = self.order == "host"
+        group = {k: v for k, v in self.param_groups[0].items() if k != "params"}
         return {
             "state": {
                 i: {
@@ -650,38 +782,65 @@ class FusedAdamW:
                     "exp_avg": st["exp_avg"].cpu() if host else st["exp_avg"],
                     "exp_avg_sq": st["exp_avg_sq"].cpu() if host else st["exp_avg_sq"],
                 }
-                for i, st in sorted(self.state.items())
+                for i, st in sorted(self._st.items())
             },
-            "param_groups": [{**self._group, "params": list(range(len(self.params)))}],
+            "param_groups": [{**group, "params": list(range(len(self.params)))}],
         }
 
     def load_state_dict(self, sd: dict) -> None:
-        """runtime/optim.py:252-274: refuses another recipe's state, other
-        parameters and wrong shapes."""
+        """adamw-host: runtime/optim.py:252-274, refusing another recipe's
+        state (any hyperparameter that differs), other parameters and wrong
+        shapes.  adamw: torch.optim.Optimizer.load_state_dict's semantics
+        (TORCH/optim/optimizer.py:877-1016): one group of as many parameters,
+        whose saved hyperparameters (lr, betas, eps, weight_decay, and keys
+        this build does not read) are adopted; amsgrad and maximize, which
+        the fused kernel does not implement, are refused.  Parameters the
+        state does not name start again from zero moments."""
         groups = sd.get("param_groups") or []
-        if len(groups) != 1:
-            raise ValueError(f"{self.recipe} state holds one param group")
-        theirs = {k: v for k, v in groups[0].items() if k != "params"}
-        mine = json_norm(self._group)
-        if json_norm(theirs) != mine:
-            raise ValueError(f"optimizer state of another recipe: {json_norm(theirs)} is not {mine}")
-        if list(groups[0]["params"]) != list(range(len(self.params))):
-            raise ValueError("optimizer state names other parameters")
-        for i, st in sd.get("state", {}).items():
-            i = int(i)
+        if self.order == "torch":
+            if len(groups) != 1:
+                raise ValueError("loaded state dict has a different number of parameter groups")
+            if len(groups[0]["params"]) != len(self.params):
+                raise ValueError("loaded state dict contains a parameter group that doesn't match the size of optimizer's group")
+            theirs = {k: v for k, v in groups[0].items() if k != "params"}
+            for flag in ("amsgrad", "maximize"):
+                if theirs.get(flag):
+                    raise ValueError(f"{self.recipe} on MI355X steps AdamW without {flag}; the state asks for it")
+            b1, b2 = theirs.get("betas", self.betas)
+            self.lr = float(theirs.get("lr", self.lr))
+            self.betas = (float(b1), float(b2))
+            self.eps = float(theirs.get("eps", self.eps))
+            self.weight_decay = float(theirs.get("weight_decay", self.weight_decay))
+            self._group = {**self._group, **theirs}
+            self.param_groups = [{**self._group, "params": self.params}]
+            # the saved list of parameter ids maps onto this optimizer's, in order
+            ids = {k: i for i, k in enumerate(groups[0]["params"])}
+        else:
+            if len(groups) != 1:
+                raise ValueError(f"{self.recipe} state holds one param group")
+            theirs = {k: v for k, v in groups[0].items() if k != "params"}
+            mine = json_norm(self._group)
+            if json_norm(theirs) != mine:
+                raise ValueError(f"optimizer state of another recipe: {json_norm(theirs)} is not {mine}")
+            if list(groups[0]["params"]) != list(range(len(self.params))):
+                raise ValueError("optimizer state names other parameters")
+            ids = {i: i for i in range(len(self.params))}
+        states = {}
+        for k, st in sd.get("state", {}).items():
+            k = int(k) if isinstance(k, str) else k  # keys read back from JSON
+            if k not in ids:
+                raise ValueError("optimizer state names other parameters")
+            i = ids[k]
             p = self.params[i]
-            for k in ("exp_avg", "exp_avg_sq"):
-                if tuple(st[k].shape) != tuple(p.shape):
-                    raise ValueError(f"optimizer state {i}.{k} has shape {tuple(st[k].shape)}")
-        self.state = {}
+            for name in ("exp_avg", "exp_avg_sq"):
+                if tuple(st[name].shape) != tuple(p.shape):
+                    raise ValueError(f"optimizer state {i}.{name} has shape {tuple(st[name].shape)}")
+            states[i] = st
+        self._st.clear()
         if self._flat_m is not None:
             self._steps.zero_()
-        for i, st in sd.get("state", {}).items():
-            i = int(i)
-            slot = self._slot(i, self.params[i])
-            slot["step"].copy_(torch.as_tensor(st["step"], dtype=torch.float32).cpu())
-            slot["exp_avg"].copy_(st["exp_avg"])
-            slot["exp_avg_sq"].copy_(st["exp_avg_sq"])
+        for i, st in sorted(states.items()):
+            self._assign(i, st)
 
 
 def clip_grad_norm_(parameters, max_norm: float, norm_type: float = 2.0, error_if_nonfinite: bool = False, foreach=None) -> torch.Tensor:

@@ -1,0 +1,114 @@
+"""The ordered microbatch fold (accumulate.OrderedAccumulator, the drop-in
+for runtime/accumulate.py:15-137) on the GPU, feeding the fused update:
+parts handed in out of order and through quarantine fold in microbatch
+order, bit for bit against the oracle's left fold; with defer_last the last
+microbatch is folded inside the update (FusedAdamW.step(grads, acc)) and
+the step equals the oracle's fold-then-HostAdamW bit for bit, norm and clip
+included (runtime/stage.py:3002-3024 then runtime/optim.py:145-174)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import bits, say
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(96, 64), (64,), (4097,), (33, 7), (8192,)]
+
+
+def _parts(seed: int, m: int, dtype):
+    gen = torch.Generator().manual_seed(seed)
+    return [[(torch.randn(s, generator=gen) * 1e-2).to(dtype) for s in SHAPES] for _ in range(m)]
+
+
+def _oracle_fold(oracle, parts, i):
+    """Microbatch order, tensor i: the first part widened, then fold_add."""
+    acc = bits(parts[0][i].float()).reshape(-1).copy()
+    for mb in range(1, len(parts)):
+        oracle.fold_add(acc, bits(parts[mb][i]).reshape(-1))
+    return acc
+
+
+@pytest.mark.parametrize("gdtype", [torch.bfloat16, torch.float32])
+def test_out_of_order_parts_fold_in_order_and_into_the_update(oracle, gdtype):
+    from elysium_wan_amd import accumulate, optim
+
+    M = 4
+    parts = _parts(3, M, gdtype)
+    gen = torch.Generator().manual_seed(4)
+    init = [torch.randn(s, generator=gen) * 0.02 for s in SHAPES]
+    ps = [t.clone().cuda().requires_grad_(True) for t in init]
+    opt = optim.FusedAdamW(ps, lr=1e-2, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, order="host", max_norm=0.5,
+                           working_copy=True)
+    plain = accumulate.OrderedAccumulator(range(M))
+    deferred = accumulate.OrderedAccumulator(range(M), defer_last=True)
+    # arrivals: mb 2 before mb 1, mb 3 (the last) early, mb 1 quarantined then released;
+    # tensors of one microbatch in scrambled order (fold_part, RUNTIME-I21)
+    arrivals = [(0, [4, 0, 2, 1, 3]), (2, [1, 3, 0, 4, 2]), (3, [0, 1, 2, 3, 4]), (1, [3, 2, 4, 0, 1])]
+    say("ordered fold", gdtype)
+    for acc in (plain, deferred):
+        for mb, order in arrivals:
+            if mb == 1:
+                acc.add(mb, [parts[mb][i].cuda() for i in range(len(SHAPES))], verified=False)
+                assert not acc.complete() and acc.pos == 1
+                acc.release(mb)
+            else:
+                for i in order:
+                    acc.fold_part(mb, i, len(SHAPES), parts[mb][i].cuda(), torch.float32)
+                acc.end_part(mb)
+        assert acc.complete()
+    grads, accs = deferred.step_inputs()
+    assert all(g.dtype == gdtype for g in grads) and all(a.dtype == torch.float32 for a in accs)
+    for i in range(len(SHAPES)):
+        prefix = bits(parts[0][i].float()).reshape(-1).copy()
+        for mb in (1, 2):
+            oracle.fold_add(prefix, bits(parts[mb][i]).reshape(-1))
+        assert np.array_equal(bits(accs[i]).reshape(-1).view(np.uint32), prefix.view(np.uint32)), i
+    opt.step(grads=grads, acc=accs)
+    torch.cuda.synchronize()
+    full = [_oracle_fold(oracle, parts, i) for i in range(len(SHAPES))]
+    for i, s in enumerate(plain.result()):
+        assert np.array_equal(bits(s).reshape(-1).view(np.uint32), full[i].view(np.uint32)), i
+    for i, s in enumerate(deferred.result()):
+        assert np.array_equal(bits(s).reshape(-1).view(np.uint32), full[i].view(np.uint32)), i
+    g = np.concatenate(full)
+    norm = float(np.float32(np.sqrt(oracle.sumsq([g]))))
+    assert abs(float(opt.grad_norm()) - norm) <= 1e-6 * norm
+    coef = float(opt._norm[12:16].view(torch.float32))
+    assert coef == oracle.clip_coef(float(opt.grad_norm()), 0.5)
+    p = np.concatenate([t.reshape(-1).numpy() for t in init])
+    m, v, cp = np.zeros_like(p), np.zeros_like(p), np.zeros(p.size, np.uint16)
+    oracle.adamw_host(p, g, m, v, oracle.host_adamw_consts(1e-2, (0.9, 0.95), 1e-8, 0.1, 1), True, coef, cp)
+    got = np.concatenate([bits(t).reshape(-1) for t in ps])
+    assert np.array_equal(got.view(np.uint32), p.view(np.uint32))
+    assert np.array_equal(np.concatenate([bits(opt.state[i]["exp_avg"]).reshape(-1) for i in range(len(SHAPES))]).view(np.uint32),
+                          m.view(np.uint32))
+    assert np.array_equal(np.concatenate([bits(c).reshape(-1) for c in opt.working_copies]), cp)
+
+
+def test_one_microbatch_defers_its_only_part(oracle):
+    """With a single microbatch the held part is the whole gradient: no
+    accumulator, and the step widens it in registers exactly as the
+    reference's widening copy would."""
+    from elysium_wan_amd import accumulate, optim
+
+    parts = _parts(5, 1, torch.bfloat16)
+    acc = accumulate.OrderedAccumulator([0], defer_last=True)
+    acc.add(0, [t.cuda() for t in parts[0]])
+    grads, accs = acc.step_inputs()
+    assert accs is None and all(g.dtype == torch.bfloat16 for g in grads)
+    gen = torch.Generator().manual_seed(6)
+    init = [torch.randn(s, generator=gen) * 0.02 for s in SHAPES]
+    a = [t.clone().cuda().requires_grad_(True) for t in init]
+    b = [t.clone().cuda().requires_grad_(True) for t in init]
+    oa = optim.FusedAdamW(a, lr=1e-2, order="host")
+    ob = optim.FusedAdamW(b, lr=1e-2, order="host")
+    oa.step(grads=grads, acc=accs)
+    full = acc.result()
+    assert all(s.dtype == torch.bfloat16 for s in full)  # no widening dtype was named: the reference's clone
+    ob.step(grads=[t.float() for t in full])
+    torch.cuda.synchronize()
+    assert all(torch.equal(x.detach().view(torch.int32), y.detach().view(torch.int32)) for x, y in zip(a, b))

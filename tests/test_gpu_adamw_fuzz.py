@@ -98,3 +98,100 @@ def test_fused_step_matches_the_oracle(oracle, specs, bf16g, order, wd, clip, wi
                 assert int(ulp_distance(gb.view(np.float32), want).max(initial=0)) <= 1
         if with_copy and order == "host":
             assert np.array_equal(bits(d[4]), c)
+
+
+fold_spec = st.tuples(st.sampled_from(SIZES), st.lists(st.sampled_from([0, 0, 1, 2, 3]), min_size=6, max_size=6))
+
+
+@FUZZ
+@given(
+    specs=st.lists(fold_spec, min_size=1, max_size=6),
+    bf16g=st.booleans(),
+    order=st.sampled_from(["host", "torch"]),
+    wd=st.sampled_from([0.0, 0.1]),
+    max_norm=st.sampled_from([None, 0.05, 1e3]),
+    with_copy=st.booleans(),
+    seed=st.integers(0, 2**16),
+)
+def test_fused_fold_step_matches_the_oracle(oracle, specs, bf16g, order, wd, max_norm, with_copy, seed):
+    """ely_grad_norm_fold + ely_adamw_fold_step (the last microbatch folded
+    inside the norm and the update, runtime/accumulate.py:93-104) against the
+    oracle's fold_add followed by its step: the norm within 1e-6 of the
+    oracle's fp64 sum of squares of the folded gradients, then host order
+    bit for bit (parameters, moments, working copy) and torch order within
+    1 ulp, with each of the six streams at its own misalignment, over two
+    steps; the accumulators are never written."""
+    from elysium_wan_amd import _lib
+
+    L = _lib.load()
+    rng = np.random.default_rng(seed)
+    say("adamw fold fuzz", order, "bf16" if bf16g else "f32", wd, max_norm, with_copy, [s for s, _ in specs])
+    host, dev = [], []
+    for n, offs in specs:
+        p = (rng.standard_normal(n) * 0.1).astype(np.float32)
+        m, v, c = np.zeros(n, np.float32), np.zeros(n, np.float32), np.zeros(n, np.uint16)
+        host.append([p, m, v, c])
+        dev.append({"p": _view(p, offs[0], torch.float32), "m": _view(m, offs[2], torch.float32),
+                    "v": _view(v, offs[3], torch.float32),
+                    "c": _view(c, offs[4], torch.bfloat16) if with_copy else None, "offs": offs})
+    n_t = len(specs)
+    stream = _lib.stream_ptr(torch.device("cuda", 0))
+    res = torch.zeros(16, dtype=torch.uint8, device="cuda")
+    for step in range(2):
+        gs, accs = [], []
+        for (n, _), d in zip(specs, dev):
+            a = (rng.standard_normal(n) * 1e-2).astype(np.float32)
+            g = (rng.standard_normal(n) * 1e-2).astype(np.float32)
+            if bf16g:
+                g = oracle.f32_to_bf16_bits(g)
+            gs.append(g)
+            accs.append(a)
+            d["g"] = _view(g, d["offs"][1], torch.bfloat16 if bf16g else torch.float32)
+            d["a"] = _view(a, d["offs"][5], torch.float32)
+        aarr = _lib.tensor_array([d["a"] for d in dev])
+        garr = _lib.tensor_array([d["g"] for d in dev])
+        coef_ptr = None
+        if max_norm is not None:
+            wsn = torch.empty(max(L.ely_grad_norm_workspace_bytes(garr, n_t), 256), dtype=torch.uint8, device="cuda")
+            _lib.check(L.ely_grad_norm_fold(aarr, garr, n_t, max_norm, res.data_ptr(), wsn.data_ptr(), wsn.numel(), stream), "norm fold")
+            coef_ptr = res.data_ptr() + 12
+        t = step + 1
+        consts = (oracle.host_adamw_consts if order == "host" else oracle.torch_adamw_consts)(LR, BETAS, EPS, wd, t)
+        ctab = (_lib.ElyConsts * n_t)()
+        for j in range(n_t):
+            ctab[j].c[:] = [float(x) for x in np.asarray(consts, dtype=np.float32).reshape(-1)[:8]] + [0.0] * max(0, 8 - len(consts))
+        copies = [_lib.ely_tensor(d["c"]) if d["c"] is not None else _lib.ElyTensor(None, 0, _lib.BF16, 0) for d in dev]
+        ws = torch.empty(L.ely_adamw_workspace_bytes(n_t), dtype=torch.uint8, device="cuda")
+        rc = L.ely_adamw_fold_step(_lib.tensor_array([d["p"] for d in dev]), aarr, garr,
+                                   _lib.tensor_array([d["m"] for d in dev]), _lib.tensor_array([d["v"] for d in dev]),
+                                   _lib.tensor_array(copies), n_t, ctab, _lib.ORDER_HOST if order == "host" else _lib.ORDER_TORCH,
+                                   int(wd != 0), coef_ptr, ws.data_ptr(), ws.numel(), stream)
+        _lib.check(rc, "adamw fold fuzz")
+        torch.cuda.synchronize()
+        folded = []
+        for a, g in zip(accs, gs):
+            f = a.copy()
+            oracle.fold_add(f, g)
+            folded.append(f)
+        coef = 1.0
+        if max_norm is not None:
+            want = oracle.sumsq(folded)
+            norm = float(res[8:12].view(torch.float32).item())
+            assert abs(float(res[0:8].view(torch.float64).item()) - want) <= 1e-6 * want + 1e-300
+            assert abs(norm - want**0.5) <= 1e-6 * want**0.5 + 1e-30
+            coef = float(res[12:16].view(torch.float32).item())
+            assert coef == oracle.clip_coef(norm, max_norm)
+        fn = oracle.adamw_host if order == "host" else oracle.adamw_torch
+        for (p, m, v, c), f in zip(host, folded):
+            fn(p, f, m, v, consts, wd != 0, coef, c if with_copy else None)
+        for a, d in zip(accs, dev):
+            assert np.array_equal(bits(d["a"]).view(np.uint32), a.view(np.uint32)), "accumulator written"
+    for (p, m, v, c), d in zip(host, dev):
+        for want, got in ((p, d["p"]), (m, d["m"]), (v, d["v"])):
+            gb = bits(got)
+            if order == "host":
+                assert np.array_equal(gb.view(np.uint32), want.view(np.uint32))
+            else:
+                assert int(ulp_distance(gb.view(np.float32), want).max(initial=0)) <= 1
+        if with_copy and order == "host":
+            assert np.array_equal(bits(d["c"]), c)

@@ -1,6 +1,11 @@
-"""Benchmark configs C2 and C3 at their full sizes on one MI355X, checked
-through properties that do not need a CPU pass over billions of elements:
+"""Benchmark configs C1, C2 and C3 at their full sizes on one MI355X,
+checked through properties that do not need a CPU pass over billions of
+elements:
 
+* C1 (the headline: the 2.8B model's stage, 192 tensors, bf16 grads, the
+  bf16 working copy, clip, 10 steps): the norm against an fp64 sum of
+  squares every step, and one million sampled elements replayed by the
+  oracle every step, bit for bit;
 * C2 (the 15.8B model's stage: ~7.9B fp32 elements, p/m/v/g resident in
   HBM, 1% of the tensors' gradients x100 so that clipping triggers): the
   global norm against an fp64 sum of squares (within 1e-6), the clip
@@ -21,7 +26,7 @@ import numpy as np
 import pytest
 import torch
 
-from gpu_util import say
+from gpu_util import gpt_block_shapes, say
 
 pytestmark = pytest.mark.gpu
 
@@ -80,6 +85,57 @@ def test_c2_full_shard_clips_and_steps_exactly(oracle):
     assert np.array_equal(got_m.view(np.uint32), m.view(np.uint32))
     assert np.array_equal(got_v.view(np.uint32), v.view(np.uint32))
     del opt, params, grads, saved
+    torch.cuda.empty_cache()
+
+
+def test_c1_full_shard_ten_steps_against_the_oracle(oracle):
+    """C1, the benchmark's headline shard: 16 GPT blocks at d = 2560 (192
+    tensors, 1,258,823,680 fp32 elements), bf16 grads N(0, 1e-4), the bf16
+    working copy, weight decay 0.1, clip 1.0, 10 steps.  Every step: the
+    norm within 1e-6 of the fp64 sum of squares of all the step's
+    gradients, and one million sampled elements (parameter, both moments,
+    working copy) equal to the oracle's HostAdamW replaying them from their
+    gathered inputs, bit for bit."""
+    from elysium_wan_amd import optim
+
+    shapes = gpt_block_shapes(2560) * 16
+    gen = torch.Generator(device="cuda").manual_seed(41)
+    params = [torch.empty(s, device="cuda").normal_(0.0, 0.02, generator=gen).requires_grad_(True) for s in shapes]
+    n = sum(p.numel() for p in params)
+    assert n == 1_258_823_680 and len(params) == 192
+    opt = optim.FusedAdamW(params, lr=LR, betas=BETAS, eps=EPS, weight_decay=WD, order="host", max_norm=MAX_NORM,
+                           working_copy=True)
+    sizes = torch.tensor([p.numel() for p in params], dtype=torch.int64)
+    cum = torch.cumsum(sizes, 0)
+    flat_idx = torch.randint(0, n, (1_000_000,), generator=torch.Generator().manual_seed(78))
+    t_idx = torch.searchsorted(cum, flat_idx, right=True)
+    local = flat_idx - (cum[t_idx] - sizes[t_idx])
+    sel = {t: local[t_idx == t].cuda() for t in torch.unique(t_idx).tolist()}
+    order = sorted(sel)
+    gather = lambda ts: torch.cat([ts[t].detach().reshape(-1)[sel[t]] for t in order])  # noqa: E731
+    p = gather(params).cpu().numpy()
+    m, v = np.zeros_like(p), np.zeros_like(p)
+    cp = np.zeros(p.size, np.uint16)
+    ggen = torch.Generator(device="cuda").manual_seed(42)
+    for step in range(10):
+        grads = [torch.empty(s, device="cuda").normal_(0.0, 1e-4, generator=ggen).to(torch.bfloat16) for s in shapes]
+        want = _fp64_sumsq(grads)
+        g_in = gather(grads).view(torch.int16).cpu().numpy().view(np.uint16)
+        say("C1 full shard, step", step)
+        opt.step(grads=grads)
+        torch.cuda.synchronize()
+        norm = float(opt.grad_norm())
+        assert abs(norm - want**0.5) <= 1e-6 * want**0.5, (step, norm, want**0.5)
+        coef = float(opt._norm[12:16].view(torch.float32))
+        assert coef == oracle.clip_coef(norm, MAX_NORM)
+        oracle.adamw_host(p, g_in, m, v, np.array(optim.host_consts(LR, BETAS, EPS, WD, float(step + 1)), dtype=np.float32),
+                          True, coef, cp)
+        assert np.array_equal(gather(params).cpu().numpy().view(np.uint32), p.view(np.uint32)), step
+        assert np.array_equal(gather([opt.state[i]["exp_avg"] for i in range(192)]).cpu().numpy().view(np.uint32), m.view(np.uint32)), step
+        assert np.array_equal(gather([opt.state[i]["exp_avg_sq"] for i in range(192)]).cpu().numpy().view(np.uint32), v.view(np.uint32)), step
+        assert np.array_equal(gather(opt.working_copies).view(torch.int16).cpu().numpy().view(np.uint16), cp), step
+        del grads
+    del opt, params
     torch.cuda.empty_cache()
 
 

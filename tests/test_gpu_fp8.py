@@ -241,18 +241,27 @@ def _c4_activation(seed: int) -> torch.Tensor:
     return z.to(torch.bfloat16)
 
 
+def _c4_gradient(seed: int) -> torch.Tensor:
+    """Config C4's gradient [16, 4096, 8192] bf16 drawn N(0, 1e-5)."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    return torch.empty((16, 4096, 8192), device="cuda").normal_(0.0, 1e-5, generator=g).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("which", ["activation", "gradient"])
 @pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
-def test_c4_per_row_and_per_tensor_equal_torch_on_the_gpu(fmt):
-    """Config C4 at full size: bytes and exponents of per-row and per-tensor
-    scaling equal torch's own ops on the GPU running model/fp8.py:28-49's
-    arithmetic (frexp of |x|max, the pow2 product in bf16, torch's fp8
-    conversion); decode is exact."""
+def test_c4_per_row_and_per_tensor_equal_torch_on_the_gpu(fmt, which):
+    """Config C4 at full size, the Student-t activation and the N(0, 1e-5)
+    gradient: bytes and exponents of per-row and per-tensor scaling equal
+    torch's own ops on the GPU running model/fp8.py:28-49's arithmetic
+    (frexp of |x|max, the pow2 product in bf16, torch's fp8 conversion);
+    decode is exact."""
     from elysium_wan_amd import fp8
 
-    x = _c4_activation(61 if fmt == "e4m3" else 62)
+    seed = (61 if fmt == "e4m3" else 62) + (0 if which == "activation" else 10)
+    x = _c4_activation(seed) if which == "activation" else _c4_gradient(seed)
     dt, ebias = fp8.FORMATS[fmt]
     for per_tensor in (False, True):
-        say("fp8 C4", fmt, "per-tensor" if per_tensor else "per-row")
+        say("fp8 C4", which, fmt, "per-tensor" if per_tensor else "per-row")
         q, k = fp8.quantize(x, fmt, per_tensor=per_tensor)
         xs = x.reshape(1, -1) if per_tensor else x
         amax = xs.abs().amax(dim=-1, keepdim=True)

@@ -140,3 +140,52 @@ def test_a_swapped_host_moment_is_refused_before_any_launch():
     torch.cuda.synchronize()
     assert all(torch.equal(a, b.detach()) for a, b in zip(before, params))
     assert all(float(opt.state[i]["step"]) == 1.0 for i in range(len(params)))
+
+
+def _check_set(n: int, seed: int):
+    """benchmarks/wan/check_host_adamw.py:19-22: four tensors of n // 4,
+    n // 4, n // 2 - 7 and 7 elements, N(0, 1) (CPU generator, seeded)."""
+    g = torch.Generator().manual_seed(seed)
+    return [torch.randn(s, generator=g) for s in (n // 4, n // 4, n // 2 - 7, 7)]
+
+
+@pytest.mark.parametrize("arm", ["in_place", "staged", "serial", "staged_half_resident", "in_place_half_resident"])
+def test_check_host_adamw_bits_equal_the_cpu(oracle, arm):
+    """benchmarks/wan/check_host_adamw.py:25-55 on this build: "adamw-host"
+    over 3,000,001 elements in four tensors, lr 3e-4 and runtime/spec.py's
+    AdamW, three steps of grads N(0, 1) x 10^-(step % 5) (seed 100 + step),
+    half the moments promoted to the GPU after the first step in the
+    half-resident arms -- parameters and moments equal the CPU's HostAdamW
+    arithmetic (the oracle) bit for bit, for every arm of the reference's
+    check plus the in-place default."""
+    import numpy as np
+
+    from elysium_wan_amd import optim
+
+    n = 3_000_001
+    init = _check_set(n, 1)
+    params = [t.clone().cuda().requires_grad_(True) for t in init]
+    pipeline = {"in_place": None, "staged": True, "serial": False,
+                "staged_half_resident": True, "in_place_half_resident": None}[arm]
+    opt = optim.build("adamw-host", params, 3e-4, pipeline=pipeline)
+    p = np.concatenate([t.numpy() for t in init])
+    m, v = np.zeros_like(p), np.zeros_like(p)
+    say("check_host_adamw arm", arm)
+    for step in range(3):
+        if step == 1 and arm.endswith("half_resident"):
+            moved = opt.promote(int(0.5 * 8 * n))
+            assert 0 < moved <= 4 * n and opt.resident
+        g = torch.Generator().manual_seed(100 + step)
+        gs = [torch.randn(t.shape, generator=g) * 10.0 ** (-(step % 5)) for t in init]
+        for x, gr in zip(params, gs):
+            x.grad = gr.cuda()
+        opt.step()
+        opt.zero_grad()
+        oracle.adamw_host(p, np.concatenate([gr.numpy() for gr in gs]), m, v,
+                          oracle.host_adamw_consts(3e-4, (0.9, 0.95), 1e-8, 0.0, step + 1), False)
+    got = np.concatenate([x.detach().cpu().numpy() for x in params])
+    assert np.array_equal(got.view(np.uint32), p.view(np.uint32))
+    gm = np.concatenate([opt.state[i]["exp_avg"].cpu().numpy().reshape(-1) for i in range(4)])
+    gv = np.concatenate([opt.state[i]["exp_avg_sq"].cpu().numpy().reshape(-1) for i in range(4)])
+    assert np.array_equal(gm.view(np.uint32), m.view(np.uint32))
+    assert np.array_equal(gv.view(np.uint32), v.view(np.uint32))

@@ -252,21 +252,32 @@ def test_host_adamw_first_step_moves_by_lr_sign_g(oracle):
     np.testing.assert_allclose(v, 0.05 * g.astype(np.float64) ** 2, rtol=1e-6)
 
 
-def test_torch_order_oracle_is_adamw(oracle):
-    """The foreach-order restatement against torch.optim.AdamW itself, at the
-    reference's own tolerance for 'it is AdamW' (test_host_adamw.py:70-77)."""
+@pytest.mark.parametrize("foreach", [False, True])
+def test_torch_order_oracle_is_adamw(oracle, foreach):
+    """The restatement of torch's GPU (foreach) op order against
+    torch.optim.AdamW itself on the CPU, at the bounds measured there: the
+    CPU kernels round some ops differently (addcmul as (value * t1) * t2
+    where the GPU fuses value * (t1 * t2) into the add; the update's
+    addcdiv likewise), so exp_avg is bit-identical, exp_avg_sq within 4 ulp,
+    and the parameters within the reference's own tolerance for 'it is
+    AdamW' (test_host_adamw.py:70-77).  The GPU kernel itself is held to
+    torch's GPU AdamW within 1 ulp on parameters and both moments
+    (tests/test_gpu_adamw.py)."""
+    from gpu_util import ulp_distance
+
     rng = np.random.default_rng(3)
-    p0 = rng.standard_normal(5000).astype(np.float32)
+    p0 = rng.standard_normal(50000).astype(np.float32)
     tp = torch.from_numpy(p0.copy()).requires_grad_(True)
-    opt = torch.optim.AdamW([tp], lr=1e-2, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, foreach=False)
+    opt = torch.optim.AdamW([tp], lr=1e-2, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, foreach=foreach)
     p, m, v = p0.copy(), np.zeros_like(p0), np.zeros_like(p0)
-    for step in range(4):
-        gr = (rng.standard_normal(5000) * 10.0 ** (-step % 4)).astype(np.float32)
+    for step in range(5):
+        gr = (rng.standard_normal(50000) * 10.0 ** (-step % 4)).astype(np.float32)
         tp.grad = torch.from_numpy(gr.copy())
         opt.step()
         oracle.adamw_torch(p, gr, m, v, oracle.torch_adamw_consts(1e-2, (0.9, 0.95), 1e-8, 0.1, step + 1), True)
     np.testing.assert_allclose(p, tp.detach().numpy(), rtol=1e-5, atol=1e-6)
-    np.testing.assert_allclose(m, opt.state[tp]["exp_avg"].numpy(), rtol=1e-5, atol=1e-7)
+    assert int(ulp_distance(m, opt.state[tp]["exp_avg"].numpy()).max()) == 0
+    assert int(ulp_distance(v, opt.state[tp]["exp_avg_sq"].numpy()).max()) <= 4
 
 
 def test_bf16_grads_equal_their_fp32_widening(oracle):
