@@ -31,6 +31,8 @@
 // per lane per step for bf16 output (4 for fp32) so every store instruction
 // covers a contiguous 1 KB; roundtrip (fp8.py:56-63) fuses both.
 #include <algorithm>
+#include <map>
+#include <mutex>
 
 #include "ely_device.hpp"
 #include "ely_host.hpp"
@@ -1273,6 +1275,35 @@ static void quant_k_launch(const void* x, bool bf16, int64_t rows, int64_t cols,
     check_launch("quant_k_kernel");
 }
 
+// ------------------------------------------------ quantize without allocation
+
+// Scratch of ely_fp8_quantize_noalloc: the split path's row maxima and
+// partial maxima live in this file-scope device array instead of a caller
+// workspace, so that entry point allocates nothing.  Each GPU holds its own
+// copy at its own address until the process ends; host code reaches it only
+// through the address hipGetSymbolAddress returns on that device (the
+// array's name in host code is a stand-in, not a device address).
+constexpr size_t kNoallocScratchBytes = (size_t)1 << 20;
+static __device__ __align__(256) unsigned char scratch[kNoallocScratchBytes];
+
+static std::mutex g_scratch_mu;
+static std::map<int, void*> g_scratch_ptr;  // device -> address of `scratch` there
+
+// The current device's address of `scratch`, looked up once per device with
+// that device current.
+static void* noalloc_scratch() {
+    int dev = 0;
+    check_hip(hipGetDevice(&dev), "hipGetDevice");
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    auto it = g_scratch_ptr.find(dev);
+    if (it != g_scratch_ptr.end()) return it->second;
+    void* ptr = nullptr;
+    check_hip(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+    if (!ptr) fail(ELY_EHIP, "hipGetSymbolAddress(scratch) returned a null address");
+    g_scratch_ptr.emplace(dev, ptr);
+    return ptr;
+}
+
 }  // namespace ely
 
 using namespace ely;
@@ -1301,6 +1332,41 @@ int ely_fp8_quantize(const void* x, int32_t x_dtype, int64_t rows, int64_t cols,
         } else {
             if (x_dtype == ELY_BF16) quantize_impl<kE5M2, true>(x, rows, cols, q, k, nullptr, workspace, ws_bytes, s);
             else quantize_impl<kE5M2, false>(x, rows, cols, q, k, nullptr, workspace, ws_bytes, s);
+        }
+    });
+}
+
+int ely_fp8_quantize_noalloc(const void* x, int32_t x_dtype, int64_t rows, int64_t cols, int32_t fmt, uint8_t* q,
+                             int32_t* k, void* stream) {
+    return guarded([&] {
+        check_fmt(fmt);
+        check_dtype(x_dtype, "x_dtype");
+        check_shape(rows, cols);
+        if (rows * cols > 0 && !x) fail(ELY_EINVAL, "ely_fp8_quantize_noalloc: null x");
+        if (rows > 0 && !k) fail(ELY_EINVAL, "ely_fp8_quantize_noalloc: null k");
+        // Only the split path (rows that fit no register path) uses scratch;
+        // its row maxima and partials must fit the static array.  Every
+        // scratch word the split launches read was written by an earlier
+        // launch of the same call, so nothing needs clearing between calls.
+        const bool split = rows > 0 && cols > 0 && rows_vpl(cols, x_dtype, x, q, nullptr) == 0;
+        void* ws = nullptr;
+        if (split) {
+            const size_t need = split_ws_bytes(rows);
+            if (need > kNoallocScratchBytes)
+                fail(ELY_EINVAL, "ely_fp8_quantize_noalloc: " + std::to_string(rows) + " rows of " + std::to_string(cols) +
+                                     " columns need " + std::to_string(need) + " scratch bytes, above the " +
+                                     std::to_string(kNoallocScratchBytes) +
+                                     "-byte static scratch; use ely_fp8_quantize with a workspace");
+            ws = noalloc_scratch();
+        }
+        hipStream_t s = static_cast<hipStream_t>(stream);
+        const int64_t wsb = split ? (int64_t)kNoallocScratchBytes : 0;
+        if (fmt == ELY_E4M3) {
+            if (x_dtype == ELY_BF16) quantize_impl<kE4M3, true>(x, rows, cols, q, k, nullptr, ws, wsb, s);
+            else quantize_impl<kE4M3, false>(x, rows, cols, q, k, nullptr, ws, wsb, s);
+        } else {
+            if (x_dtype == ELY_BF16) quantize_impl<kE5M2, true>(x, rows, cols, q, k, nullptr, ws, wsb, s);
+            else quantize_impl<kE5M2, false>(x, rows, cols, q, k, nullptr, ws, wsb, s);
         }
     });
 }

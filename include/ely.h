@@ -146,6 +146,18 @@ int64_t ely_fp8_workspace_bytes(int64_t rows, int64_t cols, int32_t x_dtype);
 int ely_fp8_quantize(const void* x, int32_t x_dtype, int64_t rows, int64_t cols, int32_t fmt,
                      uint8_t* q, int32_t* k, void* workspace, int64_t ws_bytes, void* stream);
 
+/* No counterpart in the reference: ely_fp8_quantize for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  Same results; no workspace argument and no
+ * allocation of any kind: the split path (rows longer than the register
+ * paths take, e.g. per-tensor scaling) keeps its row maxima in a 1 MiB
+ * static device array of the library, one per GPU, so it accepts at most
+ * ~131,000 such rows and refuses more with ELY_EINVAL.  Calls that overlap
+ * on one GPU (different streams, or threads without ordering) share that
+ * array and race; calls on one stream are ordered and safe. */
+int ely_fp8_quantize_noalloc(const void* x, int32_t x_dtype, int64_t rows, int64_t cols, int32_t fmt,
+                             uint8_t* q, int32_t* k, void* stream);
+
 /* fp8.dequantize (model/fp8.py:52-53): out = float(q) * 2^k in out_dtype
  * (ELY_F32 is the reference's default; ELY_BF16 is roundtrip's dtype). */
 int ely_fp8_dequantize(const uint8_t* q, const int32_t* k, int64_t rows, int64_t cols, int32_t fmt,
