@@ -30,6 +30,7 @@ adamw-host, as HostAdamW, and by parameter tensor for adamw, as torch).
 from __future__ import annotations
 
 import math
+import weakref
 from collections.abc import Iterable, MutableMapping
 
 import numpy as np
@@ -65,11 +66,24 @@ def build(optimizer: str, params: Iterable[torch.Tensor], lr: float, **kw):
     raise ValueError(f"optimizer {optimizer!r} is not one of {OPTIMIZERS}")
 
 
+def _torch_adamw_group() -> dict:
+    """The param group torch's AdamW records for the reference's constants,
+    without its "params" and "lr".  Read once, when this module loads: a
+    torch optimizer's constructor leaves collectable reference cycles among
+    its frames, and one built inside FusedAdamW.__init__ would tie the new
+    optimizer (its parameters and moments) to them until the garbage
+    collector runs."""
+    probe = torch.optim.AdamW([torch.zeros(1, requires_grad=True)], lr=1e-3, **ADAMW)
+    return {k: v for k, v in probe.state_dict()["param_groups"][0].items() if k not in ("params", "lr")}
+
+
+_TORCH_ADAMW_GROUP = _torch_adamw_group()
+
+
 def hparams(lr: float, optimizer: str = "adamw") -> dict:
     """runtime/optim.py:57-69: the param-group hyperparameters a checkpoint
-    records, read off torch's own AdamW defaults."""
-    probe = torch.optim.AdamW([torch.zeros(1, requires_grad=True)], lr=lr, **ADAMW)
-    group = {k: v for k, v in probe.state_dict()["param_groups"][0].items() if k != "params"}
+    records, read off torch's own AdamW defaults (keys in torch's order)."""
+    group = {"lr": lr, **_TORCH_ADAMW_GROUP}
     if optimizer == "adamw-host":
         group["moments"] = "host"
     elif optimizer != "adamw":
@@ -135,7 +149,17 @@ class _State(MutableMapping):
     parameter start again from zero moments at step 0."""
 
     def __init__(self, opt: FusedAdamW):
-        self._opt = opt
+        # a weak reference: the optimizer owns this mapping, and a cycle
+        # would keep its parameters and moments alive after `del opt` until
+        # the garbage collector happened to run
+        self._ref = weakref.ref(opt)
+
+    @property
+    def _opt(self) -> FusedAdamW:
+        opt = self._ref()
+        if opt is None:
+            raise ReferenceError("the optimizer of this state no longer exists")
+        return opt
 
     def _index(self, key) -> int:
         opt = self._opt
