@@ -293,6 +293,114 @@ def placement_probe(device, mode):
     del hold
 
 
+def placement_sweep(device, stream, pool_gib: int, spec: str) -> None:
+    """C1-sized AdamW streams (one tensor each: p fp32, g bf16, copy bf16,
+    m fp32, v fp32) carved from one pool of pool_gib GiB at chosen offsets,
+    printing one JSON line per placement: the fused AdamW kernel and the
+    three stream probes (ely_probe_streams: read, write, read+write, no
+    arithmetic) between HIP events.  spec: comma-separated entries, "A"
+    (all five streams packed from A GiB on, each on a 2 MiB boundary) or
+    "A:B" (p, g, copy from A GiB, m and v from B GiB + 11.7 GiB)."""
+    from elysium_wan_amd import _lib, optim
+
+    L = _lib.load()
+    gib = 1 << 30
+    n = sum(int(np.prod(s)) for s in block_shapes(D_MODEL)) * N_BLOCKS
+    rnd = lambda b: (b + (2 << 20) - 1) // (2 << 20) * (2 << 20)  # noqa: E731
+    pool = torch.empty(pool_gib * gib, dtype=torch.uint8, device=device)
+    pool.zero_()
+    sink = torch.zeros(4, device=device)
+    aws = torch.empty(L.ely_adamw_workspace_bytes(1), dtype=torch.uint8, device=device)
+    consts = (_lib.ElyConsts * 1)()
+    consts[0].c[:] = optim.host_consts(LR, BETAS, EPS, WD, 1.0)
+    sptr = _lib.stream_ptr(device)
+    torch.cuda.synchronize()
+
+    def take(off, nbytes, dt):
+        if off + nbytes > pool.numel():
+            raise SystemExit(f"placement {off / gib:.1f} GiB + {nbytes / gib:.1f} GiB does not fit the {pool_gib} GiB pool")
+        return pool[off: off + nbytes].view(dt)
+
+    for entry in spec.split(","):
+        a, _, b = entry.partition(":")
+        ca = int(a) * gib
+        p = take(ca, n * 4, torch.float32)
+        g = take(ca + rnd(n * 4), n * 2, torch.bfloat16)
+        c = take(ca + rnd(n * 4) + rnd(n * 2), n * 2, torch.bfloat16)
+        cb = (int(b) * gib if b else ca) + rnd(n * 4) + 2 * rnd(n * 2)
+        m = take(cb, n * 4, torch.float32)
+        v = take(cb + rnd(n * 4), n * 4, torch.float32)
+        arrs = [_lib.tensor_array([t]) for t in (p, g, m, v, c)]
+
+        def adam(_):
+            _lib.check(L.ely_adamw_step(arrs[0], arrs[1], arrs[2], arrs[3], arrs[4], 1, consts, _lib.ORDER_HOST, 1, None,
+                                        aws.data_ptr(), aws.numel(), sptr), "adamw")
+
+        def probe(which):
+            def run(_):
+                _lib.check(L.ely_probe_streams(which, p.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr(), c.data_ptr(), n,
+                                               8 * 256, sink.data_ptr(), sptr), "probe")
+            return run
+
+        out = {"placement": entry, "adamw_GBs": n * 28 / time_events(adam, 6, stream) / 1e6,
+               "read_GBs": n * 14 / time_events(probe(0), 6, stream) / 1e6,
+               "write_GBs": n * 14 / time_events(probe(1), 6, stream) / 1e6,
+               "rw_GBs": n * 28 / time_events(probe(2), 6, stream) / 1e6}
+        print(json.dumps({k: (round(x) if isinstance(x, float) else x) for k, x in out.items()}), flush=True)
+
+
+def pmc_summary(dbs, spec: str | None = None) -> None:
+    """Per-launch counters of the placement sweep's kernels from rocprofv3
+    --pmc --kernel-trace databases (rocpd SQLite), as markdown: per group of
+    consecutive launches of one kernel (the first, a warm-up, dropped), the
+    kernel time, each counter summed over its instances, how unevenly the
+    instances (L2 channels) share it (max / mean), and, for a counter X_sum
+    with its X_LEVEL_sum, the average number of cycles a request is
+    outstanding (LEVEL / requests).  With the sweep's SPEC, each group is
+    labelled with its placement (four kernels per placement, in order)."""
+    import collections
+    import sqlite3
+
+    kernels = ("adamw_kernel", "probe_read_kernel", "probe_write_kernel", "probe_rw_kernel")
+    for path in dbs:
+        db = sqlite3.connect(path)
+        rows = db.execute("select dispatch_id, name, duration, counter_name, counter_value from pmc_events "
+                          "order by dispatch_id, id").fetchall()
+        disp = collections.OrderedDict()
+        for did, name, dur, cn, cv in rows:
+            d = disp.setdefault(did, {"name": name, "dur": dur, "c": collections.defaultdict(list)})
+            d["c"][cn].append(cv)
+        groups = []
+        for d in disp.values():
+            k = next((k for k in kernels if k in d["name"]), None)
+            if k is None:
+                continue
+            if groups and groups[-1][0] == k:
+                groups[-1][1].append(d)
+            else:
+                groups.append((k, [d]))
+        names = sorted({cn for _, ds in groups for cn in ds[0]["c"]})
+        lat = [cn for cn in names if cn.endswith("_LEVEL_sum") and cn.replace("_LEVEL_sum", "_sum") in names]
+        labels = spec.split(",") if spec else None
+        print(f"`{os.path.basename(os.path.dirname(path))}`\n")
+        print("| # | placement | kernel | µs | " + " | ".join(names + [c.replace("_LEVEL_sum", " cycles") for c in lat]) + " |")
+        print("|---|---|---|---|" + "---|" * (len(names) + len(lat)))
+        for i, (k, ds) in enumerate(groups):
+            ds = ds[1:] or ds
+            cells, tot_of = [], {}
+            for cn in names:
+                inst = len(ds[0]["c"][cn])
+                per = [sum(x["c"][cn][j] for x in ds) / len(ds) for j in range(inst)]
+                tot = tot_of[cn] = sum(per)
+                cells.append(f"{tot:.4g}" + (f" (max/mean {max(per) / (tot / inst):.2f})" if inst > 1 and tot else ""))
+            for cn in lat:
+                req = tot_of[cn.replace("_LEVEL_sum", "_sum")]
+                cells.append(f"{tot_of[cn] / req:.0f}" if req > 1000 else "-")
+            place = labels[i // 4] if labels and i // 4 < len(labels) else ""
+            print(f"| {i} | {place} | {k} | {sum(x['dur'] for x in ds) / len(ds) / 1e3:.0f} | " + " | ".join(cells) + " |")
+        print()
+
+
 def _activations(device, rows, cols, copies, seed):
     """bf16 N(0, 1) with 0.1% of the elements x50 (config C1's activation recipe)."""
     gen = torch.Generator(device=device).manual_seed(seed)
@@ -801,12 +909,18 @@ def _pick(means: dict, fragment: str):
     return sum(hits) / len(hits)
 
 
-def traffic_summary(fetch_dir: str, write_dir: str, command: str) -> None:
+READ_SIZE_COUNTERS = ("TCC_EA0_RDREQ_32B_sum", "TCC_EA0_RDREQ_64B_sum", "TCC_EA0_RDREQ_128B_sum", "TCC_EA0_RDREQ_sum")
+
+
+def traffic_summary(fetch_dir: str, write_dir: str, command: str, sizes_dir: str | None = None) -> None:
     """HBM bytes per launch of each measured kernel from two rocprofv3 --pmc
     runs of `bench.py --profile-pass` (FETCH_SIZE, then WRITE_SIZE; KiB per
     dispatch), each scaled by the same counter's reading on the calibration
-    cast (known: 4 B read + 2 B written per element).  Writes
-    profiles/adamw_c1_traffic.json (read back by bench.py) and a text
+    cast (known: 4 B read + 2 B written per element).  The read factor is
+    cross-checked on the read-only grad-norm kernel (known: 2 B per bf16
+    gradient), and, with a third run of the request-size counters
+    (READ_SIZE_COUNTERS), by the bytes the read requests of each size carry.
+    Writes profiles/adamw_c1_traffic.json (read back by bench.py) and a text
     summary beside it."""
     fetch = _pmc_means(fetch_dir, "FETCH_SIZE")
     write = _pmc_means(write_dir, "WRITE_SIZE")
@@ -821,6 +935,8 @@ def traffic_summary(fetch_dir: str, write_dir: str, command: str) -> None:
         f"Calibration: cast_bf16_kernel over {CAL_ELEMS} fp32 -> bf16 (reads {CAL_ELEMS * 4} B, writes {CAL_ELEMS * 2} B);",
         f"FETCH_SIZE reads {cf:.4f} x the known bytes, WRITE_SIZE {cw:.4f} x.  Every figure below is divided by these factors.",
         "",
+        *_read_factor_checks(fetch, sizes_dir, cf),
+        "",
         "| kernel | FETCH_SIZE KiB | WRITE_SIZE KiB | traffic (B) | algorithmic (B) | traffic / algorithmic | what |",
         "|---|---|---|---|---|---|---|",
     ]
@@ -833,12 +949,46 @@ def traffic_summary(fetch_dir: str, write_dir: str, command: str) -> None:
         lines.append(f"| {frag} | {fk:.0f} | {wk:.0f} | {t:.4g} | {alg:.4g} | {t / alg:.3f} | {what} |")
     adam = out["kernels"].get("adamw_kernel")
     out["traffic_bytes_per_launch"] = adam["traffic_bytes"] if adam else None
+    nk = _pick(fetch, "norm_partials_kernel")
+    if nk is not None:
+        out["norm_raw_fetch_factor"] = nk * 1024.0 / _traffic_kernels()["norm_partials_kernel"][0]
     os.makedirs(os.path.join(HERE, "profiles"), exist_ok=True)
     with open(os.path.join(HERE, "profiles", "adamw_c1_traffic.json"), "w") as f:
         json.dump(out, f, indent=1)
     with open(os.path.join(HERE, "profiles", "adamw_c1_traffic.md"), "w") as f:
         f.write("\n".join(lines) + "\n")
     print("\n".join(lines))
+
+
+def _read_factor_checks(fetch: dict, sizes_dir: str | None, cf: float) -> list:
+    """Lines of the traffic summary that cross-check the FETCH_SIZE factor:
+    the read-only grad-norm kernel's raw reading against its known bytes,
+    and, from a run of READ_SIZE_COUNTERS, the bytes the read requests carry
+    (32 x 32-byte + 64 x 64-byte + 128 x 128-byte requests) against
+    FETCH_SIZE for the same kernels."""
+    lines = ["Cross-checks of the read factor:", ""]
+    nk = _pick(fetch, "norm_partials_kernel")
+    if nk is not None:
+        known = _traffic_kernels()["norm_partials_kernel"][0]
+        lines.append(f"- norm_partials_kernel, read-only, known {known} B read: raw FETCH_SIZE / known = "
+                     f"{nk * 1024.0 / known:.4f} (calibration cast: {cf:.4f})")
+    if sizes_dir:
+        m = {c: _pmc_means(sizes_dir, c) for c in READ_SIZE_COUNTERS}
+        for frag, known in (("cast_bf16_kernel", CAL_ELEMS * 4), ("norm_partials_kernel", _traffic_kernels()["norm_partials_kernel"][0]),
+                            ("adamw_kernel", None)):
+            r32, r64, r128, rall = (_pick(m[c], frag) for c in READ_SIZE_COUNTERS)
+            if rall is None:
+                continue
+            b = 32 * (r32 or 0) + 64 * (r64 or 0) + 128 * (r128 or 0)
+            fk = _pick(fetch, frag)
+            txt = (f"- {frag}: {rall:.4g} read requests, {r128 or 0:.4g} of 128 B, {r64 or 0:.4g} of 64 B, {r32 or 0:.4g} of 32 B; "
+                   f"they carry {b:.4g} B")
+            if known:
+                txt += f" = {b / known:.4f} x the known {known} B"
+            if fk:
+                txt += f"; FETCH_SIZE counts {fk * 1024.0 / b:.4f} x that"
+            lines.append(txt)
+    return lines
 
 
 def _dispatches(trace_dir: str):
@@ -1131,16 +1281,27 @@ def main():
     ap.add_argument("--placement-probe", choices=("fresh", "hold150"), help="three C1 steps only (for rocprofv3 --pmc)")
     ap.add_argument("--cpu-sample", type=int, default=256 * 1024 * 1024)
     ap.add_argument("--profile-pass", action="store_true", help="launch each measured kernel a few times, untimed, for rocprofv3 --pmc runs")
-    ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"), help="summarize two --pmc runs of --profile-pass into profiles/")
+    ap.add_argument("--traffic-summary", nargs="+", metavar="DIR",
+                    help="summarize --pmc runs of --profile-pass into profiles/: FETCH_DIR WRITE_DIR [REQUEST_SIZE_DIR]")
     ap.add_argument("--traffic-command", default="", help="the command line recorded in the traffic summary")
     ap.add_argument("--trace-summary", nargs=2, metavar=("STEP_DIR", "CODEC_DIR"), help="summarize two rocprofv3 --kernel-trace runs into profiles/")
     ap.add_argument("--bench-json", help="a bench.py output line from the same box, quoted beside the trace summary")
+    ap.add_argument("--placement-sweep", nargs=2, metavar=("POOL_GIB", "SPEC"),
+                    help="AdamW and stream probes on C1-sized streams carved from one pool (SPEC: A[,A...] or A:B[,...] GiB)")
+    ap.add_argument("--pmc-summary", nargs="+", metavar="DB", help="markdown table of rocprofv3 --pmc databases of a placement sweep")
+    ap.add_argument("--pmc-spec", help="the placement sweep's SPEC, to label --pmc-summary's rows")
     args = ap.parse_args()
     if args.traffic_summary:
-        traffic_summary(*args.traffic_summary, args.traffic_command)
+        if len(args.traffic_summary) not in (2, 3):
+            ap.error("--traffic-summary takes FETCH_DIR WRITE_DIR [REQUEST_SIZE_DIR]")
+        fd, wd = args.traffic_summary[:2]
+        traffic_summary(fd, wd, args.traffic_command, args.traffic_summary[2] if len(args.traffic_summary) == 3 else None)
         return
     if args.trace_summary:
         trace_summary(*args.trace_summary, args.bench_json)
+        return
+    if args.pmc_summary:
+        pmc_summary(args.pmc_summary, args.pmc_spec)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); run with --gpus 1", file=sys.stderr)
@@ -1158,6 +1319,10 @@ def main():
     if args.placement_probe:
         with torch.cuda.stream(stream):
             placement_probe(device, args.placement_probe)
+        return
+    if args.placement_sweep:
+        with torch.cuda.stream(stream):
+            placement_sweep(device, stream, int(args.placement_sweep[0]), args.placement_sweep[1])
         return
     with torch.cuda.stream(stream):
         if args.no_optimizer:

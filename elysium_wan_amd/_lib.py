@@ -46,12 +46,14 @@ EXPORTS = (
     "ely_cast_bf16",
     "ely_fold_add",
     "ely_scale_inplace",
+    "ely_rows_fold",
     "ely_set_max_blocks",
     "ely_host_device_pointer",
     "ely_byteplanes_split",
     "ely_byteplanes_join",
     "ely_fp8_nibbles_encode",
     "ely_fp8_nibbles_decode",
+    "ely_probe_streams",
     "ely_selftest_fp8_cvt",
     "ely_selftest_sqrt",
 )
@@ -114,12 +116,14 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
         L.ely_cast_bf16.argtypes = [P, P, I64, P]
         L.ely_fold_add.argtypes = [P, P, I32, I64, P]
         L.ely_scale_inplace.argtypes = [TP, I32, P, P]
+        L.ely_rows_fold.argtypes = [P, P, P, P, P, I64, I64, I64, I64, I32, I32, P]
         L.ely_set_max_blocks.argtypes = [I32]
         L.ely_host_device_pointer.argtypes = [P, ctypes.POINTER(ctypes.c_void_p)]
         L.ely_byteplanes_split.argtypes = [P, I64, I32, P, P]
         L.ely_byteplanes_join.argtypes = [P, I64, I32, P, P]
         L.ely_fp8_nibbles_encode.argtypes = [P, I32, I64, P, P, P, P]
         L.ely_fp8_nibbles_decode.argtypes = [P, P, I64, P, P]
+        L.ely_probe_streams.argtypes = [I32, P, P, P, P, P, I64, I32, P, P]
         L.ely_selftest_fp8_cvt.argtypes = [ctypes.c_uint32, ctypes.c_uint64, I32, P, P]
         L.ely_selftest_sqrt.argtypes = [ctypes.c_uint32, ctypes.c_uint64, P, P]
         _lib = L

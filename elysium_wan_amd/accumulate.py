@@ -1,5 +1,6 @@
-"""The fixed-order gradient fold in front of the optimizer on MI355X: the
-drop-in for wantrain's runtime/accumulate.py:15-137 (OrderedAccumulator).
+"""The fixed-order gradient folds in front of the optimizer on MI355X: the
+drop-in for wantrain's runtime/accumulate.py (OrderedAccumulator :15-137,
+TiedRowFold :140-247, CountFold :250-318).
 
 The step gradient is the iterative sum g_0 + g_1 + ... + g_{M-1} in
 microbatch order, per tensor: the first part copied (widened to the sum's
@@ -26,7 +27,9 @@ needs them is unaffected.
 
 from __future__ import annotations
 
-from . import pieces
+import torch
+
+from . import _lib, pieces
 
 
 class OrderedAccumulator:
@@ -178,3 +181,180 @@ class OrderedAccumulator:
         if self._merged:
             raise ValueError("result() already folded the last parts in")
         return list(self.last), (None if len(self.order) == 1 else list(self.acc))
+
+
+class TiedRowFold:
+    """runtime/accumulate.py:140-247: the step gradient of a tied table split
+    across stages, folded on the Head in the stock order (acc = g_0,
+    acc += g_i, g_i = h_i + e_i with e_i = +0 outside the microbatch's rows)
+    without a dense table per microbatch in flight.  A row takes h_i + 0.0
+    as soon as no earlier microbatch still holds it; the rest of h_i waits
+    for the embedding rows e_i, and the held rows resolve in microbatch order
+    as h_i + e_i.  Every row sees exactly the stock sequence of adds, so the
+    result is the stock fold bit for bit.
+
+    add_head(mb, h, rows): h the (n_rows, d) gradient of the Head's use (fp32
+    or bf16, on the GPU), rows T_mb (ascending unique ids, int64).
+    add_embed(mb, e_rows): e_mb[T_mb] in ascending id.  Either may come
+    first; out-of-order microbatches wait.  The row bookkeeping (which rows
+    are held) runs on the host; every fold of table rows is one launch of the
+    row-fold kernel (ely_rows_fold)."""
+
+    def __init__(self, n_rows: int, order) -> None:
+        self.n_rows = int(n_rows)
+        self.order = list(order)
+        self.pos = 0  # next position of `order` whose Head gradient is taken
+        self.acc = torch.empty(0)  # allocated by the first Head gradient
+        self.first = True  # no row folded yet: microbatch order[0] assigns
+        self.heads: dict = {}  # mb -> (h, rows) waiting for its prefix
+        self.embeds: dict = {}  # mb -> e_rows until its held rows resolve
+        self.held: list = []  # [(mb, held row ids, h on them, T_mb, first)], oldest first
+        self.pend = torch.zeros(self.n_rows, dtype=torch.int32)  # held-row multiplicity
+
+    def add_head(self, mb: int, h: torch.Tensor, rows: torch.Tensor) -> None:
+        if mb in self.heads or self._done(mb):
+            raise RuntimeError(f"tied fold: a second Head gradient for microbatch {mb}")
+        if h.dim() != 2 or h.shape[0] != self.n_rows:
+            raise RuntimeError(f"tied fold: Head gradient of mb {mb} has shape {tuple(h.shape)}")
+        _lib.require_gpu(h, "tied fold")
+        _lib.dtype_code(h)
+        self.heads[mb] = (h.contiguous(), rows.to(torch.int64).cpu())
+        self._advance()
+
+    def add_embed(self, mb: int, e_rows: torch.Tensor) -> None:
+        if mb in self.embeds or (self._done(mb) and not any(m == mb for m, *_ in self.held)):
+            raise RuntimeError(f"tied fold: a second embedding gradient for microbatch {mb}")
+        self.embeds[mb] = e_rows
+        self._advance()
+
+    def _done(self, mb) -> bool:
+        return mb in self.order[: self.pos]
+
+    def _advance(self) -> None:
+        while True:
+            if self.held and self.held[0][0] in self.embeds:
+                self._resolve()
+                continue
+            if self.pos < len(self.order) and self.order[self.pos] in self.heads:
+                self._take_head()
+                continue
+            return
+
+    def _fold_rows(self, a, a_rows, b, idx, first: bool) -> None:
+        """acc[idx] (=|+=) a[a_rows or all] + (b or +0.0), one launch."""
+        if idx.numel() == 0:
+            return
+        dev = self.acc.device
+        idx_d = idx.to(dev)
+        arow_d = None if a_rows is None else a_rows.to(dev)
+        L = _lib.load()
+        _lib.check(L.ely_rows_fold(self.acc.data_ptr(), a.data_ptr(), None if arow_d is None else arow_d.data_ptr(),
+                                   None if b is None else b.data_ptr(), idx_d.data_ptr(), idx.numel(), self.n_rows,
+                                   a.shape[0], self.acc.shape[1], _lib.dtype_code(self.acc), int(first),
+                                   _lib.stream_ptr(dev)), "tied fold")
+
+    def _take_head(self) -> None:
+        mb = self.order[self.pos]
+        h, rows = self.heads.pop(mb)
+        if self.first:
+            self.acc = torch.empty_like(h)
+        if rows.numel() and (int(rows.min()) < 0 or int(rows.max()) >= self.n_rows):
+            raise RuntimeError(f"tied fold: rows of mb {mb} outside [0, {self.n_rows})")
+        mask = self.pend > 0
+        mask[rows] = True
+        keep = mask.nonzero().reshape(-1)
+        free = (~mask).nonzero().reshape(-1)
+        # free rows: acc = h + 0.0 (first) or acc + (h + 0.0), read straight from h
+        self._fold_rows(h, free, None, free, self.first)
+        self.held.append((mb, keep, h[keep.to(h.device)].clone(), rows, self.first))
+        self.pend[keep] += 1
+        self.first = False
+        self.pos += 1
+
+    def _resolve(self) -> None:
+        mb, keep, hk, rows, first = self.held.pop(0)
+        e_rows = self.embeds.pop(mb)
+        if e_rows.dim() != 2 or e_rows.shape[0] != rows.numel() or e_rows.shape[1:] != hk.shape[1:]:
+            raise RuntimeError(
+                f"tied fold: embedding rows of mb {mb} have shape {tuple(e_rows.shape)}, "
+                f"want ({rows.numel()}, {tuple(hk.shape[1:])})"
+            )
+        e_on = torch.zeros_like(hk)
+        if rows.numel():
+            at = torch.searchsorted(keep, rows).to(hk.device)
+            e_on[at] = e_rows.to(hk.device, hk.dtype)
+        # held rows: acc = hk + e_on (first) or acc + (hk + e_on)
+        self._fold_rows(hk, None, e_on, keep, first)
+        self.pend[keep] -= 1
+
+    def complete(self) -> bool:
+        return self.pos == len(self.order) and not self.held
+
+    def result(self) -> torch.Tensor:
+        if not self.complete():
+            raise RuntimeError(
+                f"tied fold incomplete: {self.pos}/{len(self.order)} Head gradients, "
+                f"{len(self.held)} microbatch(es) waiting for embedding rows"
+            )
+        return self.acc
+
+
+class CountFold:
+    """runtime/accumulate.py:250-318: the int64 selection counts of one
+    step at a bias's owner, one (E,) vector per (microbatch, MoE layer),
+    checked on arrival and summed by integer add in microbatch order on the
+    host (exact, order-free).  The reference's refusals, named by
+    (step, mb, layer, peer): a microbatch outside [0, n_mb), a layer without
+    a bias here, a vector given twice, not int64, of the wrong shape, with a
+    negative count or (when `total` is given) not summing to T_mb * k; and,
+    at result(), a missing vector."""
+
+    def __init__(self, step: int, n_mb: int, layers, experts: dict, total: dict | None) -> None:
+        self.step = step
+        self.n_mb = n_mb
+        self.layers = list(layers)
+        self.experts = dict(experts)  # layer -> E
+        self.total = total  # layer -> T_mb * k, or None
+        self.got: dict = {}  # (mb, layer) -> vector
+
+    def _name(self, mb, layer, peer) -> str:
+        return f"(step {self.step}, mb {mb}, layer {layer}, peer {peer})"
+
+    def add(self, mb, layer, vec, peer) -> None:
+        name = self._name(mb, layer, peer)
+        if type(mb) is not int or not 0 <= mb < self.n_mb:
+            raise RuntimeError(f"MOE-COUNT {name}: microbatch outside [0, {self.n_mb})")
+        if layer not in self.experts:
+            raise RuntimeError(f"MOE-COUNT {name}: no selection bias of that layer here")
+        if (mb, layer) in self.got:
+            raise RuntimeError(f"MOE-COUNT {name}: count vector given twice")
+        if not isinstance(vec, torch.Tensor) or vec.dtype != torch.int64:
+            raise RuntimeError(f"MOE-COUNT {name}: not an int64 vector")
+        if tuple(vec.shape) != (self.experts[layer],):
+            raise RuntimeError(f"MOE-COUNT {name}: shape {tuple(vec.shape)}, want ({self.experts[layer]},)")
+        v = vec.detach().to("cpu", copy=True)
+        if bool((v < 0).any()):
+            raise RuntimeError(f"MOE-COUNT {name}: a negative count")
+        if self.total is not None and int(v.sum()) != self.total[layer]:
+            raise RuntimeError(f"MOE-COUNT {name}: counts sum to {int(v.sum())}, want T_mb*k = {self.total[layer]}")
+        self.got[(mb, layer)] = v
+
+    def missing(self) -> list:
+        return [(mb, layer) for layer in self.layers for mb in range(self.n_mb) if (mb, layer) not in self.got]
+
+    def complete(self) -> bool:
+        return not self.missing()
+
+    def result(self) -> dict:
+        """{layer: int64 (E,)}: the sum over microbatches in index order."""
+        gone = self.missing()
+        if gone:
+            mb, layer = gone[0]
+            raise RuntimeError(f"MOE-COUNT {self._name(mb, layer, '-')}: count vector missing at the owner ({len(gone)} missing)")
+        out = {}
+        for layer in self.layers:
+            acc = self.got[(0, layer)].clone()
+            for mb in range(1, self.n_mb):
+                acc += self.got[(mb, layer)]
+            out[layer] = acc
+        return out

@@ -1,0 +1,131 @@
+// rows.hip -- the row fold of a tied table's step gradient across stages
+// (TiedRowFold, runtime/accumulate.py:140-247).  The stock fold is
+// acc = g_0, acc += g_i in microbatch order with g_i = h_i + e_i (autograd's
+// sum of the table's two uses, e_i = +0 outside the microbatch's rows), one
+// rounding per add in the table's dtype.  TiedRowFold reaches the same bits
+// without a dense table per microbatch in flight by folding each row as
+// soon as its prefix is complete; every fold it makes is one of
+//   acc[idx[j]]  = a[rows_a[j]] + 0.0                  (first, free rows)
+//   acc[idx[j]] += a[rows_a[j]] + 0.0                  (later, free rows)
+//   acc[idx[j]]  = a[j] + b[j]      / acc[idx[j]] += a[j] + b[j]
+//                                                      (held rows resolved)
+// over a set of distinct rows, which this kernel runs: one block per row
+// (strided), 16-byte vectors across the row when it is aligned.
+#include <algorithm>
+
+#include "ely_device.hpp"
+#include "ely_host.hpp"
+
+#pragma clang fp contract(off)
+
+namespace ely {
+namespace {
+
+constexpr int kRowBlock = 256;
+
+typedef float rf4 __attribute__((ext_vector_type(4)));
+typedef uint32_t ru4 __attribute__((ext_vector_type(4)));
+
+// v = a + b (b = +0.0 when absent) rounded to the dtype, then acc = v or
+// acc + v rounded to the dtype: torch's two elementwise adds.
+template <bool BF16>
+__device__ __forceinline__ float fold1(float acc, float a, float b, bool first) {
+    float v = a + b;
+    if (BF16) v = bf16_to_f32(f32_to_bf16(v));
+    if (first) return v;
+    float s = acc + v;
+    if (BF16) s = bf16_to_f32(f32_to_bf16(s));
+    return s;
+}
+
+template <bool BF16>
+__global__ __launch_bounds__(kRowBlock) void rows_fold_kernel(void* __restrict__ acc, const void* __restrict__ a,
+                                                              const int64_t* __restrict__ a_rows,
+                                                              const void* __restrict__ b,
+                                                              const int64_t* __restrict__ idx, int64_t n_idx,
+                                                              int64_t n_rows, int64_t a_total, int64_t d, int first,
+                                                              int vec) {
+    constexpr int V = BF16 ? 8 : 4;  // elements per 16-byte vector
+    for (int64_t j = blockIdx.x; j < n_idx; j += gridDim.x) {
+        const int64_t r = idx[j];
+        const int64_t ar = a_rows ? a_rows[j] : j;
+        // the host checks every index; a row outside the tables is skipped, never touched
+        if (r < 0 || r >= n_rows || ar < 0 || ar >= a_total) continue;
+        if (BF16) {
+            uint16_t* ac = static_cast<uint16_t*>(acc) + r * d;
+            const uint16_t* av = static_cast<const uint16_t*>(a) + ar * d;
+            const uint16_t* bv = b ? static_cast<const uint16_t*>(b) + j * d : nullptr;
+            if (vec) {
+                for (int64_t c = (int64_t)threadIdx.x * V; c < d; c += (int64_t)kRowBlock * V) {
+                    const ru4 x = *reinterpret_cast<const ru4*>(av + c);
+                    const ru4 y = bv ? *reinterpret_cast<const ru4*>(bv + c) : ru4{0u, 0u, 0u, 0u};
+                    const ru4 z = first ? ru4{0u, 0u, 0u, 0u} : *reinterpret_cast<const ru4*>(ac + c);
+                    ru4 o;
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        const float lo = fold1<true>(bf16_to_f32(z[k] & 0xFFFFu), bf16_to_f32(x[k] & 0xFFFFu),
+                                                     bf16_to_f32(y[k] & 0xFFFFu), first);
+                        const float hi = fold1<true>(bf16_to_f32(z[k] >> 16), bf16_to_f32(x[k] >> 16),
+                                                     bf16_to_f32(y[k] >> 16), first);
+                        o[k] = f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);
+                    }
+                    *reinterpret_cast<ru4*>(ac + c) = o;
+                }
+            } else {
+                for (int64_t c = threadIdx.x; c < d; c += kRowBlock) {
+                    const float z = first ? 0.0f : bf16_to_f32(ac[c]);
+                    ac[c] = (uint16_t)f32_to_bf16(fold1<true>(z, bf16_to_f32(av[c]), bv ? bf16_to_f32(bv[c]) : 0.0f, first));
+                }
+            }
+        } else {
+            float* ac = static_cast<float*>(acc) + r * d;
+            const float* av = static_cast<const float*>(a) + ar * d;
+            const float* bv = b ? static_cast<const float*>(b) + j * d : nullptr;
+            if (vec) {
+                for (int64_t c = (int64_t)threadIdx.x * V; c < d; c += (int64_t)kRowBlock * V) {
+                    const rf4 x = *reinterpret_cast<const rf4*>(av + c);
+                    const rf4 y = bv ? *reinterpret_cast<const rf4*>(bv + c) : rf4{0.0f, 0.0f, 0.0f, 0.0f};
+                    const rf4 z = first ? rf4{0.0f, 0.0f, 0.0f, 0.0f} : *reinterpret_cast<const rf4*>(ac + c);
+                    rf4 o;
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) o[k] = fold1<false>(z[k], x[k], y[k], first);
+                    *reinterpret_cast<rf4*>(ac + c) = o;
+                }
+            } else {
+                for (int64_t c = threadIdx.x; c < d; c += kRowBlock) {
+                    const float z = first ? 0.0f : ac[c];
+                    ac[c] = fold1<false>(z, av[c], bv ? bv[c] : 0.0f, first);
+                }
+            }
+        }
+    }
+}
+
+}  // namespace
+}  // namespace ely
+
+using namespace ely;
+
+extern "C" int ely_rows_fold(void* acc, const void* a, const int64_t* a_rows, const void* b, const int64_t* idx,
+                             int64_t n_idx, int64_t n_rows, int64_t a_total, int64_t d, int32_t dtype, int32_t first,
+                             void* stream) {
+    return guarded([&] {
+        if (dtype != ELY_F32 && dtype != ELY_BF16) fail(ELY_EINVAL, "ely_rows_fold: dtype must be ELY_F32 or ELY_BF16");
+        if (n_idx < 0 || n_rows < 0 || a_total < 0 || d < 0) fail(ELY_EINVAL, "ely_rows_fold: negative size");
+        if (n_idx == 0 || d == 0) return;
+        if (!acc || !a || !idx) fail(ELY_EINVAL, "ely_rows_fold: null pointer");
+        if (!a_rows && a_total < n_idx) fail(ELY_EINVAL, "ely_rows_fold: a compact source holds one row per index");
+        const int64_t esz = dtype == ELY_BF16 ? 2 : 4;
+        const int64_t v = 16 / esz;
+        const int vec = (d % v == 0) && aligned16(acc) && aligned16(a) && (!b || aligned16(b)) ? 1 : 0;
+        const int64_t blocks = std::min<int64_t>(n_idx, mt_blocks(8));
+        hipStream_t s = static_cast<hipStream_t>(stream);
+        if (dtype == ELY_BF16)
+            hipLaunchKernelGGL(rows_fold_kernel<true>, dim3((unsigned)blocks), dim3(kRowBlock), 0, s, acc, a, a_rows, b,
+                               idx, n_idx, n_rows, a_total, d, first ? 1 : 0, vec);
+        else
+            hipLaunchKernelGGL(rows_fold_kernel<false>, dim3((unsigned)blocks), dim3(kRowBlock), 0, s, acc, a, a_rows, b,
+                               idx, n_idx, n_rows, a_total, d, first ? 1 : 0, vec);
+        check_launch("rows_fold_kernel");
+    });
+}

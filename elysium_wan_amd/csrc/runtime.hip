@@ -9,6 +9,10 @@
 
 #include "ely_host.hpp"
 
+#ifndef ELY_UPLOAD_SLOTS
+#define ELY_UPLOAD_SLOTS 8  // pinned upload ring slots per device (two per AdamW launch)
+#endif
+
 namespace ely {
 
 static thread_local std::string g_last_error;
@@ -43,7 +47,13 @@ int64_t mt_blocks(int per_cu) {
 
 // A ring of pinned host slots per device.  A slot is refilled only after the
 // copy that last read it has completed (its event), so a caller may issue
-// many uploads back to back without waiting.
+// many uploads back to back without waiting; the host blocks only when the
+// ring wraps onto an upload the GPU has not reached yet, which keeps a
+// staged host-moment step at most four chunk launches ahead of its copies.
+// Deeper rings (32 and 128 slots) measured slower on that step (C1 staged
+// 0.43-0.47 s against 0.40 s; 200M parameters with half the moments
+// resident 0.029-0.031 s against 0.019 s): the extra queued table copies
+// interleave with the bulk moment copies.
 namespace {
 struct Slot {
     void* host = nullptr;
@@ -52,7 +62,7 @@ struct Slot {
     bool pending = false;
 };
 struct Ring {
-    static constexpr int kSlots = 8;
+    static constexpr int kSlots = ELY_UPLOAD_SLOTS;
     Slot slots[kSlots];
     int next = 0;
 };

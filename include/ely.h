@@ -207,6 +207,21 @@ int ely_cast_bf16(const float* x, uint16_t* out, int64_t n, void* stream);
  * rounding; g_dtype ELY_F32 or ELY_BF16. */
 int ely_fold_add(float* acc, const void* g, int32_t g_dtype, int64_t n, void* stream);
 
+/* The row folds of TiedRowFold (runtime/accumulate.py:140-247), the step
+ * gradient of a tied table split across stages: for each j < n_idx, with
+ * r = idx[j] and ar = a_rows ? a_rows[j] : j,
+ *     v = a[ar] + (b ? b[j] : +0.0)              rounded to dtype,
+ *     acc[r] = first ? v : acc[r] + v            rounded to dtype
+ * (the reference's `h[fi] + 0.0` folds of a Head gradient's free rows,
+ * :210-213, and `hk + e_on` folds of its held rows, :232-235).  acc:
+ * [n_rows, d]; a: [a_total, d] rows picked by a_rows, or compact [n_idx, d]
+ * when a_rows is NULL; b: NULL or compact [n_idx, d]; idx and a_rows are
+ * device int64 arrays; the rows of idx are distinct.  An index outside its
+ * table is skipped (the caller checks them).  dtype ELY_F32 or ELY_BF16. */
+int ely_rows_fold(void* acc, const void* a, const int64_t* a_rows, const void* b, const int64_t* idx,
+                  int64_t n_idx, int64_t n_rows, int64_t a_total, int64_t d, int32_t dtype, int32_t first,
+                  void* stream);
+
 /* In-place g <- g * (*coef_dev) over a tensor list, the product rounded to
  * each tensor's dtype: the scaling step of clip_grad_norm_
  * (TORCH/nn/utils/clip_grad.py:170-183) with the coefficient ely_grad_norm
@@ -252,6 +267,20 @@ int ely_fp8_nibbles_encode(const void* t, int32_t t_dtype, int64_t n, uint8_t* h
 /* codec/fp8_planes.py:35-52: nibble planes -> n fp32 values of the e4m3
  * codes. */
 int ely_fp8_nibbles_decode(const uint8_t* hi, const uint8_t* lo, int64_t n, float* out, void* stream);
+
+/* ---------------------------------------------------------- measurement */
+
+/* No counterpart in the reference: streaming probes with the fused AdamW's
+ * five streams (p, m, v fp32; g and the working copy bf16; n elements each)
+ * and no arithmetic, so that the update's rate can be held against what the
+ * memory system gives the same traffic in the same placement.  which 0:
+ * read p, g, m, v (14 B/elem; `sink` is a device float that is never
+ * written in practice); 1: write p, m, v, copy (14 B/elem; overwrites
+ * them); 2: both (28 B/elem, the update's traffic; p, m, v rotate their
+ * values and copy := g).  n a multiple of 4; fp32 streams 16-byte
+ * aligned, bf16 ones 8-byte aligned; `blocks` blocks of 256 threads. */
+int ely_probe_streams(int32_t which, void* p, void* g, void* m, void* v, void* copy, int64_t n,
+                      int32_t blocks, void* sink, void* stream);
 
 /* ------------------------------------------------------------ self-test */
 

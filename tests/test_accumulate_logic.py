@@ -73,3 +73,30 @@ def test_deferred_last_part_and_its_merge(m):
         acc.step_inputs()
     with pytest.raises(ValueError, match="defer_last"):
         OrderedAccumulator([0]).step_inputs()
+
+
+def test_count_fold_sums_in_order_and_refuses_as_the_reference():
+    """runtime/accumulate.py:250-318 on the host: int64 (E,) vectors per
+    (microbatch, layer), summed exactly; the reference's refusals."""
+    from elysium_wan_amd.accumulate import CountFold
+
+    cf = CountFold(step=7, n_mb=2, layers=[3], experts={3: 4}, total={3: 6})
+    cf.add(1, 3, torch.tensor([1, 2, 3, 0]), peer=1)
+    assert not cf.complete() and cf.missing() == [(0, 3)]
+    with pytest.raises(RuntimeError, match=r"MOE-COUNT \(step 7, mb 0, layer 3, peer -\): count vector missing at the owner \(1 missing\)"):
+        cf.result()
+    cf.add(0, 3, torch.tensor([0, 0, 6, 0]), peer=0)
+    assert torch.equal(cf.result()[3], torch.tensor([1, 2, 9, 0]))
+    bad = [
+        ((2, 3, torch.zeros(4, dtype=torch.int64)), "microbatch outside"),
+        ((0, 9, torch.zeros(4, dtype=torch.int64)), "no selection bias"),
+        ((0, 3, torch.zeros(4, dtype=torch.int64)), "given twice"),
+    ]
+    for args, msg in bad:
+        with pytest.raises(RuntimeError, match=msg):
+            cf.add(*args, peer=2)
+    fresh = CountFold(step=1, n_mb=1, layers=[0], experts={0: 2}, total={0: 3})
+    for vec, msg in ((torch.zeros(2), "not an int64"), (torch.zeros(3, dtype=torch.int64), "shape"),
+                     (torch.tensor([-1, 4]), "negative"), (torch.tensor([1, 1]), "sum to 2, want T_mb\\*k = 3")):
+        with pytest.raises(RuntimeError, match=msg):
+            fresh.add(0, 0, vec, peer=0)

@@ -1,0 +1,82 @@
+"""The tied table's row fold (accumulate.TiedRowFold, the drop-in for
+runtime/accumulate.py:140-247) on the GPU: Head gradients and embedding rows
+handed in out of order, rows held by earlier microbatches, fp32 and bf16
+tables, aligned and unaligned rows -- the result equals the stock fold
+acc = g_0, acc = acc + g_i (g_i = h_i + e_i, e_i = +0 outside the
+microbatch's rows, each add rounded to the table's dtype) computed on the
+CPU, bit for bit, including the +0.0 that h + 0.0 makes of a -0.0."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import bits, say
+
+pytestmark = pytest.mark.gpu
+
+
+def _stock_fold(oracle, hs, rows, es, dtype):
+    """The reference's dense fold in microbatch order (numpy, IEEE fp32 adds,
+    bf16 rounding by the oracle's RNE after each add for bf16 tables)."""
+    acc = None
+    for h, r, e in zip(hs, rows, es):
+        hf = bits(h.float()).astype(np.float32)
+        E = np.zeros_like(hf)  # +0.0 outside the microbatch's rows
+        E[r.numpy()] = bits(e.float())
+        g = hf + E
+        if dtype == torch.bfloat16:
+            g = oracle.bf16_bits_to_f32(oracle.f32_to_bf16_bits(g)).reshape(hf.shape)
+        if acc is None:
+            acc = g
+        else:
+            acc = acc + g
+            if dtype == torch.bfloat16:
+                acc = oracle.bf16_bits_to_f32(oracle.f32_to_bf16_bits(acc)).reshape(hf.shape)
+    return acc
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("d", [64, 37])
+def test_out_of_order_heads_and_embeddings_equal_the_stock_fold(oracle, dtype, d):
+    from elysium_wan_amd.accumulate import TiedRowFold
+
+    n_rows, M = 1000, 5
+    gen = torch.Generator().manual_seed(90 + d)
+    hs, rows, es = [], [], []
+    for mb in range(M):
+        h = torch.randn(n_rows, d, generator=gen)
+        h[torch.rand(n_rows, d, generator=gen) < 0.01] = -0.0  # h + 0.0 turns these into +0.0
+        r = torch.randperm(n_rows, generator=gen)[: 40 + 30 * mb].sort().values
+        hs.append(h.to(dtype))
+        rows.append(r)
+        es.append(torch.randn(r.numel(), d, generator=gen).to(dtype))
+    fold = TiedRowFold(n_rows, range(M))
+    say("tied fold", dtype, d)
+    # Head gradients and embedding rows arrive out of order and interleaved
+    events = [("h", 2), ("e", 1), ("h", 0), ("e", 3), ("h", 1), ("e", 0), ("h", 4), ("h", 3), ("e", 4), ("e", 2)]
+    for kind, mb in events:
+        if kind == "h":
+            fold.add_head(mb, hs[mb].cuda(), rows[mb])
+        else:
+            fold.add_embed(mb, es[mb].cuda())
+    assert fold.complete()
+    got = fold.result()
+    torch.cuda.synchronize()
+    want = _stock_fold(oracle, hs, rows, es, dtype)
+    gotf = bits(got.float()).astype(np.float32).reshape(-1)
+    assert np.array_equal(gotf.view(np.uint32), want.reshape(-1).view(np.uint32))
+    with pytest.raises(RuntimeError, match="second Head"):
+        fold.add_head(0, hs[0].cuda(), rows[0])
+
+
+def test_incomplete_fold_names_what_it_waits_for():
+    from elysium_wan_amd.accumulate import TiedRowFold
+
+    fold = TiedRowFold(8, range(2))
+    fold.add_head(0, torch.randn(8, 4, device="cuda"), torch.tensor([1, 5]))
+    with pytest.raises(RuntimeError, match="tied fold incomplete: 1/2 Head gradients, 1 microbatch"):
+        fold.result()
+    with pytest.raises(RuntimeError, match="embedding rows of mb 0 have shape"):
+        fold.add_embed(0, torch.randn(3, 4, device="cuda"))
