@@ -1025,7 +1025,22 @@ def _row(label, ds):
     return f"| {label} | {len(ds)} | {sum(ds) / len(ds):,.0f} | {min(ds):,} | {max(ds):,} |"
 
 
-def trace_summary(step_dir: str, codec_dir: str, bench_json: str | None) -> None:
+def _last_bench_line(path: str | None):
+    """The last bench.py JSON line in a file of that run's output (rocprofv3
+    may print around it), or None.  A codec-only run's {"c1": ...} line is
+    returned in the full line's shape ({"fp8_codec": {"c1_per_row": ...}})."""
+    if not path:
+        return None
+    with open(path) as f:
+        text = f.read().splitlines()
+    rows = [ln for ln in text if ln.startswith('{"metric"')]
+    if rows:
+        return json.loads(rows[-1])
+    rows = [ln for ln in text if ln.startswith('{"c1"')]
+    return {"fp8_codec": {"c1_per_row": json.loads(rows[-1])["c1"]}} if rows else None
+
+
+def trace_summary(step_dir: str, codec_dir: str, bench_json: list | None) -> None:
     """Kernel durations from two rocprofv3 --kernel-trace runs: the C1
     optimizer step (`bench.py --no-cpu --no-codec --no-extra`) and the C1
     codec (`bench.py --no-optimizer --codec c1`).  The codec's quantize and
@@ -1033,12 +1048,12 @@ def trace_summary(step_dir: str, codec_dir: str, bench_json: str | None) -> None
     dequantized output), told apart by bench_codec's launch order: per
     format, quantize launches, dequantize launches, then as many round trips
     as dequantizes.  Writes profiles/c1_step_kernel_trace.md and
-    profiles/codec_c1_kernel_trace.md; with `bench_json` (the line of a
-    bench.py run on the same box) the HIP-event figures are set beside."""
-    b = None
-    if bench_json:
-        with open(bench_json) as f:
-            b = json.loads(f.read().strip().splitlines()[-1])
+    profiles/codec_c1_kernel_trace.md; with `bench_json` (the output files
+    of the two traced runs themselves, step then codec) each summary sets
+    the HIP-event figures of the process it traced beside the trace."""
+    bench_json = list(bench_json or [])
+    b = _last_bench_line(bench_json[0] if bench_json else None)
+    bc = _last_bench_line(bench_json[1] if len(bench_json) > 1 else None)
     n = N_BLOCKS * (12 * D_MODEL * D_MODEL + 13 * D_MODEL)
     step = _dispatches(step_dir)
     by = {}
@@ -1049,8 +1064,8 @@ def trace_summary(step_dir: str, codec_dir: str, bench_json: str | None) -> None
         "",
         "Commands (on one MI355X, from the repository root):",
         "",
-        "    rocprofv3 --kernel-trace --stats -T -d <step dir> -o kt --output-format csv -- python3 bench.py --no-cpu --no-codec --no-extra",
-        "    python bench.py --trace-summary <step dir> <codec dir> [--bench-json <bench.py line>]",
+        "    rocprofv3 --kernel-trace --stats -T -d <step dir> -o kt --output-format csv -- python3 bench.py --no-cpu --no-codec --no-extra > <step run's stdout>",
+        "    python bench.py --trace-summary <step dir> <codec dir> --bench-json <step run's stdout> <codec run's stdout>",
         "",
         "Workload: config C1's shard (16 GPT blocks at d = 2560, 192 tensors,",
         f"{n:,} fp32 params, bf16 grads N(0, 1e-4), bf16 working copy, AdamW",
@@ -1067,7 +1082,7 @@ def trace_summary(step_dir: str, codec_dir: str, bench_json: str | None) -> None
                   f"{n * ADAM_BYTES_PER_ELEM / avg / 1e6:,.0f} GB/s, {n * ADAM_BYTES_PER_ELEM / avg / 1e6 / HBM_PEAK_GBS:.3f} of 8 TB/s."]
         if b:
             ev = b["kernels"]["adamw_ms"]
-            lines += [f"bench.py's HIP-event average on the same box: {ev:.3f} ms ({abs(avg - ev) / ev * 100:.1f} % apart)."]
+            lines += [f"bench.py's HIP-event average in the traced process: {ev:.3f} ms ({abs(avg - ev) / ev * 100:.1f} % apart)."]
     with open(os.path.join(HERE, "profiles", "c1_step_kernel_trace.md"), "w") as f:
         f.write("\n".join(lines) + "\n")
     print("\n".join(lines))
@@ -1089,8 +1104,8 @@ def trace_summary(step_dir: str, codec_dir: str, bench_json: str | None) -> None
         "",
         "Commands (on one MI355X, from the repository root):",
         "",
-        "    rocprofv3 --kernel-trace --stats -T -d <codec dir> -o kc --output-format csv -- python3 bench.py --no-optimizer --codec c1",
-        "    python bench.py --trace-summary <step dir> <codec dir> [--bench-json <bench.py line>]",
+        "    rocprofv3 --kernel-trace --stats -T -d <codec dir> -o kc --output-format csv -- python3 bench.py --no-optimizer --codec c1 > <codec run's stdout>",
+        "    python bench.py --trace-summary <step dir> <codec dir> --bench-json <step run's stdout> <codec run's stdout>",
         "",
         "Workload: config C1's boundary activation [8, 2048, 2560] bf16 (N(0, 1) with",
         "0.1% of the elements x50), per-row scaling (one exponent per 2,560-element",
@@ -1109,9 +1124,9 @@ def trace_summary(step_dir: str, codec_dir: str, bench_json: str | None) -> None
         if ds:
             avg = sum(ds) / len(ds)
             lines.append(_row(kind, ds)[:-2] + f" | {na * per[kind] / avg / 1e3:.2f} TB/s |")
-    if b:
-        c = b["fp8_codec"]["c1_per_row"]["e4m3"]
-        lines += ["", "bench.py's HIP-event averages (one launch between two events, so each also",
+    if bc and bc.get("fp8_codec"):
+        c = bc["fp8_codec"]["c1_per_row"]["e4m3"]
+        lines += ["", "bench.py's HIP-event averages in the traced process (one launch between two events, so each also",
                   f"holds the launch's dispatch latency): quantize {c['quantize_ms'] * 1e3:.1f} us ({c['quantize_GBs'] / 1e3:.2f} TB/s),",
                   f"dequantize {c['dequantize_ms'] * 1e3:.1f} us ({c['dequantize_GBs'] / 1e3:.2f} TB/s), round trip "
                   f"{c['roundtrip_ms'] * 1e3:.1f} us ({c['roundtrip_GBs'] / 1e3:.2f} TB/s)."]
@@ -1285,7 +1300,7 @@ def main():
                     help="summarize --pmc runs of --profile-pass into profiles/: FETCH_DIR WRITE_DIR [REQUEST_SIZE_DIR]")
     ap.add_argument("--traffic-command", default="", help="the command line recorded in the traffic summary")
     ap.add_argument("--trace-summary", nargs=2, metavar=("STEP_DIR", "CODEC_DIR"), help="summarize two rocprofv3 --kernel-trace runs into profiles/")
-    ap.add_argument("--bench-json", help="a bench.py output line from the same box, quoted beside the trace summary")
+    ap.add_argument("--bench-json", nargs="+", metavar="OUT", help="the traced runs' own stdout (step, then codec), quoted beside the trace summary")
     ap.add_argument("--placement-sweep", nargs=2, metavar=("POOL_GIB", "SPEC"),
                     help="AdamW and stream probes on C1-sized streams carved from one pool (SPEC: A[,A...] or A:B[,...] GiB)")
     ap.add_argument("--pmc-summary", nargs="+", metavar="DB", help="markdown table of rocprofv3 --pmc databases of a placement sweep")

@@ -11,6 +11,8 @@ from __future__ import annotations
 import numpy as np
 import pytest
 import torch
+from hypothesis import HealthCheck, given, settings
+from hypothesis import strategies as st
 
 from gpu_util import bits, say
 
@@ -112,3 +114,54 @@ def test_one_microbatch_defers_its_only_part(oracle):
     ob.step(grads=[t.float() for t in full])
     torch.cuda.synchronize()
     assert all(torch.equal(x.detach().view(torch.int32), y.detach().view(torch.int32)) for x, y in zip(a, b))
+
+
+@settings(max_examples=25, deadline=None, derandomize=True, suppress_health_check=[HealthCheck.too_slow])
+@given(
+    m=st.integers(1, 5),
+    bf16=st.booleans(),
+    defer=st.booleans(),
+    quarantine=st.integers(-1, 4),
+    perm_seed=st.integers(0, 2**16),
+)
+def test_ordered_fold_fuzz_equals_the_oracle(oracle, m, bf16, defer, quarantine, perm_seed):
+    """Random microbatch counts, part dtypes, arrival orders of every
+    (microbatch, tensor) part and an optional quarantined microbatch:
+    result() equals the oracle's left fold in microbatch order bit for bit,
+    and with defer_last the prefix sums and held parts are the oracle's
+    prefix fold and last microbatch."""
+    import random
+
+    from elysium_wan_amd import accumulate
+
+    dtype = torch.bfloat16 if bf16 else torch.float32
+    parts = _parts(100 + perm_seed % 97, m, dtype)
+    acc = accumulate.OrderedAccumulator(range(m), defer_last=defer)
+    q = quarantine if 0 <= quarantine < m else None
+    events = [(mb, i) for mb in range(m) for i in range(len(SHAPES))]
+    random.Random(perm_seed).shuffle(events)
+    say("ordered fold fuzz", m, dtype, defer, q)
+    if q is not None:
+        acc.add(q, [parts[q][i].cuda() for i in range(len(SHAPES))], verified=False)
+    seen = {mb: 0 for mb in range(m)}
+    for mb, i in events:
+        if mb == q:
+            continue
+        acc.fold_part(mb, i, len(SHAPES), parts[mb][i].cuda(), torch.float32)
+        seen[mb] += 1
+        if seen[mb] == len(SHAPES):
+            acc.end_part(mb)
+    if q is not None:
+        assert not acc.complete()
+        acc.release(q)
+    assert acc.complete()
+    if defer:
+        grads, accs = acc.step_inputs()
+        for i in range(len(SHAPES)):
+            assert torch.equal(grads[i].cpu(), parts[m - 1][i])
+            if m > 1:
+                assert np.array_equal(bits(accs[i]).reshape(-1).view(np.uint32),
+                                      _oracle_fold(oracle, parts[: m - 1], i).view(np.uint32))
+        assert accs is None or m > 1
+    for i, s in enumerate(acc.result()):
+        assert np.array_equal(bits(s.float()).reshape(-1).view(np.uint32), _oracle_fold(oracle, parts, i).view(np.uint32))

@@ -11,6 +11,8 @@ from __future__ import annotations
 import numpy as np
 import pytest
 import torch
+from hypothesis import HealthCheck, given, settings
+from hypothesis import strategies as st
 
 from gpu_util import bits, say
 
@@ -80,3 +82,47 @@ def test_incomplete_fold_names_what_it_waits_for():
         fold.result()
     with pytest.raises(RuntimeError, match="embedding rows of mb 0 have shape"):
         fold.add_embed(0, torch.randn(3, 4, device="cuda"))
+
+
+@settings(max_examples=25, deadline=None, derandomize=True, suppress_health_check=[HealthCheck.too_slow])
+@given(
+    m=st.integers(1, 5),
+    n_rows=st.sampled_from([1, 7, 64, 333]),
+    d=st.sampled_from([1, 8, 24, 40]),
+    bf16=st.booleans(),
+    perm_seed=st.integers(0, 2**16),
+    data_seed=st.integers(0, 2**16),
+)
+def test_tied_fold_fuzz_equals_the_stock_fold(oracle, m, n_rows, d, bf16, perm_seed, data_seed):
+    """Random microbatch counts, table shapes (rows that fit a vector and rows
+    that do not), row sets (empty and full included) and arrival orders of
+    the 2M events: the GPU fold equals the CPU stock fold bit for bit."""
+    import random
+
+    from elysium_wan_amd.accumulate import TiedRowFold
+
+    dtype = torch.bfloat16 if bf16 else torch.float32
+    gen = torch.Generator().manual_seed(data_seed)
+    hs, rows, es = [], [], []
+    for mb in range(m):
+        h = torch.randn(n_rows, d, generator=gen)
+        h[torch.rand(n_rows, d, generator=gen) < 0.05] = -0.0
+        k = int(torch.randint(0, n_rows + 1, (1,), generator=gen))
+        r = torch.randperm(n_rows, generator=gen)[:k].sort().values
+        hs.append(h.to(dtype))
+        rows.append(r)
+        es.append(torch.randn(k, d, generator=gen).to(dtype))
+    events = [("h", mb) for mb in range(m)] + [("e", mb) for mb in range(m)]
+    random.Random(perm_seed).shuffle(events)
+    say("tied fold fuzz", m, n_rows, d, dtype, events)
+    fold = TiedRowFold(n_rows, range(m))
+    for kind, mb in events:
+        if kind == "h":
+            fold.add_head(mb, hs[mb].cuda(), rows[mb])
+        else:
+            fold.add_embed(mb, es[mb].cuda())
+    assert fold.complete()
+    got = bits(fold.result().float()).astype(np.float32).reshape(-1)
+    torch.cuda.synchronize()
+    want = _stock_fold(oracle, hs, rows, es, dtype).reshape(-1)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
