@@ -1021,6 +1021,65 @@ def _runs(disp, names):
     return [r for r in runs if r[0] is not None]
 
 
+def copy_summary(trace_dir: str) -> None:
+    """Copy and kernel durations of a rocprofv3 --kernel-trace
+    --memory-copy-trace run of `bench.py --leg host_moments`: the staged
+    host-moment step's bulk copies (chunks of 2^24 fp32 moments, 67 MB each)
+    in each direction, whether the slow ones overlapped a copy the other way,
+    and the fused update's launches.  Writes
+    profiles/host_moments_c1_copy_trace.md."""
+    import csv
+    import glob
+    import statistics
+
+    copies, kernels = [], []
+    for path in glob.glob(os.path.join(trace_dir, "**", "*memory_copy_trace.csv"), recursive=True):
+        with open(path) as f:
+            copies += [(r["Direction"], int(r["Start_Timestamp"]), int(r["End_Timestamp"])) for r in csv.DictReader(f)]
+    for path in glob.glob(os.path.join(trace_dir, "**", "*kernel_trace.csv"), recursive=True):
+        with open(path) as f:
+            kernels += [(r["Kernel_Name"], int(r["Start_Timestamp"]), int(r["End_Timestamp"])) for r in csv.DictReader(f)]
+    chunk_mb = (1 << 24) * 4 / 1e6
+    big = sorted((c for c in copies if c[2] - c[1] > 200_000), key=lambda c: c[1])  # the moment chunks, not the tables
+    lines = [
+        "# Copy durations, C1's staged host-moment step",
+        "",
+        "Commands (on one MI355X, from the repository root):",
+        "",
+        "    rocprofv3 --kernel-trace --memory-copy-trace --stats -T -d <dir> -o hm --output-format csv -- python3 bench.py --leg host_moments",
+        "    python bench.py --copy-summary <dir>",
+        "",
+        "Workload: C1's shard (192 tensors, 1,258,823,680 fp32 params, bf16 grads,",
+        "bf16 working copy, clip 1.0) with adamw-host's moments in pinned host",
+        "memory: four in-place steps (the kernel reads and writes the moments",
+        "through the GPU's mapping), then four staged steps (each 2^24-element",
+        f"chunk of m and v copied in, updated, copied out: {chunk_mb:.1f} MB per copy, 75",
+        "chunks per step, 3 staging slots).  Copies under 0.2 ms (the launch tables)",
+        "are left out.",
+        "",
+        "| copies | count | median (ms) | min (ms) | max (ms) | slower than 3 ms | of those, alone on the link | median rate |",
+        "|---|---|---|---|---|---|---|---|",
+    ]
+    for label, key in (("host to device", "HOST_TO_DEVICE"), ("device to host", "DEVICE_TO_HOST")):
+        mine = [c for c in big if c[0].endswith(key)]
+        other = [c for c in big if not c[0].endswith(key)]
+        if not mine:
+            continue
+        ds = [(c[2] - c[1]) / 1e6 for c in mine]
+        slow = [c for c in mine if c[2] - c[1] > 3_000_000]
+        alone = [c for c in slow if not any(min(c[2], o[2]) > max(c[1], o[1]) for o in other)]
+        med = statistics.median(ds)
+        lines.append(f"| {label} | {len(ds)} | {med:.2f} | {min(ds):.2f} | {max(ds):.2f} | {len(slow)} | {len(alone)} | "
+                     f"{chunk_mb / med:.0f} GB/s |")
+    adam = [(e - b) / 1e6 for n, b, e in kernels if n.startswith("adamw_kernel")]
+    if adam:
+        lines += ["", f"adamw_kernel launches: {len(adam)}, median {statistics.median(adam):.3f} ms "
+                  f"(a staged launch updates one chunk; an in-place launch the whole shard over PCIe)."]
+    with open(os.path.join(HERE, "profiles", "host_moments_c1_copy_trace.md"), "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
 def _row(label, ds):
     return f"| {label} | {len(ds)} | {sum(ds) / len(ds):,.0f} | {min(ds):,} | {max(ds):,} |"
 
@@ -1282,6 +1341,45 @@ def read_traffic():
         return json.load(f).get("traffic_bytes_per_launch")
 
 
+def extra_legs(device, stream):
+    """The extra legs of the default run, in order: (key, what, callable)."""
+    return [
+        ("fold", "fold leg", lambda: bench_fold(device, stream)),
+        ("release", "per-layer release leg", lambda: bench_release(device, stream)),
+        ("elementwise", "elementwise leg", lambda: bench_elementwise(device, stream)),
+        ("c1_torch_order", "torch-order leg", lambda: bench_torch_order(device, stream)),
+        ("host_moments", "host-moments leg", lambda: bench_host_moments(device)),
+        ("check_host_adamw", "check_host_adamw leg (200M parameters)", lambda: bench_check_host_adamw(device)),
+        ("wire", "wire leg", lambda: bench_wire(device, stream)),
+        ("hbm_reference", "vendor-kernel reference leg", lambda: hbm_reference(device, stream)),
+        ("configs", "configs leg (C0, C2, C3)", lambda: bench_configs(device, stream)),
+        ("c1_placement", "placement leg (C1 allocated while 150 GiB are held)", lambda: bench_placement(device, stream)),
+    ]
+
+
+LEG_NAMES = ("fold", "release", "elementwise", "c1_torch_order", "host_moments", "check_host_adamw", "wire",
+             "hbm_reference", "configs", "c1_placement")
+
+
+def run_legs(legs) -> dict:
+    """Run (key, what, callable) legs in order; a leg that runs out of device
+    memory or fails is recorded in its entry and the others go on."""
+    extra = {}
+    for key, what, leg in legs:
+        log(what)
+        try:
+            extra[key] = leg()
+        except torch.OutOfMemoryError as e:
+            # a box with less free HBM skips the leg; the headline stands
+            extra[key] = {"skipped": f"out of device memory: {str(e)[:160]}"}
+        except Exception as e:  # noqa: BLE001 -- recorded in the line, the headline stands
+            log(f"{what} failed: {e!r}")
+            extra[key] = {"error": repr(e)[:300]}
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+    return extra
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -1293,6 +1391,9 @@ def main():
     ap.add_argument("--codec", choices=("c1", "c4", "all"), default="all", help="activation sizes of the codec leg")
     ap.add_argument("--no-optimizer", action="store_true", help="skip the optimizer leg (profiling the other legs alone)")
     ap.add_argument("--no-configs", action="store_true", help="skip the C0/C2/C3 optimizer leg (--no-extra skips it too)")
+    ap.add_argument("--leg", action="append", choices=LEG_NAMES,
+                    help="run only these extra legs (repeatable), no headline, and print their JSON (for profiling one leg)")
+    ap.add_argument("--copy-summary", metavar="DIR", help="summarize a rocprofv3 --memory-copy-trace run of --leg host_moments into profiles/")
     ap.add_argument("--placement-probe", choices=("fresh", "hold150"), help="three C1 steps only (for rocprofv3 --pmc)")
     ap.add_argument("--cpu-sample", type=int, default=256 * 1024 * 1024)
     ap.add_argument("--profile-pass", action="store_true", help="launch each measured kernel a few times, untimed, for rocprofv3 --pmc runs")
@@ -1318,6 +1419,9 @@ def main():
     if args.pmc_summary:
         pmc_summary(args.pmc_summary, args.pmc_spec)
         return
+    if args.copy_summary:
+        copy_summary(args.copy_summary)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
@@ -1340,6 +1444,10 @@ def main():
             placement_sweep(device, stream, int(args.placement_sweep[0]), args.placement_sweep[1])
         return
     with torch.cuda.stream(stream):
+        if args.leg:
+            log("leg-only run: " + ", ".join(args.leg))
+            print(json.dumps(run_legs([leg for leg in extra_legs(device, stream) if leg[0] in args.leg])), flush=True)
+            return
         if args.no_optimizer:
             log("codec-only run")
             if args.codec in ("c1", "all"):
@@ -1360,32 +1468,7 @@ def main():
                 codec["c4"] = bench_c4(device, stream)
                 torch.cuda.empty_cache()
         if not args.no_extra:
-            extra = {}
-            legs = [
-                ("fold", "fold leg", lambda: bench_fold(device, stream)),
-                ("release", "per-layer release leg", lambda: bench_release(device, stream)),
-                ("elementwise", "elementwise leg", lambda: bench_elementwise(device, stream)),
-                ("c1_torch_order", "torch-order leg", lambda: bench_torch_order(device, stream)),
-                ("host_moments", "host-moments leg", lambda: bench_host_moments(device)),
-                ("check_host_adamw", "check_host_adamw leg (200M parameters)", lambda: bench_check_host_adamw(device)),
-                ("wire", "wire leg", lambda: bench_wire(device, stream)),
-                ("hbm_reference", "vendor-kernel reference leg", lambda: hbm_reference(device, stream)),
-            ]
-            if not args.no_configs:
-                legs.append(("configs", "configs leg (C0, C2, C3)", lambda: bench_configs(device, stream)))
-            legs.append(("c1_placement", "placement leg (C1 allocated while 150 GiB are held)", lambda: bench_placement(device, stream)))
-            for key, what, leg in legs:
-                log(what)
-                try:
-                    extra[key] = leg()
-                except torch.OutOfMemoryError as e:
-                    # a box with less free HBM skips the leg; the headline stands
-                    extra[key] = {"skipped": f"out of device memory: {str(e)[:160]}"}
-                except Exception as e:  # noqa: BLE001 -- recorded in the line, the headline stands
-                    log(f"{what} failed: {e!r}")
-                    extra[key] = {"error": repr(e)[:300]}
-                torch.cuda.synchronize()
-                torch.cuda.empty_cache()
+            extra = run_legs([leg for leg in extra_legs(device, stream) if not (args.no_configs and leg[0] == "configs")])
     n = o["n_elem"]
     adam_bytes = n * ADAM_BYTES_PER_ELEM
     achieved = adam_bytes / (o["adam_ms"] * 1e-3) / 1e9
