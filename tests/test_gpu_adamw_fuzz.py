@@ -24,6 +24,22 @@ FUZZ = settings(max_examples=60, deadline=None, derandomize=True, suppress_healt
 SIZES = [0, 1, 3, 4, 5, 1023, 1024, 2047, 2048, 2049, 4095, 4096, 4097, 8191, 12289, 65537]
 LR, BETAS, EPS = 1e-2, (0.9, 0.95), 1e-8
 
+def _consts_table(oracle, order: str, wd: float, ts):
+    """The oracle's constants of each tensor's step t."""
+    fn = oracle.host_adamw_consts if order == "host" else oracle.torch_adamw_consts
+    return [fn(LR, BETAS, EPS, wd, t) for t in ts]
+
+
+def _ctab(consts):
+    from elysium_wan_amd import _lib
+
+    ctab = (_lib.ElyConsts * len(consts))()
+    for j, c in enumerate(consts):
+        row = [float(x) for x in np.asarray(c, dtype=np.float32).reshape(-1)[:8]]
+        ctab[j].c[:] = row + [0.0] * (8 - len(row))
+    return ctab
+
+
 tensor_spec = st.tuples(st.sampled_from(SIZES), st.lists(st.sampled_from([0, 0, 1, 2, 3]), min_size=5, max_size=5))
 
 
@@ -44,14 +60,18 @@ def _view(host: np.ndarray, off: int, dtype) -> torch.Tensor:
     wd=st.sampled_from([0.0, 0.1]),
     clip=st.sampled_from([None, 0.37, 1.0]),
     with_copy=st.booleans(),
+    own_steps=st.booleans(),
     seed=st.integers(0, 2**16),
 )
-def test_fused_step_matches_the_oracle(oracle, specs, bf16g, order, wd, clip, with_copy, seed):
+def test_fused_step_matches_the_oracle(oracle, specs, bf16g, order, wd, clip, with_copy, own_steps, seed):
+    """own_steps: tensor j at step t + j, so each tensor has its own
+    constants and the launch reads them from the uploaded table; otherwise
+    the short list's shared constants ride in the kernel arguments."""
     from elysium_wan_amd import _lib
 
     L = _lib.load()
     rng = np.random.default_rng(seed)
-    say("adamw fuzz", order, "bf16" if bf16g else "f32", wd, clip, with_copy, [s for s, _ in specs])
+    say("adamw fuzz", order, "bf16" if bf16g else "f32", wd, clip, with_copy, own_steps, [s for s, _ in specs])
     host = []
     dev = []
     for n, offs in specs:
@@ -74,11 +94,8 @@ def test_fused_step_matches_the_oracle(oracle, specs, bf16g, order, wd, clip, wi
                 g = oracle.f32_to_bf16_bits(g)
             gs.append(g)
             d[1] = _view(g, d[5], torch.bfloat16 if bf16g else torch.float32)
-        t = step + 1
-        consts = (oracle.host_adamw_consts if order == "host" else oracle.torch_adamw_consts)(LR, BETAS, EPS, wd, t)
-        ctab = (_lib.ElyConsts * n_t)()
-        for j in range(n_t):
-            ctab[j].c[:] = [float(x) for x in np.asarray(consts, dtype=np.float32).reshape(-1)[:8]] + [0.0] * max(0, 8 - len(consts))
+        consts = _consts_table(oracle, order, wd, [step + 1 + (j if own_steps else 0) for j in range(n_t)])
+        ctab = _ctab(consts)
         copies = [_lib.ely_tensor(d[4]) if d[4] is not None else _lib.ElyTensor(None, 0, _lib.BF16, 0) for d in dev]
         rc = L.ely_adamw_step(_lib.tensor_array([d[0] for d in dev]), _lib.tensor_array([d[1] for d in dev]),
                               _lib.tensor_array([d[2] for d in dev]), _lib.tensor_array([d[3] for d in dev]),
@@ -86,8 +103,8 @@ def test_fused_step_matches_the_oracle(oracle, specs, bf16g, order, wd, clip, wi
                               int(wd != 0), None if coef_dev is None else coef_dev.data_ptr(), ws.data_ptr(), ws.numel(), stream)
         _lib.check(rc, "adamw fuzz")
         fn = oracle.adamw_host if order == "host" else oracle.adamw_torch
-        for (p, m, v, c), g in zip(host, gs):
-            fn(p, g, m, v, consts, wd != 0, 1.0 if clip is None else clip, c if with_copy else None)
+        for (p, m, v, c), g, cj in zip(host, gs, consts):
+            fn(p, g, m, v, cj, wd != 0, 1.0 if clip is None else clip, c if with_copy else None)
     torch.cuda.synchronize()
     for (p, m, v, c), d in zip(host, dev):
         for want, got in ((p, d[0]), (m, d[2]), (v, d[3])):
@@ -111,21 +128,23 @@ fold_spec = st.tuples(st.sampled_from(SIZES), st.lists(st.sampled_from([0, 0, 1,
     wd=st.sampled_from([0.0, 0.1]),
     max_norm=st.sampled_from([None, 0.05, 1e3]),
     with_copy=st.booleans(),
+    own_steps=st.booleans(),
     seed=st.integers(0, 2**16),
 )
-def test_fused_fold_step_matches_the_oracle(oracle, specs, bf16g, order, wd, max_norm, with_copy, seed):
+def test_fused_fold_step_matches_the_oracle(oracle, specs, bf16g, order, wd, max_norm, with_copy, own_steps, seed):
     """ely_grad_norm_fold + ely_adamw_fold_step (the last microbatch folded
     inside the norm and the update, runtime/accumulate.py:93-104) against the
     oracle's fold_add followed by its step: the norm within 1e-6 of the
     oracle's fp64 sum of squares of the folded gradients, then host order
     bit for bit (parameters, moments, working copy) and torch order within
     1 ulp, with each of the six streams at its own misalignment, over two
-    steps; the accumulators are never written."""
+    steps, shared or per-tensor constants (own_steps); the accumulators are
+    never written."""
     from elysium_wan_amd import _lib
 
     L = _lib.load()
     rng = np.random.default_rng(seed)
-    say("adamw fold fuzz", order, "bf16" if bf16g else "f32", wd, max_norm, with_copy, [s for s, _ in specs])
+    say("adamw fold fuzz", order, "bf16" if bf16g else "f32", wd, max_norm, with_copy, own_steps, [s for s, _ in specs])
     host, dev = [], []
     for n, offs in specs:
         p = (rng.standard_normal(n) * 0.1).astype(np.float32)
@@ -155,11 +174,8 @@ def test_fused_fold_step_matches_the_oracle(oracle, specs, bf16g, order, wd, max
             wsn = torch.empty(max(L.ely_grad_norm_workspace_bytes(garr, n_t), 256), dtype=torch.uint8, device="cuda")
             _lib.check(L.ely_grad_norm_fold(aarr, garr, n_t, max_norm, res.data_ptr(), wsn.data_ptr(), wsn.numel(), stream), "norm fold")
             coef_ptr = res.data_ptr() + 12
-        t = step + 1
-        consts = (oracle.host_adamw_consts if order == "host" else oracle.torch_adamw_consts)(LR, BETAS, EPS, wd, t)
-        ctab = (_lib.ElyConsts * n_t)()
-        for j in range(n_t):
-            ctab[j].c[:] = [float(x) for x in np.asarray(consts, dtype=np.float32).reshape(-1)[:8]] + [0.0] * max(0, 8 - len(consts))
+        consts = _consts_table(oracle, order, wd, [step + 1 + (j if own_steps else 0) for j in range(n_t)])
+        ctab = _ctab(consts)
         copies = [_lib.ely_tensor(d["c"]) if d["c"] is not None else _lib.ElyTensor(None, 0, _lib.BF16, 0) for d in dev]
         ws = torch.empty(L.ely_adamw_workspace_bytes(n_t), dtype=torch.uint8, device="cuda")
         rc = L.ely_adamw_fold_step(_lib.tensor_array([d["p"] for d in dev]), aarr, garr,
@@ -182,8 +198,8 @@ def test_fused_fold_step_matches_the_oracle(oracle, specs, bf16g, order, wd, max
             coef = float(res[12:16].view(torch.float32).item())
             assert coef == oracle.clip_coef(norm, max_norm)
         fn = oracle.adamw_host if order == "host" else oracle.adamw_torch
-        for (p, m, v, c), f in zip(host, folded):
-            fn(p, f, m, v, consts, wd != 0, coef, c if with_copy else None)
+        for (p, m, v, c), f, cj in zip(host, folded, consts):
+            fn(p, f, m, v, cj, wd != 0, coef, c if with_copy else None)
         for a, d in zip(accs, dev):
             assert np.array_equal(bits(d["a"]).view(np.uint32), a.view(np.uint32)), "accumulator written"
     for (p, m, v, c), d in zip(host, dev):
@@ -195,3 +211,44 @@ def test_fused_fold_step_matches_the_oracle(oracle, specs, bf16g, order, wd, max
                 assert int(ulp_distance(gb.view(np.float32), want).max(initial=0)) <= 1
         if with_copy and order == "host":
             assert np.array_equal(bits(d["c"]), c)
+
+
+@pytest.mark.parametrize("n_t", [47, 48, 49, 120])
+def test_argument_table_limit(oracle, n_t):
+    """Lists of up to 48 tensors at one step carry their descriptors in the
+    kernel arguments, longer ones upload a table: either side of the limit
+    the step equals the oracle's HostAdamW bit for bit (parameters, moments,
+    working copy), ragged sizes, bf16 gradients, clip coefficient."""
+    from elysium_wan_amd import _lib
+
+    L = _lib.load()
+    rng = np.random.default_rng(1000 + n_t)
+    sizes = [int(x) for x in rng.integers(1, 9000, n_t)]
+    say("argument table limit", n_t)
+    host, dev = [], []
+    for n in sizes:
+        p = (rng.standard_normal(n) * 0.1).astype(np.float32)
+        m, v, c = np.zeros(n, np.float32), np.zeros(n, np.float32), np.zeros(n, np.uint16)
+        host.append([p, m, v, c])
+        dev.append([_view(p, 0, torch.float32), None, _view(m, 0, torch.float32), _view(v, 0, torch.float32),
+                    _view(c, 0, torch.bfloat16)])
+    coef_dev = torch.tensor([0.5], dtype=torch.float32, device="cuda")
+    ws = torch.empty(L.ely_adamw_workspace_bytes(n_t), dtype=torch.uint8, device="cuda")
+    stream = _lib.stream_ptr(torch.device("cuda", 0))
+    for step in range(2):
+        gs = [oracle.f32_to_bf16_bits((rng.standard_normal(n) * 1e-2).astype(np.float32)) for n in sizes]
+        for d, g in zip(dev, gs):
+            d[1] = _view(g, 0, torch.bfloat16)
+        consts = _consts_table(oracle, "host", 0.1, [step + 1] * n_t)
+        rc = L.ely_adamw_step(_lib.tensor_array([d[0] for d in dev]), _lib.tensor_array([d[1] for d in dev]),
+                              _lib.tensor_array([d[2] for d in dev]), _lib.tensor_array([d[3] for d in dev]),
+                              _lib.tensor_array([d[4] for d in dev]), n_t, _ctab(consts), _lib.ORDER_HOST, 1,
+                              coef_dev.data_ptr(), ws.data_ptr(), ws.numel(), stream)
+        _lib.check(rc, "argument table limit")
+        for (p, m, v, c), g, cj in zip(host, gs, consts):
+            oracle.adamw_host(p, g, m, v, cj, True, 0.5, c)
+    torch.cuda.synchronize()
+    for (p, m, v, c), d in zip(host, dev):
+        for want, got in ((p, d[0]), (m, d[2]), (v, d[3])):
+            assert np.array_equal(bits(got).view(np.uint32), want.view(np.uint32))
+        assert np.array_equal(bits(d[4]), c)
