@@ -236,9 +236,17 @@ __device__ __forceinline__ void load8_any(const NormDesc& d, int64_t i, int64_t 
 // (the tile loop is then compiled for that dtype only, which keeps the
 // kernel's registers, and so its occupancy, to what that dtype needs), or -1
 // for a mixed list, dispatched per tile.
-template <bool FOLD, int DT, int64_t TILE>
-__global__ __launch_bounds__(kBlock) void norm_partials_kernel(const NormDesc* __restrict__ desc, int32_t n,
-                                                               int64_t total_tiles, double* __restrict__ partials) {
+// A norm call of at most kNormArgTensors gradients carries its descriptors
+// in the kernel arguments (40 bytes each, 1,920 in all), as a short AdamW
+// list does: no table copy ahead of the launch.  Longer lists read the
+// table uploaded to the workspace.
+constexpr int kNormArgTensors = 48;
+struct NormArgTable {
+    NormDesc d[kNormArgTensors];
+};
+
+template <bool FOLD, int DT, int64_t TILE, class Desc>
+__device__ __forceinline__ void norm_partials_body(const Desc* desc, int32_t n, int64_t total_tiles, double* partials) {
     const int lane = threadIdx.x & (kWave - 1);
     const int64_t waves = (int64_t)gridDim.x * (kBlock / kWave);
     const int64_t w = (int64_t)blockIdx.x * (kBlock / kWave) + wave_uniform(threadIdx.x / kWave);
@@ -269,6 +277,18 @@ __global__ __launch_bounds__(kBlock) void norm_partials_kernel(const NormDesc* _
         acc = wave_sum_f64(acc);
         if (lane == 0) partials[tile] = acc;
     }
+}
+
+template <bool FOLD, int DT, int64_t TILE>
+__global__ __launch_bounds__(kBlock) void norm_partials_kernel(const NormDesc* __restrict__ desc, int32_t n,
+                                                               int64_t total_tiles, double* __restrict__ partials) {
+    norm_partials_body<FOLD, DT, TILE>(desc, n, total_tiles, partials);
+}
+
+template <bool FOLD, int DT, int64_t TILE>
+__global__ __launch_bounds__(kBlock) void norm_partials_args_kernel(const NormArgTable tab, int32_t n,
+                                                                    int64_t total_tiles, double* __restrict__ partials) {
+    norm_partials_body<FOLD, DT, TILE>(tab.d, n, total_tiles, partials);
 }
 
 __global__ __launch_bounds__(kFinalThreads) void norm_final_kernel(const double* __restrict__ partials, int64_t tiles,
@@ -318,9 +338,8 @@ __global__ __launch_bounds__(kFinalThreads) void norm_final_kernel(const double*
 // own tile table: wave w scales tiles w, w + W, ...  A full, aligned tile
 // moves 16-byte vectors, lane l taking vectors l, l + 64, ...; others go
 // element by element.  DT as norm_partials_kernel.
-template <int DT, int64_t TILE>
-__global__ __launch_bounds__(kBlock) void clip_scale_kernel(const NormDesc* __restrict__ desc, int32_t n,
-                                                            int64_t total_tiles, const float* __restrict__ coef_ptr) {
+template <int DT, int64_t TILE, class Desc>
+__device__ __forceinline__ void clip_scale_body(const Desc* desc, int32_t n, int64_t total_tiles, const float* coef_ptr) {
     constexpr int U = ELY_CLIP_UNROLL;
     const int lane = threadIdx.x & (kWave - 1);
     const int64_t waves = (int64_t)gridDim.x * (kBlock / kWave);
@@ -366,6 +385,18 @@ __global__ __launch_bounds__(kBlock) void clip_scale_kernel(const NormDesc* __re
     }
 }
 
+template <int DT, int64_t TILE>
+__global__ __launch_bounds__(kBlock) void clip_scale_kernel(const NormDesc* __restrict__ desc, int32_t n,
+                                                            int64_t total_tiles, const float* __restrict__ coef_ptr) {
+    clip_scale_body<DT, TILE>(desc, n, total_tiles, coef_ptr);
+}
+
+template <int DT, int64_t TILE>
+__global__ __launch_bounds__(kBlock) void clip_scale_args_kernel(const NormArgTable tab, int32_t n, int64_t total_tiles,
+                                                                 const float* __restrict__ coef_ptr) {
+    clip_scale_body<DT, TILE>(tab.d, n, total_tiles, coef_ptr);
+}
+
 static_assert((kNormSmallTile * 2 / 16) % (64 * ELY_CLIP_UNROLL) == 0,
               "a full clip tile is whole unrolled rounds of 16-byte vectors");
 
@@ -388,6 +419,7 @@ static int64_t norm_tiles(const ely_tensor* grads, int32_t n, int64_t tile) {
 static size_t norm_table_bytes(int32_t n) { return align_up((size_t)n * sizeof(NormDesc), 256); }
 
 typedef void (*NormKernel)(const NormDesc*, int32_t, int64_t, double*);
+typedef void (*NormArgsKernel)(const NormArgTable, int32_t, int64_t, double*);
 
 template <int64_t TILE>
 static NormKernel pick_norm(bool fold, int dt) {
@@ -396,6 +428,17 @@ static NormKernel pick_norm(bool fold, int dt) {
                               : dt == ELY_F32 ? norm_partials_kernel<true, ELY_F32, TILE> : norm_partials_kernel<true, -1, TILE>;
     return dt == ELY_BF16 ? norm_partials_kernel<false, ELY_BF16, TILE>
                           : dt == ELY_F32 ? norm_partials_kernel<false, ELY_F32, TILE> : norm_partials_kernel<false, -1, TILE>;
+}
+
+template <int64_t TILE>
+static NormArgsKernel pick_norm_args(bool fold, int dt) {
+    if (fold)
+        return dt == ELY_BF16 ? norm_partials_args_kernel<true, ELY_BF16, TILE>
+                              : dt == ELY_F32 ? norm_partials_args_kernel<true, ELY_F32, TILE>
+                                              : norm_partials_args_kernel<true, -1, TILE>;
+    return dt == ELY_BF16 ? norm_partials_args_kernel<false, ELY_BF16, TILE>
+                          : dt == ELY_F32 ? norm_partials_args_kernel<false, ELY_F32, TILE>
+                                          : norm_partials_args_kernel<false, -1, TILE>;
 }
 
 // ------------------------------------------------------------- (b) AdamW
@@ -703,7 +746,8 @@ namespace ely {
 
 // What a norm call left in the workspace for a clip scale to reuse.
 struct NormLaunch {
-    const NormDesc* dtable = nullptr;
+    const NormDesc* dtable = nullptr;  // the uploaded table, or null when the call's descriptors went by argument
+    NormArgTable args;                 // the descriptors themselves for a short list
     int32_t entries = 0;
     int64_t tiles = 0, tile = 0;
     int dt = -1;
@@ -740,22 +784,31 @@ static NormLaunch grad_norm_impl(const ely_tensor* accs, const ely_tensor* grads
     NormDesc* dtable = reinterpret_cast<NormDesc*>(ws);
     double* partials = reinterpret_cast<double*>(ws + norm_table_bytes(n));
     NormLaunch out;
-    out.dtable = dtable;
     out.entries = (int32_t)table.size();
     out.tiles = tiles;
     out.tile = tile;
     if (tiles > 0) {
-        upload(dtable, table.data(), table.size() * sizeof(NormDesc), s);
         const int64_t waves = std::min<int64_t>(tiles, mt_blocks(ELY_NORM_BPC) * (kBlock / kWave));
         const int64_t blocks = (waves + 3) / 4;
         int dt = table[0].dtype;
         for (const NormDesc& d : table)
             if (d.dtype != dt) dt = -1;
         out.dt = dt;
-        const NormKernel kern = tile == kNormTile ? pick_norm<kNormTile>(accs != nullptr, dt)
-                                                  : pick_norm<kNormSmallTile>(accs != nullptr, dt);
-        hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(kBlock), 0, s, dtable, (int32_t)table.size(), tiles,
-                           partials);
+        if (table.size() <= (size_t)kNormArgTensors) {
+            memset(&out.args, 0, sizeof out.args);
+            memcpy(out.args.d, table.data(), table.size() * sizeof(NormDesc));
+            const NormArgsKernel kern = tile == kNormTile ? pick_norm_args<kNormTile>(accs != nullptr, dt)
+                                                          : pick_norm_args<kNormSmallTile>(accs != nullptr, dt);
+            hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(kBlock), 0, s, out.args, (int32_t)table.size(), tiles,
+                               partials);
+        } else {
+            upload(dtable, table.data(), table.size() * sizeof(NormDesc), s);
+            out.dtable = dtable;
+            const NormKernel kern = tile == kNormTile ? pick_norm<kNormTile>(accs != nullptr, dt)
+                                                      : pick_norm<kNormSmallTile>(accs != nullptr, dt);
+            hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(kBlock), 0, s, (const NormDesc*)dtable,
+                               (int32_t)table.size(), tiles, partials);
+        }
         check_launch("norm_partials_kernel");
     }
     hipLaunchKernelGGL(norm_final_kernel, dim3(1), dim3(kFinalThreads), 0, s, partials, tiles, max_norm,
@@ -765,6 +818,7 @@ static NormLaunch grad_norm_impl(const ely_tensor* accs, const ely_tensor* grads
 }
 
 typedef void (*ClipKernel)(const NormDesc*, int32_t, int64_t, const float*);
+typedef void (*ClipArgsKernel)(const NormArgTable, int32_t, int64_t, const float*);
 
 template <int64_t TILE>
 static ClipKernel pick_clip(int dt) {
@@ -772,16 +826,27 @@ static ClipKernel pick_clip(int dt) {
                           : dt == ELY_F32 ? clip_scale_kernel<ELY_F32, TILE> : clip_scale_kernel<-1, TILE>;
 }
 
+template <int64_t TILE>
+static ClipArgsKernel pick_clip_args(int dt) {
+    return dt == ELY_BF16 ? clip_scale_args_kernel<ELY_BF16, TILE>
+                          : dt == ELY_F32 ? clip_scale_args_kernel<ELY_F32, TILE> : clip_scale_args_kernel<-1, TILE>;
+}
+
 // Scale every gradient of a finished norm call by its clip coefficient, from
-// the tile table that call uploaded (same stream, so the table and the
-// coefficient are in place when this runs).
+// that call's tile table (uploaded to the workspace, or its descriptors by
+// argument again; same stream, so the coefficient is in place when this runs).
 static void clip_scale(const NormLaunch& nl, ely_norm_result* out_dev, void* stream) {
     if (nl.tiles == 0) return;
     const int64_t waves = std::min<int64_t>(nl.tiles, mt_blocks(ELY_CLIP_BPC) * (kBlock / kWave));
     const int64_t blocks = (waves + 3) / 4;
-    const ClipKernel k = nl.tile == kNormTile ? pick_clip<kNormTile>(nl.dt) : pick_clip<kNormSmallTile>(nl.dt);
-    hipLaunchKernelGGL(k, dim3((unsigned)blocks), dim3(kBlock), 0, static_cast<hipStream_t>(stream), nl.dtable,
-                       nl.entries, nl.tiles, &out_dev->coef);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (nl.dtable) {
+        const ClipKernel k = nl.tile == kNormTile ? pick_clip<kNormTile>(nl.dt) : pick_clip<kNormSmallTile>(nl.dt);
+        hipLaunchKernelGGL(k, dim3((unsigned)blocks), dim3(kBlock), 0, s, nl.dtable, nl.entries, nl.tiles, &out_dev->coef);
+    } else {
+        const ClipArgsKernel k = nl.tile == kNormTile ? pick_clip_args<kNormTile>(nl.dt) : pick_clip_args<kNormSmallTile>(nl.dt);
+        hipLaunchKernelGGL(k, dim3((unsigned)blocks), dim3(kBlock), 0, s, nl.args, nl.entries, nl.tiles, &out_dev->coef);
+    }
     check_launch("clip_scale_kernel");
 }
 

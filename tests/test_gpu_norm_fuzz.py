@@ -76,3 +76,45 @@ def test_norm_and_clip_match_the_oracle(oracle, specs, max_norm, seed):
             assert np.array_equal(bits(g), want)
         else:
             assert np.array_equal(bits(g).view(np.uint32), (h * np.float32(coef)).astype(np.float32).view(np.uint32))
+
+
+@pytest.mark.parametrize("n_t", [48, 49])
+def test_argument_table_limit(oracle, n_t):
+    """A norm call of up to 48 gradients carries its descriptors in the
+    kernel arguments, a longer one uploads a table; either side of the limit
+    the sum of squares is within 1e-6 of the oracle's, the one-call clip
+    (which reuses the call's descriptors) scales every gradient exactly,
+    and a capped grid gives the same bits."""
+    from elysium_wan_amd import _lib
+
+    L = _lib.load()
+    rng = np.random.default_rng(500 + n_t)
+    gs, host = [], []
+    for j in range(n_t):
+        n = int(rng.integers(1, 20000))
+        x = (rng.standard_normal(n) * 1e-2).astype(np.float32)
+        if j % 3 == 0:
+            h = oracle.f32_to_bf16_bits(x)
+            g = torch.from_numpy(h.view(np.int16).copy()).view(torch.bfloat16).cuda()
+        else:
+            h = x
+            g = torch.from_numpy(x.copy()).cuda()
+        gs.append(g)
+        host.append(h)
+    say("norm argument table limit", n_t)
+    exact = oracle.sumsq(host)
+    s0, norm, coef = _run(L, _lib, gs, 0.5, clip=False)
+    assert abs(s0 - exact) <= 1e-6 * exact
+    L.ely_set_max_blocks(5)
+    try:
+        s1, _, _ = _run(L, _lib, gs, 0.5, clip=False)
+    finally:
+        L.ely_set_max_blocks(0)
+    assert np.float64(s1).view(np.uint64) == np.float64(s0).view(np.uint64)
+    s2, _, c2 = _run(L, _lib, gs, 0.5, clip=True)
+    assert np.float64(s2).view(np.uint64) == np.float64(s0).view(np.uint64) and c2 == coef < 1.0
+    for g, h in zip(gs, host):
+        if g.dtype == torch.bfloat16:
+            assert np.array_equal(bits(g), oracle.f32_to_bf16_bits(oracle.bf16_bits_to_f32(h) * np.float32(coef)))
+        else:
+            assert np.array_equal(bits(g).view(np.uint32), (h * np.float32(coef)).astype(np.float32).view(np.uint32))
