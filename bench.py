@@ -242,7 +242,10 @@ def bench_configs(device, stream, names=("c0", "c2", "c3"), steps=3, warmup=1):
         params, grads = config_shard(name, device)
         log(f"{name} shard: {len(params)} tensors, {sum(p.numel() for p in params)} elements")
         gbytes = grads[0].element_size()
-        o = measure_shard(params, grads, device, stream, steps, warmup)
+        # C0's steps take ~0.2 ms: time 50 of them, so the window's start and
+        # sync do not weigh on the figure; the large shards take `steps`
+        k, w = (max(steps, 50), max(warmup, 5)) if name == "c0" else (steps, warmup)
+        o = measure_shard(params, grads, device, stream, k, w)
         out[name] = _shard_rates(o, gbytes, len(params))
         del params, grads
         torch.cuda.empty_cache()
