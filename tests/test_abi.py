@@ -270,3 +270,20 @@ def test_header_is_c_and_links_from_c(tmp_path):
     version, rc, ws_ok, neg_ok, msg = r.stdout.split(" ", 4)
     assert (int(version), int(rc), int(ws_ok), int(neg_ok)) == (1, _lib.EINVAL, 1, 1)
     assert "negative n" in msg
+
+
+def test_adamw_refuses_more_tiles_than_its_descriptors_hold(lib):
+    """A call whose tensors add up to more than 2^31 - 1 tiles of 4,096
+    elements (the descriptors keep the first tile of each tensor in 32 bits)
+    is refused before anything is launched: the pointers below are never
+    dereferenced."""
+    from elysium_wan_amd import _lib
+
+    fake = 1 << 20
+    n = 4096 * (1 << 30)  # 2^30 tiles each: the second tensor crosses the limit
+    t = _lib.tensor_array([_lib.ElyTensor(fake, n, _lib.F32, 0)] * 2)
+    g = _lib.tensor_array([_lib.ElyTensor(fake, n, _lib.BF16, 0)] * 2)
+    c = (_lib.ElyConsts * 2)()
+    ws = lib.ely_adamw_workspace_bytes(2)
+    st = lib.ely_adamw_step(t, g, t, t, None, 2, c, _lib.ORDER_HOST, 0, None, fake, ws, None)
+    assert st == _lib.EINVAL and b"tiles" in lib.ely_last_error()
