@@ -79,6 +79,42 @@ def test_norm_and_clip_match_the_oracle(oracle, specs, max_norm, seed):
 
 
 @pytest.mark.parametrize("n_t", [48, 49])
+def test_fold_norm_either_side_of_the_argument_table_limit(oracle, n_t):
+    """ely_grad_norm_fold (the sum of squares of acc + widen(g)) with 48
+    descriptors by argument and 49 from the uploaded table: within 1e-6 of
+    the oracle's fold then sum."""
+    from elysium_wan_amd import _lib
+
+    L = _lib.load()
+    rng = np.random.default_rng(700 + n_t)
+    accs, gs, folded = [], [], []
+    for j in range(n_t):
+        n = int(rng.integers(1, 20000))
+        a = (rng.standard_normal(n) * 1e-2).astype(np.float32)
+        x = (rng.standard_normal(n) * 1e-2).astype(np.float32)
+        if j % 2:
+            h = oracle.f32_to_bf16_bits(x)
+            g = torch.from_numpy(h.view(np.int16).copy()).view(torch.bfloat16).cuda()
+        else:
+            h = x
+            g = torch.from_numpy(x.copy()).cuda()
+        f = a.copy()
+        oracle.fold_add(f, h)
+        accs.append(torch.from_numpy(a).cuda())
+        gs.append(g)
+        folded.append(f)
+    say("fold norm argument table limit", n_t)
+    res = torch.zeros(16, dtype=torch.uint8, device="cuda")
+    garr, aarr = _lib.tensor_array(gs), _lib.tensor_array(accs)
+    ws = torch.empty(L.ely_grad_norm_workspace_bytes(garr, n_t), dtype=torch.uint8, device="cuda")
+    _lib.check(L.ely_grad_norm_fold(aarr, garr, n_t, 1.0, res.data_ptr(), ws.data_ptr(), ws.numel(),
+                                    _lib.stream_ptr(torch.device("cuda", 0))), "norm fold")
+    got = float(res[0:8].view(torch.float64).item())
+    want = oracle.sumsq(folded)
+    assert abs(got - want) <= 1e-6 * want
+
+
+@pytest.mark.parametrize("n_t", [48, 49])
 def test_argument_table_limit(oracle, n_t):
     """A norm call of up to 48 gradients carries its descriptors in the
     kernel arguments, a longer one uploads a table; either side of the limit
