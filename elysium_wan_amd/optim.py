@@ -460,24 +460,30 @@ class FusedAdamW:
         sts = [self._slot(i, p) for i, p in zip(idx, ps)]
         ms = [st["exp_avg"] for st in sts]
         vs = [st["exp_avg_sq"] for st in sts]
-        host = [j for j, m in enumerate(ms) if m.device.type != "cuda"]
+        host = [j for j, m in enumerate(ms) if not m.is_cuda]
         if host:
             self._check_host_moments([idx[j] for j in host], [ms[j] for j in host], [vs[j] for j in host])
         # the step counters are views of one flat tensor: one increment for all
-        it = torch.tensor(idx, dtype=torch.int64)
-        self._steps[it] += 1
-        ts = self._steps[it].tolist()
-        cs = [self.working_copies[i] if self.working_copies is not None else None for i in idx]
+        if len(idx) == len(self.params):
+            self._steps[: len(idx)] += 1
+            ts = self._steps[: len(idx)].tolist()
+        else:
+            it = torch.tensor(idx, dtype=torch.int64)
+            self._steps[it] += 1
+            ts = self._steps[it].tolist()
+        cs = [self.working_copies[i] for i in idx] if self.working_copies is not None else [None] * len(idx)
         lr, betas, eps, wd = self._hyper()
         per_t = {t: self._consts(t, lr, betas, eps, wd) for t in set(ts)}
-        consts = [per_t[t] for t in ts]
+        consts = [per_t[t] for t in ts]  # tensors at one step share one list object
         dev = ps[0].device
         groups = [list(range(len(idx)))] if on_param is None else self._release_groups(ps)
+        # the gradients' table, built once for the norm and a launch over all of them
+        garr = _lib.tensor_array(gs)
         with torch.cuda.device(dev):
             # the norm covers every gradient of the step, before any group updates
-            coef_ptr = self._clip_coef(gs, accs) if self.max_norm is not None else None
+            coef_ptr = self._clip_coef(gs, accs, garr) if self.max_norm is not None else None
             for grp in groups:
-                self._issue(grp, idx, ps, gs, ms, vs, cs, consts, coef_ptr, accs, wd != 0)
+                self._issue(grp, idx, ps, gs, ms, vs, cs, consts, coef_ptr, accs, wd != 0, garr)
                 if on_param is not None:
                     for j in grp:
                         on_param(idx[j])
@@ -509,17 +515,19 @@ class FusedAdamW:
             groups.append(cur)
         return groups
 
-    def _issue(self, grp, idx, ps, gs, ms, vs, cs, consts, coef_ptr, accs, wd: bool) -> None:
+    def _issue(self, grp, idx, ps, gs, ms, vs, cs, consts, coef_ptr, accs, wd: bool, garr=None) -> None:
         """The update of the stepped parameters at positions `grp`: one launch
         per gradient dtype for HBM moments (torch groups by dtype the same
         way), then the host moments' update (in place through the mapping,
-        or staged)."""
-        direct = [j for j in grp if ms[j].device.type == "cuda"]
-        streamed = [j for j in grp if ms[j].device.type != "cuda"]
+        or staged).  garr: the table of all the step's gradients, reused by
+        a launch that covers them all."""
+        direct = [j for j in grp if ms[j].is_cuda]
+        streamed = [j for j in grp if not ms[j].is_cuda]
         for gdt in (torch.bfloat16, torch.float32):
             sel = [j for j in direct if gs[j].dtype == gdt]
             if sel:
-                self._launch_cached(sel, idx, ps, gs, ms, vs, cs, consts, coef_ptr, accs, wd)
+                whole = garr if len(sel) == len(gs) else None
+                self._launch_cached(sel, idx, ps, gs, ms, vs, cs, consts, coef_ptr, accs, wd, whole)
         if streamed:
             sub = lambda xs: [xs[j] for j in streamed]  # noqa: E731
             if self._mapped is not None:
@@ -535,28 +543,31 @@ class FusedAdamW:
         """The reference's refusals (runtime/optim.py:98-99, 177-178) plus the
         GPU-side contract, one pass over the stepped parameters."""
         f32, gdts = torch.float32, self._GRAD_DTYPES
+        # devices compared by index (get_device(): -1 off the GPU), the
+        # cheapest of torch's device queries in this per-tensor loop
+        want = -2 if self.device is None else (self.device.index if self.device.type == "cuda" else -1)
         for k, (i, p, g) in enumerate(zip(idx, ps, gs)):
-            pd = p.device
             if p.dtype != f32:
                 raise ValueError(f"{self.recipe} trains fp32 parameters, got {p.dtype}")
             if not p.is_contiguous():
                 raise ValueError(f"{self.recipe} steps contiguous parameters only")
-            if g.shape != p.shape or not g.is_contiguous() or g.device != pd:
+            pdi = p.get_device()
+            if g.get_device() != pdi or g.shape != p.shape or not g.is_contiguous():
                 raise ValueError(f"{self.recipe}: the gradient of parameter {i} must be contiguous, shaped like it, on its device")
             if g.dtype not in gdts:
                 raise ValueError(f"{self.recipe}: gradients are float32 or bfloat16, got {g.dtype}")
-            if pd.type != "cuda":
+            if pdi < 0:
                 _lib.require_gpu(p, self.recipe)
-            if self.device is None:
-                self.device = pd
-            elif pd != self.device:
-                raise ValueError(f"{self.recipe}: parameter {i} is on {pd}, the optimizer's moments on {self.device}")
+            if want == -2:
+                self.device, want = p.device, pdi
+            elif pdi != want:
+                raise ValueError(f"{self.recipe}: parameter {i} is on {p.device}, the optimizer's moments on {self.device}")
             if accs is not None:
                 a = accs[k]
-                if a is None or a.dtype != f32 or a.shape != p.shape or not a.is_contiguous() or a.device != pd:
+                if a is None or a.dtype != f32 or a.shape != p.shape or not a.is_contiguous() or a.get_device() != pdi:
                     raise ValueError(f"{self.recipe}: the fold accumulator of parameter {i} must be a contiguous float32 tensor shaped like it, on its device")
 
-    def _launch_cached(self, sel, idx, ps, gs, ms, vs, cs, consts, coef_ptr, accs, wd: bool) -> None:
+    def _launch_cached(self, sel, idx, ps, gs, ms, vs, cs, consts, coef_ptr, accs, wd: bool, garr=None) -> None:
         """_launch over the stepped parameters at positions `sel`, with the
         descriptor arrays of the parameters, moments and working copies kept
         from the last launch of the same parameters while every one of their
@@ -580,8 +591,8 @@ class FusedAdamW:
                 "v": _lib.tensor_array([vs[j] for j in sel]),
                 "c": _lib.tensor_array(copies),
             }
-        self._launch_arrays(len(sel), t["p"], _lib.tensor_array([gs[j] for j in sel]), t["m"], t["v"], t["c"],
-                            [consts[j] for j in sel], coef_ptr,
+        self._launch_arrays(len(sel), t["p"], garr if garr is not None else _lib.tensor_array([gs[j] for j in sel]),
+                            t["m"], t["v"], t["c"], [consts[j] for j in sel], coef_ptr,
                             None if accs is None else _lib.tensor_array([accs[j] for j in sel]), ps[sel[0]].device, wd)
 
     def _check_host_moments(self, idx, ms, vs) -> None:
@@ -734,15 +745,16 @@ class FusedAdamW:
             torch.cuda.synchronize()
         return moved
 
-    def _clip_coef(self, grads, accs=None) -> int:
+    def _clip_coef(self, grads, accs=None, garr=None) -> int:
         """Launch the deterministic norm of every gradient of the step (any
         dtype; with accs, of the folded sums); returns the device address of
-        its fp32 clip coefficient."""
+        its fp32 clip coefficient.  garr: the gradients' table, if built."""
         L = _lib.load()
         dev = grads[0].device
         if self._norm is None or self._norm.device != dev:
             self._norm = torch.empty(16, dtype=torch.uint8, device=dev)
-        garr = _lib.tensor_array(grads)
+        if garr is None:
+            garr = _lib.tensor_array(grads)
         ws = _lib.workspace(dev, L.ely_grad_norm_workspace_bytes(garr, len(grads)))
         if accs is None:
             rc = L.ely_grad_norm(garr, len(grads), self.max_norm, self._norm.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_ptr(dev))
@@ -760,10 +772,15 @@ class FusedAdamW:
     def _launch_arrays(self, n, parr, garr, marr, varr, carr, consts, coef_ptr, aarr, dev, wd: bool) -> None:
         L = _lib.load()
         stream = _lib.stream_ptr(dev)
-        ctab = np.asarray(consts, dtype=np.float32).reshape(n, -1)
-        if ctab.shape[1] < 8:
-            ctab = np.pad(ctab, ((0, 0), (0, 8 - ctab.shape[1])))
-        ctab = np.ascontiguousarray(ctab)
+        if all(c is consts[0] for c in consts):
+            # every tensor at one step: one row, repeated
+            ctab = np.zeros((n, 8), dtype=np.float32)
+            ctab[:, : len(consts[0])] = np.asarray(consts[0], dtype=np.float32)
+        else:
+            ctab = np.asarray(consts, dtype=np.float32).reshape(n, -1)
+            if ctab.shape[1] < 8:
+                ctab = np.pad(ctab, ((0, 0), (0, 8 - ctab.shape[1])))
+            ctab = np.ascontiguousarray(ctab)
         carr_c = (_lib.ElyConsts * n).from_buffer(ctab)
         ws = _lib.workspace(dev, L.ely_adamw_workspace_bytes(n))
         order = _lib.ORDER_HOST if self.order == "host" else _lib.ORDER_TORCH
