@@ -62,7 +62,7 @@ def build(optimizer: str, params: Iterable[torch.Tensor], lr: float, **kw):
     if optimizer == "adamw-host":
         # the reference's memory contract (8 device bytes per element): moments
         # in host memory, streamed through the GPU; moments="device" keeps them in HBM
-        return FusedAdamW(params, lr=lr, order="host", **{**ADAMW, "moments": "host", **kw})
+        return HostAdamW(params, lr=lr, **{**ADAMW, **kw})
     raise ValueError(f"optimizer {optimizer!r} is not one of {OPTIMIZERS}")
 
 
@@ -882,6 +882,35 @@ class FusedAdamW:
             self._steps.zero_()
         for i, st in sorted(states.items()):
             self._assign(i, st)
+
+
+class HostAdamW(FusedAdamW):
+    """The "adamw-host" recipe under the reference's class name
+    (runtime/optim.py:77-298) and with its constructor's arguments:
+    HostAdamW's op order, moments in pinned host memory.  The reference's
+    runtime tests isinstance(opt, optim.HostAdamW) before promoting moments
+    (runtime/stage.py:3134); build("adamw-host") returns this class, so that
+    test holds for this build's optimizer.  FusedAdamW's other options
+    (max_norm, working_copy, release_elems, moments="device") pass by
+    keyword.  pipeline=None updates the moments in place through the GPU's
+    mapping (this build's default); True and False are the reference's
+    staged and serial copies."""
+
+    def __init__(
+        self,
+        params: Iterable[torch.Tensor],
+        lr: float,
+        betas: tuple = (0.9, 0.999),
+        eps: float = 1e-8,
+        weight_decay: float = 0.0,
+        chunk: int = CHUNK,
+        pipeline: bool | None = None,
+        slots: int = 3,
+        **kw,
+    ):
+        kw.setdefault("moments", "host")
+        super().__init__(params, lr, betas, eps, weight_decay, order="host", chunk=chunk, pipeline=pipeline,
+                         slots=slots, **kw)
 
 
 def clip_grad_norm_(parameters, max_norm: float, norm_type: float = 2.0, error_if_nonfinite: bool = False, foreach=None) -> torch.Tensor:

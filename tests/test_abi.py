@@ -186,6 +186,10 @@ def test_recipes_refuse_what_the_reference_refuses():
             optim.build("adamw", params, **kw)
         assert str(got.value) == str(want.value)
     host = optim.build("adamw-host", [], 1e-3)
+    # the reference's runtime gates promote() on isinstance(opt, optim.HostAdamW) (runtime/stage.py:3134)
+    assert isinstance(host, optim.HostAdamW) and host.moments == "host" and host.order == "host"
+    assert not isinstance(optim.build("adamw", [torch.zeros(1)], 1e-3), optim.HostAdamW)  # a frozen tensor: no GPU needed
+    assert optim.HostAdamW([], 1e-3, moments="device").moments == "device"
     host.step()
     sd = host.state_dict()
     assert sd["state"] == {} and sd["param_groups"][0]["params"] == [] and sd["param_groups"][0]["moments"] == "host"
