@@ -1024,6 +1024,101 @@ def _runs(disp, names):
     return [r for r in runs if r[0] is not None]
 
 
+def c4_summary(trace_dir: str, bench_out: str | None) -> None:
+    """Kernel durations of a rocprofv3 --kernel-trace run of `bench.py
+    --no-optimizer --codec c4`: per scaling (per-row, per-tensor) and
+    operation, summed over both inputs and formats.  A call is told apart by
+    bench_codec's launch order: per format, quantize launches, dequantize
+    launches, then as many round trips as dequantizes (quantize and round
+    trip are one kernel), then the stats pass's one quantize and one
+    dequantize; a per-tensor quantize or round trip is its two
+    row-max kernels plus quant_split_kernel, added up.  Writes
+    profiles/codec_c4_kernel_trace.md."""
+    disp = _dispatches(trace_dir)
+    quant = ("quant_block_row_kernel", "quant_rows_kernel", "quant_split_kernel")
+    pre = ("rowmax_partial_kernel", "rowmax_reduce_kernel")
+    calls = {}  # (scaling, op) -> [total ns per call]
+    parts = {}  # kernel -> [ns] of the per-tensor quantize / round trip
+    pending = 0  # ns of row-max kernels waiting for their quant_split_kernel
+    pend_parts = []
+    rt_left = 0
+    deq_run = 0
+    scaling = None
+    for name, ns in disp:
+        if name in pre:
+            pending += ns
+            pend_parts.append((name, ns))
+            continue
+        if name.startswith("dequant"):
+            deq_run += 1
+            calls.setdefault((scaling or "per-row", "dequantize"), []).append(ns)
+            continue
+        if name in quant:
+            if deq_run:
+                # a timed run of dequantizes is followed by as many round trips;
+                # the stats pass's lone dequantize by none
+                rt_left, deq_run = (deq_run if deq_run > 1 else 0), 0
+            scaling = "per-tensor" if name == "quant_split_kernel" else "per-row"
+            op = "round trip" if rt_left > 0 else "quantize"
+            rt_left = max(0, rt_left - 1)
+            calls.setdefault((scaling, op), []).append(ns + pending)
+            if scaling == "per-tensor":
+                for k, v in pend_parts + [(name, ns)]:
+                    parts.setdefault((op, k), []).append(v)
+            pending, pend_parts = 0, []
+    n = 16 * 4096 * 8192
+    per = {"quantize": 3, "dequantize": 3, "round trip": 4}
+    actual = {("per-tensor", "quantize"): 5, ("per-tensor", "round trip"): 6}
+    lines = [
+        "# Kernel durations, fp8 codec on C4's tensors",
+        "",
+        "Commands (on one MI355X, from the repository root):",
+        "",
+        "    rocprofv3 --kernel-trace --stats -T -d <dir> -o c4 --output-format csv -- python3 bench.py --no-optimizer --codec c4 > <run's stdout>",
+        "    python bench.py --c4-summary <dir> --bench-json <run's stdout>",
+        "",
+        f"Workload: config C4's bf16 activation and gradient [16, 4096, 8192] ({n:,} elements,",
+        "1.07 GB each; Student-t(3) with 0.01 % +-1e4 outliers, and N(0, 1e-5)), e4m3 and",
+        "e5m2, per-row (8,192-wide rows) and per-tensor scaling, two copies of each",
+        "input rotating.  Algorithmic bytes per element: 3 for quantize and",
+        "dequantize, 4 for the fused round trip; per-tensor quantize reads x twice",
+        "(its |x|max, then the codes), 5 B/element of actual traffic (6 for the",
+        "round trip).  Times summed over both inputs and formats; a per-tensor",
+        "call is its three kernels added up.",
+        "",
+        "| scaling | operation | calls | average (µs) | algorithmic rate | fraction of 8 TB/s | actual-traffic rate |",
+        "|---|---|---|---|---|---|---|",
+    ]
+    for sc in ("per-row", "per-tensor"):
+        for op in ("quantize", "dequantize", "round trip"):
+            ds = calls.get((sc, op))
+            if not ds:
+                continue
+            avg = sum(ds) / len(ds)
+            rate = n * per[op] / avg / 1e3
+            act = actual.get((sc, op))
+            lines.append(f"| {sc} | {op} | {len(ds)} | {avg / 1e3:,.1f} | {rate:.2f} TB/s | {rate / 8:.2f} | "
+                         + (f"{n * act / avg / 1e3:.2f} TB/s |" if act else "— |"))
+    if parts:
+        lines += ["", "Per-tensor calls by kernel (average µs):", "", "| operation | kernel | calls | average (µs) |", "|---|---|---|---|"]
+        for (op, k), ds in sorted(parts.items()):
+            lines.append(f"| {op} | {k} | {len(ds)} | {sum(ds) / len(ds) / 1e3:,.1f} |")
+    b = None
+    if bench_out:
+        with open(bench_out) as f:
+            rows = [ln for ln in f.read().splitlines() if ln.startswith('{"c4"')]
+        b = json.loads(rows[-1])["c4"] if rows else None
+    if b:
+        lines += ["", "bench.py's HIP-event figures in the traced process (activation, e4m3):"]
+        for sc, key in (("per-row", "per_row"), ("per-tensor", "per_tensor")):
+            e = b["activation"][key]["e4m3"]
+            lines.append(f"{sc}: quantize {e['quantize_GBs'] / 1e3:.2f} TB/s, dequantize {e['dequantize_GBs'] / 1e3:.2f} TB/s, "
+                         f"round trip {e['roundtrip_GBs'] / 1e3:.2f} TB/s.")
+    with open(os.path.join(HERE, "profiles", "codec_c4_kernel_trace.md"), "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
 def copy_summary(trace_dir: str) -> None:
     """Copy and kernel durations of a rocprofv3 --kernel-trace
     --memory-copy-trace run of `bench.py --leg host_moments`: the staged
@@ -1396,6 +1491,7 @@ def main():
     ap.add_argument("--no-configs", action="store_true", help="skip the C0/C2/C3 optimizer leg (--no-extra skips it too)")
     ap.add_argument("--leg", action="append", choices=LEG_NAMES,
                     help="run only these extra legs (repeatable), no headline, and print their JSON (for profiling one leg)")
+    ap.add_argument("--c4-summary", metavar="DIR", help="summarize a rocprofv3 --kernel-trace run of --no-optimizer --codec c4 into profiles/")
     ap.add_argument("--copy-summary", metavar="DIR", help="summarize a rocprofv3 --memory-copy-trace run of --leg host_moments into profiles/")
     ap.add_argument("--placement-probe", choices=("fresh", "hold150"), help="three C1 steps only (for rocprofv3 --pmc)")
     ap.add_argument("--cpu-sample", type=int, default=256 * 1024 * 1024)
@@ -1424,6 +1520,9 @@ def main():
         return
     if args.copy_summary:
         copy_summary(args.copy_summary)
+        return
+    if args.c4_summary:
+        c4_summary(args.c4_summary, (args.bench_json or [None])[0])
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); run with --gpus 1", file=sys.stderr)
