@@ -45,6 +45,7 @@ EXPORTS = (
     "ely_fp8_quantize_k",
     "ely_cast_bf16",
     "ely_fold_add",
+    "ely_fold_add_bf16",
     "ely_scale_inplace",
     "ely_rows_fold",
     "ely_set_max_blocks",
@@ -115,6 +116,7 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
         L.ely_fp8_quantize_k.argtypes = [P, I32, I64, I64, I32, P, P, P]
         L.ely_cast_bf16.argtypes = [P, P, I64, P]
         L.ely_fold_add.argtypes = [P, P, I32, I64, P]
+        L.ely_fold_add_bf16.argtypes = [P, P, I32, I64, P]
         L.ely_scale_inplace.argtypes = [TP, I32, P, P]
         L.ely_rows_fold.argtypes = [P, P, P, P, P, I64, I64, I64, I64, I32, I32, P]
         L.ely_set_max_blocks.argtypes = [I32]

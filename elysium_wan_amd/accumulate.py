@@ -12,7 +12,9 @@ there until it is released or replaced.
 
 Sums are fp32 on the GPU (the fp32 masters' gradients, with bf16 or fp32
 parts): the adds run through pieces.fold_add's kernel (acc + widen(g), one
-fp32 rounding).  int64 count lanes fold by torch's exact integer add, as
+fp32 rounding).  A bf16 sum (bf16 parts with no wider dtype asked for)
+folds through ely_fold_add_bf16, the fp32 add rounded to bf16 as torch's
+add_ does.  int64 count lanes fold by torch's exact integer add, as
 runtime/pieces.py:206-214 does.
 
 defer_last=True (an addition to the reference's interface): each tensor's
@@ -108,9 +110,21 @@ class OrderedAccumulator:
         return t.clone()
 
     def _add(self, i: int, t) -> None:
-        """acc[i] += t in place: fp32 sums on the GPU kernel, int64 count
-        lanes by integer add (pieces.fold_add refuses other sums)."""
-        pieces.fold_add(self.acc[i], t)
+        """acc[i] += t in place: fp32 sums through pieces.fold_add's kernel,
+        int64 count lanes by integer add, bf16 sums (a bf16 part folded with
+        no wider dtype asked for) through ely_fold_add_bf16: the fp32 add
+        rounded to bf16, as torch's add_ on a bf16 tensor."""
+        acc = self.acc[i]
+        if acc.dtype != torch.bfloat16:
+            pieces.fold_add(acc, t)
+            return
+        _lib.require_gpu(acc, "ordered fold")
+        t = t.detach().contiguous()
+        if not acc.is_contiguous() or t.numel() != acc.numel() or t.device != acc.device:
+            raise ValueError("ordered fold: part and bf16 sum differ in size or device, or the sum is not contiguous")
+        L = _lib.load()
+        _lib.check(L.ely_fold_add_bf16(acc.data_ptr(), t.data_ptr(), _lib.dtype_code(t), acc.numel(),
+                                       _lib.stream_ptr(acc.device)), "ordered fold")
 
     def _fold(self, i: int) -> None:
         last = len(self.order) - 1

@@ -1,7 +1,8 @@
 // elementwise.hip -- the stand-alone elementwise ops of the sharded "pieces"
 // update: the fp32 master -> bf16 working-copy cast (pieces.cast_piece,
 // runtime/pieces.py:192-195), the fp32 fold of a microbatch gradient
-// (pieces.fold_add, runtime/pieces.py:206-214) and the clip's in-place
+// (pieces.fold_add, runtime/pieces.py:206-214; into a bf16 sum for
+// OrderedAccumulator, runtime/accumulate.py:101-102) and the clip's in-place
 // scaling (clip_grad_norm_).  Each is one HBM pass over 4-element quads
 // (16-byte fp32, 8-byte bf16 vectors, nontemporal) on a persistent grid,
 // with a per-kernel number of quads in flight per thread.
@@ -135,6 +136,32 @@ __global__ __launch_bounds__(kEwBlock) void fold_add_kernel(float* __restrict__ 
     }
 }
 
+// OrderedAccumulator's fold into a bf16 sum (runtime/accumulate.py:101-102,
+// `acc.add_(t)` on a bf16 tensor): acc = bf16(float(acc) + widen(g)), the
+// fp32 add rounded once more to bf16, as torch's in-place add computes it.
+template <bool BF16G>
+__global__ __launch_bounds__(kEwBlock) void fold_add_bf16_kernel(uint16_t* __restrict__ acc, const void* __restrict__ g,
+                                                                 int64_t n, int vec) {
+    int64_t done = 0;
+    if (vec)
+        done = quad_loop<kFoldShape.unroll>(
+            n / 4,
+            [&](int64_t q) {
+                AccG r;
+                r.acc = widen4(ldh4(acc + 4 * q));
+                r.g = BF16G ? widen4(ldh4(static_cast<const uint16_t*>(g) + 4 * q)) : ld4(static_cast<const float*>(g) + 4 * q);
+                return r;
+            },
+            [&](int64_t q, AccG r) {
+                sth4(acc + 4 * q, narrow4(ef4{r.acc[0] + r.g[0], r.acc[1] + r.g[1], r.acc[2] + r.g[2], r.acc[3] + r.g[3]}));
+            });
+    const int64_t T = (int64_t)gridDim.x * kEwBlock;
+    for (int64_t i = done + (int64_t)blockIdx.x * kEwBlock + threadIdx.x; i < n; i += T) {
+        const float gv = BF16G ? bf16_to_f32(static_cast<const uint16_t*>(g)[i]) : static_cast<const float*>(g)[i];
+        acc[i] = (uint16_t)f32_to_bf16(bf16_to_f32(acc[i]) + gv);
+    }
+}
+
 // g <- g * coef (coef read from device memory), one fp32 multiply rounded to
 // g's dtype: torch's _foreach_mul_(grads, clip_coef) (clip_grad.py:170-177).
 template <bool BF16G>
@@ -207,6 +234,23 @@ int ely_fold_add(float* acc, const void* g, int32_t g_dtype, int64_t n, void* st
         else
             hipLaunchKernelGGL(fold_add_kernel<false>, dim3(ew_blocks(n, kFoldShape)), dim3(kEwBlock), 0, s, acc, g, n, vec);
         check_launch("fold_add_kernel");
+    });
+}
+
+int ely_fold_add_bf16(uint16_t* acc, const void* g, int32_t g_dtype, int64_t n, void* stream) {
+    return guarded([&] {
+        if (n < 0) fail(ELY_EINVAL, "ely_fold_add_bf16: negative n");
+        if (g_dtype != ELY_F32 && g_dtype != ELY_BF16) fail(ELY_EINVAL, "ely_fold_add_bf16: g_dtype");
+        if (n == 0) return;
+        if (!acc || !g) fail(ELY_EINVAL, "ely_fold_add_bf16: null pointer");
+        const int vec = (reinterpret_cast<uintptr_t>(acc) % 8 == 0) &&
+                        (reinterpret_cast<uintptr_t>(g) % (g_dtype == ELY_BF16 ? 8 : 16) == 0);
+        hipStream_t s = static_cast<hipStream_t>(stream);
+        if (g_dtype == ELY_BF16)
+            hipLaunchKernelGGL(fold_add_bf16_kernel<true>, dim3(ew_blocks(n, kFoldShape)), dim3(kEwBlock), 0, s, acc, g, n, vec);
+        else
+            hipLaunchKernelGGL(fold_add_bf16_kernel<false>, dim3(ew_blocks(n, kFoldShape)), dim3(kEwBlock), 0, s, acc, g, n, vec);
+        check_launch("fold_add_bf16_kernel");
     });
 }
 

@@ -207,6 +207,12 @@ int ely_cast_bf16(const float* x, uint16_t* out, int64_t n, void* stream);
  * rounding; g_dtype ELY_F32 or ELY_BF16. */
 int ely_fold_add(float* acc, const void* g, int32_t g_dtype, int64_t n, void* stream);
 
+/* OrderedAccumulator._fold into a bf16 sum (runtime/accumulate.py:101-102,
+ * `self.acc[i].add_(t)` when the running sum is bf16): acc = bf16(float(acc)
+ * + float(g)), the fp32 add rounded to bf16 (RNE, every NaN -> 0x7FC0), as
+ * torch's in-place add on a bf16 tensor; g_dtype ELY_F32 or ELY_BF16. */
+int ely_fold_add_bf16(uint16_t* acc, const void* g, int32_t g_dtype, int64_t n, void* stream);
+
 /* The row folds of TiedRowFold (runtime/accumulate.py:140-247), the step
  * gradient of a tied table split across stages: for each j < n_idx, with
  * r = idx[j] and ar = a_rows ? a_rows[j] : j,

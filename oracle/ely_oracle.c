@@ -27,6 +27,7 @@
  *   grad sum of squares  TORCH/nn/utils/clip_grad.py:91-108 (the norm the clip
  *                      uses), here in long double as a brute-force bound.
  *   fold_add           runtime/pieces.py:206-214
+ *   fold_add_bf16      runtime/accumulate.py:101-102 on a bf16 sum
  *
  * Build: gcc -O2 -ffp-contract=off -fno-fast-math (see oracle/Makefile).  No
  * FMA contraction: each C operation is one correctly rounded IEEE operation,
@@ -338,4 +339,11 @@ void orc_cast_bf16(const float* x, uint16_t* out, int64_t n) {
 /* pieces.fold_add (runtime/pieces.py:206-214): acc += float(g), one fp32 add. */
 void orc_fold_add(float* acc, const void* g, int gdtype, int64_t n) {
     for (int64_t i = 0; i < n; ++i) acc[i] = acc[i] + load_elem(g, gdtype, i);
+}
+
+/* OrderedAccumulator's fold into a bf16 sum (runtime/accumulate.py:101-102,
+ * `acc.add_(t)` on a bf16 tensor): torch computes the add in fp32 (its
+ * opmath type for bf16) and rounds the fp32 sum to bf16. */
+void orc_fold_add_bf16(uint16_t* acc, const void* g, int gdtype, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) acc[i] = orc_f32_to_bf16(orc_bf16_to_f32(acc[i]) + load_elem(g, gdtype, i));
 }

@@ -82,6 +82,7 @@ def lib():
         L.orc_clip_coef.argtypes = [F, F]
         L.orc_cast_bf16.argtypes = [P, P, I64]
         L.orc_fold_add.argtypes = [P, P, I32, I64]
+        L.orc_fold_add_bf16.argtypes = [P, P, I32, I64]
         _lib = L
     return _lib
 
@@ -323,6 +324,15 @@ def cast_bf16(x: np.ndarray) -> np.ndarray:
 def fold_add(acc: np.ndarray, g: np.ndarray) -> None:
     g = np.ascontiguousarray(g)
     lib().orc_fold_add(_ptr(acc), _ptr(g), _dt(g), acc.size)
+
+
+def fold_add_bf16(acc: np.ndarray, g: np.ndarray) -> None:
+    """runtime/accumulate.py:101-102 on a bf16 sum, in place on acc (bf16
+    bits as uint16): acc = bf16(float(acc) + float(g))."""
+    if acc.dtype != np.uint16 or not acc.flags.c_contiguous:
+        raise TypeError("a bf16 sum is contiguous bf16 bits (uint16)")
+    g = np.ascontiguousarray(g)
+    lib().orc_fold_add_bf16(_ptr(acc), _ptr(g), _dt(g), acc.size)
 
 
 # ----------------------------------------------------------- plane codecs

@@ -165,3 +165,68 @@ def test_ordered_fold_fuzz_equals_the_oracle(oracle, m, bf16, defer, quarantine,
         assert accs is None or m > 1
     for i, s in enumerate(acc.result()):
         assert np.array_equal(bits(s.float()).reshape(-1).view(np.uint32), _oracle_fold(oracle, parts, i).view(np.uint32))
+
+
+@settings(max_examples=30, deadline=None, derandomize=True, suppress_health_check=[HealthCheck.too_slow])
+@given(
+    n=st.sampled_from([1, 3, 4, 5, 1023, 1024, 4097, 100_003]),
+    bf16g=st.booleans(),
+    acc_off=st.integers(0, 3),
+    g_off=st.integers(0, 3),
+    seed=st.integers(0, 2**16),
+)
+def test_fold_into_a_bf16_sum_equals_the_oracle_and_torch(oracle, n, bf16g, acc_off, g_off, seed):
+    """ely_fold_add_bf16 (the ordered fold into a bf16 sum,
+    runtime/accumulate.py:101-102): bit for bit the oracle's fold and torch's
+    own add_ on the GPU, with the sum and the part at their own element
+    offsets (vector and scalar paths), NaN/Inf/-0 sprinkled in."""
+    from elysium_wan_amd import _lib
+
+    L = _lib.load()
+    rng = np.random.default_rng(seed)
+    acc = oracle.f32_to_bf16_bits((rng.standard_normal(n) * 10.0 ** rng.integers(-3, 3)).astype(np.float32))
+    x = (rng.standard_normal(n) * 1e-2).astype(np.float32)
+    x[rng.random(n) < 0.01] = np.inf
+    x[rng.random(n) < 0.01] = np.nan
+    x[rng.random(n) < 0.01] = -0.0
+    g = oracle.f32_to_bf16_bits(x) if bf16g else x
+    say("bf16-sum fold", n, bf16g, acc_off, g_off)
+    abuf = torch.zeros(n + acc_off, dtype=torch.bfloat16, device="cuda")
+    a = abuf[acc_off:]
+    a.copy_(torch.from_numpy(acc.view(np.int16).copy()).view(torch.bfloat16))
+    gdt = torch.bfloat16 if bf16g else torch.float32
+    gbuf = torch.zeros(n + g_off, dtype=gdt, device="cuda")
+    gt = gbuf[g_off:]
+    gt.copy_(torch.from_numpy(g.view(np.int16).copy()).view(torch.bfloat16) if bf16g else torch.from_numpy(g.copy()))
+    ref = a.clone()
+    ref.add_(gt)  # torch's own add on the GPU
+    _lib.check(L.ely_fold_add_bf16(a.data_ptr(), gt.data_ptr(), _lib.dtype_code(gt), n, _lib.stream_ptr(a.device)), "fold bf16")
+    want = acc.copy()
+    oracle.fold_add_bf16(want, g)
+    got = bits(a)
+    assert np.array_equal(got, want)
+    assert np.array_equal(got, bits(ref))
+
+
+def test_ordered_fold_of_bf16_parts_keeps_a_bf16_sum(oracle):
+    """bf16 parts folded with no wider dtype asked for (fold_part without
+    `dtype`, or add): the sum stays bf16, first part copied, then each later
+    part added in fp32 and rounded to bf16, as the reference's add_ on a bf16
+    tensor; out-of-order arrival changes no bit."""
+    from elysium_wan_amd import accumulate
+
+    M = 4
+    parts = _parts(77, M, torch.bfloat16)
+    acc = accumulate.OrderedAccumulator(range(M))
+    say("bf16-sum ordered fold")
+    for mb in (2, 0, 3, 1):
+        for i in reversed(range(len(SHAPES))):
+            acc.fold_part(mb, i, len(SHAPES), parts[mb][i].cuda())
+        acc.end_part(mb)
+    assert acc.complete()
+    for i, s in enumerate(acc.result()):
+        assert s.dtype == torch.bfloat16
+        want = bits(parts[0][i]).reshape(-1).copy()
+        for mb in range(1, M):
+            oracle.fold_add_bf16(want, bits(parts[mb][i]).reshape(-1))
+        assert np.array_equal(bits(s).reshape(-1), want), i

@@ -448,3 +448,38 @@ def test_nibble_packing_is_numpys_packbits(oracle):
         for plane, nib in ((hi, c >> 4), (lo, c & 0x0F)):
             ref = np.packbits(np.unpackbits(nib.reshape(-1, 1), axis=1, count=8)[:, 4:])
             assert np.array_equal(plane, ref)
+
+
+@pytest.mark.parametrize("gdt", ["bf16", "f32"])
+def test_fold_add_bf16_equals_torch_add_on_a_bf16_sum(oracle, gdt):
+    """OrderedAccumulator's fold into a bf16 sum is torch's in-place add on a
+    bf16 tensor (runtime/accumulate.py:101-102): bit for bit torch's CPU
+    add_, over random bf16 sums (every exponent, subnormals, +-0, +-Inf)
+    and bf16 or fp32 parts; NaN results compared as NaN (torch's AVX2 cast
+    writes another NaN pattern than c10's 0x7FC0, which the oracle and the
+    GPU use)."""
+    rng = np.random.default_rng(7 if gdt == "bf16" else 8)
+    n = 400_000
+    acc = rng.integers(0, 1 << 16, size=n, dtype=np.uint32).astype(np.uint16)
+    acc[:6] = [0x0000, 0x8000, 0x7F80, 0xFF80, 0x0001, 0x8001]
+    if gdt == "bf16":
+        g = rng.integers(0, 1 << 16, size=n, dtype=np.uint32).astype(np.uint16)
+        g[:6] = [0x8000, 0x0000, 0xFF80, 0x7F80, 0x8001, 0x0001]
+        g_t = torch.from_numpy(g.view(np.int16).copy()).view(torch.bfloat16)
+    else:
+        g = rng.integers(0, 1 << 32, size=n, dtype=np.uint64).astype(np.uint32).view(np.float32)
+        g_t = torch.from_numpy(g.copy())
+    acc_t = torch.from_numpy(acc.view(np.int16).copy()).view(torch.bfloat16)
+    acc_t.add_(g_t)
+    want = acc_t.view(torch.int16).numpy().view(np.uint16)
+    mine = acc.copy()
+    oracle.fold_add_bf16(mine, g)
+    nan = np.isnan(oracle.bf16_bits_to_f32(want))
+    assert np.array_equal(mine[~nan], want[~nan])
+    assert np.all(mine[nan] == 0x7FC0)
+    # a planted mistake: the add rounded straight from the two bf16 values
+    # in bf16 (no fp32 step) would differ from torch somewhere
+    if gdt == "f32":
+        with np.errstate(over="ignore", invalid="ignore"):
+            wrong = oracle.f32_to_bf16_bits(oracle.bf16_bits_to_f32(acc) + oracle.bf16_bits_to_f32(oracle.f32_to_bf16_bits(g)))
+        assert not np.array_equal(wrong[~nan], want[~nan])
