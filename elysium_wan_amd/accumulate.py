@@ -110,21 +110,11 @@ class OrderedAccumulator:
         return t.clone()
 
     def _add(self, i: int, t) -> None:
-        """acc[i] += t in place: fp32 sums through pieces.fold_add's kernel,
-        int64 count lanes by integer add, bf16 sums (a bf16 part folded with
-        no wider dtype asked for) through ely_fold_add_bf16: the fp32 add
-        rounded to bf16, as torch's add_ on a bf16 tensor."""
-        acc = self.acc[i]
-        if acc.dtype != torch.bfloat16:
-            pieces.fold_add(acc, t)
-            return
-        _lib.require_gpu(acc, "ordered fold")
-        t = t.detach().contiguous()
-        if not acc.is_contiguous() or t.numel() != acc.numel() or t.device != acc.device:
-            raise ValueError("ordered fold: part and bf16 sum differ in size or device, or the sum is not contiguous")
-        L = _lib.load()
-        _lib.check(L.ely_fold_add_bf16(acc.data_ptr(), t.data_ptr(), _lib.dtype_code(t), acc.numel(),
-                                       _lib.stream_ptr(acc.device)), "ordered fold")
+        """acc[i] += t in place through pieces.fold_add: fp32 sums on its
+        kernel, int64 count lanes by integer add, bf16 sums (a bf16 part
+        folded with no wider dtype asked for) as the fp32 add rounded to
+        bf16, torch's add_ on a bf16 tensor."""
+        pieces.fold_add(self.acc[i], t)
 
     def _fold(self, i: int) -> None:
         last = len(self.order) - 1

@@ -47,20 +47,24 @@ def fold_start(g: torch.Tensor) -> torch.Tensor:
 
 
 def fold_add(acc: torch.Tensor, g: torch.Tensor) -> None:
-    """runtime/pieces.py:206-214: acc += widen(g), one fp32 rounding per element."""
+    """runtime/pieces.py:206-214: acc += widen(g), one fp32 rounding per
+    element.  An accumulator that is not fold_start's fp32 (a bf16 one) takes
+    the reference's in-place add as torch computes it there: the fp32 sum
+    rounded to bf16 (ely_fold_add_bf16)."""
     if acc.dtype == torch.int64:
         if g.dtype != torch.int64:
             raise ValueError(f"a count lane folds int64 only, got {g.dtype}")
         acc.add_(g)
         return
     _lib.require_gpu(acc, "fold_add")
-    if acc.dtype != torch.float32 or not acc.is_contiguous():
-        raise ValueError("fold_add accumulates into a contiguous float32 tensor")
+    if acc.dtype not in (torch.float32, torch.bfloat16) or not acc.is_contiguous():
+        raise ValueError("fold_add accumulates into a contiguous float32 (or bfloat16) tensor")
     g = g.detach().contiguous()
     if g.numel() != acc.numel() or g.device != acc.device:
         raise ValueError("fold_add: gradient and accumulator differ in size or device")
     L = _lib.load()
-    _lib.check(L.ely_fold_add(acc.data_ptr(), g.data_ptr(), _lib.dtype_code(g), acc.numel(), _lib.stream_ptr(acc.device)), "fold_add")
+    fn = L.ely_fold_add if acc.dtype == torch.float32 else L.ely_fold_add_bf16
+    _lib.check(fn(acc.data_ptr(), g.data_ptr(), _lib.dtype_code(g), acc.numel(), _lib.stream_ptr(acc.device)), "fold_add")
 
 
 def fold(gs: Iterable[torch.Tensor]) -> torch.Tensor:
