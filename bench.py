@@ -577,6 +577,63 @@ def bench_fold(device, stream, iters=5):
     }
 
 
+def bench_tied_fold(device, stream, n_mb: int = 8, n_rows: int = 32768, rows_per_mb: int = 4096, iters: int = 3):
+    """The tied table's row fold (accumulate.TiedRowFold, the drop-in for
+    runtime/accumulate.py:140-247) on the Head of C1's model: a 32,768-row
+    table (the reference presets' vocabulary, model/gpt.py:257-266) at
+    d = 2560 in fp32, 8 microbatches each touching 4,096 random rows, the
+    embedding rows arriving one microbatch behind the Head gradients.
+    Against the stock dense fold in torch ops (e_i scattered into a dense
+    zero table, g_i = h_i + e_i, acc = g_0 then acc += g_i); both are timed
+    between HIP events over the whole fold and must agree bit for bit."""
+    from elysium_wan_amd.accumulate import TiedRowFold
+
+    d = D_MODEL
+    gen = torch.Generator(device=device).manual_seed(21)
+    hs = [torch.randn(n_rows, d, device=device, generator=gen) * 1e-3 for _ in range(n_mb)]
+    rows = [torch.randperm(n_rows, device=device, generator=gen)[:rows_per_mb].sort().values.cpu() for _ in range(n_mb)]
+    es = [torch.randn(rows_per_mb, d, device=device, generator=gen) * 1e-3 for _ in range(n_mb)]
+
+    def row_fold():
+        fold = TiedRowFold(n_rows, range(n_mb))
+        for mb in range(n_mb):
+            fold.add_head(mb, hs[mb], rows[mb])
+            if mb:
+                fold.add_embed(mb - 1, es[mb - 1])
+        fold.add_embed(n_mb - 1, es[n_mb - 1])
+        return fold.result()
+
+    def dense_fold():
+        acc = None
+        for mb in range(n_mb):
+            e = torch.zeros(n_rows, d, device=device)
+            e[rows[mb].to(device)] = es[mb]
+            g = hs[mb] + e
+            acc = g if acc is None else acc.add_(g)
+        return acc
+
+    def timed(fn):
+        out = fn()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(iters):
+            out = fn()
+        end.record(stream)
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / iters, out
+
+    t_row, a = timed(row_fold)
+    t_dense, b = timed(dense_fold)
+    same = bool(torch.equal(a.view(torch.int32), b.view(torch.int32)))
+    # compulsory traffic: each h read once (4 B/elem), the sum written once per
+    # microbatch and read back from the second on (4 + 4), the embedding rows once
+    nbytes = n_rows * d * (8 + 12 * (n_mb - 1)) + n_mb * rows_per_mb * d * 4
+    del hs, es, a, b
+    return {"rows": n_rows, "d": d, "microbatches": n_mb, "rows_per_mb": rows_per_mb, "row_fold_ms": t_row,
+            "dense_fold_ms": t_dense, "row_fold_GBs": nbytes / (t_row * 1e-3) / 1e9, "bits_equal": same}
+
+
 def bench_release(device, stream, tokens: int = 2048, iters: int = 3):
     """Per-layer release (runtime/stage.py:3080-3099, RUNTIME-I23): the C1
     step runs on a side stream with on_param recording one event per block
@@ -1444,6 +1501,7 @@ def extra_legs(device, stream):
     return [
         ("fold", "fold leg", lambda: bench_fold(device, stream)),
         ("release", "per-layer release leg", lambda: bench_release(device, stream)),
+        ("tied_fold", "tied-table row fold leg", lambda: bench_tied_fold(device, stream)),
         ("elementwise", "elementwise leg", lambda: bench_elementwise(device, stream)),
         ("c1_torch_order", "torch-order leg", lambda: bench_torch_order(device, stream)),
         ("host_moments", "host-moments leg", lambda: bench_host_moments(device)),
@@ -1455,7 +1513,7 @@ def extra_legs(device, stream):
     ]
 
 
-LEG_NAMES = ("fold", "release", "elementwise", "c1_torch_order", "host_moments", "check_host_adamw", "wire",
+LEG_NAMES = ("fold", "release", "tied_fold", "elementwise", "c1_torch_order", "host_moments", "check_host_adamw", "wire",
              "hbm_reference", "configs", "c1_placement")
 
 

@@ -7,10 +7,14 @@
 // soon as its prefix is complete; every fold it makes is one of
 //   acc[idx[j]]  = a[rows_a[j]] + 0.0                  (first, free rows)
 //   acc[idx[j]] += a[rows_a[j]] + 0.0                  (later, free rows)
-//   acc[idx[j]]  = a[j] + b[j]      / acc[idx[j]] += a[j] + b[j]
+//   acc[idx[j]]  = a[j] + e_j       / acc[idx[j]] += a[j] + e_j
 //                                                      (held rows resolved)
 // over a set of distinct rows, which this kernel runs: one block per row
-// (strided), 16-byte vectors across the row when it is aligned.
+// (strided), 16-byte vectors across the row when it is aligned.  e_j is the
+// embedding row b[b_rows[j]] of a held row the microbatch touched, +0.0 for
+// one it did not (b_rows[j] < 0), or b[j] of a compact b.  A second kernel
+// gathers the held rows of a Head gradient, bit for bit, before the
+// gradient itself is released.
 #include <algorithm>
 
 #include "ely_device.hpp"
@@ -42,19 +46,21 @@ template <bool BF16>
 __global__ __launch_bounds__(kRowBlock) void rows_fold_kernel(void* __restrict__ acc, const void* __restrict__ a,
                                                               const int64_t* __restrict__ a_rows,
                                                               const void* __restrict__ b,
+                                                              const int64_t* __restrict__ b_rows,
                                                               const int64_t* __restrict__ idx, int64_t n_idx,
-                                                              int64_t n_rows, int64_t a_total, int64_t d, int first,
-                                                              int vec) {
+                                                              int64_t n_rows, int64_t a_total, int64_t b_total,
+                                                              int64_t d, int first, int vec) {
     constexpr int V = BF16 ? 8 : 4;  // elements per 16-byte vector
     for (int64_t j = blockIdx.x; j < n_idx; j += gridDim.x) {
         const int64_t r = idx[j];
         const int64_t ar = a_rows ? a_rows[j] : j;
+        const int64_t br = b ? (b_rows ? b_rows[j] : j) : -1;  // < 0: the row adds +0.0
         // the host checks every index; a row outside the tables is skipped, never touched
-        if (r < 0 || r >= n_rows || ar < 0 || ar >= a_total) continue;
+        if (r < 0 || r >= n_rows || ar < 0 || ar >= a_total || br >= b_total) continue;
         if (BF16) {
             uint16_t* ac = static_cast<uint16_t*>(acc) + r * d;
             const uint16_t* av = static_cast<const uint16_t*>(a) + ar * d;
-            const uint16_t* bv = b ? static_cast<const uint16_t*>(b) + j * d : nullptr;
+            const uint16_t* bv = br >= 0 ? static_cast<const uint16_t*>(b) + br * d : nullptr;
             if (vec) {
                 for (int64_t c = (int64_t)threadIdx.x * V; c < d; c += (int64_t)kRowBlock * V) {
                     const ru4 x = *reinterpret_cast<const ru4*>(av + c);
@@ -80,7 +86,7 @@ __global__ __launch_bounds__(kRowBlock) void rows_fold_kernel(void* __restrict__
         } else {
             float* ac = static_cast<float*>(acc) + r * d;
             const float* av = static_cast<const float*>(a) + ar * d;
-            const float* bv = b ? static_cast<const float*>(b) + j * d : nullptr;
+            const float* bv = br >= 0 ? static_cast<const float*>(b) + br * d : nullptr;
             if (vec) {
                 for (int64_t c = (int64_t)threadIdx.x * V; c < d; c += (int64_t)kRowBlock * V) {
                     const rf4 x = *reinterpret_cast<const rf4*>(av + c);
@@ -101,20 +107,95 @@ __global__ __launch_bounds__(kRowBlock) void rows_fold_kernel(void* __restrict__
     }
 }
 
+// The free rows of a Head gradient by mask instead of by index list: every
+// row r with held[r] == 0 takes acc[r] = a[r] + 0.0 (first) or
+// acc[r] + (a[r] + 0.0), each add rounded to the dtype; held rows are left.
+template <bool BF16>
+__global__ __launch_bounds__(kRowBlock) void rows_fold_masked_kernel(void* __restrict__ acc, const void* __restrict__ a,
+                                                                     const uint8_t* __restrict__ held, int64_t n_rows,
+                                                                     int64_t d, int first, int vec) {
+    constexpr int V = BF16 ? 8 : 4;
+    for (int64_t r = blockIdx.x; r < n_rows; r += gridDim.x) {
+        if (held[r]) continue;
+        if (BF16) {
+            uint16_t* ac = static_cast<uint16_t*>(acc) + r * d;
+            const uint16_t* av = static_cast<const uint16_t*>(a) + r * d;
+            if (vec) {
+                for (int64_t c = (int64_t)threadIdx.x * V; c < d; c += (int64_t)kRowBlock * V) {
+                    const ru4 x = *reinterpret_cast<const ru4*>(av + c);
+                    const ru4 z = first ? ru4{0u, 0u, 0u, 0u} : *reinterpret_cast<const ru4*>(ac + c);
+                    ru4 o;
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        const float lo = fold1<true>(bf16_to_f32(z[k] & 0xFFFFu), bf16_to_f32(x[k] & 0xFFFFu), 0.0f, first);
+                        const float hi = fold1<true>(bf16_to_f32(z[k] >> 16), bf16_to_f32(x[k] >> 16), 0.0f, first);
+                        o[k] = f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);
+                    }
+                    *reinterpret_cast<ru4*>(ac + c) = o;
+                }
+            } else {
+                for (int64_t c = threadIdx.x; c < d; c += kRowBlock) {
+                    const float z = first ? 0.0f : bf16_to_f32(ac[c]);
+                    ac[c] = (uint16_t)f32_to_bf16(fold1<true>(z, bf16_to_f32(av[c]), 0.0f, first));
+                }
+            }
+        } else {
+            float* ac = static_cast<float*>(acc) + r * d;
+            const float* av = static_cast<const float*>(a) + r * d;
+            if (vec) {
+                for (int64_t c = (int64_t)threadIdx.x * V; c < d; c += (int64_t)kRowBlock * V) {
+                    const rf4 x = *reinterpret_cast<const rf4*>(av + c);
+                    const rf4 z = first ? rf4{0.0f, 0.0f, 0.0f, 0.0f} : *reinterpret_cast<const rf4*>(ac + c);
+                    rf4 o;
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) o[k] = fold1<false>(z[k], x[k], 0.0f, first);
+                    *reinterpret_cast<rf4*>(ac + c) = o;
+                }
+            } else {
+                for (int64_t c = threadIdx.x; c < d; c += kRowBlock) {
+                    const float z = first ? 0.0f : ac[c];
+                    ac[c] = fold1<false>(z, av[c], 0.0f, first);
+                }
+            }
+        }
+    }
+}
+
+// dst[j] = src[rows[j]], bit for bit, `bytes` per row: one block per row
+// (strided), 16-byte vectors when both tables are aligned.
+__global__ __launch_bounds__(kRowBlock) void rows_gather_kernel(char* __restrict__ dst, const char* __restrict__ src,
+                                                                const int64_t* __restrict__ rows, int64_t n,
+                                                                int64_t src_rows, int64_t bytes, int vec) {
+    for (int64_t j = blockIdx.x; j < n; j += gridDim.x) {
+        const int64_t r = rows[j];
+        if (r < 0 || r >= src_rows) continue;  // the host checks every index
+        char* o = dst + j * bytes;
+        const char* x = src + r * bytes;
+        if (vec) {
+            for (int64_t c = (int64_t)threadIdx.x * 16; c < bytes; c += (int64_t)kRowBlock * 16)
+                *reinterpret_cast<ru4*>(o + c) = *reinterpret_cast<const ru4*>(x + c);
+        } else {
+            for (int64_t c = threadIdx.x; c < bytes; c += kRowBlock) o[c] = x[c];
+        }
+    }
+}
+
 }  // namespace
 }  // namespace ely
 
 using namespace ely;
 
-extern "C" int ely_rows_fold(void* acc, const void* a, const int64_t* a_rows, const void* b, const int64_t* idx,
-                             int64_t n_idx, int64_t n_rows, int64_t a_total, int64_t d, int32_t dtype, int32_t first,
-                             void* stream) {
+extern "C" int ely_rows_fold(void* acc, const void* a, const int64_t* a_rows, const void* b, const int64_t* b_rows,
+                             const int64_t* idx, int64_t n_idx, int64_t n_rows, int64_t a_total, int64_t b_total,
+                             int64_t d, int32_t dtype, int32_t first, void* stream) {
     return guarded([&] {
         if (dtype != ELY_F32 && dtype != ELY_BF16) fail(ELY_EINVAL, "ely_rows_fold: dtype must be ELY_F32 or ELY_BF16");
-        if (n_idx < 0 || n_rows < 0 || a_total < 0 || d < 0) fail(ELY_EINVAL, "ely_rows_fold: negative size");
+        if (n_idx < 0 || n_rows < 0 || a_total < 0 || b_total < 0 || d < 0) fail(ELY_EINVAL, "ely_rows_fold: negative size");
         if (n_idx == 0 || d == 0) return;
         if (!acc || !a || !idx) fail(ELY_EINVAL, "ely_rows_fold: null pointer");
         if (!a_rows && a_total < n_idx) fail(ELY_EINVAL, "ely_rows_fold: a compact source holds one row per index");
+        if (b_rows && !b) fail(ELY_EINVAL, "ely_rows_fold: b_rows without b");
+        if (b && !b_rows && b_total < n_idx) fail(ELY_EINVAL, "ely_rows_fold: a compact b holds one row per index");
         const int64_t esz = dtype == ELY_BF16 ? 2 : 4;
         const int64_t v = 16 / esz;
         const int vec = (d % v == 0) && aligned16(acc) && aligned16(a) && (!b || aligned16(b)) ? 1 : 0;
@@ -122,10 +203,47 @@ extern "C" int ely_rows_fold(void* acc, const void* a, const int64_t* a_rows, co
         hipStream_t s = static_cast<hipStream_t>(stream);
         if (dtype == ELY_BF16)
             hipLaunchKernelGGL(rows_fold_kernel<true>, dim3((unsigned)blocks), dim3(kRowBlock), 0, s, acc, a, a_rows, b,
-                               idx, n_idx, n_rows, a_total, d, first ? 1 : 0, vec);
+                               b_rows, idx, n_idx, n_rows, a_total, b ? b_total : 0, d, first ? 1 : 0, vec);
         else
             hipLaunchKernelGGL(rows_fold_kernel<false>, dim3((unsigned)blocks), dim3(kRowBlock), 0, s, acc, a, a_rows, b,
-                               idx, n_idx, n_rows, a_total, d, first ? 1 : 0, vec);
+                               b_rows, idx, n_idx, n_rows, a_total, b ? b_total : 0, d, first ? 1 : 0, vec);
         check_launch("rows_fold_kernel");
+    });
+}
+
+extern "C" int ely_rows_fold_masked(void* acc, const void* a, const uint8_t* held, int64_t n_rows, int64_t d,
+                                    int32_t dtype, int32_t first, void* stream) {
+    return guarded([&] {
+        if (dtype != ELY_F32 && dtype != ELY_BF16) fail(ELY_EINVAL, "ely_rows_fold_masked: dtype must be ELY_F32 or ELY_BF16");
+        if (n_rows < 0 || d < 0) fail(ELY_EINVAL, "ely_rows_fold_masked: negative size");
+        if (n_rows == 0 || d == 0) return;
+        if (!acc || !a || !held) fail(ELY_EINVAL, "ely_rows_fold_masked: null pointer");
+        const int64_t v = dtype == ELY_BF16 ? 8 : 4;
+        const int vec = (d % v == 0) && aligned16(acc) && aligned16(a) ? 1 : 0;
+        const int64_t blocks = std::min<int64_t>(n_rows, mt_blocks(8));
+        hipStream_t s = static_cast<hipStream_t>(stream);
+        if (dtype == ELY_BF16)
+            hipLaunchKernelGGL(rows_fold_masked_kernel<true>, dim3((unsigned)blocks), dim3(kRowBlock), 0, s, acc, a, held,
+                               n_rows, d, first ? 1 : 0, vec);
+        else
+            hipLaunchKernelGGL(rows_fold_masked_kernel<false>, dim3((unsigned)blocks), dim3(kRowBlock), 0, s, acc, a, held,
+                               n_rows, d, first ? 1 : 0, vec);
+        check_launch("rows_fold_masked_kernel");
+    });
+}
+
+extern "C" int ely_rows_gather(void* dst, const void* src, const int64_t* rows, int64_t n, int64_t src_rows,
+                               int64_t d, int32_t dtype, void* stream) {
+    return guarded([&] {
+        if (dtype != ELY_F32 && dtype != ELY_BF16) fail(ELY_EINVAL, "ely_rows_gather: dtype must be ELY_F32 or ELY_BF16");
+        if (n < 0 || src_rows < 0 || d < 0) fail(ELY_EINVAL, "ely_rows_gather: negative size");
+        if (n == 0 || d == 0) return;
+        if (!dst || !src || !rows) fail(ELY_EINVAL, "ely_rows_gather: null pointer");
+        const int64_t bytes = d * (dtype == ELY_BF16 ? 2 : 4);
+        const int vec = bytes % 16 == 0 && aligned16(dst) && aligned16(src) ? 1 : 0;
+        const int64_t blocks = std::min<int64_t>(n, mt_blocks(8));
+        hipLaunchKernelGGL(rows_gather_kernel, dim3((unsigned)blocks), dim3(kRowBlock), 0, static_cast<hipStream_t>(stream),
+                           static_cast<char*>(dst), static_cast<const char*>(src), rows, n, src_rows, bytes, vec);
+        check_launch("rows_gather_kernel");
     });
 }

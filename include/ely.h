@@ -215,18 +215,37 @@ int ely_fold_add_bf16(uint16_t* acc, const void* g, int32_t g_dtype, int64_t n, 
 
 /* The row folds of TiedRowFold (runtime/accumulate.py:140-247), the step
  * gradient of a tied table split across stages: for each j < n_idx, with
- * r = idx[j] and ar = a_rows ? a_rows[j] : j,
- *     v = a[ar] + (b ? b[j] : +0.0)              rounded to dtype,
+ * r = idx[j], ar = a_rows ? a_rows[j] : j and e the row b[b_rows[j]]
+ * (b_rows[j] >= 0), b[j] (b compact, b_rows NULL), or +0.0 (no b, or
+ * b_rows[j] < 0),
+ *     v = a[ar] + e                              rounded to dtype,
  *     acc[r] = first ? v : acc[r] + v            rounded to dtype
  * (the reference's `h[fi] + 0.0` folds of a Head gradient's free rows,
- * :210-213, and `hk + e_on` folds of its held rows, :232-235).  acc:
- * [n_rows, d]; a: [a_total, d] rows picked by a_rows, or compact [n_idx, d]
- * when a_rows is NULL; b: NULL or compact [n_idx, d]; idx and a_rows are
- * device int64 arrays; the rows of idx are distinct.  An index outside its
- * table is skipped (the caller checks them).  dtype ELY_F32 or ELY_BF16. */
-int ely_rows_fold(void* acc, const void* a, const int64_t* a_rows, const void* b, const int64_t* idx,
-                  int64_t n_idx, int64_t n_rows, int64_t a_total, int64_t d, int32_t dtype, int32_t first,
-                  void* stream);
+ * :210-213, and `hk + e_on` folds of its held rows, :232-235, e_on being
+ * the embedding rows where the microbatch has them and +0 elsewhere).
+ * acc: [n_rows, d]; a: [a_total, d] rows picked by a_rows, or compact
+ * [n_idx, d] when a_rows is NULL; b: NULL, [b_total, d] rows picked by
+ * b_rows, or compact [n_idx, d]; idx, a_rows and b_rows are device int64
+ * arrays; the rows of idx are distinct.  An index outside its table is
+ * skipped (the caller checks them).  dtype ELY_F32 or ELY_BF16. */
+int ely_rows_fold(void* acc, const void* a, const int64_t* a_rows, const void* b, const int64_t* b_rows,
+                  const int64_t* idx, int64_t n_idx, int64_t n_rows, int64_t a_total, int64_t b_total, int64_t d,
+                  int32_t dtype, int32_t first, void* stream);
+
+/* ely_rows_fold over the free rows of a Head gradient, given by a mask
+ * instead of an index list (runtime/accumulate.py:210-213): every row r of
+ * [n_rows, d] with held[r] == 0 takes acc[r] = a[r] + 0.0 (first) or
+ * acc[r] + (a[r] + 0.0), each add rounded to dtype; rows with held[r] != 0
+ * are left.  held: device uint8 [n_rows].  dtype ELY_F32 or ELY_BF16. */
+int ely_rows_fold_masked(void* acc, const void* a, const uint8_t* held, int64_t n_rows, int64_t d, int32_t dtype,
+                         int32_t first, void* stream);
+
+/* TiedRowFold's copy of a Head gradient's held rows (runtime/accumulate.py:
+ * 221, `h[ki].clone()`): dst[j] = src[rows[j]] bit for bit, j < n; src:
+ * [src_rows, d], dst: compact [n, d]; rows a device int64 array (an index
+ * outside src is skipped).  dtype ELY_F32 or ELY_BF16. */
+int ely_rows_gather(void* dst, const void* src, const int64_t* rows, int64_t n, int64_t src_rows, int64_t d,
+                    int32_t dtype, void* stream);
 
 /* In-place g <- g * (*coef_dev) over a tensor list, the product rounded to
  * each tensor's dtype: the scaling step of clip_grad_norm_
