@@ -291,3 +291,26 @@ def test_adamw_refuses_more_tiles_than_its_descriptors_hold(lib):
     ws = lib.ely_adamw_workspace_bytes(2)
     st = lib.ely_adamw_step(t, g, t, t, None, 2, c, _lib.ORDER_HOST, 0, None, fake, ws, None)
     assert st == _lib.EINVAL and b"tiles" in lib.ely_last_error()
+
+
+def test_argument_errors_of_the_row_entry_points(lib):
+    """The tied fold's row entry points check their arguments before the
+    HIP runtime is touched; the pointers below are never dereferenced."""
+    from elysium_wan_amd import _lib
+
+    fake = 1 << 20
+    assert lib.ely_rows_fold(fake, fake, None, None, None, fake, 4, 8, 8, 0, 16, 7, 0, None) == _lib.EINVAL
+    assert b"dtype" in lib.ely_last_error()
+    assert lib.ely_rows_fold(None, fake, None, None, None, fake, 4, 8, 8, 0, 16, _lib.F32, 0, None) == _lib.EINVAL
+    assert lib.ely_rows_fold(fake, fake, None, None, fake, fake, 4, 8, 8, 0, 16, _lib.F32, 0, None) == _lib.EINVAL
+    assert b"b_rows without b" in lib.ely_last_error()
+    assert lib.ely_rows_fold(fake, fake, None, fake, None, fake, 4, 8, 8, 2, 16, _lib.F32, 0, None) == _lib.EINVAL
+    assert b"compact b" in lib.ely_last_error()
+    assert lib.ely_rows_fold(fake, fake, None, None, None, fake, 4, 8, 2, 0, 16, _lib.F32, 0, None) == _lib.EINVAL
+    assert lib.ely_rows_fold(None, None, None, None, None, None, 0, 8, 0, 0, 16, _lib.F32, 0, None) == _lib.OK
+    assert lib.ely_rows_gather(fake, fake, None, 4, 8, 16, _lib.BF16, None) == _lib.EINVAL
+    assert lib.ely_rows_gather(fake, fake, fake, -1, 8, 16, _lib.BF16, None) == _lib.EINVAL
+    assert lib.ely_rows_gather(None, None, None, 0, 8, 16, _lib.BF16, None) == _lib.OK
+    assert lib.ely_rows_fold_masked(fake, fake, None, 8, 16, _lib.F32, 1, None) == _lib.EINVAL
+    assert lib.ely_rows_fold_masked(fake, fake, fake, 8, 16, 9, 1, None) == _lib.EINVAL
+    assert lib.ely_rows_fold_masked(None, None, None, 0, 16, _lib.F32, 1, None) == _lib.OK
