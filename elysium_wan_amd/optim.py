@@ -4,7 +4,8 @@
 (runtime/optim.py:32-69):
 
 * "adamw"      -> FusedAdamW(order="torch"): torch.optim.AdamW's arithmetic
-                  (TORCH/optim/adam.py:554-800), within 1 ulp of it.
+                  (TORCH/optim/adam.py:554-800), within 1 ulp of it
+                  (bit for bit torch's GPU foreach kernels on this image).
 * "adamw-host" -> FusedAdamW(order="host", moments="host"): HostAdamW's
                   single-rounding op order (runtime/optim.py:277-298), bit for
                   bit, with its moments in pinned host memory streamed through

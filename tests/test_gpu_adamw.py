@@ -193,9 +193,12 @@ def test_extreme_values_follow_the_oracle(oracle, gdtype):
 @pytest.mark.parametrize("case", ["small", "c0"])
 def test_torch_order_is_within_one_ulp_of_torch_adamw(case):
     """optim.build("adamw") against torch.optim.AdamW (foreach, the GPU
-    default) on the same GPU, 5 steps, weight decay on: parameters, exp_avg
-    and exp_avg_sq each within 1 ulp, on small ragged shapes and on config
-    C0's 38-tensor shard (21,265,152 elements)."""
+    default) on the same GPU, 5 steps, weight decay on, on small ragged
+    shapes and on config C0's 38-tensor shard (21,265,152 elements).  The
+    contract is 1 ulp; with this image's torch the kernel's fused
+    multiply-adds fall where torch's foreach kernels have theirs, so
+    parameters, exp_avg and exp_avg_sq come out bit for bit, and the test
+    holds it to that."""
     from elysium_wan_amd import optim
 
     gen = torch.Generator().manual_seed(4)
@@ -229,7 +232,7 @@ def test_torch_order_is_within_one_ulp_of_torch_adamw(case):
         worst[name] = max(int(x.max()) for x in d)
         exact = sum(int((x == 0).sum()) for x in d) / sum(x.size for x in d)
         say(f"  {name}: max ulp {worst[name]}, bit-identical fraction {exact:.6f}")
-    assert max(worst.values()) <= 1, worst
+    assert max(worst.values()) == 0, worst
 
 
 def test_state_dict_layout_resume_and_refusals():

@@ -139,6 +139,39 @@ def test_c1_full_shard_ten_steps_against_the_oracle(oracle):
     torch.cuda.empty_cache()
 
 
+def test_c1_torch_order_equals_torch_adamw_bit_for_bit():
+    """C1's shard (192 tensors, 1,258,823,680 elements) under the "adamw"
+    recipe (build("adamw"): torch.optim.AdamW's op order) against
+    torch.optim.AdamW itself (foreach, the GPU default) on the same GPU,
+    fp32 grads N(0, 1e-4), weight decay 0.1, 3 steps: every parameter and
+    both moments equal bit for bit (the contract is 1 ulp)."""
+    from elysium_wan_amd import optim
+
+    shapes = gpt_block_shapes(2560) * 16
+    gen = torch.Generator(device="cuda").manual_seed(43)
+    mine = [torch.empty(s, device="cuda").normal_(0.0, 0.02, generator=gen).requires_grad_(True) for s in shapes]
+    ref = [p.detach().clone().requires_grad_(True) for p in mine]
+    a = optim.build("adamw", mine, LR, weight_decay=WD)
+    b = torch.optim.AdamW(ref, lr=LR, betas=BETAS, eps=EPS, weight_decay=WD)
+    ggen = torch.Generator(device="cuda").manual_seed(44)
+    for step in range(3):
+        say("C1 torch order vs torch.optim.AdamW, step", step)
+        for p, q in zip(mine, ref):
+            g = torch.empty(p.shape, device="cuda").normal_(0.0, 1e-4, generator=ggen)
+            p.grad, q.grad = g, g.clone()
+        a.step()
+        b.step()
+        for p, q in zip(mine, ref):
+            p.grad = q.grad = None
+    torch.cuda.synchronize()
+    for i, (p, q) in enumerate(zip(mine, ref)):
+        assert torch.equal(p.detach().view(torch.int32), q.detach().view(torch.int32)), i
+        assert torch.equal(a.state[p]["exp_avg"].view(torch.int32), b.state[q]["exp_avg"].view(torch.int32)), i
+        assert torch.equal(a.state[p]["exp_avg_sq"].view(torch.int32), b.state[q]["exp_avg_sq"].view(torch.int32)), i
+    del a, b, mine, ref
+    torch.cuda.empty_cache()
+
+
 def _c3_shard(seed: int):
     """C3: 1,000 vectors of 6,144 interleaved with 100 matrices of
     6,144 x 10,240 (ten vectors, then one matrix), 6,297,600,000 elements;
