@@ -726,9 +726,10 @@ def bench_elementwise(device, stream, iters=5):
     one launch per tensor as the reference's callers make them: the fp32 ->
     bf16 working-copy cast (pieces.cast_piece, 6 B/elem), the fold of a bf16
     microbatch gradient into its fp32 sum (pieces.fold_add, 10 B/elem),
-    the in-place scale of bf16 gradients by a device coefficient (one launch
-    per tensor, 4 B/elem) and clip_grad_norm_ in one call (the norm, then one
-    launch scaling every gradient: 6 B/elem)."""
+    the in-place scale of bf16 gradients by a device coefficient
+    (ely_scale_inplace over the list, one launch per 48 tensors, 4 B/elem)
+    and clip_grad_norm_ in one call (the norm, then one launch scaling every
+    gradient: 6 B/elem)."""
     from elysium_wan_amd import _lib
 
     L = _lib.load()

@@ -2,8 +2,9 @@
 // update: the fp32 master -> bf16 working-copy cast (pieces.cast_piece,
 // runtime/pieces.py:192-195), the fp32 fold of a microbatch gradient
 // (pieces.fold_add, runtime/pieces.py:206-214; into a bf16 sum for
-// OrderedAccumulator, runtime/accumulate.py:101-102) and the clip's in-place
-// scaling (clip_grad_norm_).  Each is one HBM pass over 4-element quads
+// OrderedAccumulator, runtime/accumulate.py:101-102).  (The clip's in-place
+// scaling of a tensor list is one multi-tensor launch in mta.hip.)  Each is
+// one HBM pass over 4-element quads
 // (16-byte fp32, 8-byte bf16 vectors, nontemporal) on a persistent grid,
 // with a per-kernel number of quads in flight per thread.
 #include <algorithm>
@@ -17,8 +18,7 @@
 // and the persistent grid's blocks per CU (_BPC).  Together they set the
 // bytes each CU has outstanding, which is what bounds a streaming pass on
 // this part; the passes reading 16-24 B per quad run fastest at about 16-25
-// KB of reads in flight per CU, the bf16 scale (8 B per quad) wants more
-// waves.
+// KB of reads in flight per CU.
 #ifndef ELY_CAST_UNROLL
 #define ELY_CAST_UNROLL 1
 #endif
@@ -31,18 +31,6 @@
 #ifndef ELY_FOLD_BPC
 #define ELY_FOLD_BPC 3
 #endif
-#ifndef ELY_SCALE32_UNROLL
-#define ELY_SCALE32_UNROLL 1
-#endif
-#ifndef ELY_SCALE32_BPC
-#define ELY_SCALE32_BPC 4
-#endif
-#ifndef ELY_SCALE16_UNROLL
-#define ELY_SCALE16_UNROLL 2
-#endif
-#ifndef ELY_SCALE16_BPC
-#define ELY_SCALE16_BPC 8
-#endif
 
 namespace ely {
 
@@ -54,8 +42,6 @@ struct EwShape {
 };
 constexpr EwShape kCastShape{ELY_CAST_UNROLL, ELY_CAST_BPC};
 constexpr EwShape kFoldShape{ELY_FOLD_UNROLL, ELY_FOLD_BPC};
-constexpr EwShape kScale32Shape{ELY_SCALE32_UNROLL, ELY_SCALE32_BPC};
-constexpr EwShape kScale16Shape{ELY_SCALE16_UNROLL, ELY_SCALE16_BPC};
 
 typedef float ef4 __attribute__((ext_vector_type(4)));
 typedef uint32_t eu2 __attribute__((ext_vector_type(2)));
@@ -162,38 +148,6 @@ __global__ __launch_bounds__(kEwBlock) void fold_add_bf16_kernel(uint16_t* __res
     }
 }
 
-// g <- g * coef (coef read from device memory), one fp32 multiply rounded to
-// g's dtype: torch's _foreach_mul_(grads, clip_coef) (clip_grad.py:170-177).
-template <bool BF16G>
-__global__ __launch_bounds__(kEwBlock) void scale_kernel(void* __restrict__ g, int64_t n, int vec,
-                                                         const float* __restrict__ coef_ptr) {
-    const float coef = *coef_ptr;
-    int64_t done = 0;
-    if (vec) {
-        if (BF16G) {
-            uint16_t* p = static_cast<uint16_t*>(g);
-            done = quad_loop<kScale16Shape.unroll>(
-                n / 4, [&](int64_t q) { return widen4(ldh4(p + 4 * q)); },
-                [&](int64_t q, ef4 v) { sth4(p + 4 * q, narrow4(ef4{v[0] * coef, v[1] * coef, v[2] * coef, v[3] * coef})); });
-        } else {
-            float* p = static_cast<float*>(g);
-            done = quad_loop<kScale32Shape.unroll>(
-                n / 4, [&](int64_t q) { return ld4(p + 4 * q); },
-                [&](int64_t q, ef4 v) { st4(p + 4 * q, ef4{v[0] * coef, v[1] * coef, v[2] * coef, v[3] * coef}); });
-        }
-    }
-    const int64_t T = (int64_t)gridDim.x * kEwBlock;
-    for (int64_t i = done + (int64_t)blockIdx.x * kEwBlock + threadIdx.x; i < n; i += T) {
-        if (BF16G) {
-            uint16_t* p = static_cast<uint16_t*>(g);
-            p[i] = (uint16_t)f32_to_bf16(bf16_to_f32(p[i]) * coef);
-        } else {
-            float* p = static_cast<float*>(g);
-            p[i] = p[i] * coef;
-        }
-    }
-}
-
 // Blocks for n elements: one quad per thread per unrolled slot, capped at
 // the shape's blocks per CU.
 static unsigned ew_blocks(int64_t n, EwShape sh) {
@@ -251,29 +205,6 @@ int ely_fold_add_bf16(uint16_t* acc, const void* g, int32_t g_dtype, int64_t n, 
         else
             hipLaunchKernelGGL(fold_add_bf16_kernel<false>, dim3(ew_blocks(n, kFoldShape)), dim3(kEwBlock), 0, s, acc, g, n, vec);
         check_launch("fold_add_bf16_kernel");
-    });
-}
-
-int ely_scale_inplace(const ely_tensor* ts, int32_t n, const float* coef_dev, void* stream) {
-    return guarded([&] {
-        if (n < 0 || (n > 0 && !ts)) fail(ELY_EINVAL, "ely_scale_inplace: bad tensor list");
-        if (!coef_dev) fail(ELY_EINVAL, "ely_scale_inplace: null coefficient");
-        hipStream_t s = static_cast<hipStream_t>(stream);
-        for (int32_t i = 0; i < n; ++i) {
-            const ely_tensor& t = ts[i];
-            if (t.numel < 0 || (t.numel > 0 && !t.ptr)) fail(ELY_EINVAL, "ely_scale_inplace: bad tensor");
-            if (t.numel == 0) continue;
-            const int vec = reinterpret_cast<uintptr_t>(t.ptr) % (t.dtype == ELY_BF16 ? 8 : 16) == 0;
-            if (t.dtype == ELY_BF16)
-                hipLaunchKernelGGL(scale_kernel<true>, dim3(ew_blocks(t.numel, kScale16Shape)), dim3(kEwBlock), 0, s, t.ptr, t.numel,
-                                   vec, coef_dev);
-            else if (t.dtype == ELY_F32)
-                hipLaunchKernelGGL(scale_kernel<false>, dim3(ew_blocks(t.numel, kScale32Shape)), dim3(kEwBlock), 0, s, t.ptr, t.numel,
-                                   vec, coef_dev);
-            else
-                fail(ELY_EINVAL, "ely_scale_inplace: dtype");
-            check_launch("scale_kernel");
-        }
     });
 }
 

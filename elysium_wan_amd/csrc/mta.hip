@@ -835,17 +835,17 @@ static ClipArgsKernel pick_clip_args(int dt) {
 // Scale every gradient of a finished norm call by its clip coefficient, from
 // that call's tile table (uploaded to the workspace, or its descriptors by
 // argument again; same stream, so the coefficient is in place when this runs).
-static void clip_scale(const NormLaunch& nl, ely_norm_result* out_dev, void* stream) {
+static void clip_scale(const NormLaunch& nl, const float* coef_dev, void* stream) {
     if (nl.tiles == 0) return;
     const int64_t waves = std::min<int64_t>(nl.tiles, mt_blocks(ELY_CLIP_BPC) * (kBlock / kWave));
     const int64_t blocks = (waves + 3) / 4;
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (nl.dtable) {
         const ClipKernel k = nl.tile == kNormTile ? pick_clip<kNormTile>(nl.dt) : pick_clip<kNormSmallTile>(nl.dt);
-        hipLaunchKernelGGL(k, dim3((unsigned)blocks), dim3(kBlock), 0, s, nl.dtable, nl.entries, nl.tiles, &out_dev->coef);
+        hipLaunchKernelGGL(k, dim3((unsigned)blocks), dim3(kBlock), 0, s, nl.dtable, nl.entries, nl.tiles, coef_dev);
     } else {
         const ClipArgsKernel k = nl.tile == kNormTile ? pick_clip_args<kNormTile>(nl.dt) : pick_clip_args<kNormSmallTile>(nl.dt);
-        hipLaunchKernelGGL(k, dim3((unsigned)blocks), dim3(kBlock), 0, s, nl.args, nl.entries, nl.tiles, &out_dev->coef);
+        hipLaunchKernelGGL(k, dim3((unsigned)blocks), dim3(kBlock), 0, s, nl.args, nl.entries, nl.tiles, coef_dev);
     }
     check_launch("clip_scale_kernel");
 }
@@ -963,7 +963,7 @@ int ely_grad_norm_clip(const ely_tensor* grads, int32_t n, float max_norm, ely_n
                        int64_t ws_bytes, void* stream) {
     return guarded([&] {
         const NormLaunch nl = grad_norm_impl(nullptr, grads, n, max_norm, out_dev, workspace, ws_bytes, stream);
-        clip_scale(nl, out_dev, stream);
+        clip_scale(nl, &out_dev->coef, stream);
     });
 }
 
@@ -972,6 +972,49 @@ int ely_grad_norm_fold(const ely_tensor* accs, const ely_tensor* grads, int32_t 
     return guarded([&] {
         if (n > 0 && !accs) fail(ELY_EINVAL, "ely_grad_norm_fold: null accumulator list");
         grad_norm_impl(accs, grads, n, max_norm, out_dev, workspace, ws_bytes, stream);
+    });
+}
+
+// In-place g <- g * coef over a tensor list: the clip's scale kernel over
+// the norm's tiles, with the descriptors in the kernel arguments, one launch
+// per kNormArgTensors non-empty tensors (no workspace, no table copy).
+int ely_scale_inplace(const ely_tensor* ts, int32_t n, const float* coef_dev, void* stream) {
+    return guarded([&] {
+        if (n < 0 || (n > 0 && !ts)) fail(ELY_EINVAL, "ely_scale_inplace: bad tensor list");
+        if (!coef_dev) fail(ELY_EINVAL, "ely_scale_inplace: null coefficient");
+        for (int32_t i = 0; i < n; ++i) {
+            if (ts[i].numel < 0 || (ts[i].numel > 0 && !ts[i].ptr)) fail(ELY_EINVAL, "ely_scale_inplace: bad tensor");
+            if (ts[i].dtype != ELY_F32 && ts[i].dtype != ELY_BF16) fail(ELY_EINVAL, "ely_scale_inplace: dtype");
+        }
+        hipStream_t s = static_cast<hipStream_t>(stream);
+        const int64_t tile = norm_tile(ts, n);
+        NormLaunch nl;
+        nl.tile = tile;
+        memset(&nl.args, 0, sizeof nl.args);
+        auto flush = [&] {
+            if (nl.entries == 0) return;
+            clip_scale(nl, coef_dev, s);
+            nl.entries = 0;
+            nl.tiles = 0;
+            nl.dt = -2;
+            memset(&nl.args, 0, sizeof nl.args);
+        };
+        nl.dt = -2;  // no tensor yet
+        for (int32_t i = 0; i < n; ++i) {
+            if (ts[i].numel == 0) continue;
+            NormDesc d;
+            d.g = ts[i].ptr;
+            d.acc = nullptr;
+            d.numel = ts[i].numel;
+            d.tile_begin = nl.tiles;
+            d.dtype = ts[i].dtype;
+            d.aligned = aligned16(ts[i].ptr) ? 1 : 0;
+            nl.args.d[nl.entries++] = d;
+            nl.tiles += (d.numel + tile - 1) / tile;
+            nl.dt = nl.dt == -2 ? d.dtype : (nl.dt == d.dtype ? nl.dt : -1);
+            if (nl.entries == kNormArgTensors) flush();
+        }
+        flush();
     });
 }
 

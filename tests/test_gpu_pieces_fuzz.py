@@ -7,6 +7,7 @@ Derandomized."""
 
 from __future__ import annotations
 
+import numpy as np
 import pytest
 import torch
 from hypothesis import HealthCheck, given, settings
@@ -54,3 +55,27 @@ def test_elementwise_passes_match_torch(n, offs, bf16g, coef, seed):
         want = (h.float() * c).to(gdt)
         _lib.check(L.ely_scale_inplace(_lib.tensor_array([h]), 1, c.data_ptr(), _lib.stream_ptr(h.device)), "scale")
         assert _same(h, want)
+
+
+@pytest.mark.parametrize("n_t", [1, 48, 49, 130])
+def test_scale_over_a_tensor_list_equals_torch(n_t):
+    """ely_scale_inplace over a list (one launch per 48 tensors): every
+    tensor, bf16 or fp32, aligned or at an odd offset, empty or not, equals
+    torch's g * coef rounded to its dtype on the GPU."""
+    from elysium_wan_amd import _lib
+
+    L = _lib.load()
+    gen = torch.Generator(device="cuda").manual_seed(900 + n_t)
+    rng = np.random.default_rng(n_t)
+    c = torch.tensor([0.37], dtype=torch.float32, device="cuda")
+    hs, wants = [], []
+    for j in range(n_t):
+        n = int(rng.choice([0, 1, 7, 4096, 4097, 20000]))
+        dt = torch.bfloat16 if j % 2 else torch.float32
+        h = _at(torch.randn(n, device="cuda", generator=gen).to(dt), int(rng.integers(0, 4)))
+        wants.append((h.float() * c).to(dt))
+        hs.append(h)
+    say("scale over a list", n_t)
+    _lib.check(L.ely_scale_inplace(_lib.tensor_array(hs), n_t, c.data_ptr(), _lib.stream_ptr(torch.device("cuda", 0))), "scale")
+    for h, w in zip(hs, wants):
+        assert _same(h, w)
