@@ -42,6 +42,71 @@ __device__ __forceinline__ float fold1(float acc, float a, float b, bool first) 
     return s;
 }
 
+constexpr int kRowUnroll = 4;  // 16-byte vectors per thread loaded before the first is stored
+
+// One vector of 4 fp32 or 8 bf16 elements: acc (=|+=) x + y, each add rounded
+// to the dtype (y = 0 when the row has no b).
+template <bool BF16>
+__device__ __forceinline__ ru4 fold_vec(ru4 z, ru4 x, ru4 y, int first) {
+    ru4 o;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        if (BF16) {
+            const float lo = fold1<true>(bf16_to_f32(z[k] & 0xFFFFu), bf16_to_f32(x[k] & 0xFFFFu), bf16_to_f32(y[k] & 0xFFFFu), first);
+            const float hi = fold1<true>(bf16_to_f32(z[k] >> 16), bf16_to_f32(x[k] >> 16), bf16_to_f32(y[k] >> 16), first);
+            o[k] = f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);
+        } else {
+            o[k] = __float_as_uint(fold1<false>(__uint_as_float(z[k]), __uint_as_float(x[k]), __uint_as_float(y[k]), first));
+        }
+    }
+    return o;
+}
+
+// One row of d elements: ac (=|+=) av + (bv or +0.0).  Aligned rows move
+// 16-byte vectors, kRowUnroll per thread loaded before any is stored, so a
+// row's loads are in flight together; others go element by element.
+template <bool BF16>
+__device__ __forceinline__ void fold_row(void* ac_, const void* av_, const void* bv_, int64_t d, int first, int vec) {
+    if (vec) {
+        const int64_t nvec = d / (BF16 ? 8 : 4);
+        ru4* ac = static_cast<ru4*>(ac_);
+        const ru4* av = static_cast<const ru4*>(av_);
+        const ru4* bv = static_cast<const ru4*>(bv_);
+        for (int64_t v0 = threadIdx.x; v0 < nvec; v0 += (int64_t)kRowBlock * kRowUnroll) {
+            ru4 x[kRowUnroll], y[kRowUnroll], z[kRowUnroll];
+#pragma unroll
+            for (int u = 0; u < kRowUnroll; ++u) {
+                const int64_t v = v0 + (int64_t)u * kRowBlock;
+                const ru4 zero = {0u, 0u, 0u, 0u};
+                x[u] = v < nvec ? av[v] : zero;
+                y[u] = (v < nvec && bv) ? bv[v] : zero;
+                z[u] = (v < nvec && !first) ? ac[v] : zero;
+            }
+#pragma unroll
+            for (int u = 0; u < kRowUnroll; ++u) {
+                const int64_t v = v0 + (int64_t)u * kRowBlock;
+                if (v < nvec) ac[v] = fold_vec<BF16>(z[u], x[u], y[u], first);
+            }
+        }
+    } else if (BF16) {
+        uint16_t* ac = static_cast<uint16_t*>(ac_);
+        const uint16_t* av = static_cast<const uint16_t*>(av_);
+        const uint16_t* bv = static_cast<const uint16_t*>(bv_);
+        for (int64_t c = threadIdx.x; c < d; c += kRowBlock) {
+            const float z = first ? 0.0f : bf16_to_f32(ac[c]);
+            ac[c] = (uint16_t)f32_to_bf16(fold1<true>(z, bf16_to_f32(av[c]), bv ? bf16_to_f32(bv[c]) : 0.0f, first));
+        }
+    } else {
+        float* ac = static_cast<float*>(ac_);
+        const float* av = static_cast<const float*>(av_);
+        const float* bv = static_cast<const float*>(bv_);
+        for (int64_t c = threadIdx.x; c < d; c += kRowBlock) {
+            const float z = first ? 0.0f : ac[c];
+            ac[c] = fold1<false>(z, av[c], bv ? bv[c] : 0.0f, first);
+        }
+    }
+}
+
 template <bool BF16>
 __global__ __launch_bounds__(kRowBlock) void rows_fold_kernel(void* __restrict__ acc, const void* __restrict__ a,
                                                               const int64_t* __restrict__ a_rows,
@@ -50,60 +115,15 @@ __global__ __launch_bounds__(kRowBlock) void rows_fold_kernel(void* __restrict__
                                                               const int64_t* __restrict__ idx, int64_t n_idx,
                                                               int64_t n_rows, int64_t a_total, int64_t b_total,
                                                               int64_t d, int first, int vec) {
-    constexpr int V = BF16 ? 8 : 4;  // elements per 16-byte vector
+    const int64_t esz = BF16 ? 2 : 4;
     for (int64_t j = blockIdx.x; j < n_idx; j += gridDim.x) {
         const int64_t r = idx[j];
         const int64_t ar = a_rows ? a_rows[j] : j;
         const int64_t br = b ? (b_rows ? b_rows[j] : j) : -1;  // < 0: the row adds +0.0
         // the host checks every index; a row outside the tables is skipped, never touched
         if (r < 0 || r >= n_rows || ar < 0 || ar >= a_total || br >= b_total) continue;
-        if (BF16) {
-            uint16_t* ac = static_cast<uint16_t*>(acc) + r * d;
-            const uint16_t* av = static_cast<const uint16_t*>(a) + ar * d;
-            const uint16_t* bv = br >= 0 ? static_cast<const uint16_t*>(b) + br * d : nullptr;
-            if (vec) {
-                for (int64_t c = (int64_t)threadIdx.x * V; c < d; c += (int64_t)kRowBlock * V) {
-                    const ru4 x = *reinterpret_cast<const ru4*>(av + c);
-                    const ru4 y = bv ? *reinterpret_cast<const ru4*>(bv + c) : ru4{0u, 0u, 0u, 0u};
-                    const ru4 z = first ? ru4{0u, 0u, 0u, 0u} : *reinterpret_cast<const ru4*>(ac + c);
-                    ru4 o;
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        const float lo = fold1<true>(bf16_to_f32(z[k] & 0xFFFFu), bf16_to_f32(x[k] & 0xFFFFu),
-                                                     bf16_to_f32(y[k] & 0xFFFFu), first);
-                        const float hi = fold1<true>(bf16_to_f32(z[k] >> 16), bf16_to_f32(x[k] >> 16),
-                                                     bf16_to_f32(y[k] >> 16), first);
-                        o[k] = f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);
-                    }
-                    *reinterpret_cast<ru4*>(ac + c) = o;
-                }
-            } else {
-                for (int64_t c = threadIdx.x; c < d; c += kRowBlock) {
-                    const float z = first ? 0.0f : bf16_to_f32(ac[c]);
-                    ac[c] = (uint16_t)f32_to_bf16(fold1<true>(z, bf16_to_f32(av[c]), bv ? bf16_to_f32(bv[c]) : 0.0f, first));
-                }
-            }
-        } else {
-            float* ac = static_cast<float*>(acc) + r * d;
-            const float* av = static_cast<const float*>(a) + ar * d;
-            const float* bv = br >= 0 ? static_cast<const float*>(b) + br * d : nullptr;
-            if (vec) {
-                for (int64_t c = (int64_t)threadIdx.x * V; c < d; c += (int64_t)kRowBlock * V) {
-                    const rf4 x = *reinterpret_cast<const rf4*>(av + c);
-                    const rf4 y = bv ? *reinterpret_cast<const rf4*>(bv + c) : rf4{0.0f, 0.0f, 0.0f, 0.0f};
-                    const rf4 z = first ? rf4{0.0f, 0.0f, 0.0f, 0.0f} : *reinterpret_cast<const rf4*>(ac + c);
-                    rf4 o;
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) o[k] = fold1<false>(z[k], x[k], y[k], first);
-                    *reinterpret_cast<rf4*>(ac + c) = o;
-                }
-            } else {
-                for (int64_t c = threadIdx.x; c < d; c += kRowBlock) {
-                    const float z = first ? 0.0f : ac[c];
-                    ac[c] = fold1<false>(z, av[c], bv ? bv[c] : 0.0f, first);
-                }
-            }
-        }
+        fold_row<BF16>(static_cast<char*>(acc) + r * d * esz, static_cast<const char*>(a) + ar * d * esz,
+                       br >= 0 ? static_cast<const char*>(b) + br * d * esz : nullptr, d, first, vec);
     }
 }
 
@@ -114,55 +134,17 @@ template <bool BF16>
 __global__ __launch_bounds__(kRowBlock) void rows_fold_masked_kernel(void* __restrict__ acc, const void* __restrict__ a,
                                                                      const uint8_t* __restrict__ held, int64_t n_rows,
                                                                      int64_t d, int first, int vec) {
-    constexpr int V = BF16 ? 8 : 4;
+    const int64_t esz = BF16 ? 2 : 4;
     for (int64_t r = blockIdx.x; r < n_rows; r += gridDim.x) {
         if (held[r]) continue;
-        if (BF16) {
-            uint16_t* ac = static_cast<uint16_t*>(acc) + r * d;
-            const uint16_t* av = static_cast<const uint16_t*>(a) + r * d;
-            if (vec) {
-                for (int64_t c = (int64_t)threadIdx.x * V; c < d; c += (int64_t)kRowBlock * V) {
-                    const ru4 x = *reinterpret_cast<const ru4*>(av + c);
-                    const ru4 z = first ? ru4{0u, 0u, 0u, 0u} : *reinterpret_cast<const ru4*>(ac + c);
-                    ru4 o;
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        const float lo = fold1<true>(bf16_to_f32(z[k] & 0xFFFFu), bf16_to_f32(x[k] & 0xFFFFu), 0.0f, first);
-                        const float hi = fold1<true>(bf16_to_f32(z[k] >> 16), bf16_to_f32(x[k] >> 16), 0.0f, first);
-                        o[k] = f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);
-                    }
-                    *reinterpret_cast<ru4*>(ac + c) = o;
-                }
-            } else {
-                for (int64_t c = threadIdx.x; c < d; c += kRowBlock) {
-                    const float z = first ? 0.0f : bf16_to_f32(ac[c]);
-                    ac[c] = (uint16_t)f32_to_bf16(fold1<true>(z, bf16_to_f32(av[c]), 0.0f, first));
-                }
-            }
-        } else {
-            float* ac = static_cast<float*>(acc) + r * d;
-            const float* av = static_cast<const float*>(a) + r * d;
-            if (vec) {
-                for (int64_t c = (int64_t)threadIdx.x * V; c < d; c += (int64_t)kRowBlock * V) {
-                    const rf4 x = *reinterpret_cast<const rf4*>(av + c);
-                    const rf4 z = first ? rf4{0.0f, 0.0f, 0.0f, 0.0f} : *reinterpret_cast<const rf4*>(ac + c);
-                    rf4 o;
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) o[k] = fold1<false>(z[k], x[k], 0.0f, first);
-                    *reinterpret_cast<rf4*>(ac + c) = o;
-                }
-            } else {
-                for (int64_t c = threadIdx.x; c < d; c += kRowBlock) {
-                    const float z = first ? 0.0f : ac[c];
-                    ac[c] = fold1<false>(z, av[c], 0.0f, first);
-                }
-            }
-        }
+        fold_row<BF16>(static_cast<char*>(acc) + r * d * esz, static_cast<const char*>(a) + r * d * esz, nullptr, d,
+                       first, vec);
     }
 }
 
 // dst[j] = src[rows[j]], bit for bit, `bytes` per row: one block per row
-// (strided), 16-byte vectors when both tables are aligned.
+// (strided), 16-byte vectors (kRowUnroll per thread in flight) when both
+// tables are aligned.
 __global__ __launch_bounds__(kRowBlock) void rows_gather_kernel(char* __restrict__ dst, const char* __restrict__ src,
                                                                 const int64_t* __restrict__ rows, int64_t n,
                                                                 int64_t src_rows, int64_t bytes, int vec) {
@@ -172,8 +154,20 @@ __global__ __launch_bounds__(kRowBlock) void rows_gather_kernel(char* __restrict
         char* o = dst + j * bytes;
         const char* x = src + r * bytes;
         if (vec) {
-            for (int64_t c = (int64_t)threadIdx.x * 16; c < bytes; c += (int64_t)kRowBlock * 16)
-                *reinterpret_cast<ru4*>(o + c) = *reinterpret_cast<const ru4*>(x + c);
+            const int64_t nvec = bytes / 16;
+            for (int64_t v0 = threadIdx.x; v0 < nvec; v0 += (int64_t)kRowBlock * kRowUnroll) {
+                ru4 t[kRowUnroll];
+#pragma unroll
+                for (int u = 0; u < kRowUnroll; ++u) {
+                    const int64_t v = v0 + (int64_t)u * kRowBlock;
+                    if (v < nvec) t[u] = reinterpret_cast<const ru4*>(x)[v];
+                }
+#pragma unroll
+                for (int u = 0; u < kRowUnroll; ++u) {
+                    const int64_t v = v0 + (int64_t)u * kRowBlock;
+                    if (v < nvec) reinterpret_cast<ru4*>(o)[v] = t[u];
+                }
+            }
         } else {
             for (int64_t c = threadIdx.x; c < bytes; c += kRowBlock) o[c] = x[c];
         }
