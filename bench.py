@@ -634,7 +634,7 @@ def bench_tied_fold(device, stream, n_mb: int = 8, n_rows: int = 32768, rows_per
             "dense_fold_ms": t_dense, "row_fold_GBs": nbytes / (t_row * 1e-3) / 1e9, "bits_equal": same}
 
 
-def bench_release(device, stream, tokens: int = 2048, iters: int = 3):
+def bench_release(device, stream, tokens: int = 2048, iters: int = 3, moments: str = "device"):
     """Per-layer release (runtime/stage.py:3080-3099, RUNTIME-I23): the C1
     step runs on a side stream with on_param recording one event per block
     (12 tensors) as its update group is issued, while a forward-style
@@ -643,13 +643,17 @@ def bench_release(device, stream, tokens: int = 2048, iters: int = 3):
     working-copy matrices.  Against: the single-launch step, then the same
     forward after it.  Reported: time from the step's start to block 0's
     release and to the last block's, and the wall time of step + forward
-    both ways (HIP events)."""
+    both ways (HIP events).  moments="host" runs the "adamw-host" recipe's
+    memory contract (moments in pinned host memory, updated in place over
+    PCIe), the case the reference built the release for, with one
+    iteration."""
     from elysium_wan_amd import optim
 
     params, grads = make_shard(device)
     per_block = len(block_shapes(D_MODEL))
     opt = optim.FusedAdamW(params, lr=LR, betas=BETAS, eps=EPS, weight_decay=WD, order="host", max_norm=MAX_NORM,
-                           working_copy=True, release_elems=12 * D_MODEL * D_MODEL + 13 * D_MODEL)  # one group per block
+                           working_copy=True, moments=moments,
+                           release_elems=12 * D_MODEL * D_MODEL + 13 * D_MODEL)  # one group per block
     copies = opt.working_copies
     x = torch.randn(tokens, D_MODEL, device=device).bfloat16()
     side = torch.cuda.Stream(device)
@@ -676,8 +680,14 @@ def bench_release(device, stream, tokens: int = 2048, iters: int = 3):
         return start.elapsed_time(end)
 
     def overlapped():
+        """The reference's overlapped step (runtime/stage.py:3094-3099): the
+        step on a side thread and stream, the forward on this thread waiting
+        for each block's event as the side thread records it."""
+        import threading
+
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         events = [None] * N_BLOCKS
+        ready = [threading.Event() for _ in range(N_BLOCKS)]
         left = [per_block] * N_BLOCKS
         start.record(stream)
         side.wait_stream(stream)
@@ -689,13 +699,21 @@ def bench_release(device, stream, tokens: int = 2048, iters: int = 3):
                 ev = torch.cuda.Event(enable_timing=True)
                 ev.record(side)
                 events[b] = ev
+                ready[b].set()
 
-        with torch.cuda.stream(side):
-            opt.step(grads=grads, on_param=release)
+        def run_step():
+            torch.cuda.set_device(device)
+            with torch.cuda.stream(side):
+                opt.step(grads=grads, on_param=release)
+
+        t = threading.Thread(target=run_step)
+        t.start()
         for b in range(N_BLOCKS):
+            ready[b].wait()
             stream.wait_event(events[b])
             forward(b, stream)
         end.record(stream)
+        t.join()
         stream.wait_stream(side)
         torch.cuda.synchronize()
         return start.elapsed_time(end), start.elapsed_time(events[0]), start.elapsed_time(events[-1])
@@ -712,6 +730,7 @@ def bench_release(device, stream, tokens: int = 2048, iters: int = 3):
     torch.cuda.synchronize()
     del opt, params, grads, copies
     return {
+        "moments": moments,
         "forward_tokens": tokens,
         "forward_alone_ms": fwd_start.elapsed_time(fwd_end),
         "serial_step_then_forward_ms": min(ser),
@@ -1502,6 +1521,8 @@ def extra_legs(device, stream):
     return [
         ("fold", "fold leg", lambda: bench_fold(device, stream)),
         ("release", "per-layer release leg", lambda: bench_release(device, stream)),
+        ("release_host_moments", "per-layer release leg, host moments",
+         lambda: bench_release(device, stream, iters=1, moments="host")),
         ("tied_fold", "tied-table row fold leg", lambda: bench_tied_fold(device, stream)),
         ("elementwise", "elementwise leg", lambda: bench_elementwise(device, stream)),
         ("c1_torch_order", "torch-order leg", lambda: bench_torch_order(device, stream)),
@@ -1514,7 +1535,7 @@ def extra_legs(device, stream):
     ]
 
 
-LEG_NAMES = ("fold", "release", "tied_fold", "elementwise", "c1_torch_order", "host_moments", "check_host_adamw", "wire",
+LEG_NAMES = ("fold", "release", "release_host_moments", "tied_fold", "elementwise", "c1_torch_order", "host_moments", "check_host_adamw", "wire",
              "hbm_reference", "configs", "c1_placement")
 
 
