@@ -1370,12 +1370,14 @@ def trace_summary(step_dir: str, codec_dir: str, bench_json: list | None) -> Non
 
 
 def bench_wire(device, stream, iters: int = 10):
-    """The GPU half of the lossless boundary wires on C1's activation
-    [8, 2048, 2560] bf16 (the host half, zlib, is not timed): the byte-plane
-    split and join (4 B/elem), the e4m3 nibble encode (2 B read + 1 B written)
-    and decode (1 B + 4 B fp32), and the scaled-fp8 wire's exponent recovery
-    plus byte image in one call (ely_fp8_recover_image: 2 B read, 1 B
-    written), rotating through 4 inputs."""
+    """The lossless boundary wires on C1's activation [8, 2048, 2560] bf16.
+    The GPU half, between HIP events: the byte-plane split and join
+    (4 B/elem), the e4m3 nibble encode (2 B read + 1 B written) and decode
+    (1 B + 4 B fp32), and the scaled-fp8 wire's exponent recovery plus byte
+    image in one call (ely_fp8_recover_image: 2 B read, 1 B written),
+    rotating through 4 inputs.  Then the whole planes.encode / decode and
+    encode_scaled_fp8 / decode calls (GPU half, the copy to the host and the
+    host's zlib), wall-clock seconds."""
     from elysium_wan_amd import _lib, fp8
 
     L = _lib.load()
@@ -1420,6 +1422,24 @@ def bench_wire(device, stream, iters: int = 10):
     torch.cuda.synchronize()
     if int(bad.item()):
         raise RuntimeError("bench_wire: a recipe round trip was not recoverable")
+    # the whole wire call as the reference's caller makes it (GPU half, the
+    # copy to the host and the host's zlib), wall-clock seconds, one call
+    from elysium_wan_amd import planes as _planes
+
+    def wall(fn):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        r = fn()
+        torch.cuda.synchronize()
+        return time.perf_counter() - t0, r
+
+    _planes.encode(xs[0])  # warm: library load, thread pool
+    secs, (payload, shape) = wall(lambda: _planes.encode(xs[0]))
+    out["planes_encode_bf16_s"] = secs
+    out["planes_decode_bf16_s"], _ = wall(lambda: _planes.decode(payload, shape))
+    secs, (payload, shape) = wall(lambda: _planes.encode_scaled_fp8(rts[0], "e4m3"))
+    out["scaled_fp8_encode_s"] = secs
+    out["scaled_fp8_decode_s"], _ = wall(lambda: _planes.decode(payload, shape))
     del xs, planes, back, rts, ks, qs
     return out
 

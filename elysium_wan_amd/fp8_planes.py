@@ -19,7 +19,7 @@ import numpy as np
 import torch
 
 from . import _lib
-from .planes import _compress, _decompress
+from .planes import _compress_all, _decompress
 
 _HDR = struct.Struct("<QII")
 
@@ -46,8 +46,7 @@ def encode(t: torch.Tensor):
     )
     if int(bad.item()):
         raise AssertionError("boundary is not FP8-representable: recipe mismatch")
-    c_hi = _compress(hi.cpu().numpy().tobytes())
-    c_lo = _compress(lo.cpu().numpy().tobytes())
+    c_hi, c_lo = _compress_all([hi.cpu().numpy(), lo.cpu().numpy()])
     return _HDR.pack(n, len(c_hi), len(c_lo)) + c_hi + c_lo, tuple(t.shape)
 
 
