@@ -21,6 +21,7 @@ reference's message.
 from __future__ import annotations
 
 import math
+import os
 import struct
 import threading
 import zlib
@@ -54,6 +55,7 @@ def _compress(b) -> bytes:
 
 
 _POOL = None
+_POOL_PID = None
 _POOL_LOCK = threading.Lock()
 
 
@@ -61,14 +63,18 @@ def _compress_all(bufs) -> list:
     """Each buffer compressed on its own (zlib level 1), the payload's blobs
     in order: the same bytes as one after the other, but the planes go
     through zlib on host threads at once (zlib releases the GIL), so the
-    host half of an encode takes its slowest plane's time, not their sum."""
-    global _POOL
-    if len(bufs) < 2 or sum(len(memoryview(b).cast("B")) for b in bufs) < (1 << 20):
+    host half of an encode takes its slowest plane's time, not their sum.
+    A forked child starts its own pool: the parent's threads do not exist
+    there."""
+    global _POOL, _POOL_PID
+    if len(bufs) < 2 or sum(memoryview(b).nbytes for b in bufs) < (1 << 20):
         return [_compress(b) for b in bufs]
     with _POOL_LOCK:
-        if _POOL is None:
+        if _POOL is None or _POOL_PID != os.getpid():
             _POOL = ThreadPoolExecutor(max_workers=8, thread_name_prefix="ely-planes")
-    return list(_POOL.map(_compress, bufs))
+            _POOL_PID = os.getpid()
+        pool = _POOL
+    return list(pool.map(_compress, bufs))
 
 
 def _decompress(b: bytes) -> bytes:

@@ -314,3 +314,34 @@ def test_argument_errors_of_the_row_entry_points(lib):
     assert lib.ely_rows_fold_masked(fake, fake, None, 8, 16, _lib.F32, 1, None) == _lib.EINVAL
     assert lib.ely_rows_fold_masked(fake, fake, fake, 8, 16, 9, 1, None) == _lib.EINVAL
     assert lib.ely_rows_fold_masked(None, None, None, 0, 16, _lib.F32, 1, None) == _lib.OK
+
+
+def _compress_in_child(q, bufs):
+    from elysium_wan_amd import planes
+
+    q.put(planes._compress_all(bufs))
+
+
+def test_plane_compression_keeps_the_serial_bytes_and_survives_a_fork():
+    """The byte planes go through zlib on host threads; the blobs are the
+    serial ones, in order, and a forked child (whose copy of the parent's
+    pool has no threads) compresses with a pool of its own."""
+    import multiprocessing as mp
+    import zlib
+
+    import numpy as np
+
+    from elysium_wan_amd import planes
+
+    rng = np.random.default_rng(5)
+    bufs = [rng.integers(0, 4, size=(1 << 19) + j, dtype=np.uint8) for j in range(4)]
+    serial = [zlib.compress(b, 1) for b in bufs]
+    assert planes._compress_all(bufs) == serial  # the parent's pool now exists
+    ctx = mp.get_context("fork")
+    q = ctx.Queue()
+    p = ctx.Process(target=_compress_in_child, args=(q, bufs))
+    p.start()
+    got = q.get(timeout=60)
+    p.join(timeout=60)
+    assert p.exitcode == 0
+    assert got == serial
