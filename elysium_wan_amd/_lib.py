@@ -48,8 +48,7 @@ EXPORTS = (
     "ely_fold_add_bf16",
     "ely_scale_inplace",
     "ely_rows_fold",
-    "ely_rows_gather",
-    "ely_rows_fold_masked",
+    "ely_rows_split",
     "ely_set_max_blocks",
     "ely_host_device_pointer",
     "ely_byteplanes_split",
@@ -121,8 +120,7 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
         L.ely_fold_add_bf16.argtypes = [P, P, I32, I64, P]
         L.ely_scale_inplace.argtypes = [TP, I32, P, P]
         L.ely_rows_fold.argtypes = [P, P, P, P, P, P, I64, I64, I64, I64, I64, I32, I32, P]
-        L.ely_rows_gather.argtypes = [P, P, P, I64, I64, I64, I32, P]
-        L.ely_rows_fold_masked.argtypes = [P, P, P, I64, I64, I32, I32, P]
+        L.ely_rows_split.argtypes = [P, P, P, P, I64, I64, I64, I32, I32, P]
         L.ely_set_max_blocks.argtypes = [I32]
         L.ely_host_device_pointer.argtypes = [P, ctypes.POINTER(ctypes.c_void_p)]
         L.ely_byteplanes_split.argtypes = [P, I64, I32, P, P]

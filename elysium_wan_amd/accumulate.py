@@ -202,14 +202,15 @@ class TiedRowFold:
     or bf16, on the GPU), rows T_mb (ascending unique ids, int64).
     add_embed(mb, e_rows): e_mb[T_mb] in ascending id.  Either may come
     first; out-of-order microbatches wait.  The row bookkeeping (which rows
-    are held) runs on the host in numpy; a Head gradient's free rows fold in
-    one launch by mask (ely_rows_fold_masked), its held rows are copied out
-    by one gather (ely_rows_gather), and they resolve in one launch of the
-    row fold (ely_rows_fold) that reads the embedding rows in place, by
-    index."""
+    are held) runs on the host in numpy; one launch takes a Head gradient
+    (ely_rows_split: its free rows fold, its held rows are copied out), and
+    the held rows resolve in one launch of the row fold (ely_rows_fold) that
+    reads the embedding rows in place, by index."""
 
     def __init__(self, n_rows: int, order) -> None:
         self.n_rows = int(n_rows)
+        if not 0 <= self.n_rows < 2**31:
+            raise ValueError(f"tied fold: a table of {self.n_rows} rows (the row slots are int32)")
         self.order = list(order)
         self.pos = 0  # next position of `order` whose Head gradient is taken
         self.acc = torch.empty(0)  # allocated by the first Head gradient
@@ -217,7 +218,7 @@ class TiedRowFold:
         self.heads: dict = {}  # mb -> (h, rows) waiting for its prefix
         self.embeds: dict = {}  # mb -> e_rows until its held rows resolve
         # [(mb, held row ids, the same on the GPU, h on them, T_mb, first, each
-        # held row's place in T_mb or -1)], oldest first
+        # held row's place in T_mb or -1 on the GPU)], oldest first
         self.held: list = []
         # held-row multiplicity; the row bookkeeping runs in numpy (torch's CPU
         # nonzero over a 32,768-row mask took ~0.1 ms a call)
@@ -252,25 +253,17 @@ class TiedRowFold:
                 continue
             return
 
-    @staticmethod
-    def _to_dev(a: np.ndarray, dev) -> torch.Tensor:
-        """A host int64 index list on the GPU without a host wait: staged
-        through torch's pinned-memory cache and copied on the current stream
-        (the cache keeps the staging block until that copy is done)."""
-        return torch.from_numpy(np.ascontiguousarray(a, dtype=np.int64)).pin_memory().to(dev, non_blocking=True)
-
-    def _fold_rows(self, a, a_rows_d, b, b_rows_d, idx_d, n_idx: int, first: bool) -> None:
+    def _fold_rows(self, a, a_rows_d, b, b_rows_d, idx_d, n_idx: int, first: bool, stream) -> None:
         """acc[idx] (=|+=) a[a_rows, or row j] + (b[b_rows, or row j], or
         +0.0 where b_rows is negative or there is no b), one launch; every
         index list already on the GPU."""
         if n_idx == 0:
             return
-        dev = self.acc.device
         L = _lib.load()
         _lib.check(L.ely_rows_fold(self.acc.data_ptr(), a.data_ptr(), None if a_rows_d is None else a_rows_d.data_ptr(),
                                    None if b is None else b.data_ptr(), None if b_rows_d is None else b_rows_d.data_ptr(),
                                    idx_d.data_ptr(), n_idx, self.n_rows, a.shape[0], 0 if b is None else b.shape[0],
-                                   self.acc.shape[1], _lib.dtype_code(self.acc), int(first), _lib.stream_ptr(dev)),
+                                   self.acc.shape[1], _lib.dtype_code(self.acc), int(first), stream),
                    "tied fold")
 
     def _take_head(self) -> None:
@@ -278,47 +271,54 @@ class TiedRowFold:
         h, rows = self.heads.pop(mb)
         if self.first:
             self.acc = torch.empty_like(h)
-        if rows.size and (int(rows.min()) < 0 or int(rows.max()) >= self.n_rows):
-            raise RuntimeError(f"tied fold: rows of mb {mb} outside [0, {self.n_rows})")
+        n = self.n_rows
+        if rows.size and (int(rows.min()) < 0 or int(rows.max()) >= n):
+            raise RuntimeError(f"tied fold: rows of mb {mb} outside [0, {n})")
         mask = self.pend > 0
         mask[rows] = True
         keep = np.flatnonzero(mask)
-        dev = h.device
-        L = _lib.load()
-        # free rows: acc = h + 0.0 (first) or acc + (h + 0.0), read straight
-        # from h, every row the mask does not hold
-        held_d = torch.from_numpy(mask.view(np.uint8)).pin_memory().to(dev, non_blocking=True)
-        _lib.check(L.ely_rows_fold_masked(self.acc.data_ptr(), h.data_ptr(), held_d.data_ptr(), self.n_rows, h.shape[1],
-                                          _lib.dtype_code(self.acc), int(self.first), _lib.stream_ptr(dev)), "tied fold")
-        # held rows: copied out of h (bit for bit) so that h itself can go
-        keep_d = self._to_dev(keep, dev)
-        hk = torch.empty((keep.size, h.shape[1]), dtype=h.dtype, device=dev)
-        if keep.size:
-            _lib.check(L.ely_rows_gather(hk.data_ptr(), h.data_ptr(), keep_d.data_ptr(), keep.size, self.n_rows,
-                                         h.shape[1], _lib.dtype_code(h), _lib.stream_ptr(dev)), "tied fold")
+        k = keep.size
         # each held row's place among the microbatch's rows, -1 for a row it
         # did not touch (that row adds +0.0 when it resolves)
-        at = np.full(self.n_rows, -1, dtype=np.int64)
+        at = np.full(n, -1, dtype=np.int64)
         at[rows] = np.arange(rows.size, dtype=np.int64)
-        self.held.append((mb, keep, keep_d, hk, rows, self.first, at[keep]))
+        # one upload per Head gradient: the held rows, their places and each
+        # row's slot among the held ones (-1: free), packed in one pinned block
+        # (from torch's pinned-memory cache, which keeps it until the copy on
+        # this stream is done)
+        stage = torch.empty(2 * k + (n + 1) // 2, dtype=torch.int64, pin_memory=True)
+        host = stage.numpy()
+        host[:k] = keep
+        host[k : 2 * k] = at[keep]
+        slot = host[2 * k :].view(np.int32)[:n]
+        slot.fill(-1)
+        slot[keep] = np.arange(k, dtype=np.int32)
+        dev = h.device
+        up = stage.to(dev, non_blocking=True)
+        keep_d, b_rows_d, slot_d = up[:k], up[k : 2 * k], up[2 * k :].view(torch.int32)
+        # free rows: acc = h + 0.0 (first) or acc + (h + 0.0); held rows:
+        # copied out of h (bit for bit) so that h itself can go; one pass
+        hk = torch.empty((k, h.shape[1]), dtype=h.dtype, device=dev)
+        L = _lib.load()
+        _lib.check(L.ely_rows_split(self.acc.data_ptr(), h.data_ptr(), slot_d.data_ptr(), hk.data_ptr() if k else None,
+                                    n, k, h.shape[1], _lib.dtype_code(self.acc), int(self.first), _lib.stream_ptr(dev)),
+                   "tied fold")
+        self.held.append((mb, keep, keep_d, hk, rows, self.first, b_rows_d))
         self.pend[keep] += 1
         self.first = False
         self.pos += 1
 
     def _resolve(self) -> None:
-        mb, keep, keep_d, hk, rows, first, b_rows = self.held.pop(0)
+        mb, keep, keep_d, hk, rows, first, b_rows_d = self.held.pop(0)
         e_rows = self.embeds.pop(mb)
         if e_rows.dim() != 2 or e_rows.shape[0] != rows.size or e_rows.shape[1:] != hk.shape[1:]:
             raise RuntimeError(
                 f"tied fold: embedding rows of mb {mb} have shape {tuple(e_rows.shape)}, "
                 f"want ({rows.size}, {tuple(hk.shape[1:])})"
             )
-        e, b_rows_d = None, None
-        if rows.size:
-            b_rows_d = self._to_dev(b_rows, hk.device)
-            e = e_rows.to(hk.device, hk.dtype).contiguous()
+        e = e_rows.to(hk.device, hk.dtype).contiguous() if rows.size else None
         # held rows: acc = hk + e_on (first) or acc + (hk + e_on)
-        self._fold_rows(hk, None, e, b_rows_d, keep_d, keep.size, first)
+        self._fold_rows(hk, None, e, None if e is None else b_rows_d, keep_d, keep.size, first, _lib.stream_ptr(hk.device))
         self.pend[keep] -= 1
 
     def complete(self) -> bool:

@@ -13,8 +13,8 @@
 // (strided), 16-byte vectors across the row when it is aligned.  e_j is the
 // embedding row b[b_rows[j]] of a held row the microbatch touched, +0.0 for
 // one it did not (b_rows[j] < 0), or b[j] of a compact b.  A second kernel
-// gathers the held rows of a Head gradient, bit for bit, before the
-// gradient itself is released.
+// takes a whole Head gradient in one pass: its free rows fold, its held
+// rows are copied out bit for bit, so that the gradient itself can go.
 #include <algorithm>
 
 #include "ely_device.hpp"
@@ -26,6 +26,8 @@ namespace ely {
 namespace {
 
 constexpr int kRowBlock = 256;
+// one block per row up to this many; longer lists stride
+constexpr int64_t kRowGrid = 1 << 16;
 
 typedef float rf4 __attribute__((ext_vector_type(4)));
 typedef uint32_t ru4 __attribute__((ext_vector_type(4)));
@@ -127,50 +129,47 @@ __global__ __launch_bounds__(kRowBlock) void rows_fold_kernel(void* __restrict__
     }
 }
 
-// The free rows of a Head gradient by mask instead of by index list: every
-// row r with held[r] == 0 takes acc[r] = a[r] + 0.0 (first) or
-// acc[r] + (a[r] + 0.0), each add rounded to the dtype; held rows are left.
-template <bool BF16>
-__global__ __launch_bounds__(kRowBlock) void rows_fold_masked_kernel(void* __restrict__ acc, const void* __restrict__ a,
-                                                                     const uint8_t* __restrict__ held, int64_t n_rows,
-                                                                     int64_t d, int first, int vec) {
-    const int64_t esz = BF16 ? 2 : 4;
-    for (int64_t r = blockIdx.x; r < n_rows; r += gridDim.x) {
-        if (held[r]) continue;
-        fold_row<BF16>(static_cast<char*>(acc) + r * d * esz, static_cast<const char*>(a) + r * d * esz, nullptr, d,
-                       first, vec);
+// A row of `bytes` bytes copied bit for bit: 16-byte vectors (kRowUnroll per
+// thread in flight) when both rows are aligned, bytes otherwise.
+__device__ __forceinline__ void copy_row(char* o, const char* x, int64_t bytes, int vec) {
+    if (vec) {
+        const int64_t nvec = bytes / 16;
+        for (int64_t v0 = threadIdx.x; v0 < nvec; v0 += (int64_t)kRowBlock * kRowUnroll) {
+            ru4 t[kRowUnroll];
+#pragma unroll
+            for (int u = 0; u < kRowUnroll; ++u) {
+                const int64_t v = v0 + (int64_t)u * kRowBlock;
+                if (v < nvec) t[u] = reinterpret_cast<const ru4*>(x)[v];
+            }
+#pragma unroll
+            for (int u = 0; u < kRowUnroll; ++u) {
+                const int64_t v = v0 + (int64_t)u * kRowBlock;
+                if (v < nvec) reinterpret_cast<ru4*>(o)[v] = t[u];
+            }
+        }
+    } else {
+        for (int64_t c = threadIdx.x; c < bytes; c += kRowBlock) o[c] = x[c];
     }
 }
 
-// dst[j] = src[rows[j]], bit for bit, `bytes` per row: one block per row
-// (strided), 16-byte vectors (kRowUnroll per thread in flight) when both
-// tables are aligned.
-__global__ __launch_bounds__(kRowBlock) void rows_gather_kernel(char* __restrict__ dst, const char* __restrict__ src,
-                                                                const int64_t* __restrict__ rows, int64_t n,
-                                                                int64_t src_rows, int64_t bytes, int vec) {
-    for (int64_t j = blockIdx.x; j < n; j += gridDim.x) {
-        const int64_t r = rows[j];
-        if (r < 0 || r >= src_rows) continue;  // the host checks every index
-        char* o = dst + j * bytes;
-        const char* x = src + r * bytes;
-        if (vec) {
-            const int64_t nvec = bytes / 16;
-            for (int64_t v0 = threadIdx.x; v0 < nvec; v0 += (int64_t)kRowBlock * kRowUnroll) {
-                ru4 t[kRowUnroll];
-#pragma unroll
-                for (int u = 0; u < kRowUnroll; ++u) {
-                    const int64_t v = v0 + (int64_t)u * kRowBlock;
-                    if (v < nvec) t[u] = reinterpret_cast<const ru4*>(x)[v];
-                }
-#pragma unroll
-                for (int u = 0; u < kRowUnroll; ++u) {
-                    const int64_t v = v0 + (int64_t)u * kRowBlock;
-                    if (v < nvec) reinterpret_cast<ru4*>(o)[v] = t[u];
-                }
-            }
-        } else {
-            for (int64_t c = threadIdx.x; c < bytes; c += kRowBlock) o[c] = x[c];
-        }
+// A Head gradient in one pass, one block per row: a row r with
+// slot[r] < 0 is free and takes acc[r] = a[r] + 0.0 (first) or
+// acc[r] + (a[r] + 0.0), each add rounded to the dtype; a held row
+// (slot[r] >= 0) is copied to held_out[slot[r]] bit for bit and acc[r] is
+// left for its resolve.
+template <bool BF16>
+__global__ __launch_bounds__(kRowBlock) void rows_split_kernel(void* __restrict__ acc, const void* __restrict__ a,
+                                                               const int32_t* __restrict__ slot,
+                                                               void* __restrict__ held_out, int64_t n_rows,
+                                                               int64_t n_held, int64_t d, int first, int vec) {
+    const int64_t row_bytes = d * (BF16 ? 2 : 4);
+    for (int64_t r = blockIdx.x; r < n_rows; r += gridDim.x) {
+        const int64_t s = slot[r];
+        const char* x = static_cast<const char*>(a) + r * row_bytes;
+        if (s < 0)
+            fold_row<BF16>(static_cast<char*>(acc) + r * row_bytes, x, nullptr, d, first, vec);
+        else if (s < n_held)  // the host numbers the held rows 0..n_held-1
+            copy_row(static_cast<char*>(held_out) + s * row_bytes, x, row_bytes, vec);
     }
 }
 
@@ -193,7 +192,7 @@ extern "C" int ely_rows_fold(void* acc, const void* a, const int64_t* a_rows, co
         const int64_t esz = dtype == ELY_BF16 ? 2 : 4;
         const int64_t v = 16 / esz;
         const int vec = (d % v == 0) && aligned16(acc) && aligned16(a) && (!b || aligned16(b)) ? 1 : 0;
-        const int64_t blocks = std::min<int64_t>(n_idx, mt_blocks(8));
+        const int64_t blocks = std::min<int64_t>(n_idx, kRowGrid);
         hipStream_t s = static_cast<hipStream_t>(stream);
         if (dtype == ELY_BF16)
             hipLaunchKernelGGL(rows_fold_kernel<true>, dim3((unsigned)blocks), dim3(kRowBlock), 0, s, acc, a, a_rows, b,
@@ -205,39 +204,24 @@ extern "C" int ely_rows_fold(void* acc, const void* a, const int64_t* a_rows, co
     });
 }
 
-extern "C" int ely_rows_fold_masked(void* acc, const void* a, const uint8_t* held, int64_t n_rows, int64_t d,
-                                    int32_t dtype, int32_t first, void* stream) {
+extern "C" int ely_rows_split(void* acc, const void* a, const int32_t* slot, void* held_out, int64_t n_rows,
+                              int64_t n_held, int64_t d, int32_t dtype, int32_t first, void* stream) {
     return guarded([&] {
-        if (dtype != ELY_F32 && dtype != ELY_BF16) fail(ELY_EINVAL, "ely_rows_fold_masked: dtype must be ELY_F32 or ELY_BF16");
-        if (n_rows < 0 || d < 0) fail(ELY_EINVAL, "ely_rows_fold_masked: negative size");
+        if (dtype != ELY_F32 && dtype != ELY_BF16) fail(ELY_EINVAL, "ely_rows_split: dtype must be ELY_F32 or ELY_BF16");
+        if (n_rows < 0 || n_held < 0 || d < 0) fail(ELY_EINVAL, "ely_rows_split: negative size");
+        if (n_held > n_rows) fail(ELY_EINVAL, "ely_rows_split: more held rows than rows");
         if (n_rows == 0 || d == 0) return;
-        if (!acc || !a || !held) fail(ELY_EINVAL, "ely_rows_fold_masked: null pointer");
+        if (!acc || !a || !slot || (n_held && !held_out)) fail(ELY_EINVAL, "ely_rows_split: null pointer");
         const int64_t v = dtype == ELY_BF16 ? 8 : 4;
-        const int vec = (d % v == 0) && aligned16(acc) && aligned16(a) ? 1 : 0;
-        const int64_t blocks = std::min<int64_t>(n_rows, mt_blocks(8));
+        const int vec = (d % v == 0) && aligned16(acc) && aligned16(a) && (!n_held || aligned16(held_out)) ? 1 : 0;
+        const int64_t blocks = std::min<int64_t>(n_rows, kRowGrid);
         hipStream_t s = static_cast<hipStream_t>(stream);
         if (dtype == ELY_BF16)
-            hipLaunchKernelGGL(rows_fold_masked_kernel<true>, dim3((unsigned)blocks), dim3(kRowBlock), 0, s, acc, a, held,
-                               n_rows, d, first ? 1 : 0, vec);
+            hipLaunchKernelGGL(rows_split_kernel<true>, dim3((unsigned)blocks), dim3(kRowBlock), 0, s, acc, a, slot,
+                               held_out, n_rows, n_held, d, first ? 1 : 0, vec);
         else
-            hipLaunchKernelGGL(rows_fold_masked_kernel<false>, dim3((unsigned)blocks), dim3(kRowBlock), 0, s, acc, a, held,
-                               n_rows, d, first ? 1 : 0, vec);
-        check_launch("rows_fold_masked_kernel");
-    });
-}
-
-extern "C" int ely_rows_gather(void* dst, const void* src, const int64_t* rows, int64_t n, int64_t src_rows,
-                               int64_t d, int32_t dtype, void* stream) {
-    return guarded([&] {
-        if (dtype != ELY_F32 && dtype != ELY_BF16) fail(ELY_EINVAL, "ely_rows_gather: dtype must be ELY_F32 or ELY_BF16");
-        if (n < 0 || src_rows < 0 || d < 0) fail(ELY_EINVAL, "ely_rows_gather: negative size");
-        if (n == 0 || d == 0) return;
-        if (!dst || !src || !rows) fail(ELY_EINVAL, "ely_rows_gather: null pointer");
-        const int64_t bytes = d * (dtype == ELY_BF16 ? 2 : 4);
-        const int vec = bytes % 16 == 0 && aligned16(dst) && aligned16(src) ? 1 : 0;
-        const int64_t blocks = std::min<int64_t>(n, mt_blocks(8));
-        hipLaunchKernelGGL(rows_gather_kernel, dim3((unsigned)blocks), dim3(kRowBlock), 0, static_cast<hipStream_t>(stream),
-                           static_cast<char*>(dst), static_cast<const char*>(src), rows, n, src_rows, bytes, vec);
-        check_launch("rows_gather_kernel");
+            hipLaunchKernelGGL(rows_split_kernel<false>, dim3((unsigned)blocks), dim3(kRowBlock), 0, s, acc, a, slot,
+                               held_out, n_rows, n_held, d, first ? 1 : 0, vec);
+        check_launch("rows_split_kernel");
     });
 }

@@ -232,20 +232,16 @@ int ely_rows_fold(void* acc, const void* a, const int64_t* a_rows, const void* b
                   const int64_t* idx, int64_t n_idx, int64_t n_rows, int64_t a_total, int64_t b_total, int64_t d,
                   int32_t dtype, int32_t first, void* stream);
 
-/* ely_rows_fold over the free rows of a Head gradient, given by a mask
- * instead of an index list (runtime/accumulate.py:210-213): every row r of
- * [n_rows, d] with held[r] == 0 takes acc[r] = a[r] + 0.0 (first) or
- * acc[r] + (a[r] + 0.0), each add rounded to dtype; rows with held[r] != 0
- * are left.  held: device uint8 [n_rows].  dtype ELY_F32 or ELY_BF16. */
-int ely_rows_fold_masked(void* acc, const void* a, const uint8_t* held, int64_t n_rows, int64_t d, int32_t dtype,
-                         int32_t first, void* stream);
-
-/* TiedRowFold's copy of a Head gradient's held rows (runtime/accumulate.py:
- * 221, `h[ki].clone()`): dst[j] = src[rows[j]] bit for bit, j < n; src:
- * [src_rows, d], dst: compact [n, d]; rows a device int64 array (an index
- * outside src is skipped).  dtype ELY_F32 or ELY_BF16. */
-int ely_rows_gather(void* dst, const void* src, const int64_t* rows, int64_t n, int64_t src_rows, int64_t d,
-                    int32_t dtype, void* stream);
+/* A Head gradient taken in one pass (runtime/accumulate.py:203-221): a row r
+ * of [n_rows, d] with slot[r] < 0 is free and takes acc[r] = a[r] + 0.0
+ * (first) or acc[r] + (a[r] + 0.0), each add rounded to dtype (the
+ * reference's `h[fi] + 0.0` folds, :210-213); a held row, slot[r] >= 0, is
+ * copied bit for bit to held_out[slot[r]] (`h[ki].clone()`, :221) and acc[r]
+ * is left.  slot: device int32 [n_rows], the held rows numbered
+ * 0..n_held-1 (a slot at or past n_held is skipped); held_out: [n_held, d].
+ * dtype ELY_F32 or ELY_BF16. */
+int ely_rows_split(void* acc, const void* a, const int32_t* slot, void* held_out, int64_t n_rows, int64_t n_held,
+                   int64_t d, int32_t dtype, int32_t first, void* stream);
 
 /* In-place g <- g * (*coef_dev) over a tensor list, the product rounded to
  * each tensor's dtype: the scaling step of clip_grad_norm_

@@ -308,12 +308,14 @@ def test_argument_errors_of_the_row_entry_points(lib):
     assert b"compact b" in lib.ely_last_error()
     assert lib.ely_rows_fold(fake, fake, None, None, None, fake, 4, 8, 2, 0, 16, _lib.F32, 0, None) == _lib.EINVAL
     assert lib.ely_rows_fold(None, None, None, None, None, None, 0, 8, 0, 0, 16, _lib.F32, 0, None) == _lib.OK
-    assert lib.ely_rows_gather(fake, fake, None, 4, 8, 16, _lib.BF16, None) == _lib.EINVAL
-    assert lib.ely_rows_gather(fake, fake, fake, -1, 8, 16, _lib.BF16, None) == _lib.EINVAL
-    assert lib.ely_rows_gather(None, None, None, 0, 8, 16, _lib.BF16, None) == _lib.OK
-    assert lib.ely_rows_fold_masked(fake, fake, None, 8, 16, _lib.F32, 1, None) == _lib.EINVAL
-    assert lib.ely_rows_fold_masked(fake, fake, fake, 8, 16, 9, 1, None) == _lib.EINVAL
-    assert lib.ely_rows_fold_masked(None, None, None, 0, 16, _lib.F32, 1, None) == _lib.OK
+    assert lib.ely_rows_split(fake, fake, None, fake, 8, 2, 16, _lib.F32, 1, None) == _lib.EINVAL
+    assert lib.ely_rows_split(fake, fake, fake, None, 8, 2, 16, _lib.F32, 1, None) == _lib.EINVAL
+    assert b"null pointer" in lib.ely_last_error()
+    assert lib.ely_rows_split(fake, fake, fake, fake, 8, 2, 16, 9, 1, None) == _lib.EINVAL
+    assert lib.ely_rows_split(fake, fake, fake, fake, 8, 9, 16, _lib.BF16, 1, None) == _lib.EINVAL
+    assert b"more held rows" in lib.ely_last_error()
+    assert lib.ely_rows_split(fake, fake, fake, fake, -1, 0, 16, _lib.BF16, 1, None) == _lib.EINVAL
+    assert lib.ely_rows_split(None, None, None, None, 0, 0, 16, _lib.F32, 1, None) == _lib.OK
 
 
 def _compress_in_child(q, bufs):
