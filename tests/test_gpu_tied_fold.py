@@ -126,3 +126,38 @@ def test_tied_fold_fuzz_equals_the_stock_fold(oracle, m, n_rows, d, bf16, perm_s
     torch.cuda.synchronize()
     want = _stock_fold(oracle, hs, rows, es, dtype).reshape(-1)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_tied_fold_at_the_benchmark_size_equals_the_dense_fold(dtype):
+    """The tied_fold leg's shape: a 32,768 x 2,560 table, 8 microbatches of
+    4,096 rows, the embedding rows one microbatch behind the Head gradients
+    (the held set grows to the union of the rows seen): the result equals
+    the reference's dense fold in torch ops (e scattered into a zero table,
+    g = h + e, acc = g_0 then acc += g_i, runtime/accumulate.py:145-160)
+    bit for bit."""
+    from elysium_wan_amd.accumulate import TiedRowFold
+
+    n_mb, n_rows, d, k = 8, 32768, 2560, 4096
+    dev = torch.device("cuda")
+    gen = torch.Generator(device=dev).manual_seed(23)
+    hs = [(torch.randn(n_rows, d, device=dev, generator=gen) * 1e-3).to(dtype) for _ in range(n_mb)]
+    rows = [torch.randperm(n_rows, device=dev, generator=gen)[:k].sort().values.cpu() for _ in range(n_mb)]
+    es = [(torch.randn(k, d, device=dev, generator=gen) * 1e-3).to(dtype) for _ in range(n_mb)]
+    say("tied fold at the benchmark size", dtype)
+    fold = TiedRowFold(n_rows, range(n_mb))
+    for mb in range(n_mb):
+        fold.add_head(mb, hs[mb], rows[mb])
+        if mb:
+            fold.add_embed(mb - 1, es[mb - 1])
+    fold.add_embed(n_mb - 1, es[n_mb - 1])
+    got = fold.result()
+    acc = None
+    for mb in range(n_mb):
+        e = torch.zeros(n_rows, d, device=dev, dtype=dtype)
+        e[rows[mb].to(dev)] = es[mb]
+        g = hs[mb] + e
+        acc = g if acc is None else acc.add_(g)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16 if dtype == torch.bfloat16 else torch.int32),
+                       acc.view(torch.int16 if dtype == torch.bfloat16 else torch.int32))
