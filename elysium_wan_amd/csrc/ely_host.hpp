@@ -38,6 +38,11 @@ struct DeviceInfo {
 // Properties of the current device (cached per device).
 const DeviceInfo& device_info();
 
+// True when `p` is pinned host memory the GPU reaches through its mapping
+// (a kernel's accesses to it cross PCIe); false for device memory and for
+// addresses the runtime does not know.
+bool host_resident(const void* p);
+
 // Blocks for a persistent multi-tensor launch: `per_cu` per compute unit,
 // capped by ely_set_max_blocks.
 int64_t mt_blocks(int per_cu);

@@ -68,6 +68,15 @@ namespace ely {
 #ifndef ELY_ADAM_BPC
 #define ELY_ADAM_BPC 1           // AdamW blocks per compute unit
 #endif
+#ifndef ELY_ADAM_MAPPED_DIV
+// An AdamW launch whose moments live in pinned host memory, read and
+// written in place through the GPU's mapping, is bound by PCIe, not HBM:
+// one block per this many compute units keeps the link busy.  On C1's
+// shard: 40-64 blocks 206 ms a step (97.5 GB/s each way), 128 blocks 218 ms,
+// 256 blocks 221 ms; the compute units left free also take a concurrent
+// forward's work.
+#define ELY_ADAM_MAPPED_DIV 4
+#endif
 #ifndef ELY_NORM_TILE
 #define ELY_NORM_TILE 16384      // grad-norm elements per tile (one wave's share; fixes the summation order)
 #endif
@@ -910,7 +919,9 @@ static void adamw_impl(const ely_tensor* params, const ely_tensor* accs, const e
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool wd = weight_decay_nonzero != 0;
     const bool clip = coef_dev != nullptr;
-    const int64_t blocks = std::min<int64_t>(tiles, mt_blocks(ELY_ADAM_BPC));
+    int64_t blocks = std::min<int64_t>(tiles, mt_blocks(ELY_ADAM_BPC));
+    if (host_resident(table[0].m))
+        blocks = std::min<int64_t>(blocks, std::max<int64_t>(1, device_info().cus / ELY_ADAM_MAPPED_DIV));
     bool shared = true;  // one set of constants for every tensor
     for (const ely_adamw_consts& c : cs) shared = shared && memcmp(&c, &cs[0], sizeof c) == 0;
     if (shared && table.size() <= (size_t)kArgTensors) {

@@ -36,6 +36,15 @@ const DeviceInfo& device_info() {
     return g_devices.emplace(dev, info).first->second;
 }
 
+bool host_resident(const void* p) {
+    hipPointerAttribute_t a;
+    if (hipPointerGetAttributes(&a, p) != hipSuccess) {
+        (void)hipGetLastError();  // an unknown address is not an error of the caller's next call
+        return false;
+    }
+    return a.type == hipMemoryTypeHost;
+}
+
 static std::atomic<int32_t> g_max_blocks{0};
 
 int64_t mt_blocks(int per_cu) {

@@ -257,7 +257,7 @@ int ely_scale_inplace(const ely_tensor* tensors, int32_t n, const float* coef_de
 int ely_host_device_pointer(const void* host, void** device);
 
 /* Cap on the blocks one multi-tensor launch (grad-norm, AdamW) may use; 0
- * restores the default (8 per compute unit).  For tuning and for the tests
+ * restores each kernel's own grid.  For tuning and for the tests
  * that prove results do not depend on the grid.  Process-wide. */
 int ely_set_max_blocks(int32_t max_blocks);
 
