@@ -10,8 +10,10 @@
 // persistent grid.  AdamW: in round r block b takes tile r*G + b, so at any
 // moment the whole chip streams one small window of the shard (4,096-element
 // tiles measured best: a smaller window keeps DRAM pages busy).  Norm: wave
-// w takes the contiguous tile range [w*T/W, (w+1)*T/W).  A table of tensor
-// descriptors is staged into the caller's workspace per call.
+// w takes the contiguous tile range [w*T/W, (w+1)*T/W), its last tiles
+// (ELY_NORM_CACHED_MB in all) with plain loads, the rest nontemporal.  A
+// table of tensor descriptors is staged into the caller's workspace per
+// call.
 //
 // Determinism of (a): a tile's partial sum is a fixed function of its
 // elements (lane l owns the 8-element groups l, l+64, ...; each group is
@@ -45,6 +47,12 @@ namespace ely {
 #endif
 #ifndef ELY_NORM_NT
 #define ELY_NORM_NT 1            // nontemporal grad-norm loads
+#endif
+#ifndef ELY_NORM_CACHED_MB
+#define ELY_NORM_CACHED_MB 384   // grad-norm bytes read last with plain loads, to stay in the MALL (norm_partials_body)
+#endif
+#ifndef ELY_NORM_CACHED_LIMIT_MB
+#define ELY_NORM_CACHED_LIMIT_MB 3072  // ... for lists of at most this many bytes; larger ones stay nontemporal
 #endif
 #ifndef ELY_NORM_UNROLL
 #define ELY_NORM_UNROLL 8        // 8-element groups a grad-norm lane loads before summing (divides 32)
@@ -150,13 +158,10 @@ __device__ __forceinline__ const ELY_GLOBAL T* gp(const T* p) {
 typedef float nf32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t nu32x4 __attribute__((ext_vector_type(4)));
 
-template <typename T>
+template <typename T, bool NT = ELY_NORM_NT != 0>
 __device__ __forceinline__ T ld_norm(const ELY_GLOBAL T* p) {
-#if ELY_NORM_NT
-    return __builtin_nontemporal_load(p);
-#else
+    if (NT) return __builtin_nontemporal_load(p);
     return *p;
-#endif
 }
 
 // The raw 16-byte vectors of one 8-element group: 1 (bf16) or 2 (fp32)
@@ -167,15 +172,15 @@ struct Raw8 {
     nf32x4 a[FOLD ? 2 : 1];
 };
 
-template <bool BF16, bool FOLD>
+template <bool BF16, bool FOLD, bool NT>
 __device__ __forceinline__ void raw8_load(const NormDesc& d, int64_t i, Raw8<BF16, FOLD>& r) {
     const ELY_GLOBAL nu32x4* p = gp(reinterpret_cast<const nu32x4*>(static_cast<const char*>(d.g) + i * (BF16 ? 2 : 4)));
-    r.g[0] = ld_norm(p);
-    if (!BF16) r.g[BF16 ? 0 : 1] = ld_norm(p + 1);
+    r.g[0] = ld_norm<nu32x4, NT>(p);
+    if (!BF16) r.g[BF16 ? 0 : 1] = ld_norm<nu32x4, NT>(p + 1);
     if (FOLD) {
         const ELY_GLOBAL nf32x4* q = gp(reinterpret_cast<const nf32x4*>(d.acc + i));
-        r.a[0] = ld_norm(q);
-        r.a[FOLD ? 1 : 0] = ld_norm(q + 1);
+        r.a[0] = ld_norm<nf32x4, NT>(q);
+        r.a[FOLD ? 1 : 0] = ld_norm<nf32x4, NT>(q + 1);
     }
 }
 
@@ -209,7 +214,7 @@ __device__ __forceinline__ float raw8_sumsq(const Raw8<BF16, FOLD>& r) {
 // Sum of squares of one full, aligned tile: lane l owns the 8-element groups
 // j*64 + l, j = 0..TILE/512-1, added in order; kNormUnroll groups' raw vectors are
 // loaded before the first of them is summed.
-template <bool BF16, bool FOLD, int64_t TILE>
+template <bool BF16, bool FOLD, int64_t TILE, bool NT>
 __device__ __forceinline__ double tile_sumsq_vec(const NormDesc& d, int64_t e0, int lane) {
     constexpr int G = (int)(TILE / (kWave * 8));
     constexpr int U = kNormUnroll;
@@ -218,7 +223,7 @@ __device__ __forceinline__ double tile_sumsq_vec(const NormDesc& d, int64_t e0, 
     for (int j0 = 0; j0 < G; j0 += U) {
         Raw8<BF16, FOLD> r[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) raw8_load<BF16, FOLD>(d, e0 + ((int64_t)(j0 + u) * kWave + lane) * 8, r[u]);
+        for (int u = 0; u < U; ++u) raw8_load<BF16, FOLD, NT>(d, e0 + ((int64_t)(j0 + u) * kWave + lane) * 8, r[u]);
 #pragma unroll
         for (int u = 0; u < U; ++u) acc += (double)raw8_sumsq<BF16, FOLD>(r[u]);
     }
@@ -254,19 +259,13 @@ struct NormArgTable {
     NormDesc d[kNormArgTensors];
 };
 
-template <bool FOLD, int DT, int64_t TILE, class Desc>
-__device__ __forceinline__ void norm_partials_body(const Desc* desc, int32_t n, int64_t total_tiles, double* partials) {
-    const int lane = threadIdx.x & (kWave - 1);
-    const int64_t waves = (int64_t)gridDim.x * (kBlock / kWave);
-    const int64_t w = (int64_t)blockIdx.x * (kBlock / kWave) + wave_uniform(threadIdx.x / kWave);
-#if ELY_NORM_SCHED == 0
-    const int64_t t0 = w * total_tiles / waves, t1 = (w + 1) * total_tiles / waves, tstep = 1;
-#else
-    const int64_t t0 = w, t1 = total_tiles, tstep = waves;
-#endif
-    if (t0 >= t1) return;
-    int ti = find_tensor(desc, n, t0);
-    for (int64_t tile = t0; tile < t1; tile += tstep) {
+// One wave's tiles `tile`, tile + tstep, ... below `to`: each tile's
+// partial sum of squares, with nontemporal (NT) or plain loads.  Advances
+// `tile` and the tensor index `ti`.
+template <bool FOLD, int DT, int64_t TILE, bool NT, class Desc>
+__device__ __forceinline__ void norm_tiles(const Desc* desc, int32_t n, int64_t& tile, int64_t to, int64_t tstep,
+                                           int& ti, int lane, double* partials) {
+    for (; tile < to; tile += tstep) {
         while (ti + 1 < n && desc[ti + 1].tile_begin <= tile) ++ti;
         const NormDesc d = desc[ti];
         const int64_t e0 = (tile - d.tile_begin) * TILE;
@@ -274,8 +273,8 @@ __device__ __forceinline__ void norm_partials_body(const Desc* desc, int32_t n, 
         double acc = 0.0;
         // lane l owns groups j*64 + l of 8 elements, in the same order on both paths
         if (d.aligned && e1 - e0 == TILE) {
-            if (DT == ELY_BF16 || (DT < 0 && d.dtype == ELY_BF16)) acc = tile_sumsq_vec<true, FOLD, TILE>(d, e0, lane);
-            else acc = tile_sumsq_vec<false, FOLD, TILE>(d, e0, lane);
+            if (DT == ELY_BF16 || (DT < 0 && d.dtype == ELY_BF16)) acc = tile_sumsq_vec<true, FOLD, TILE, NT>(d, e0, lane);
+            else acc = tile_sumsq_vec<false, FOLD, TILE, NT>(d, e0, lane);
         } else {
             for (int j = 0; j < (int)(TILE / (kWave * 8)); ++j) {
                 float x[8];
@@ -288,16 +287,44 @@ __device__ __forceinline__ void norm_partials_body(const Desc* desc, int32_t n, 
     }
 }
 
+// The last tiles each wave reads, about ELY_NORM_CACHED_MB of the call's
+// bytes in all, take plain loads, so that they are still in the MALL when
+// the update (or the clip's scale) reads the same gradients next: each
+// wave's last cached_q tiles, and one more for the first cached_r waves.
+// The two kinds of tiles run as two loops in sequence (one loop choosing
+// per tile let the compiler merge both kinds into plain loads).  The bits
+// do not depend on it.
+template <bool FOLD, int DT, int64_t TILE, class Desc>
+__device__ __forceinline__ void norm_partials_body(const Desc* desc, int32_t n, int64_t total_tiles, int64_t cached_q,
+                                                   int64_t cached_r, double* partials) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t waves = (int64_t)gridDim.x * (kBlock / kWave);
+    const int64_t w = (int64_t)blockIdx.x * (kBlock / kWave) + wave_uniform(threadIdx.x / kWave);
+#if ELY_NORM_SCHED == 0
+    const int64_t t0 = w * total_tiles / waves, t1 = (w + 1) * total_tiles / waves, tstep = 1;
+#else
+    const int64_t t0 = w, t1 = total_tiles, tstep = waves;
+#endif
+    if (t0 >= t1) return;
+    const int64_t cached_from = t1 - (cached_q + (w < cached_r ? 1 : 0)) * tstep;
+    int64_t tile = t0;
+    int ti = find_tensor(desc, n, t0);
+    norm_tiles<FOLD, DT, TILE, ELY_NORM_NT != 0>(desc, n, tile, cached_from, tstep, ti, lane, partials);
+    norm_tiles<FOLD, DT, TILE, false>(desc, n, tile, t1, tstep, ti, lane, partials);
+}
+
 template <bool FOLD, int DT, int64_t TILE>
 __global__ __launch_bounds__(kBlock) void norm_partials_kernel(const NormDesc* __restrict__ desc, int32_t n,
-                                                               int64_t total_tiles, double* __restrict__ partials) {
-    norm_partials_body<FOLD, DT, TILE>(desc, n, total_tiles, partials);
+                                                               int64_t total_tiles, int64_t cached_q, int64_t cached_r,
+                                                               double* __restrict__ partials) {
+    norm_partials_body<FOLD, DT, TILE>(desc, n, total_tiles, cached_q, cached_r, partials);
 }
 
 template <bool FOLD, int DT, int64_t TILE>
 __global__ __launch_bounds__(kBlock) void norm_partials_args_kernel(const NormArgTable tab, int32_t n,
-                                                                    int64_t total_tiles, double* __restrict__ partials) {
-    norm_partials_body<FOLD, DT, TILE>(tab.d, n, total_tiles, partials);
+                                                                    int64_t total_tiles, int64_t cached_q,
+                                                                    int64_t cached_r, double* __restrict__ partials) {
+    norm_partials_body<FOLD, DT, TILE>(tab.d, n, total_tiles, cached_q, cached_r, partials);
 }
 
 __global__ __launch_bounds__(kFinalThreads) void norm_final_kernel(const double* __restrict__ partials, int64_t tiles,
@@ -427,8 +454,8 @@ static int64_t norm_tiles(const ely_tensor* grads, int32_t n, int64_t tile) {
 
 static size_t norm_table_bytes(int32_t n) { return align_up((size_t)n * sizeof(NormDesc), 256); }
 
-typedef void (*NormKernel)(const NormDesc*, int32_t, int64_t, double*);
-typedef void (*NormArgsKernel)(const NormArgTable, int32_t, int64_t, double*);
+typedef void (*NormKernel)(const NormDesc*, int32_t, int64_t, int64_t, int64_t, double*);
+typedef void (*NormArgsKernel)(const NormArgTable, int32_t, int64_t, int64_t, int64_t, double*);
 
 template <int64_t TILE>
 static NormKernel pick_norm(bool fold, int dt) {
@@ -803,20 +830,33 @@ static NormLaunch grad_norm_impl(const ely_tensor* accs, const ely_tensor* grads
         for (const NormDesc& d : table)
             if (d.dtype != dt) dt = -1;
         out.dt = dt;
+        // ~ELY_NORM_CACHED_MB of the last tiles read, spread over the kernel's
+        // waves (a list that small is read with plain loads throughout).
+        // Measured step (norm + update) against nontemporal loads throughout:
+        // C0 (85 MB) -6 %, 256 MB and 1 GB of fp32 gradients -7 % and -3.4 %,
+        // C1 (2.5 GB) -0.4 %; 4 and 8 GB lists +0.3 % and 0, so lists past
+        // ELY_NORM_CACHED_LIMIT_MB keep nontemporal loads.
+        const int64_t tile_bytes = tile * ((dt == ELY_BF16 ? 2 : 4) + (accs ? 4 : 0));
+        const int64_t cached = tiles * tile_bytes > ((int64_t)ELY_NORM_CACHED_LIMIT_MB << 20)
+                                   ? 0
+                                   : ((int64_t)ELY_NORM_CACHED_MB << 20) / tile_bytes;
+        const int64_t kwaves = blocks * (kBlock / kWave);
+        const int64_t cached_q = cached >= tiles ? tiles : cached / kwaves;
+        const int64_t cached_r = cached >= tiles ? 0 : cached % kwaves;
         if (table.size() <= (size_t)kNormArgTensors) {
             memset(&out.args, 0, sizeof out.args);
             memcpy(out.args.d, table.data(), table.size() * sizeof(NormDesc));
             const NormArgsKernel kern = tile == kNormTile ? pick_norm_args<kNormTile>(accs != nullptr, dt)
                                                           : pick_norm_args<kNormSmallTile>(accs != nullptr, dt);
             hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(kBlock), 0, s, out.args, (int32_t)table.size(), tiles,
-                               partials);
+                               cached_q, cached_r, partials);
         } else {
             upload(dtable, table.data(), table.size() * sizeof(NormDesc), s);
             out.dtable = dtable;
             const NormKernel kern = tile == kNormTile ? pick_norm<kNormTile>(accs != nullptr, dt)
                                                       : pick_norm<kNormSmallTile>(accs != nullptr, dt);
             hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(kBlock), 0, s, (const NormDesc*)dtable,
-                               (int32_t)table.size(), tiles, partials);
+                               (int32_t)table.size(), tiles, cached_q, cached_r, partials);
         }
         check_launch("norm_partials_kernel");
     }
