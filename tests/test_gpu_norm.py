@@ -172,3 +172,30 @@ def test_clip_grad_norm_in_one_call_scales_every_gradient(oracle):
     with pytest.raises(RuntimeError, match="non-finite"):
         optim.clip_grad_norm_([p], 1.0, error_if_nonfinite=True)
     assert torch.equal(p.grad, g)
+
+
+def test_norm_over_both_load_kinds_is_bitwise_stable_across_grids():
+    """A list past the bytes the norm reads last with plain loads (each
+    wave's final tiles; the rest nontemporal): both kinds of tiles run, and
+    how many of each a wave takes moves with the grid.  The sum of squares
+    is bitwise the same for every grid and within 1e-8 of an fp64 sum."""
+    from elysium_wan_amd import _lib
+
+    gen = torch.Generator(device="cuda").manual_seed(31)
+    gs = [(torch.randn(24 << 20, device="cuda", generator=gen) * 1e-3).bfloat16() for _ in range(10)]
+    gs += [torch.randn(5 << 20, device="cuda", generator=gen) * 1e-3 for _ in range(3)]
+    gs.append(torch.randn(4097, device="cuda", generator=gen)[1:])  # unaligned tail
+    nbytes = sum(g.numel() * g.element_size() for g in gs)
+    assert nbytes > (400 << 20)
+    exact = sum(float((g.double() ** 2).sum()) for g in gs)
+    runs = []
+    for cap in (0, 7, 64, 999):
+        _lib.check(_lib.load().ely_set_max_blocks(cap), "cap")
+        try:
+            say("norm over both load kinds, cap", cap, nbytes)
+            r = _norm(gs)
+            runs.append(r[3])
+        finally:
+            _lib.load().ely_set_max_blocks(0)
+        assert abs(r[0] - exact) <= 1e-8 * exact
+    assert all(np.array_equal(runs[0], r) for r in runs[1:])
