@@ -39,3 +39,18 @@ def test_optimizer_is_freed_without_the_garbage_collector(order):
         assert ref() is None
     finally:
         gc.enable()
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU: asked for more it exits with status 2 and
+    says so, before it touches a device."""
+    import os
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "8"], capture_output=True, text=True,
+                       cwd=root, timeout=300)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr and "--gpus 8" in r.stderr
+    assert r.stdout == ""
