@@ -159,6 +159,16 @@ def require_gpu(t: torch.Tensor, what: str) -> None:
         raise ValueError(f"{what}: the MI355X path runs on the GPU, got a {t.device.type} tensor")
 
 
+def to_gpu(t: torch.Tensor, what: str) -> torch.Tensor:
+    """A wire encoder's input on the GPU: the reference's encoders take a
+    tensor on any device (they copy it to the host first), so a host tensor
+    is copied to the current GPU; with no GPU this raises as require_gpu."""
+    if t.device.type != "cuda" and torch.cuda.is_available():
+        return t.to(torch.device("cuda", torch.cuda.current_device()))
+    require_gpu(t, what)
+    return t
+
+
 def ely_tensor(t: torch.Tensor | None, dtype: int | None = None) -> ElyTensor:
     if t is None:
         return ElyTensor(None, 0, F32 if dtype is None else dtype, 0)

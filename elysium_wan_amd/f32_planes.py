@@ -24,7 +24,7 @@ from elysium_wan_amd.planes import _compress, _decompress, _device
 def encode(t: torch.Tensor):
     """codec/f32_planes.py:17-26: float32 tensor -> (payload, shape)."""
     assert t.dtype == torch.float32  # the reference's own check (an AssertionError)
-    _lib.require_gpu(t, "f32_planes.encode")
+    t = _lib.to_gpu(t, "f32_planes.encode")
     t = t.detach().contiguous()
     n = t.numel()
     host = np.empty((4, 0), dtype=np.uint8)

@@ -28,7 +28,7 @@ def encode(t: torch.Tensor):
     """codec/fp8_planes.py:19-32: -> (payload, shape).  AssertionError
     "boundary is not FP8-representable: recipe mismatch" when some element
     is not exactly an e4m3 value (NaN never is; -0 counts as 0)."""
-    _lib.require_gpu(t, "fp8_planes.encode")
+    t = _lib.to_gpu(t, "fp8_planes.encode")
     t = t.detach().contiguous()
     if t.dtype not in (torch.float32, torch.bfloat16):
         if not t.is_floating_point():

@@ -93,7 +93,7 @@ def encode_scaled_fp8(t: torch.Tensor, fmt: str = "e4m3"):
     the tensor must be exactly representable with it, else ValueError."""
     if fmt not in _SCALED_ID:
         raise ValueError(f"fp8 format {fmt!r} is not one of {tuple(_SCALED_ID)}")
-    _lib.require_gpu(t, "encode_scaled_fp8")
+    t = _lib.to_gpu(t, "encode_scaled_fp8")
     t = t.detach().contiguous()
     flat = t.reshape(-1, t.shape[-1]) if t.dim() > 1 else t.reshape(1, -1)
     rows, cols = flat.shape
@@ -127,7 +127,7 @@ def encode(t: torch.Tensor):
     (payload, shape), lossless.  The byte planes are split on the GPU."""
     if t.dtype not in _ID:
         raise ValueError(f"no wire encoding for dtype {t.dtype}")
-    _lib.require_gpu(t, "encode")
+    t = _lib.to_gpu(t, "encode")
     t = t.detach().contiguous()
     esz = t.element_size()
     n = t.numel()

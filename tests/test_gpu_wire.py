@@ -184,3 +184,21 @@ def test_recover_image_equals_the_oracle(oracle, fmt, dname, cols):
     off[0, cols // 3] = (1 + 2.0**-6) * 2.0 ** int(bits(k)[0])
     with pytest.raises(ValueError, match="^boundary tensor is not scaled-FP8 representable: recipe mismatch$"):
         planes.encode_scaled_fp8(off, fmt)
+
+
+def test_encoders_take_host_tensors_as_the_reference_does():
+    """The reference's encoders copy their input to the host first, so any
+    device's tensor goes in (codec/planes.py:87, 143; fp8_planes.py:21;
+    f32_planes.py:19): a host tensor here is copied to the GPU and gives
+    the same payload as the same tensor on the GPU."""
+    from elysium_wan_amd import f32_planes, fp8, fp8_planes, planes
+
+    gen = torch.Generator().manual_seed(12)
+    x = torch.randn(6, 40, generator=gen)
+    scaled = fp8.roundtrip(x.cuda().bfloat16()).cpu()  # a tensor that is its own scaled-fp8 round trip
+    e4m3 = x.to(torch.float8_e4m3fn).float()  # every element an e4m3 value
+    say("wire encoders on host tensors")
+    for enc, t in ((planes.encode, x.bfloat16()), (planes.encode, x), (planes.encode_scaled_fp8, scaled),
+                   (fp8_planes.encode, e4m3), (f32_planes.encode, x)):
+        assert t.device.type == "cpu"
+        assert enc(t) == enc(t.cuda())
