@@ -48,6 +48,14 @@
 #ifndef ELY_SPLIT_WAVES
 #define ELY_SPLIT_WAVES 2048  // split path: waves of the partial-max launch (at most)
 #endif
+#ifndef ELY_SPLIT_CACHED_MB
+// split path: MB of x the |x|max launch reads last with plain loads instead
+// of nontemporal ones.  C4 per-tensor: quantize 0.408 -> 0.403 ms, round
+// trip 0.509 -> 0.499 ms (0, 192, 256 and 384 MB measured; a convert launch
+// taking the segments last to first, to start on the cached ones, was
+// slower)
+#define ELY_SPLIT_CACHED_MB 256
+#endif
 #ifndef ELY_SPLIT_BATCH
 #define ELY_SPLIT_BATCH 1  // split path: vectors per lane per load batch of the convert launch (0: all)
 #endif
@@ -129,14 +137,14 @@ __device__ __forceinline__ uint32_t ld_u32(const void* p) {
 }
 
 // One 16-byte load of streamed data.
+template <bool NT = (ELY_FP8_NT & 1) != 0>
 __device__ __forceinline__ uint4 ld_vec(const uint4* p) {
-#if ELY_FP8_NT & 1
-    typedef uint32_t v4u __attribute__((ext_vector_type(4)));
-    const v4u v = __builtin_nontemporal_load((const __attribute__((address_space(1))) v4u*)(const void*)p);
-    return make_uint4(v[0], v[1], v[2], v[3]);
-#else
+    if (NT) {
+        typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+        const v4u v = __builtin_nontemporal_load((const __attribute__((address_space(1))) v4u*)(const void*)p);
+        return make_uint4(v[0], v[1], v[2], v[3]);
+    }
     return *p;
-#endif
 }
 
 template <bool BF16>
@@ -426,7 +434,7 @@ struct Seg {
 };
 
 // |x|max bits of elements [e0, e1) of row `row` (e1 - e0 <= kSegElems).
-template <bool BF16>
+template <bool BF16, bool NT>
 __device__ __forceinline__ uint32_t seg_absmax(const void* x, int64_t row, int64_t cols, int64_t e0, int64_t e1,
                                                int vec, int lane) {
     constexpr int EPV = Seg<BF16>::EPV, VPL = Seg<BF16>::VPL, ESZ = BF16 ? 2 : 4;
@@ -438,7 +446,7 @@ __device__ __forceinline__ uint32_t seg_absmax(const void* x, int64_t row, int64
 #pragma unroll
         for (int j = 0; j < VPL; ++j) {
             const int64_t vi = lane + (int64_t)kWave * j;
-            buf[j] = ld_vec(xr + (vi < nv ? vi : nv - 1));
+            buf[j] = ld_vec<NT>(xr + (vi < nv ? vi : nv - 1));
         }
 #pragma unroll
         for (int j = 0; j < VPL; ++j)
@@ -455,16 +463,24 @@ __device__ __forceinline__ uint32_t seg_absmax(const void* x, int64_t row, int64
 
 template <bool BF16>
 __global__ __launch_bounds__(kQBlock) void rowmax_partial_kernel(const void* __restrict__ x, int64_t rows, int64_t cols,
-                                                                 int64_t segs, int64_t wpr, int vec,
+                                                                 int64_t segs, int64_t wpr, int vec, int64_t cached,
                                                                  uint32_t* __restrict__ partial) {
     const int lane = threadIdx.x & (kWave - 1);
     const int64_t gw = (int64_t)blockIdx.x * kWavesPerBlock + wave_uniform(threadIdx.x / kWave);
     if (gw >= rows * wpr) return;
     const int64_t row = gw / wpr, j = gw % wpr;
     uint32_t amax = 0;
-    for (int64_t seg = j; seg < segs; seg += wpr) {
+    // a row's last `cached` segments are read last, with plain loads; two
+    // loops in sequence keep the two kinds of loads apart
+    const int64_t cut = segs - cached;
+    int64_t seg = j;
+    for (; seg < cut; seg += wpr) {
         const int64_t e0 = seg * kSegElems;
-        amax = max(amax, seg_absmax<BF16>(x, row, cols, e0, min(e0 + kSegElems, cols), vec, lane));
+        amax = max(amax, seg_absmax<BF16, (ELY_FP8_NT & 1) != 0>(x, row, cols, e0, min(e0 + kSegElems, cols), vec, lane));
+    }
+    for (; seg < segs; seg += wpr) {
+        const int64_t e0 = seg * kSegElems;
+        amax = max(amax, seg_absmax<BF16, false>(x, row, cols, e0, min(e0 + kSegElems, cols), vec, lane));
     }
     amax = wave_max_u32(amax);
     if (lane == 0) partial[gw] = amax;
@@ -1089,8 +1105,10 @@ static void split_rowmax(const void* x, int64_t rows, int64_t cols, int vec, voi
     const int64_t wpr = split_wpr(rows, segs);
     if (rows > INT64_MAX / wpr) fail(ELY_EINVAL, "too many rows");
     uint32_t* partial = wpr == 1 ? rowmax : reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + rowmax_bytes(rows));
+    const int64_t seg_bytes = kSegElems * (BF16 ? 2 : 4);
+    const int64_t cached = std::min<int64_t>(segs, ((int64_t)ELY_SPLIT_CACHED_MB << 20) / (seg_bytes * rows));
     hipLaunchKernelGGL((rowmax_partial_kernel<BF16>), dim3(blocks_for_waves(rows * wpr)), dim3(kQBlock), 0, s, x, rows,
-                       cols, segs, wpr, vec, partial);
+                       cols, segs, wpr, vec, cached, partial);
     check_launch("rowmax_partial_kernel");
     if (wpr > 1) {
         hipLaunchKernelGGL(rowmax_reduce_kernel, dim3((unsigned)std::min<int64_t>(rows, 65536)), dim3(kQBlock), 0, s,
