@@ -743,7 +743,8 @@ def bench_release(device, stream, tokens: int = 2048, iters: int = 3, moments: s
 def bench_elementwise(device, stream, iters=5):
     """The stand-alone passes of the unfused path over C1's 192-tensor shard,
     one launch per tensor as the reference's callers make them: the fp32 ->
-    bf16 working-copy cast (pieces.cast_piece, 6 B/elem), the fold of a bf16
+    bf16 working-copy cast (pieces.cast_piece, 6 B/elem), the first term of
+    the fold widened to fp32 (pieces.fold_start, 6 B/elem), the fold of a bf16
     microbatch gradient into its fp32 sum (pieces.fold_add, 10 B/elem),
     the in-place scale of bf16 gradients by a device coefficient
     (ely_scale_inplace over the list, one launch per 48 tensors, 4 B/elem)
@@ -757,6 +758,7 @@ def bench_elementwise(device, stream, iters=5):
     n = sum(p.numel() for p in params)
     copies = [torch.empty(p.shape, dtype=torch.bfloat16, device=device) for p in params]
     accs = [torch.zeros_like(p) for p in params]
+    wide = [torch.empty_like(p) for p in params]
     garr = _lib.tensor_array(grads)
     one = torch.ones(1, dtype=torch.float32, device=device)
 
@@ -767,6 +769,10 @@ def bench_elementwise(device, stream, iters=5):
     def fold(_):
         for a, g in zip(accs, grads):
             _lib.check(L.ely_fold_add(a.data_ptr(), g.data_ptr(), _lib.BF16, a.numel(), sptr), "fold")
+
+    def widen(_):
+        for w, g in zip(wide, grads):
+            _lib.check(L.ely_widen_bf16(g.data_ptr(), w.data_ptr(), w.numel(), sptr), "widen")
 
     def scale(_):
         _lib.check(L.ely_scale_inplace(garr, len(grads), one.data_ptr(), sptr), "scale")
@@ -779,10 +785,11 @@ def bench_elementwise(device, stream, iters=5):
         _lib.check(L.ely_grad_norm_clip(garr, len(grads), MAX_NORM, res.data_ptr(), nws.data_ptr(), nws.numel(), sptr), "clip")
 
     out = {}
-    for name, fn, b in (("cast_bf16", cast, 6), ("fold_add_bf16", fold, 10), ("scale_bf16", scale, 4), ("clip_grad_norm_bf16", clip, 6)):
+    for name, fn, b in (("cast_bf16", cast, 6), ("widen_bf16", widen, 6), ("fold_add_bf16", fold, 10), ("scale_bf16", scale, 4),
+                        ("clip_grad_norm_bf16", clip, 6)):
         ms = time_events(fn, iters, stream)
         out[name] = {"ms": ms, "GBs": n * b / ms / 1e6}
-    del params, grads, copies, accs
+    del params, grads, copies, accs, wide
     return out
 
 

@@ -49,6 +49,7 @@ EXPORTS = (
     "ely_scale_inplace",
     "ely_rows_fold",
     "ely_rows_split",
+    "ely_widen_bf16",
     "ely_set_max_blocks",
     "ely_host_device_pointer",
     "ely_byteplanes_split",
@@ -121,6 +122,7 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
         L.ely_scale_inplace.argtypes = [TP, I32, P, P]
         L.ely_rows_fold.argtypes = [P, P, P, P, P, P, I64, I64, I64, I64, I64, I32, I32, P]
         L.ely_rows_split.argtypes = [P, P, P, P, I64, I64, I64, I32, I32, P]
+        L.ely_widen_bf16.argtypes = [P, P, I64, P]
         L.ely_set_max_blocks.argtypes = [I32]
         L.ely_host_device_pointer.argtypes = [P, ctypes.POINTER(ctypes.c_void_p)]
         L.ely_byteplanes_split.argtypes = [P, I64, I32, P, P]

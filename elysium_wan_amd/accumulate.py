@@ -104,9 +104,12 @@ class OrderedAccumulator:
 
     def _first(self, i: int, t):
         """The sum's first value: the part itself, copied (widened exactly
-        when the sum is kept wider)."""
+        when the sum is kept wider; bf16 to fp32 by pieces.fold_start's
+        kernel)."""
         want = self.widen.get(i)
         if want is not None and t.dtype != want:
+            if want == torch.float32 and t.dtype == torch.bfloat16 and t.is_cuda:
+                return pieces.fold_start(t)
             return t.to(want, copy=True)
         return t.clone()
 

@@ -25,6 +25,12 @@
 #ifndef ELY_CAST_BPC
 #define ELY_CAST_BPC 4
 #endif
+#ifndef ELY_WIDEN_UNROLL
+#define ELY_WIDEN_UNROLL 1
+#endif
+#ifndef ELY_WIDEN_BPC
+#define ELY_WIDEN_BPC 4
+#endif
 #ifndef ELY_FOLD_UNROLL
 #define ELY_FOLD_UNROLL 1
 #endif
@@ -42,6 +48,7 @@ struct EwShape {
 };
 constexpr EwShape kCastShape{ELY_CAST_UNROLL, ELY_CAST_BPC};
 constexpr EwShape kFoldShape{ELY_FOLD_UNROLL, ELY_FOLD_BPC};
+constexpr EwShape kWidenShape{ELY_WIDEN_UNROLL, ELY_WIDEN_BPC};
 
 typedef float ef4 __attribute__((ext_vector_type(4)));
 typedef uint32_t eu2 __attribute__((ext_vector_type(2)));
@@ -94,6 +101,17 @@ __global__ __launch_bounds__(kEwBlock) void cast_bf16_kernel(const float* __rest
             n / 4, [&](int64_t q) { return ld4(x + 4 * q); }, [&](int64_t q, ef4 v) { sth4(out + 4 * q, narrow4(v)); });
     const int64_t T = (int64_t)gridDim.x * kEwBlock;
     for (int64_t i = done + (int64_t)blockIdx.x * kEwBlock + threadIdx.x; i < n; i += T) out[i] = (uint16_t)f32_to_bf16(x[i]);
+}
+
+// pieces.fold_start: bf16 -> fp32, exact (the 16 bits moved to the top).
+__global__ __launch_bounds__(kEwBlock) void widen_bf16_kernel(const uint16_t* __restrict__ x, float* __restrict__ out,
+                                                              int64_t n, int vec) {
+    int64_t done = 0;
+    if (vec)
+        done = quad_loop<kWidenShape.unroll>(
+            n / 4, [&](int64_t q) { return ldh4(x + 4 * q); }, [&](int64_t q, eu2 w) { st4(out + 4 * q, widen4(w)); });
+    const int64_t T = (int64_t)gridDim.x * kEwBlock;
+    for (int64_t i = done + (int64_t)blockIdx.x * kEwBlock + threadIdx.x; i < n; i += T) out[i] = bf16_to_f32(x[i]);
 }
 
 struct AccG {
@@ -172,6 +190,18 @@ int ely_cast_bf16(const float* x, uint16_t* out, int64_t n, void* stream) {
         hipLaunchKernelGGL(cast_bf16_kernel, dim3(ew_blocks(n, kCastShape)), dim3(kEwBlock), 0, static_cast<hipStream_t>(stream),
                            x, out, n, vec);
         check_launch("cast_bf16_kernel");
+    });
+}
+
+int ely_widen_bf16(const uint16_t* x, float* out, int64_t n, void* stream) {
+    return guarded([&] {
+        if (n < 0) fail(ELY_EINVAL, "ely_widen_bf16: negative n");
+        if (n == 0) return;
+        if (!x || !out) fail(ELY_EINVAL, "ely_widen_bf16: null pointer");
+        const int vec = aligned16(out) && (reinterpret_cast<uintptr_t>(x) % 8 == 0);
+        hipLaunchKernelGGL(widen_bf16_kernel, dim3(ew_blocks(n, kWidenShape)), dim3(kEwBlock), 0,
+                           static_cast<hipStream_t>(stream), x, out, n, vec);
+        check_launch("widen_bf16_kernel");
     });
 }
 

@@ -6,10 +6,13 @@
 // Work decomposition.  Every tensor is cut into fixed tiles (kAdamTile /
 // the norm tile of the call, kNormTile or, for lists under 2^29 elements,
 // kNormSmallTile; a tensor's last tile may be short) numbered
-// consecutively across the list, so the ragged list costs one launch on a
-// persistent grid.  AdamW: in round r block b takes tile r*G + b, so at any
-// moment the whole chip streams one small window of the shard (4,096-element
-// tiles measured best: a smaller window keeps DRAM pages busy).  Norm: wave
+// consecutively across the list, so the ragged list costs one launch.
+// AdamW: one 64-lane block per 256-element tile, each block taking its one
+// tile and exiting, so the hardware dispatcher keeps every compute unit
+// full of short-lived waves streaming one small window of the shard (C1:
+// 5.94 ms against 6.64 for the persistent grid of one 256-thread block per
+// CU looping over 4,096-element tiles, and 7.5-8.7 ms for persistent grids
+// of these small tiles).  Norm: wave
 // w takes the contiguous tile range [w*T/W, (w+1)*T/W), its last tiles
 // (ELY_NORM_CACHED_MB in all) with plain loads, the rest nontemporal.  A
 // table of tensor descriptors is staged into the caller's workspace per
@@ -37,10 +40,13 @@ namespace ely {
 
 // Compile-time tunables (chosen by measurement on MI355X; see the defaults).
 #ifndef ELY_ADAM_TILE
-#define ELY_ADAM_TILE 4096       // elements per AdamW tile (two unrolled block steps)
+// elements per AdamW tile: one block's work (C1, one-shot grids: 256 with
+// 64-lane blocks 5.94 ms, 512 with 128 lanes and 1,024 with 256 lanes
+// 6.05, 2,048 6.39, 4,096 6.45, 8,192 6.65)
+#define ELY_ADAM_TILE 256
 #endif
 #ifndef ELY_ADAM_SCHED
-#define ELY_ADAM_SCHED 1         // 0: contiguous tile range per block, 1: interleaved rounds
+#define ELY_ADAM_SCHED 1         // 0: contiguous tile range per block, 1: interleaved rounds (a capped grid)
 #endif
 #ifndef ELY_NORM_SCHED
 #define ELY_NORM_SCHED 0         // same choice for the grad-norm waves
@@ -66,10 +72,10 @@ namespace ely {
 #define ELY_NT 3                 // bit 0: nontemporal AdamW loads, bit 1: nontemporal stores
 #endif
 #ifndef ELY_ADAM_UNROLL
-#define ELY_ADAM_UNROLL 2        // 2,048-element block steps a thread keeps in flight (1, 2, 4 or 8)
+#define ELY_ADAM_UNROLL 1        // block steps a thread keeps in flight
 #endif
 #ifndef ELY_ADAM_HALVES
-#define ELY_ADAM_HALVES 2        // 1,024-element halves per block step (1 or 2)
+#define ELY_ADAM_HALVES 1        // quads per thread per block step (1 or 2)
 #endif
 #ifndef ELY_ADAM_ONE_UPLOAD
 // 1: AdamW descriptors and constants staged in one host-to-device copy.
@@ -79,16 +85,16 @@ namespace ely {
 #define ELY_ADAM_ONE_UPLOAD 0
 #endif
 #ifndef ELY_ADAM_BPC
-#define ELY_ADAM_BPC 1           // AdamW blocks per compute unit
+#define ELY_ADAM_BPC (1 << 20)   // AdamW grid cap, blocks per compute unit: in practice one block per tile
 #endif
-#ifndef ELY_ADAM_MAPPED_DIV
+#ifndef ELY_ADAM_MAPPED_BPC
 // An AdamW launch whose moments live in pinned host memory, read and
 // written in place through the GPU's mapping, is bound by PCIe, not HBM:
-// one block per this many compute units keeps the link busy.  On C1's
-// shard: 40-64 blocks 206 ms a step (97.5 GB/s each way), 128 blocks 218 ms,
-// 256 blocks 221 ms; the compute units left free also take a concurrent
-// forward's work.
-#define ELY_ADAM_MAPPED_DIV 4
+// a persistent grid of this many blocks per compute unit keeps the link
+// busy.  On C1's shard: 64-256 blocks 203 ms a step (99 GB/s each way),
+// 1,024 to 65,536 blocks and the one-shot grid 220 ms; the compute units
+// left free also take a concurrent forward's work.
+#define ELY_ADAM_MAPPED_BPC 1
 #endif
 #ifndef ELY_NORM_TILE
 #define ELY_NORM_TILE 16384      // grad-norm elements per tile (one wave's share; fixes the summation order)
@@ -114,6 +120,10 @@ static_assert(kNormTile % (64 * 8 * ELY_NORM_UNROLL) == 0 && kNormSmallTile % (6
 constexpr int kNormUnroll = ELY_NORM_UNROLL;
 constexpr int kFinalUnroll = ELY_FINAL_UNROLL;
 constexpr int kBlock = 256;
+#ifndef ELY_ADAM_BLOCK
+#define ELY_ADAM_BLOCK 64      // AdamW threads per block: one wave
+#endif
+constexpr int kAdamBlock = ELY_ADAM_BLOCK;
 constexpr int kFinalThreads = 1024;
 
 // --------------------------------------------------------------- (a) norm
@@ -551,15 +561,15 @@ __device__ __forceinline__ void st_stream(ELY_GLOBAL T* p, T v) {
 #endif
 }
 
-// The vector path's unit of work is a block step of kStep = kHalves * 1,024
-// elements.  Thread t owns the quads [4t, 4t+4), [1024+4t, 1024+4t+4), ...
-// of the step, one per 1,024-element half, so each load or store
+// The vector path's unit of work is a block step of kStep = kHalves * kHalf
+// elements (kHalf = 4 per thread).  Thread t owns the quads [4t, 4t+4),
+// [kHalf+4t, kHalf+4t+4), ... of the step, so each load or store
 // instruction of a wave covers one contiguous 1 KB (fp32) or 512 B (bf16)
 // run: every request is a full, aligned line, and the halves of a step never
 // share a line.  ELY_ADAM_UNROLL steps are loaded before the first is
 // updated, keeping 7 * kHalves * U 16- or 8-byte loads per thread in flight.
 constexpr int kHalves = ELY_ADAM_HALVES;
-constexpr int64_t kHalf = (int64_t)kBlock * 4;
+constexpr int64_t kHalf = (int64_t)kAdamBlock * 4;
 constexpr int64_t kStep = kHalf * kHalves;
 static_assert(kAdamTile % kStep == 0, "an AdamW tile is a whole number of block steps");
 
@@ -650,7 +660,7 @@ __device__ __forceinline__ void adam_range(const AdamDesc& d, const ely_adamw_co
         done = e0 + steps * kStep;
     }
     // Scalar path: unaligned tensors entirely, aligned tensors' last partial step.
-    for (int64_t i = done + threadIdx.x; i < e1; i += kBlock) {
+    for (int64_t i = done + threadIdx.x; i < e1; i += kAdamBlock) {
         float p = *gp(d.p + i), m = *gp(d.m + i), v = *gp(d.v + i);
         float g = BF16G ? bf16_to_f32(*gp(static_cast<const uint16_t*>(d.g) + i)) : *gp(static_cast<const float*>(d.g) + i);
         if (FOLD) g = *gp(d.acc + i) + g;
@@ -705,14 +715,14 @@ __device__ __forceinline__ void adamw_body(const Tab& tab, int32_t n, int64_t to
 // slower C1 launch).  The argument kernel's tables sit in the kernel-argument
 // segment, which is constant memory.
 template <bool BF16G, int ORDER, bool WD, bool CLIP, bool FOLD>
-__global__ __launch_bounds__(kBlock) void adamw_kernel(const AdamDesc* __restrict__ desc,
+__global__ __launch_bounds__(kAdamBlock) void adamw_kernel(const AdamDesc* __restrict__ desc,
                                                        const ely_adamw_consts* __restrict__ consts, int32_t n,
                                                        int64_t total_tiles, const float* __restrict__ coef_ptr) {
     adamw_body<BF16G, ORDER, WD, CLIP, FOLD>(AdamTableRef{desc, consts}, n, total_tiles, coef_ptr);
 }
 
 template <bool BF16G, int ORDER, bool WD, bool CLIP, bool FOLD>
-__global__ __launch_bounds__(kBlock) void adamw_args_kernel(const AdamArgTable tab, int32_t n, int64_t total_tiles,
+__global__ __launch_bounds__(kAdamBlock) void adamw_args_kernel(const AdamArgTable tab, int32_t n, int64_t total_tiles,
                                                             const float* __restrict__ coef_ptr) {
     adamw_body<BF16G, ORDER, WD, CLIP, FOLD>(tab, n, total_tiles, coef_ptr);
 }
@@ -965,8 +975,8 @@ static void adamw_impl(const ely_tensor* params, const ely_tensor* accs, const e
     const bool wd = weight_decay_nonzero != 0;
     const bool clip = coef_dev != nullptr;
     int64_t blocks = std::min<int64_t>(tiles, mt_blocks(ELY_ADAM_BPC));
-    if (host_resident(table[0].m))
-        blocks = std::min<int64_t>(blocks, std::max<int64_t>(1, device_info().cus / ELY_ADAM_MAPPED_DIV));
+    if (ELY_ADAM_MAPPED_BPC > 0 && host_resident(table[0].m))
+        blocks = std::min<int64_t>(blocks, (int64_t)device_info().cus * ELY_ADAM_MAPPED_BPC);
     bool shared = true;  // one set of constants for every tensor
     for (const ely_adamw_consts& c : cs) shared = shared && memcmp(&c, &cs[0], sizeof c) == 0;
     if (shared && table.size() <= (size_t)kArgTensors) {
@@ -976,7 +986,7 @@ static void adamw_impl(const ely_tensor* params, const ely_tensor* accs, const e
         memcpy(at.d, table.data(), table.size() * sizeof(AdamDesc));
         at.c = cs[0];
         const AdamArgsKernel k = pick_adam_kernel<AdamArgsKernel>(accs != nullptr, gdt == ELY_BF16, order, wd, clip);
-        hipLaunchKernelGGL(k, dim3((unsigned)blocks), dim3(kBlock), 0, s, at, (int32_t)table.size(), tiles, coef_dev);
+        hipLaunchKernelGGL(k, dim3((unsigned)blocks), dim3(kAdamBlock), 0, s, at, (int32_t)table.size(), tiles, coef_dev);
         check_launch("adamw_kernel");
         return;
     }
@@ -995,7 +1005,7 @@ static void adamw_impl(const ely_tensor* params, const ely_tensor* accs, const e
     upload(dconsts, cs.data(), cs.size() * sizeof(ely_adamw_consts), s);
 #endif
     const AdamKernel k = pick_adam_kernel<AdamKernel>(accs != nullptr, gdt == ELY_BF16, order, wd, clip);
-    hipLaunchKernelGGL(k, dim3((unsigned)blocks), dim3(kBlock), 0, s, (const AdamDesc*)dtable,
+    hipLaunchKernelGGL(k, dim3((unsigned)blocks), dim3(kAdamBlock), 0, s, (const AdamDesc*)dtable,
                        (const ely_adamw_consts*)dconsts, (int32_t)table.size(), tiles, coef_dev);
     check_launch("adamw_kernel");
 }

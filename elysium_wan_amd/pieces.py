@@ -42,8 +42,14 @@ def fold_start(g: torch.Tensor) -> torch.Tensor:
     _lib.require_gpu(g, "fold_start")
     if g.dtype not in (torch.float32, torch.bfloat16):
         raise TypeError(f"fold_start widens float32 or bfloat16 gradients, got {g.dtype}")
-    # widening is exact (the fp32 value of a bf16 is its bits shifted up): a copy
-    return g.detach().to(torch.float32, copy=True)
+    if g.dtype == torch.float32:
+        return g.detach().clone()
+    # widening is exact: the fp32 value of a bf16 is its bits moved to the top
+    src = g.detach().contiguous()
+    out = torch.empty(src.shape, dtype=torch.float32, device=src.device)
+    L = _lib.load()
+    _lib.check(L.ely_widen_bf16(src.data_ptr(), out.data_ptr(), src.numel(), _lib.stream_ptr(src.device)), "fold_start")
+    return out
 
 
 def fold_add(acc: torch.Tensor, g: torch.Tensor) -> None:

@@ -203,6 +203,12 @@ int ely_fp8_quantize_k(const void* x, int32_t x_dtype, int64_t rows, int64_t col
  * every NaN -> 0x7FC0. */
 int ely_cast_bf16(const float* x, uint16_t* out, int64_t n, void* stream);
 
+/* The first microbatch's term of the ordered fold, widened to the fp32 sum
+ * (runtime/pieces.py:198-203 `fold_start`, `g.to(torch.float32)`; and
+ * runtime/accumulate.py:98-100, `t.to(want, copy=True)`): out[i] = x[i] as
+ * fp32, exact.  x: n bf16; out: n fp32. */
+int ely_widen_bf16(const uint16_t* x, float* out, int64_t n, void* stream);
+
 /* pieces.fold_add (runtime/pieces.py:206-214): acc += float(g), one fp32
  * rounding; g_dtype ELY_F32 or ELY_BF16. */
 int ely_fold_add(float* acc, const void* g, int32_t g_dtype, int64_t n, void* stream);

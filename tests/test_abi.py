@@ -277,14 +277,14 @@ def test_header_is_c_and_links_from_c(tmp_path):
 
 
 def test_adamw_refuses_more_tiles_than_its_descriptors_hold(lib):
-    """A call whose tensors add up to more than 2^31 - 1 tiles of 4,096
+    """A call whose tensors add up to more than 2^31 - 1 tiles of 256
     elements (the descriptors keep the first tile of each tensor in 32 bits)
     is refused before anything is launched: the pointers below are never
     dereferenced."""
     from elysium_wan_amd import _lib
 
     fake = 1 << 20
-    n = 4096 * (1 << 30)  # 2^30 tiles each: the second tensor crosses the limit
+    n = 256 * (1 << 30)  # 2^30 tiles each: the second tensor crosses the limit
     t = _lib.tensor_array([_lib.ElyTensor(fake, n, _lib.F32, 0)] * 2)
     g = _lib.tensor_array([_lib.ElyTensor(fake, n, _lib.BF16, 0)] * 2)
     c = (_lib.ElyConsts * 2)()

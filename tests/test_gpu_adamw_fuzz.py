@@ -22,7 +22,7 @@ from gpu_util import bits, say
 pytestmark = pytest.mark.gpu
 
 FUZZ = settings(max_examples=60, deadline=None, derandomize=True, suppress_health_check=[HealthCheck.too_slow])
-SIZES = [0, 1, 3, 4, 5, 1023, 1024, 2047, 2048, 2049, 4095, 4096, 4097, 8191, 12289, 65537]
+SIZES = [0, 1, 3, 4, 5, 63, 64, 65, 255, 256, 257, 511, 513, 1023, 1024, 2047, 2048, 2049, 4095, 4096, 4097, 8191, 12289, 65537]
 LR, BETAS, EPS = 1e-2, (0.9, 0.95), 1e-8
 
 def _consts_table(oracle, order: str, wd: float, ts):

@@ -1,5 +1,6 @@
 """Property-based fuzz of the stand-alone elementwise passes on the GPU:
-pieces.cast_piece, pieces.fold_add and the in-place scale over random sizes
+pieces.cast_piece, pieces.fold_start, pieces.fold_add and the in-place
+scale over random sizes
 (quad tails, several grid strides) and element offsets (the vector and the
 scalar paths), bit for bit against torch on the GPU -- each is one IEEE
 rounding per element (runtime/pieces.py:192-214, clip_grad.py:170-177).
@@ -48,6 +49,8 @@ def test_elementwise_passes_match_torch(n, offs, bf16g, coef, seed):
     want = acc + g.float()
     pieces.fold_add(acc, g)
     assert _same(acc, want)
+    gb = g if bf16g else _at(g.to(torch.bfloat16), offs[1])
+    assert _same(pieces.fold_start(gb), gb.float())  # the widening kernel, vector and scalar paths
     if n:
         L = _lib.load()
         c = torch.tensor([coef], dtype=torch.float32, device="cuda")
@@ -79,3 +82,20 @@ def test_scale_over_a_tensor_list_equals_torch(n_t):
     _lib.check(L.ely_scale_inplace(_lib.tensor_array(hs), n_t, c.data_ptr(), _lib.stream_ptr(torch.device("cuda", 0))), "scale")
     for h, w in zip(hs, wants):
         assert _same(h, w)
+
+
+def test_fold_start_widens_every_bf16_pattern_exactly():
+    """pieces.fold_start's bf16 -> fp32 kernel on all 65,536 bf16 bit
+    patterns (NaNs, infinities, subnormals and both zeros included), aligned
+    and one element off: the fp32 bits are the bf16 bits moved to the top,
+    which is also what torch's widening gives."""
+    from elysium_wan_amd import pieces
+
+    pats = torch.arange(65536, dtype=torch.int32, device="cuda").to(torch.int16).view(torch.bfloat16)
+    want = (pats.view(torch.int16).to(torch.int32) << 16).view(torch.float32)
+    for off in (0, 1):
+        x = _at(pats, off)
+        say("fold_start exhaustive, offset", off)
+        got = pieces.fold_start(x)
+        assert torch.equal(got.view(torch.int32), want.view(torch.int32))
+        assert torch.equal(got.view(torch.int32), x.float().view(torch.int32))
