@@ -305,7 +305,8 @@ __device__ __forceinline__ void norm_tiles(const Desc* desc, int32_t n, int64_t&
 // The last tiles each wave reads, about ELY_NORM_CACHED_MB of the call's
 // bytes in all, take plain loads, so that they are still in the MALL when
 // the update (or the clip's scale) reads the same gradients next: each
-// wave's last cached_q tiles, and one more for the first cached_r waves.
+// wave's last cached_q tiles, and one more for the last cached_r waves (the
+// last dispatched, when a wave takes one tile).
 // The two kinds of tiles run as two loops in sequence (one loop choosing
 // per tile let the compiler merge both kinds into plain loads).  The bits
 // do not depend on it.
@@ -321,7 +322,7 @@ __device__ __forceinline__ void norm_partials_body(const Desc* desc, int32_t n, 
     const int64_t t0 = w, t1 = total_tiles, tstep = waves;
 #endif
     if (t0 >= t1) return;
-    const int64_t cached_from = t1 - (cached_q + (w < cached_r ? 1 : 0)) * tstep;
+    const int64_t cached_from = t1 - (cached_q + (w >= waves - cached_r ? 1 : 0)) * tstep;
     int64_t tile = t0;
     int ti = find_tensor(desc, n, t0);
     norm_tiles<FOLD, DT, TILE, ELY_NORM_NT != 0>(desc, n, tile, cached_from, tstep, ti, lane, partials);
