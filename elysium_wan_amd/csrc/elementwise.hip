@@ -175,7 +175,9 @@ static unsigned ew_blocks(int64_t n, EwShape sh) {
     const DeviceInfo& dev = device_info();
     const int64_t per_block = (int64_t)kEwBlock * 4 * sh.unroll;
     const int64_t want = (n + per_block - 1) / per_block;
-    return (unsigned)std::max<int64_t>(1, std::min<int64_t>(want, (int64_t)dev.cus * sh.bpc));
+    // a dispatch counts its work-items in 32 bits: past that the grid strides
+    const int64_t cap = std::min<int64_t>((int64_t)dev.cus * sh.bpc, 0xFFFFFFFFLL / kEwBlock);
+    return (unsigned)std::max<int64_t>(1, std::min<int64_t>(want, cap));
 }
 
 }  // namespace ely

@@ -1047,7 +1047,8 @@ static void check_shape(int64_t rows, int64_t cols) {
 
 static unsigned blocks_for_waves(int64_t waves) {
     const int64_t b = (waves + kWavesPerBlock - 1) / kWavesPerBlock;
-    if (b > 0x7FFFFFFF) fail(ELY_EINVAL, "grid too large");
+    // a dispatch counts its work-items in 32 bits
+    if (b > 0xFFFFFFFFLL / kQBlock) fail(ELY_EINVAL, "grid too large: more than 2^32 - 1 threads in one launch");
     return (unsigned)b;
 }
 
@@ -1134,7 +1135,7 @@ static void quantize_impl(const void* x, int64_t rows, int64_t cols, uint8_t* q,
     const int vpl = rows_vpl(cols, dt, x, q, out);
     if (vpl > kMaxWaveVpl) {
         // one block per row: kWavesPerBlock waves of ceil(vpl / kWavesPerBlock) vectors per lane
-        if (rows > 0x7FFFFFFF) fail(ELY_EINVAL, "fp8 quantize: too many rows for one launch");
+        if (rows > 0xFFFFFFFFLL / kQBlock) fail(ELY_EINVAL, "fp8 quantize: too many rows for one launch");
         switch ((vpl + kWavesPerBlock - 1) / kWavesPerBlock) {
             case 2: hipLaunchKernelGGL((quant_block_row_kernel<FMT, BF16, 2>), dim3((unsigned)rows), dim3(kQBlock), 0, s, x, cols, q, k, out); break;
             case 3: hipLaunchKernelGGL((quant_block_row_kernel<FMT, BF16, 3>), dim3((unsigned)rows), dim3(kQBlock), 0, s, x, cols, q, k, out); break;

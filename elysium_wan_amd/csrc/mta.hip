@@ -903,7 +903,7 @@ static ClipArgsKernel pick_clip_args(int dt) {
 // argument again; same stream, so the coefficient is in place when this runs).
 static void clip_scale(const NormLaunch& nl, const float* coef_dev, void* stream) {
     if (nl.tiles == 0) return;
-    const int64_t waves = std::min<int64_t>(nl.tiles, mt_blocks(ELY_CLIP_BPC) * (kBlock / kWave));
+    const int64_t waves = std::min<int64_t>({nl.tiles, mt_blocks(ELY_CLIP_BPC) * (kBlock / kWave), 0xFFFFFFFFLL / kWave});
     const int64_t blocks = (waves + 3) / 4;
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (nl.dtable) {
@@ -976,7 +976,9 @@ static void adamw_impl(const ely_tensor* params, const ely_tensor* accs, const e
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool wd = weight_decay_nonzero != 0;
     const bool clip = coef_dev != nullptr;
-    int64_t blocks = std::min<int64_t>(tiles, mt_blocks(ELY_ADAM_BPC));
+    // one block per tile, up to the 2^32 - 1 work-items a dispatch counts;
+    // a longer list's blocks stride over the rest
+    int64_t blocks = std::min<int64_t>({tiles, mt_blocks(ELY_ADAM_BPC), 0xFFFFFFFFLL / kAdamBlock});
     if (ELY_ADAM_MAPPED_BPC > 0 && host_resident(table[0].m))
         blocks = std::min<int64_t>(blocks, (int64_t)device_info().cus * ELY_ADAM_MAPPED_BPC);
     bool shared = true;  // one set of constants for every tensor
