@@ -5,8 +5,10 @@
 // OrderedAccumulator, runtime/accumulate.py:101-102).  (The clip's in-place
 // scaling of a tensor list is one multi-tensor launch in mta.hip.)  Each is
 // one HBM pass over 4-element quads
-// (16-byte fp32, 8-byte bf16 vectors, nontemporal) on a persistent grid,
-// with a per-kernel number of quads in flight per thread.
+// (16-byte fp32, 8-byte bf16 vectors, nontemporal) with a per-kernel launch
+// shape: quads in flight per thread, threads per block, and a grid that is
+// either persistent (a few blocks per CU, striding) or one-shot (a block per
+// run of quads, exiting after it).
 #include <algorithm>
 
 #include "ely_device.hpp"
@@ -15,7 +17,8 @@
 #pragma clang fp contract(off)
 
 // Tunables, per kernel: quads of 4 elements a thread has in flight (_UNROLL)
-// and the persistent grid's blocks per CU (_BPC).  Together they set the
+// and the grid's cap in blocks per CU (_BPC; a cap above what the largest
+// tensor needs makes the grid one-shot).  Together they set the
 // bytes each CU has outstanding, which is what bounds a streaming pass on
 // this part; the passes reading 16-24 B per quad run fastest at about 16-25
 // KB of reads in flight per CU.
@@ -38,20 +41,27 @@
 #define ELY_FOLD_UNROLL 1
 #endif
 #ifndef ELY_FOLD_BPC
-#define ELY_FOLD_BPC 3
+// one quad per thread, 64-thread blocks, a one-shot grid: 2^28 elements
+// 6.75 TB/s against 6.17 on 256-thread blocks at 3 per CU, C1's tensors one
+// launch each 5.66 against 5.49.  The cast and the widen on 64-thread blocks
+// gained 3-4% on C1's tensors and lost as much on one 2^28 tensor, so they
+// stay on 256-thread blocks.
+#define ELY_FOLD_BPC 262144
+#endif
+#ifndef ELY_FOLD_BLOCK
+#define ELY_FOLD_BLOCK 64
 #endif
 
 namespace ely {
 
-constexpr int kEwBlock = 256;
-
-// A launch shape: quads in flight per thread, blocks per CU.
+// A launch shape: quads in flight per thread, blocks per CU, threads per
+// block.
 struct EwShape {
-    int unroll, bpc;
+    int unroll, bpc, block;
 };
-constexpr EwShape kCastShape{ELY_CAST_UNROLL, ELY_CAST_BPC};
-constexpr EwShape kFoldShape{ELY_FOLD_UNROLL, ELY_FOLD_BPC};
-constexpr EwShape kWidenShape{ELY_WIDEN_UNROLL, ELY_WIDEN_BPC};
+constexpr EwShape kCastShape{ELY_CAST_UNROLL, ELY_CAST_BPC, 256};
+constexpr EwShape kFoldShape{ELY_FOLD_UNROLL, ELY_FOLD_BPC, ELY_FOLD_BLOCK};
+constexpr EwShape kWidenShape{ELY_WIDEN_UNROLL, ELY_WIDEN_BPC, 256};
 
 typedef float ef4 __attribute__((ext_vector_type(4)));
 typedef uint32_t eu2 __attribute__((ext_vector_type(2)));
@@ -75,10 +85,10 @@ __device__ __forceinline__ eu2 narrow4(ef4 v) {
 // or store instruction of a wave covers one contiguous run.  load(q) reads
 // quad q into registers, store(q, regs) computes and writes it; returns the
 // elements covered.
-template <int U, class Load, class Store>
+template <int U, int B, class Load, class Store>
 __device__ __forceinline__ int64_t quad_loop(int64_t nq, Load load, Store store) {
-    const int64_t T = (int64_t)gridDim.x * kEwBlock;
-    const int64_t t = (int64_t)blockIdx.x * kEwBlock + threadIdx.x;
+    const int64_t T = (int64_t)gridDim.x * B;
+    const int64_t t = (int64_t)blockIdx.x * B + threadIdx.x;
     for (int64_t base = t; base < nq; base += T * U) {
         decltype(load(0)) r[U];
 #pragma unroll
@@ -96,25 +106,25 @@ __device__ __forceinline__ int64_t quad_loop(int64_t nq, Load load, Store store)
 }
 
 // pieces.cast_piece: fp32 -> bf16 (RNE, NaN -> 0x7FC0).
-__global__ __launch_bounds__(kEwBlock) void cast_bf16_kernel(const float* __restrict__ x, uint16_t* __restrict__ out,
+__global__ __launch_bounds__(kCastShape.block) void cast_bf16_kernel(const float* __restrict__ x, uint16_t* __restrict__ out,
                                                              int64_t n, int vec) {
     int64_t done = 0;
     if (vec)
-        done = quad_loop<kCastShape.unroll>(
+        done = quad_loop<kCastShape.unroll, kCastShape.block>(
             n / 4, [&](int64_t q) { return ld4(x + 4 * q); }, [&](int64_t q, ef4 v) { sth4(out + 4 * q, narrow4(v)); });
-    const int64_t T = (int64_t)gridDim.x * kEwBlock;
-    for (int64_t i = done + (int64_t)blockIdx.x * kEwBlock + threadIdx.x; i < n; i += T) out[i] = (uint16_t)f32_to_bf16(x[i]);
+    const int64_t T = (int64_t)gridDim.x * kCastShape.block;
+    for (int64_t i = done + (int64_t)blockIdx.x * kCastShape.block + threadIdx.x; i < n; i += T) out[i] = (uint16_t)f32_to_bf16(x[i]);
 }
 
 // pieces.fold_start: bf16 -> fp32, exact (the 16 bits moved to the top).
-__global__ __launch_bounds__(kEwBlock) void widen_bf16_kernel(const uint16_t* __restrict__ x, float* __restrict__ out,
+__global__ __launch_bounds__(kWidenShape.block) void widen_bf16_kernel(const uint16_t* __restrict__ x, float* __restrict__ out,
                                                               int64_t n, int vec) {
     int64_t done = 0;
     if (vec)
-        done = quad_loop<kWidenShape.unroll>(
+        done = quad_loop<kWidenShape.unroll, kWidenShape.block>(
             n / 4, [&](int64_t q) { return ldh4(x + 4 * q); }, [&](int64_t q, eu2 w) { st4(out + 4 * q, widen4(w)); });
-    const int64_t T = (int64_t)gridDim.x * kEwBlock;
-    for (int64_t i = done + (int64_t)blockIdx.x * kEwBlock + threadIdx.x; i < n; i += T) out[i] = bf16_to_f32(x[i]);
+    const int64_t T = (int64_t)gridDim.x * kWidenShape.block;
+    for (int64_t i = done + (int64_t)blockIdx.x * kWidenShape.block + threadIdx.x; i < n; i += T) out[i] = bf16_to_f32(x[i]);
 }
 
 struct AccG {
@@ -123,11 +133,11 @@ struct AccG {
 
 // pieces.fold_add: acc += widen(g), one fp32 rounding per element.
 template <bool BF16G>
-__global__ __launch_bounds__(kEwBlock) void fold_add_kernel(float* __restrict__ acc, const void* __restrict__ g,
+__global__ __launch_bounds__(kFoldShape.block) void fold_add_kernel(float* __restrict__ acc, const void* __restrict__ g,
                                                             int64_t n, int vec) {
     int64_t done = 0;
     if (vec)
-        done = quad_loop<kFoldShape.unroll>(
+        done = quad_loop<kFoldShape.unroll, kFoldShape.block>(
             n / 4,
             [&](int64_t q) {
                 AccG r;
@@ -136,8 +146,8 @@ __global__ __launch_bounds__(kEwBlock) void fold_add_kernel(float* __restrict__ 
                 return r;
             },
             [&](int64_t q, AccG r) { st4(acc + 4 * q, ef4{r.acc[0] + r.g[0], r.acc[1] + r.g[1], r.acc[2] + r.g[2], r.acc[3] + r.g[3]}); });
-    const int64_t T = (int64_t)gridDim.x * kEwBlock;
-    for (int64_t i = done + (int64_t)blockIdx.x * kEwBlock + threadIdx.x; i < n; i += T) {
+    const int64_t T = (int64_t)gridDim.x * kFoldShape.block;
+    for (int64_t i = done + (int64_t)blockIdx.x * kFoldShape.block + threadIdx.x; i < n; i += T) {
         const float gv = BF16G ? bf16_to_f32(static_cast<const uint16_t*>(g)[i]) : static_cast<const float*>(g)[i];
         acc[i] = acc[i] + gv;
     }
@@ -147,11 +157,11 @@ __global__ __launch_bounds__(kEwBlock) void fold_add_kernel(float* __restrict__ 
 // `acc.add_(t)` on a bf16 tensor): acc = bf16(float(acc) + widen(g)), the
 // fp32 add rounded once more to bf16, as torch's in-place add computes it.
 template <bool BF16G>
-__global__ __launch_bounds__(kEwBlock) void fold_add_bf16_kernel(uint16_t* __restrict__ acc, const void* __restrict__ g,
+__global__ __launch_bounds__(kFoldShape.block) void fold_add_bf16_kernel(uint16_t* __restrict__ acc, const void* __restrict__ g,
                                                                  int64_t n, int vec) {
     int64_t done = 0;
     if (vec)
-        done = quad_loop<kFoldShape.unroll>(
+        done = quad_loop<kFoldShape.unroll, kFoldShape.block>(
             n / 4,
             [&](int64_t q) {
                 AccG r;
@@ -162,8 +172,8 @@ __global__ __launch_bounds__(kEwBlock) void fold_add_bf16_kernel(uint16_t* __res
             [&](int64_t q, AccG r) {
                 sth4(acc + 4 * q, narrow4(ef4{r.acc[0] + r.g[0], r.acc[1] + r.g[1], r.acc[2] + r.g[2], r.acc[3] + r.g[3]}));
             });
-    const int64_t T = (int64_t)gridDim.x * kEwBlock;
-    for (int64_t i = done + (int64_t)blockIdx.x * kEwBlock + threadIdx.x; i < n; i += T) {
+    const int64_t T = (int64_t)gridDim.x * kFoldShape.block;
+    for (int64_t i = done + (int64_t)blockIdx.x * kFoldShape.block + threadIdx.x; i < n; i += T) {
         const float gv = BF16G ? bf16_to_f32(static_cast<const uint16_t*>(g)[i]) : static_cast<const float*>(g)[i];
         acc[i] = (uint16_t)f32_to_bf16(bf16_to_f32(acc[i]) + gv);
     }
@@ -173,10 +183,10 @@ __global__ __launch_bounds__(kEwBlock) void fold_add_bf16_kernel(uint16_t* __res
 // the shape's blocks per CU.
 static unsigned ew_blocks(int64_t n, EwShape sh) {
     const DeviceInfo& dev = device_info();
-    const int64_t per_block = (int64_t)kEwBlock * 4 * sh.unroll;
+    const int64_t per_block = (int64_t)sh.block * 4 * sh.unroll;
     const int64_t want = (n + per_block - 1) / per_block;
     // a dispatch counts its work-items in 32 bits: past that the grid strides
-    const int64_t cap = std::min<int64_t>((int64_t)dev.cus * sh.bpc, 0xFFFFFFFFLL / kEwBlock);
+    const int64_t cap = std::min<int64_t>((int64_t)dev.cus * sh.bpc, 0xFFFFFFFFLL / sh.block);
     return (unsigned)std::max<int64_t>(1, std::min<int64_t>(want, cap));
 }
 
@@ -192,7 +202,7 @@ int ely_cast_bf16(const float* x, uint16_t* out, int64_t n, void* stream) {
         if (n == 0) return;
         if (!x || !out) fail(ELY_EINVAL, "ely_cast_bf16: null pointer");
         const int vec = aligned16(x) && (reinterpret_cast<uintptr_t>(out) % 8 == 0);
-        hipLaunchKernelGGL(cast_bf16_kernel, dim3(ew_blocks(n, kCastShape)), dim3(kEwBlock), 0, static_cast<hipStream_t>(stream),
+        hipLaunchKernelGGL(cast_bf16_kernel, dim3(ew_blocks(n, kCastShape)), dim3(kCastShape.block), 0, static_cast<hipStream_t>(stream),
                            x, out, n, vec);
         check_launch("cast_bf16_kernel");
     });
@@ -204,7 +214,7 @@ int ely_widen_bf16(const uint16_t* x, float* out, int64_t n, void* stream) {
         if (n == 0) return;
         if (!x || !out) fail(ELY_EINVAL, "ely_widen_bf16: null pointer");
         const int vec = aligned16(out) && (reinterpret_cast<uintptr_t>(x) % 8 == 0);
-        hipLaunchKernelGGL(widen_bf16_kernel, dim3(ew_blocks(n, kWidenShape)), dim3(kEwBlock), 0,
+        hipLaunchKernelGGL(widen_bf16_kernel, dim3(ew_blocks(n, kWidenShape)), dim3(kWidenShape.block), 0,
                            static_cast<hipStream_t>(stream), x, out, n, vec);
         check_launch("widen_bf16_kernel");
     });
@@ -219,9 +229,9 @@ int ely_fold_add(float* acc, const void* g, int32_t g_dtype, int64_t n, void* st
         const int vec = aligned16(acc) && (reinterpret_cast<uintptr_t>(g) % (g_dtype == ELY_BF16 ? 8 : 16) == 0);
         hipStream_t s = static_cast<hipStream_t>(stream);
         if (g_dtype == ELY_BF16)
-            hipLaunchKernelGGL(fold_add_kernel<true>, dim3(ew_blocks(n, kFoldShape)), dim3(kEwBlock), 0, s, acc, g, n, vec);
+            hipLaunchKernelGGL(fold_add_kernel<true>, dim3(ew_blocks(n, kFoldShape)), dim3(kFoldShape.block), 0, s, acc, g, n, vec);
         else
-            hipLaunchKernelGGL(fold_add_kernel<false>, dim3(ew_blocks(n, kFoldShape)), dim3(kEwBlock), 0, s, acc, g, n, vec);
+            hipLaunchKernelGGL(fold_add_kernel<false>, dim3(ew_blocks(n, kFoldShape)), dim3(kFoldShape.block), 0, s, acc, g, n, vec);
         check_launch("fold_add_kernel");
     });
 }
@@ -236,9 +246,9 @@ int ely_fold_add_bf16(uint16_t* acc, const void* g, int32_t g_dtype, int64_t n, 
                         (reinterpret_cast<uintptr_t>(g) % (g_dtype == ELY_BF16 ? 8 : 16) == 0);
         hipStream_t s = static_cast<hipStream_t>(stream);
         if (g_dtype == ELY_BF16)
-            hipLaunchKernelGGL(fold_add_bf16_kernel<true>, dim3(ew_blocks(n, kFoldShape)), dim3(kEwBlock), 0, s, acc, g, n, vec);
+            hipLaunchKernelGGL(fold_add_bf16_kernel<true>, dim3(ew_blocks(n, kFoldShape)), dim3(kFoldShape.block), 0, s, acc, g, n, vec);
         else
-            hipLaunchKernelGGL(fold_add_bf16_kernel<false>, dim3(ew_blocks(n, kFoldShape)), dim3(kEwBlock), 0, s, acc, g, n, vec);
+            hipLaunchKernelGGL(fold_add_bf16_kernel<false>, dim3(ew_blocks(n, kFoldShape)), dim3(kFoldShape.block), 0, s, acc, g, n, vec);
         check_launch("fold_add_bf16_kernel");
     });
 }
