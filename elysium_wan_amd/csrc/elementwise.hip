@@ -16,36 +16,37 @@
 
 #pragma clang fp contract(off)
 
-// Tunables, per kernel: quads of 4 elements a thread has in flight (_UNROLL)
-// and the grid's cap in blocks per CU (_BPC; a cap above what the largest
-// tensor needs makes the grid one-shot).  Together they set the
-// bytes each CU has outstanding, which is what bounds a streaming pass on
-// this part; the passes reading 16-24 B per quad run fastest at about 16-25
-// KB of reads in flight per CU.
+// Tunables, per kernel: quads of 4 elements a thread has in flight (_UNROLL),
+// the grid's cap in blocks per CU (_BPC; a cap above what the largest
+// tensor needs makes the grid one-shot) and threads per block (_BLOCK).
+// Each pass below runs one quad per thread on 64-thread blocks, one-shot (a
+// block per 256 elements).  Against 256-thread blocks in the same process
+// and buffers: at 2^28 elements the fold (bf16 g) 6.78 TB/s against 6.18 at
+// 3 blocks per CU, the cast 6.87 against 6.08 at 4 per CU, the widen 6.75
+// against 6.44 one-shot; over C1's tensors one launch each, 5.69 against
+// 5.50, 5.12 against 4.79 and 4.99 against 4.80.
 #ifndef ELY_CAST_UNROLL
 #define ELY_CAST_UNROLL 1
 #endif
 #ifndef ELY_CAST_BPC
-#define ELY_CAST_BPC 4
+#define ELY_CAST_BPC 262144
+#endif
+#ifndef ELY_CAST_BLOCK
+#define ELY_CAST_BLOCK 64
 #endif
 #ifndef ELY_WIDEN_UNROLL
 #define ELY_WIDEN_UNROLL 1
 #endif
 #ifndef ELY_WIDEN_BPC
-// one quad per thread, a one-shot grid: 2^28 elements 6.35 TB/s against
-// 5.66 at 4 blocks per CU (torch's copy: 5.9), C1's tensors one launch each
-// 4.74 against 4.58; the fold and the cast measured slower on C1 that way
-#define ELY_WIDEN_BPC 65536
+#define ELY_WIDEN_BPC 262144
+#endif
+#ifndef ELY_WIDEN_BLOCK
+#define ELY_WIDEN_BLOCK 64
 #endif
 #ifndef ELY_FOLD_UNROLL
 #define ELY_FOLD_UNROLL 1
 #endif
 #ifndef ELY_FOLD_BPC
-// one quad per thread, 64-thread blocks, a one-shot grid: 2^28 elements
-// 6.75 TB/s against 6.17 on 256-thread blocks at 3 per CU, C1's tensors one
-// launch each 5.66 against 5.49.  The cast and the widen on 64-thread blocks
-// gained 3-4% on C1's tensors and lost as much on one 2^28 tensor, so they
-// stay on 256-thread blocks.
 #define ELY_FOLD_BPC 262144
 #endif
 #ifndef ELY_FOLD_BLOCK
@@ -59,9 +60,9 @@ namespace ely {
 struct EwShape {
     int unroll, bpc, block;
 };
-constexpr EwShape kCastShape{ELY_CAST_UNROLL, ELY_CAST_BPC, 256};
+constexpr EwShape kCastShape{ELY_CAST_UNROLL, ELY_CAST_BPC, ELY_CAST_BLOCK};
 constexpr EwShape kFoldShape{ELY_FOLD_UNROLL, ELY_FOLD_BPC, ELY_FOLD_BLOCK};
-constexpr EwShape kWidenShape{ELY_WIDEN_UNROLL, ELY_WIDEN_BPC, 256};
+constexpr EwShape kWidenShape{ELY_WIDEN_UNROLL, ELY_WIDEN_BPC, ELY_WIDEN_BLOCK};
 
 typedef float ef4 __attribute__((ext_vector_type(4)));
 typedef uint32_t eu2 __attribute__((ext_vector_type(2)));

@@ -63,7 +63,12 @@
 #define ELY_Q_BATCH 1  // register paths: vectors per lane per load batch (0: the whole row at once)
 #endif
 #ifndef ELY_Q_LDS
-#define ELY_Q_LDS 40960  // wave-per-row quantize: unused dynamic LDS per block, capping it at 4 blocks (16 waves) per CU
+// wave-per-row quantize: unused dynamic LDS per block, capping it at 16
+// blocks (16 waves) per CU.  C1 back to back over 8 inputs, in one process:
+// quantize 5.89-5.92 TB/s and round trip 5.92-5.96 against 5.80-5.82 and
+// 5.74-5.85 with no cap (256-thread blocks capped at 4 per CU: 5.86-5.88,
+// 5.93-5.94)
+#define ELY_Q_LDS 10240
 #endif
 #ifndef ELY_DEQ_LDS
 #define ELY_DEQ_LDS 0  // dequantize: unused dynamic LDS per block capping its blocks per CU (caps measured slower)
@@ -80,8 +85,16 @@
 
 namespace ely {
 
-constexpr int kQBlock = 256;                   // 4 waves, one row (or segment) each
+#ifndef ELY_QBLOCK
+// 64: in one process on the same buffers, dequantize 6.55-6.58 TB/s on C4
+// and 5.86 on C1 against 6.29-6.46 and 5.68-5.71 on 256-thread blocks;
+// the wave-per-row quantize the same (C1 6.0-6.1)
+#define ELY_QBLOCK 64
+#endif
+constexpr int kQBlock = ELY_QBLOCK;            // threads per block; each wave takes its own row or segment
 constexpr int kWavesPerBlock = kQBlock / kWave;
+constexpr int kRowBlock = 256;                 // the block-row quantize and the row-max reduce: 4 waves share one row
+constexpr int kRowWaves = kRowBlock / kWave;
 constexpr int64_t kSegElems = 2048;            // split-path segment, elements
 constexpr int64_t kDeqSegCodes = ELY_DEQ_SEG;  // dequantize segment, codes
 constexpr int kRecoverKeepVpl = ELY_RECOVER_KEEP_VPL;
@@ -349,13 +362,13 @@ __global__ __launch_bounds__(kQBlock) void quant_rows_kernel(const void* __restr
 // The host launches exactly one block per row, so every wave of a block
 // reaches the barrier.
 template <int FMT, bool BF16, int VPLW>
-__global__ __launch_bounds__(kQBlock) void quant_block_row_kernel(const void* __restrict__ x, int64_t cols,
+__global__ __launch_bounds__(kRowBlock) void quant_block_row_kernel(const void* __restrict__ x, int64_t cols,
                                                                   uint8_t* __restrict__ q, int32_t* __restrict__ k,
                                                                   void* __restrict__ out) {
     constexpr int EPV = BF16 ? 8 : 4;
     constexpr int ESZ = BF16 ? 2 : 4;
     constexpr int QB = (ELY_Q_BATCH <= 0 || ELY_Q_BATCH > VPLW) ? VPLW : ELY_Q_BATCH;
-    __shared__ uint32_t wmax[kWavesPerBlock];
+    __shared__ uint32_t wmax[kRowWaves];
     const int lane = threadIdx.x & (kWave - 1);
     const int w = wave_uniform(threadIdx.x / kWave);
     const int64_t row = blockIdx.x;
@@ -384,7 +397,7 @@ __global__ __launch_bounds__(kQBlock) void quant_block_row_kernel(const void* __
     __syncthreads();
     amax = wmax[0];
 #pragma unroll
-    for (int i = 1; i < kWavesPerBlock; ++i) amax = max(amax, wmax[i]);
+    for (int i = 1; i < kRowWaves; ++i) amax = max(amax, wmax[i]);
     const RowScale rs = row_scale<FMT>(to_f32_bits<BF16>(amax), BF16, BF16);
     if (threadIdx.x == 0 && k) k[row] = rs.k;
     if (!rs.fast) {
@@ -486,19 +499,19 @@ __global__ __launch_bounds__(kQBlock) void rowmax_partial_kernel(const void* __r
     if (lane == 0) partial[gw] = amax;
 }
 
-__global__ __launch_bounds__(kQBlock) void rowmax_reduce_kernel(const uint32_t* __restrict__ partial, int64_t rows,
+__global__ __launch_bounds__(kRowBlock) void rowmax_reduce_kernel(const uint32_t* __restrict__ partial, int64_t rows,
                                                                 int64_t wpr, uint32_t* __restrict__ rowmax) {
-    __shared__ uint32_t red[kWavesPerBlock];
+    __shared__ uint32_t red[kRowWaves];
     const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
     for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
         uint32_t m = 0;
-        for (int64_t i = threadIdx.x; i < wpr; i += kQBlock) m = max(m, partial[r * wpr + i]);
+        for (int64_t i = threadIdx.x; i < wpr; i += kRowBlock) m = max(m, partial[r * wpr + i]);
         m = wave_max_u32(m);
         if (lane == 0) red[w] = m;
         __syncthreads();
         if (threadIdx.x == 0) {
             uint32_t t = red[0];
-            for (int k = 1; k < kWavesPerBlock; ++k) t = max(t, red[k]);
+            for (int k = 1; k < kRowWaves; ++k) t = max(t, red[k]);
             rowmax[r] = t;
         }
         __syncthreads();
@@ -1053,7 +1066,7 @@ static unsigned blocks_for_waves(int64_t waves) {
 }
 
 // Vectors per lane of the register paths: a wave per row up to kMaxWaveVpl,
-// a block of kWavesPerBlock waves per row above (the block's loads in flight
+// a block of kRowWaves waves per row above (the block's loads in flight
 // per row stay the same, and more rows stream at once).
 constexpr int kVplChoices[] = {1, 2, 3, 4, 5, 6, 8, 10, 12, 16};
 constexpr int kMaxWaveVpl = 6;
@@ -1112,7 +1125,7 @@ static void split_rowmax(const void* x, int64_t rows, int64_t cols, int vec, voi
                        cols, segs, wpr, vec, cached, partial);
     check_launch("rowmax_partial_kernel");
     if (wpr > 1) {
-        hipLaunchKernelGGL(rowmax_reduce_kernel, dim3((unsigned)std::min<int64_t>(rows, 65536)), dim3(kQBlock), 0, s,
+        hipLaunchKernelGGL(rowmax_reduce_kernel, dim3((unsigned)std::min<int64_t>(rows, 65536)), dim3(kRowBlock), 0, s,
                            (const uint32_t*)partial, rows, wpr, rowmax);
         check_launch("rowmax_reduce_kernel");
     }
@@ -1134,12 +1147,12 @@ static void quantize_impl(const void* x, int64_t rows, int64_t cols, uint8_t* q,
     const int32_t dt = BF16 ? ELY_BF16 : ELY_F32;
     const int vpl = rows_vpl(cols, dt, x, q, out);
     if (vpl > kMaxWaveVpl) {
-        // one block per row: kWavesPerBlock waves of ceil(vpl / kWavesPerBlock) vectors per lane
-        if (rows > 0xFFFFFFFFLL / kQBlock) fail(ELY_EINVAL, "fp8 quantize: too many rows for one launch");
-        switch ((vpl + kWavesPerBlock - 1) / kWavesPerBlock) {
-            case 2: hipLaunchKernelGGL((quant_block_row_kernel<FMT, BF16, 2>), dim3((unsigned)rows), dim3(kQBlock), 0, s, x, cols, q, k, out); break;
-            case 3: hipLaunchKernelGGL((quant_block_row_kernel<FMT, BF16, 3>), dim3((unsigned)rows), dim3(kQBlock), 0, s, x, cols, q, k, out); break;
-            case 4: hipLaunchKernelGGL((quant_block_row_kernel<FMT, BF16, 4>), dim3((unsigned)rows), dim3(kQBlock), 0, s, x, cols, q, k, out); break;
+        // one block per row: kRowWaves waves of ceil(vpl / kRowWaves) vectors per lane
+        if (rows > 0xFFFFFFFFLL / kRowBlock) fail(ELY_EINVAL, "fp8 quantize: too many rows for one launch");
+        switch ((vpl + kRowWaves - 1) / kRowWaves) {
+            case 2: hipLaunchKernelGGL((quant_block_row_kernel<FMT, BF16, 2>), dim3((unsigned)rows), dim3(kRowBlock), 0, s, x, cols, q, k, out); break;
+            case 3: hipLaunchKernelGGL((quant_block_row_kernel<FMT, BF16, 3>), dim3((unsigned)rows), dim3(kRowBlock), 0, s, x, cols, q, k, out); break;
+            case 4: hipLaunchKernelGGL((quant_block_row_kernel<FMT, BF16, 4>), dim3((unsigned)rows), dim3(kRowBlock), 0, s, x, cols, q, k, out); break;
             default: fail(ELY_EINVAL, "internal: no block-row path for this row length");
         }
         check_launch("quant_block_row_kernel");
