@@ -119,7 +119,10 @@ static_assert(kNormTile % (64 * 8 * ELY_NORM_UNROLL) == 0 && kNormSmallTile % (6
               "a grad-norm tile is whole unrolled rounds of 8-element groups");
 constexpr int kNormUnroll = ELY_NORM_UNROLL;
 constexpr int kFinalUnroll = ELY_FINAL_UNROLL;
-constexpr int kBlock = 256;
+#ifndef ELY_MTA_BLOCK
+#define ELY_MTA_BLOCK 256        // threads per block of the grad-norm and clip-scale kernels
+#endif
+constexpr int kBlock = ELY_MTA_BLOCK;
 #ifndef ELY_ADAM_BLOCK
 #define ELY_ADAM_BLOCK 64      // AdamW threads per block: one wave
 #endif
@@ -842,7 +845,7 @@ static NormLaunch grad_norm_impl(const ely_tensor* accs, const ely_tensor* grads
     out.tile = tile;
     if (tiles > 0) {
         const int64_t waves = std::min<int64_t>(tiles, mt_blocks(ELY_NORM_BPC) * (kBlock / kWave));
-        const int64_t blocks = (waves + 3) / 4;
+        const int64_t blocks = (waves + kBlock / kWave - 1) / (kBlock / kWave);
         int dt = table[0].dtype;
         for (const NormDesc& d : table)
             if (d.dtype != dt) dt = -1;
@@ -904,7 +907,7 @@ static ClipArgsKernel pick_clip_args(int dt) {
 static void clip_scale(const NormLaunch& nl, const float* coef_dev, void* stream) {
     if (nl.tiles == 0) return;
     const int64_t waves = std::min<int64_t>({nl.tiles, mt_blocks(ELY_CLIP_BPC) * (kBlock / kWave), 0xFFFFFFFFLL / kWave});
-    const int64_t blocks = (waves + 3) / 4;
+    const int64_t blocks = (waves + kBlock / kWave - 1) / (kBlock / kWave);
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (nl.dtable) {
         const ClipKernel k = nl.tile == kNormTile ? pick_clip<kNormTile>(nl.dt) : pick_clip<kNormSmallTile>(nl.dt);
