@@ -26,7 +26,7 @@ namespace ely {
 #define ELY_PLANES_UNROLL 1  // byte planes: 16-byte vectors a lane keeps in flight
 #endif
 #ifndef ELY_PLANES_BPC
-#define ELY_PLANES_BPC 4  // byte planes: blocks per compute unit
+#define ELY_PLANES_BPC 262144  // byte planes: grid cap in blocks per compute unit (one-shot)
 #endif
 #ifndef ELY_NIBBLES_UNROLL
 #define ELY_NIBBLES_UNROLL 2  // nibble planes: vectors a lane keeps in flight
@@ -38,11 +38,21 @@ namespace ely {
 #define ELY_NIBBLES_BPC 8  // nibble planes: blocks per compute unit
 #endif
 
-constexpr int kPBlock = 256;
+#ifndef ELY_PLANES_BLOCK
+// byte planes: threads per block.  64-thread blocks on a one-shot grid,
+// against 256-thread blocks at 4 per CU in one process on the same buffers
+// (identical planes): 2^28 fp32 split 6.02 TB/s against 5.56, join 5.89
+// against 5.23; 2^29 bf16 6.53 and 6.53 against 5.75 and 5.56; C1's
+// activation 6.20 and 6.28-6.39 against 5.92 and 5.78-5.88.
+#define ELY_PLANES_BLOCK 64
+#endif
+constexpr int kPBlock = ELY_PLANES_BLOCK;
+constexpr int kNBlock = 256;  // nibble planes: threads per block
 
-static unsigned grid_for(int64_t work, int per_cu) {
-    const int64_t cap = (int64_t)device_info().cus * per_cu;
-    const int64_t b = std::max<int64_t>(1, std::min<int64_t>((work + kPBlock - 1) / kPBlock, cap));
+static unsigned grid_for(int64_t work, int per_cu, int block = kPBlock) {
+    // a dispatch counts its work-items in 32 bits: past that the grid strides
+    const int64_t cap = std::min<int64_t>((int64_t)device_info().cus * per_cu, 0xFFFFFFFFLL / block);
+    const int64_t b = std::max<int64_t>(1, std::min<int64_t>((work + block - 1) / block, cap));
     return (unsigned)b;
 }
 
@@ -250,12 +260,12 @@ __device__ __forceinline__ uint32_t e4m3_quad(float a, float b, float c, float d
 // share of each nibble plane is EPL/2 bytes (4 or 2) and every load and
 // store instruction of a wave covers one contiguous run.
 template <bool BF16>
-__global__ __launch_bounds__(kPBlock) void nibbles_encode_kernel(const void* __restrict__ t, int64_t n, int vec,
+__global__ __launch_bounds__(kNBlock) void nibbles_encode_kernel(const void* __restrict__ t, int64_t n, int vec,
                                                                  uint8_t* __restrict__ hi, uint8_t* __restrict__ lo,
                                                                  unsigned long long* __restrict__ bad) {
     constexpr int EPL = BF16 ? 8 : 4;
-    const int64_t T = (int64_t)gridDim.x * kPBlock;
-    const int64_t tid = (int64_t)blockIdx.x * kPBlock + threadIdx.x;
+    const int64_t T = (int64_t)gridDim.x * kNBlock;
+    const int64_t tid = (int64_t)blockIdx.x * kNBlock + threadIdx.x;
     uint32_t nbad = 0;  // this lane's mismatches
     uint32_t qbad = 0;  // the vector path's (the wave's, with ELY_NIB_BALLOT)
     int64_t done = 0;  // elements covered by the vector path
@@ -332,11 +342,11 @@ __global__ __launch_bounds__(kPBlock) void nibbles_encode_kernel(const void* __r
 
 // Decode: a lane takes 4 codes (2 bytes of each plane) and writes one 16-byte
 // fp32 vector, so every store instruction covers one contiguous 1 KB.
-__global__ __launch_bounds__(kPBlock) void nibbles_decode_kernel(const uint8_t* __restrict__ hi,
+__global__ __launch_bounds__(kNBlock) void nibbles_decode_kernel(const uint8_t* __restrict__ hi,
                                                                  const uint8_t* __restrict__ lo, int64_t n, int vec,
                                                                  float* __restrict__ out) {
-    const int64_t T = (int64_t)gridDim.x * kPBlock;
-    const int64_t tid = (int64_t)blockIdx.x * kPBlock + threadIdx.x;
+    const int64_t T = (int64_t)gridDim.x * kNBlock;
+    const int64_t tid = (int64_t)blockIdx.x * kNBlock + threadIdx.x;
     int64_t done = 0;
     if (vec) {
         const int64_t nq = n / 4;
@@ -444,11 +454,11 @@ int ely_fp8_nibbles_encode(const void* t, int32_t t_dtype, int64_t n, uint8_t* h
         if (!t || !hi || !lo || !bad_dev) fail(ELY_EINVAL, "ely_fp8_nibbles_encode: null pointer");
         hipStream_t s = static_cast<hipStream_t>(stream);
         const int vec = aligned16(t) && (reinterpret_cast<uintptr_t>(hi) % 4 == 0) && (reinterpret_cast<uintptr_t>(lo) % 4 == 0);
-        const unsigned g = grid_for(std::max<int64_t>(n / 8 / kNUnroll, 1), ELY_NIBBLES_BPC);
+        const unsigned g = grid_for(std::max<int64_t>(n / 8 / kNUnroll, 1), ELY_NIBBLES_BPC, kNBlock);
         if (t_dtype == ELY_BF16)
-            hipLaunchKernelGGL(nibbles_encode_kernel<true>, dim3(g), dim3(kPBlock), 0, s, t, n, vec, hi, lo, bad_dev);
+            hipLaunchKernelGGL(nibbles_encode_kernel<true>, dim3(g), dim3(kNBlock), 0, s, t, n, vec, hi, lo, bad_dev);
         else
-            hipLaunchKernelGGL(nibbles_encode_kernel<false>, dim3(g), dim3(kPBlock), 0, s, t, n, vec, hi, lo, bad_dev);
+            hipLaunchKernelGGL(nibbles_encode_kernel<false>, dim3(g), dim3(kNBlock), 0, s, t, n, vec, hi, lo, bad_dev);
         check_launch("nibbles_encode_kernel");
     });
 }
@@ -460,7 +470,7 @@ int ely_fp8_nibbles_decode(const uint8_t* hi, const uint8_t* lo, int64_t n, floa
         if (!out || !hi || !lo) fail(ELY_EINVAL, "ely_fp8_nibbles_decode: null pointer");
         hipStream_t s = static_cast<hipStream_t>(stream);
         const int vec = aligned16(out) && (reinterpret_cast<uintptr_t>(hi) % 2 == 0) && (reinterpret_cast<uintptr_t>(lo) % 2 == 0);
-        hipLaunchKernelGGL(nibbles_decode_kernel, dim3(grid_for(std::max<int64_t>(n / 4 / kNUnroll, 1), ELY_NIBBLES_BPC)), dim3(kPBlock), 0, s,
+        hipLaunchKernelGGL(nibbles_decode_kernel, dim3(grid_for(std::max<int64_t>(n / 4 / kNUnroll, 1), ELY_NIBBLES_BPC, kNBlock)), dim3(kNBlock), 0, s,
                            hi, lo, n, vec, out);
         check_launch("nibbles_decode_kernel");
     });
