@@ -35,7 +35,7 @@ namespace ely {
 #define ELY_NIB_BALLOT 1  // nibble encode: count mismatches per wave on the scalar unit
 #endif
 #ifndef ELY_NIBBLES_BPC
-#define ELY_NIBBLES_BPC 8  // nibble planes: blocks per compute unit
+#define ELY_NIBBLES_BPC 262144  // nibble planes: grid cap in blocks per compute unit (one-shot)
 #endif
 
 #ifndef ELY_PLANES_BLOCK
@@ -47,7 +47,15 @@ namespace ely {
 #define ELY_PLANES_BLOCK 64
 #endif
 constexpr int kPBlock = ELY_PLANES_BLOCK;
-constexpr int kNBlock = 256;  // nibble planes: threads per block
+#ifndef ELY_NIBBLES_BLOCK
+// nibble planes: threads per block.  64-thread blocks on a one-shot grid,
+// against 256-thread blocks at 8 per CU in one process on the same buffers
+// (exact round trips): encode 5.89-6.15 TB/s on C1's activation against
+// 5.62-5.76 and 6.48-6.51 on 2^29 elements against 5.68-5.73; decode equal
+// on C1 (5.3) and 5.65-5.70 against 5.03-5.05 on 2^29
+#define ELY_NIBBLES_BLOCK 64
+#endif
+constexpr int kNBlock = ELY_NIBBLES_BLOCK;
 
 static unsigned grid_for(int64_t work, int per_cu, int block = kPBlock) {
     // a dispatch counts its work-items in 32 bits: past that the grid strides
