@@ -266,9 +266,8 @@ def bench_placement(device, stream, hold_gib=150):
     """C1's step with its shard allocated while `hold_gib` GiB of other device
     memory are held, so that its pages come from another physical range
     than a fresh process's first allocation. The kernel and the bytes are
-    the same; what changes is the DRAM side (the average EA read latency of
-    the AdamW launch, measured with rocprofv3 --pmc through
-    --placement-probe)."""
+    the same; what changes is the DRAM side (how long the L2 channels wait
+    for DRAM credits)."""
     hold = torch.empty(hold_gib << 30, dtype=torch.uint8, device=device)
     params, grads = make_shard(device)
     o = measure_shard(params, grads, device, stream, 3, 1)
@@ -278,130 +277,6 @@ def bench_placement(device, stream, hold_gib=150):
     r = _shard_rates(o, 2, 192)
     r["held_GiB"] = hold_gib
     return r
-
-
-def placement_probe(device, mode):
-    """Three C1 optimizer steps, for a rocprofv3 --pmc run: in a fresh
-    process ("fresh") or with the shard allocated while 150 GiB are held
-    ("hold150")."""
-    from elysium_wan_amd import optim
-
-    hold = torch.empty(150 << 30, dtype=torch.uint8, device=device) if mode == "hold150" else None
-    params, grads = make_shard(device)
-    opt = optim.FusedAdamW(params, lr=LR, betas=BETAS, eps=EPS, weight_decay=WD, order="host", max_norm=MAX_NORM, working_copy=True)
-    for _ in range(3):
-        opt.step(grads=grads)
-    torch.cuda.synchronize()
-    log(f"placement probe {mode}: 3 steps done")
-    del hold
-
-
-def placement_sweep(device, stream, pool_gib: int, spec: str) -> None:
-    """C1-sized AdamW streams (one tensor each: p fp32, g bf16, copy bf16,
-    m fp32, v fp32) carved from one pool of pool_gib GiB at chosen offsets,
-    printing one JSON line per placement: the fused AdamW kernel and the
-    three stream probes (ely_probe_streams: read, write, read+write, no
-    arithmetic) between HIP events.  spec: comma-separated entries, "A"
-    (all five streams packed from A GiB on, each on a 2 MiB boundary) or
-    "A:B" (p, g, copy from A GiB, m and v from B GiB + 11.7 GiB)."""
-    from elysium_wan_amd import _lib, optim
-
-    L = _lib.load()
-    gib = 1 << 30
-    n = sum(int(np.prod(s)) for s in block_shapes(D_MODEL)) * N_BLOCKS
-    rnd = lambda b: (b + (2 << 20) - 1) // (2 << 20) * (2 << 20)  # noqa: E731
-    pool = torch.empty(pool_gib * gib, dtype=torch.uint8, device=device)
-    pool.zero_()
-    sink = torch.zeros(4, device=device)
-    aws = torch.empty(L.ely_adamw_workspace_bytes(1), dtype=torch.uint8, device=device)
-    consts = (_lib.ElyConsts * 1)()
-    consts[0].c[:] = optim.host_consts(LR, BETAS, EPS, WD, 1.0)
-    sptr = _lib.stream_ptr(device)
-    torch.cuda.synchronize()
-
-    def take(off, nbytes, dt):
-        if off + nbytes > pool.numel():
-            raise SystemExit(f"placement {off / gib:.1f} GiB + {nbytes / gib:.1f} GiB does not fit the {pool_gib} GiB pool")
-        return pool[off: off + nbytes].view(dt)
-
-    for entry in spec.split(","):
-        a, _, b = entry.partition(":")
-        ca = int(a) * gib
-        p = take(ca, n * 4, torch.float32)
-        g = take(ca + rnd(n * 4), n * 2, torch.bfloat16)
-        c = take(ca + rnd(n * 4) + rnd(n * 2), n * 2, torch.bfloat16)
-        cb = (int(b) * gib if b else ca) + rnd(n * 4) + 2 * rnd(n * 2)
-        m = take(cb, n * 4, torch.float32)
-        v = take(cb + rnd(n * 4), n * 4, torch.float32)
-        arrs = [_lib.tensor_array([t]) for t in (p, g, m, v, c)]
-
-        def adam(_):
-            _lib.check(L.ely_adamw_step(arrs[0], arrs[1], arrs[2], arrs[3], arrs[4], 1, consts, _lib.ORDER_HOST, 1, None,
-                                        aws.data_ptr(), aws.numel(), sptr), "adamw")
-
-        def probe(which):
-            def run(_):
-                _lib.check(L.ely_probe_streams(which, p.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr(), c.data_ptr(), n,
-                                               8 * 256, sink.data_ptr(), sptr), "probe")
-            return run
-
-        out = {"placement": entry, "adamw_GBs": n * 28 / time_events(adam, 6, stream) / 1e6,
-               "read_GBs": n * 14 / time_events(probe(0), 6, stream) / 1e6,
-               "write_GBs": n * 14 / time_events(probe(1), 6, stream) / 1e6,
-               "rw_GBs": n * 28 / time_events(probe(2), 6, stream) / 1e6}
-        print(json.dumps({k: (round(x) if isinstance(x, float) else x) for k, x in out.items()}), flush=True)
-
-
-def pmc_summary(dbs, spec: str | None = None) -> None:
-    """Per-launch counters of the placement sweep's kernels from rocprofv3
-    --pmc --kernel-trace databases (rocpd SQLite), as markdown: per group of
-    consecutive launches of one kernel (the first, a warm-up, dropped), the
-    kernel time, each counter summed over its instances, how unevenly the
-    instances (L2 channels) share it (max / mean), and, for a counter X_sum
-    with its X_LEVEL_sum, the average number of cycles a request is
-    outstanding (LEVEL / requests).  With the sweep's SPEC, each group is
-    labelled with its placement (four kernels per placement, in order)."""
-    import collections
-    import sqlite3
-
-    kernels = ("adamw_kernel", "probe_read_kernel", "probe_write_kernel", "probe_rw_kernel")
-    for path in dbs:
-        db = sqlite3.connect(path)
-        rows = db.execute("select dispatch_id, name, duration, counter_name, counter_value from pmc_events "
-                          "order by dispatch_id, id").fetchall()
-        disp = collections.OrderedDict()
-        for did, name, dur, cn, cv in rows:
-            d = disp.setdefault(did, {"name": name, "dur": dur, "c": collections.defaultdict(list)})
-            d["c"][cn].append(cv)
-        groups = []
-        for d in disp.values():
-            k = next((k for k in kernels if k in d["name"]), None)
-            if k is None:
-                continue
-            if groups and groups[-1][0] == k:
-                groups[-1][1].append(d)
-            else:
-                groups.append((k, [d]))
-        names = sorted({cn for _, ds in groups for cn in ds[0]["c"]})
-        lat = [cn for cn in names if cn.endswith("_LEVEL_sum") and cn.replace("_LEVEL_sum", "_sum") in names]
-        labels = spec.split(",") if spec else None
-        print(f"`{os.path.basename(os.path.dirname(path))}`\n")
-        print("| # | placement | kernel | µs | " + " | ".join(names + [c.replace("_LEVEL_sum", " cycles") for c in lat]) + " |")
-        print("|---|---|---|---|" + "---|" * (len(names) + len(lat)))
-        for i, (k, ds) in enumerate(groups):
-            ds = ds[1:] or ds
-            cells, tot_of = [], {}
-            for cn in names:
-                inst = len(ds[0]["c"][cn])
-                per = [sum(x["c"][cn][j] for x in ds) / len(ds) for j in range(inst)]
-                tot = tot_of[cn] = sum(per)
-                cells.append(f"{tot:.4g}" + (f" (max/mean {max(per) / (tot / inst):.2f})" if inst > 1 and tot else ""))
-            for cn in lat:
-                req = tot_of[cn.replace("_LEVEL_sum", "_sum")]
-                cells.append(f"{tot_of[cn] / req:.0f}" if req > 1000 else "-")
-            place = labels[i // 4] if labels and i // 4 < len(labels) else ""
-            print(f"| {i} | {place} | {k} | {sum(x['dur'] for x in ds) / len(ds) / 1e3:.0f} | " + " | ".join(cells) + " |")
-        print()
 
 
 def _activations(device, rows, cols, copies, seed):
@@ -1600,7 +1475,6 @@ def main():
                     help="run only these extra legs (repeatable), no headline, and print their JSON (for profiling one leg)")
     ap.add_argument("--c4-summary", metavar="DIR", help="summarize a rocprofv3 --kernel-trace run of --no-optimizer --codec c4 into profiles/")
     ap.add_argument("--copy-summary", metavar="DIR", help="summarize a rocprofv3 --memory-copy-trace run of --leg host_moments into profiles/")
-    ap.add_argument("--placement-probe", choices=("fresh", "hold150"), help="three C1 steps only (for rocprofv3 --pmc)")
     ap.add_argument("--cpu-sample", type=int, default=256 * 1024 * 1024)
     ap.add_argument("--profile-pass", action="store_true", help="launch each measured kernel a few times, untimed, for rocprofv3 --pmc runs")
     ap.add_argument("--traffic-summary", nargs="+", metavar="DIR",
@@ -1608,10 +1482,6 @@ def main():
     ap.add_argument("--traffic-command", default="", help="the command line recorded in the traffic summary")
     ap.add_argument("--trace-summary", nargs=2, metavar=("STEP_DIR", "CODEC_DIR"), help="summarize two rocprofv3 --kernel-trace runs into profiles/")
     ap.add_argument("--bench-json", nargs="+", metavar="OUT", help="the traced runs' own stdout (step, then codec), quoted beside the trace summary")
-    ap.add_argument("--placement-sweep", nargs=2, metavar=("POOL_GIB", "SPEC"),
-                    help="AdamW and stream probes on C1-sized streams carved from one pool (SPEC: A[,A...] or A:B[,...] GiB)")
-    ap.add_argument("--pmc-summary", nargs="+", metavar="DB", help="markdown table of rocprofv3 --pmc databases of a placement sweep")
-    ap.add_argument("--pmc-spec", help="the placement sweep's SPEC, to label --pmc-summary's rows")
     args = ap.parse_args()
     if args.traffic_summary:
         if len(args.traffic_summary) not in (2, 3):
@@ -1621,9 +1491,6 @@ def main():
         return
     if args.trace_summary:
         trace_summary(*args.trace_summary, args.bench_json)
-        return
-    if args.pmc_summary:
-        pmc_summary(args.pmc_summary, args.pmc_spec)
         return
     if args.copy_summary:
         copy_summary(args.copy_summary)
@@ -1643,14 +1510,6 @@ def main():
     if args.profile_pass:
         with torch.cuda.stream(stream):
             profile_pass(device)
-        return
-    if args.placement_probe:
-        with torch.cuda.stream(stream):
-            placement_probe(device, args.placement_probe)
-        return
-    if args.placement_sweep:
-        with torch.cuda.stream(stream):
-            placement_sweep(device, stream, int(args.placement_sweep[0]), args.placement_sweep[1])
         return
     with torch.cuda.stream(stream):
         if args.leg:

@@ -56,7 +56,6 @@ EXPORTS = (
     "ely_byteplanes_join",
     "ely_fp8_nibbles_encode",
     "ely_fp8_nibbles_decode",
-    "ely_probe_streams",
     "ely_selftest_fp8_cvt",
     "ely_selftest_sqrt",
 )
@@ -129,7 +128,6 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
         L.ely_byteplanes_join.argtypes = [P, I64, I32, P, P]
         L.ely_fp8_nibbles_encode.argtypes = [P, I32, I64, P, P, P, P]
         L.ely_fp8_nibbles_decode.argtypes = [P, P, I64, P, P]
-        L.ely_probe_streams.argtypes = [I32, P, P, P, P, P, I64, I32, P, P]
         L.ely_selftest_fp8_cvt.argtypes = [ctypes.c_uint32, ctypes.c_uint64, I32, P, P]
         L.ely_selftest_sqrt.argtypes = [ctypes.c_uint32, ctypes.c_uint64, P, P]
         _lib = L

@@ -68,21 +68,11 @@ namespace ely {
 // lists 1 group reads 10 % faster than 8 (2: 7 %), small lists the same
 #define ELY_NORM_UNROLL_F32 1
 #endif
-#ifndef ELY_NT
-#define ELY_NT 3                 // bit 0: nontemporal AdamW loads, bit 1: nontemporal stores
-#endif
-#ifndef ELY_ADAM_UNROLL
-#define ELY_ADAM_UNROLL 1        // block steps a thread keeps in flight
-#endif
-#ifndef ELY_ADAM_HALVES
-#define ELY_ADAM_HALVES 1        // quads per thread per block step (1 or 2)
-#endif
-#ifndef ELY_ADAM_ONE_UPLOAD
-// 1: AdamW descriptors and constants staged in one host-to-device copy.
-// Measured in alternating processes: C0's launch 0.127 against 0.133 ms,
-// but the staged host-moment step (small per-chunk tables queued behind the
-// moment copies) 0.60 against 0.39 s, so the two copies stay.
-#define ELY_ADAM_ONE_UPLOAD 0
+#ifndef ELY_ADAM_MAP_CHUNKS
+// entries of the tile -> tensor chunk map a table launch looks its first
+// tensor up in (one scalar load instead of a binary search of dependent
+// loads over the descriptors)
+#define ELY_ADAM_MAP_CHUNKS 4096
 #endif
 #ifndef ELY_ADAM_BPC
 #define ELY_ADAM_BPC (1 << 20)   // AdamW grid cap, blocks per compute unit: in practice one block per tile
@@ -522,13 +512,20 @@ static_assert(sizeof(AdamDesc) == 64, "AdamDesc is 64 bytes");
 struct AdamTableRef {
     const AdamDesc* d;
     const ely_adamw_consts* c;
+    const int32_t* map;  // tensor holding the first tile of each 2^shift-tile chunk, or null
+    int32_t shift;
     __device__ __forceinline__ const ely_adamw_consts& consts(int i) const { return c[i]; }
+    // a tensor at or before the one holding `tile` (the caller walks forward)
+    __device__ __forceinline__ int start(int n, int64_t tile) const {
+        return map ? map[tile >> shift] : find_tensor(d, n, tile);
+    }
 };
 constexpr int kArgTensors = 48;
 struct AdamArgTable {
     AdamDesc d[kArgTensors];
     ely_adamw_consts c;
     __device__ __forceinline__ const ely_adamw_consts& consts(int) const { return c; }
+    __device__ __forceinline__ int start(int n, int64_t tile) const { return find_tensor(d, n, tile); }
 };
 
 template <bool BF16G, int ORDER, bool WD, bool CLIP, bool FOLD>
@@ -544,97 +541,82 @@ struct AdamOp {
     }
 };
 
-// Native vector types, so the nontemporal builtins apply to 16-byte accesses.
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-template <typename T>
-__device__ __forceinline__ T ld_stream(const ELY_GLOBAL T* p) {
-#if ELY_NT & 1
-    return __builtin_nontemporal_load(p);
-#else
-    return *p;
-#endif
-}
-
-template <typename T>
-__device__ __forceinline__ void st_stream(ELY_GLOBAL T* p, T v) {
-#if ELY_NT & 2
-    __builtin_nontemporal_store(v, p);
-#else
-    *p = v;
-#endif
-}
-
-// The vector path's unit of work is a block step of kStep = kHalves * kHalf
-// elements (kHalf = 4 per thread).  Thread t owns the quads [4t, 4t+4),
-// [kHalf+4t, kHalf+4t+4), ... of the step, so each load or store
-// instruction of a wave covers one contiguous 1 KB (fp32) or 512 B (bf16)
-// run: every request is a full, aligned line, and the halves of a step never
-// share a line.  ELY_ADAM_UNROLL steps are loaded before the first is
-// updated, keeping 7 * kHalves * U 16- or 8-byte loads per thread in flight.
-constexpr int kHalves = ELY_ADAM_HALVES;
-constexpr int64_t kHalf = (int64_t)kAdamBlock * 4;
-constexpr int64_t kStep = kHalf * kHalves;
+// The vector path works in block steps of kStep = 4 * kAdamBlock elements:
+// lane t owns the quad [4t, 4t+4) of a step, so each load or store
+// instruction of the wave covers one contiguous 1 KB (fp32) or 512 B (bf16)
+// run, full aligned lines.  Its loads and stores are buffer instructions
+// on resources whose base is the range's first element (the descriptor
+// words in scalar registers, one 32-bit lane offset per access, accesses
+// past the range's bytes dropped by the hardware), all with the
+// nontemporal hint: C1's launch ran 1.5-2 % faster than with the same
+// accesses as global instructions on 64-bit lane addresses.
+constexpr int64_t kStep = (int64_t)kAdamBlock * 4;
 static_assert(kAdamTile % kStep == 0, "an AdamW tile is a whole number of block steps");
 
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x2 __attribute__((ext_vector_type(2)));
+constexpr int kBufNT = 2;  // cache-policy operand of the buffer accesses: nt
 
-template <bool BF16G>
-struct Quad2 {
-    f32x4 p[kHalves], m[kHalves], v[kHalves];
-    float g[4 * kHalves];
-};
+// Buffer resource over `bytes` bytes from `base` (raw, stride 0; the third
+// word the CDNA3/4 buffer format takes for untyped 32-bit data).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, int32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+}
 
-template <bool BF16G, bool FOLD>
-__device__ __forceinline__ void quad_load(const AdamDesc& d, int64_t i, Quad2<BF16G>& Q) {
-#pragma unroll
-    for (int h = 0; h < kHalves; ++h) {
-        const int64_t e = i + h * kHalf;
-        Q.p[h] = ld_stream(gp(reinterpret_cast<const f32x4*>(d.p + e)));
-        Q.m[h] = ld_stream(gp(reinterpret_cast<const f32x4*>(d.m + e)));
-        Q.v[h] = ld_stream(gp(reinterpret_cast<const f32x4*>(d.v + e)));
+__device__ __forceinline__ i32x4 bits4(const float (&x)[4]) {
+    return i32x4{__float_as_int(x[0]), __float_as_int(x[1]), __float_as_int(x[2]), __float_as_int(x[3])};
+}
+
+// Whole block steps of elements [e0, e0 + steps * kStep) of an aligned tensor.
+template <bool BF16G, int ORDER, bool WD, bool CLIP, bool FOLD>
+__device__ __forceinline__ void adam_steps(const AdamDesc& d, const ely_adamw_consts& c, float coef, int64_t e0,
+                                           int64_t steps) {
+    using Op = AdamOp<BF16G, ORDER, WD, CLIP, FOLD>;
+    const int32_t ne = (int32_t)(steps * kStep);  // a tile's range: at most kAdamTile elements
+    const __amdgpu_buffer_rsrc_t rp = buf_rsrc(d.p + e0, ne * 4), rm = buf_rsrc(d.m + e0, ne * 4),
+                                 rv = buf_rsrc(d.v + e0, ne * 4);
+    const __amdgpu_buffer_rsrc_t rg = BF16G ? buf_rsrc(static_cast<const uint16_t*>(d.g) + e0, ne * 2)
+                                            : buf_rsrc(static_cast<const float*>(d.g) + e0, ne * 4);
+    const __amdgpu_buffer_rsrc_t ra = FOLD ? buf_rsrc(d.acc + e0, ne * 4) : rp;
+    const __amdgpu_buffer_rsrc_t rc = d.copy ? buf_rsrc(d.copy + e0, ne * 2) : rp;
+    for (int64_t s = 0; s < steps; ++s) {
+        const int32_t o = (int32_t)(s * kStep) + (int32_t)threadIdx.x * 4;  // the lane's first element
+        const i32x4 P = __builtin_amdgcn_raw_buffer_load_b128(rp, o * 4, 0, kBufNT);
+        const i32x4 M = __builtin_amdgcn_raw_buffer_load_b128(rm, o * 4, 0, kBufNT);
+        const i32x4 V = __builtin_amdgcn_raw_buffer_load_b128(rv, o * 4, 0, kBufNT);
+        float g[4];
         if (BF16G) {
-            const u32x2 w = ld_stream(gp(reinterpret_cast<const u32x2*>(static_cast<const uint16_t*>(d.g) + e)));
-            Q.g[4 * h + 0] = bf16_to_f32(w[0] & 0xFFFFu);
-            Q.g[4 * h + 1] = bf16_to_f32(w[0] >> 16);
-            Q.g[4 * h + 2] = bf16_to_f32(w[1] & 0xFFFFu);
-            Q.g[4 * h + 3] = bf16_to_f32(w[1] >> 16);
+            const i32x2 w = __builtin_amdgcn_raw_buffer_load_b64(rg, o * 2, 0, kBufNT);
+            g[0] = bf16_to_f32((uint32_t)w[0] & 0xFFFFu);
+            g[1] = bf16_to_f32((uint32_t)w[0] >> 16);
+            g[2] = bf16_to_f32((uint32_t)w[1] & 0xFFFFu);
+            g[3] = bf16_to_f32((uint32_t)w[1] >> 16);
         } else {
-            const f32x4 a = ld_stream(gp(reinterpret_cast<const f32x4*>(static_cast<const float*>(d.g) + e)));
+            const i32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rg, o * 4, 0, kBufNT);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) Q.g[4 * h + j] = a[j];
+            for (int j = 0; j < 4; ++j) g[j] = __int_as_float(a[j]);
         }
         if (FOLD) {
             // the last microbatch folded in: acc + widen(g), one fp32 rounding
-            const f32x4 a = ld_stream(gp(reinterpret_cast<const f32x4*>(d.acc + e)));
+            const i32x4 a = __builtin_amdgcn_raw_buffer_load_b128(ra, o * 4, 0, kBufNT);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) Q.g[4 * h + j] = a[j] + Q.g[4 * h + j];
+            for (int j = 0; j < 4; ++j) g[j] = __int_as_float(a[j]) + g[j];
         }
-    }
-}
-
-template <bool BF16G, int ORDER, bool WD, bool CLIP, bool FOLD>
-__device__ __forceinline__ void quad_update_store(const AdamDesc& d, int64_t i, Quad2<BF16G>& Q,
-                                                  const ely_adamw_consts& c, float coef) {
-    using Op = AdamOp<BF16G, ORDER, WD, CLIP, FOLD>;
-#pragma unroll
-    for (int h = 0; h < kHalves; ++h) {
         float p[4], m[4], v[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            p[j] = Q.p[h][j];
-            m[j] = Q.m[h][j];
-            v[j] = Q.v[h][j];
-            Op::elem(p[j], Q.g[4 * h + j], m[j], v[j], c, coef);
+            p[j] = __int_as_float(P[j]);
+            m[j] = __int_as_float(M[j]);
+            v[j] = __int_as_float(V[j]);
+            Op::elem(p[j], g[j], m[j], v[j], c, coef);
         }
-        const int64_t e = i + h * kHalf;
-        st_stream(gp(reinterpret_cast<f32x4*>(d.p + e)), f32x4{p[0], p[1], p[2], p[3]});
-        st_stream(gp(reinterpret_cast<f32x4*>(d.m + e)), f32x4{m[0], m[1], m[2], m[3]});
-        st_stream(gp(reinterpret_cast<f32x4*>(d.v + e)), f32x4{v[0], v[1], v[2], v[3]});
+        __builtin_amdgcn_raw_buffer_store_b128(bits4(p), rp, o * 4, 0, kBufNT);
+        __builtin_amdgcn_raw_buffer_store_b128(bits4(m), rm, o * 4, 0, kBufNT);
+        __builtin_amdgcn_raw_buffer_store_b128(bits4(v), rv, o * 4, 0, kBufNT);
         if (d.copy) {
-            const u32x2 o = {f32_to_bf16(p[0]) | (f32_to_bf16(p[1]) << 16), f32_to_bf16(p[2]) | (f32_to_bf16(p[3]) << 16)};
-            st_stream(gp(reinterpret_cast<u32x2*>(d.copy + e)), o);
+            const i32x2 w = {(int32_t)(f32_to_bf16(p[0]) | (f32_to_bf16(p[1]) << 16)),
+                             (int32_t)(f32_to_bf16(p[2]) | (f32_to_bf16(p[3]) << 16))};
+            __builtin_amdgcn_raw_buffer_store_b64(w, rc, o * 2, 0, kBufNT);
         }
     }
 }
@@ -643,25 +625,10 @@ template <bool BF16G, int ORDER, bool WD, bool CLIP, bool FOLD>
 __device__ __forceinline__ void adam_range(const AdamDesc& d, const ely_adamw_consts& c, float coef, int64_t e0,
                                            int64_t e1) {
     using Op = AdamOp<BF16G, ORDER, WD, CLIP, FOLD>;
-    constexpr int U = ELY_ADAM_UNROLL;
     int64_t done = e0;
     if (d.aligned) {
         const int64_t steps = (e1 - e0) / kStep;
-        const int64_t t4 = (int64_t)threadIdx.x * 4;
-        int64_t s = 0;
-        for (; s + U <= steps; s += U) {
-            Quad2<BF16G> Q[U];
-#pragma unroll
-            for (int u = 0; u < U; ++u) quad_load<BF16G, FOLD>(d, e0 + (s + u) * kStep + t4, Q[u]);
-#pragma unroll
-            for (int u = 0; u < U; ++u)
-                quad_update_store<BF16G, ORDER, WD, CLIP, FOLD>(d, e0 + (s + u) * kStep + t4, Q[u], c, coef);
-        }
-        for (; s < steps; ++s) {
-            Quad2<BF16G> Q;
-            quad_load<BF16G, FOLD>(d, e0 + s * kStep + t4, Q);
-            quad_update_store<BF16G, ORDER, WD, CLIP, FOLD>(d, e0 + s * kStep + t4, Q, c, coef);
-        }
+        if (steps > 0) adam_steps<BF16G, ORDER, WD, CLIP, FOLD>(d, c, coef, e0, steps);
         done = e0 + steps * kStep;
     }
     // Scalar path: unaligned tensors entirely, aligned tensors' last partial step.
@@ -687,7 +654,7 @@ __device__ __forceinline__ void adamw_body(const Tab& tab, int32_t n, int64_t to
     const int64_t t0 = b * total_tiles / G, t1 = (b + 1) * total_tiles / G;
     if (t0 >= t1) return;
     int64_t tile = t0;
-    for (int ti = find_tensor(tab.d, n, t0); ti < n && tile < t1; ++ti) {
+    for (int ti = tab.start(n, t0); ti < n && tile < t1; ++ti) {
         const AdamDesc d = tab.d[ti];
         const int64_t ntiles = (d.numel + kAdamTile - 1) / kAdamTile;
         const int64_t tend = min(t1, (int64_t)d.tile_begin + ntiles);
@@ -702,7 +669,7 @@ __device__ __forceinline__ void adamw_body(const Tab& tab, int32_t n, int64_t to
     // interleaved: in round r block b takes tile r*G + b, so at any moment the
     // whole grid streams one contiguous window of the shard
     if (b >= total_tiles) return;
-    int ti = find_tensor(tab.d, n, b);
+    int ti = tab.start(n, b);
     for (int64_t tile = b; tile < total_tiles; tile += G) {
         while (ti + 1 < n && tab.d[ti + 1].tile_begin <= tile) ++ti;
         const AdamDesc d = tab.d[ti];
@@ -721,9 +688,10 @@ __device__ __forceinline__ void adamw_body(const Tab& tab, int32_t n, int64_t to
 // segment, which is constant memory.
 template <bool BF16G, int ORDER, bool WD, bool CLIP, bool FOLD>
 __global__ __launch_bounds__(kAdamBlock) void adamw_kernel(const AdamDesc* __restrict__ desc,
-                                                       const ely_adamw_consts* __restrict__ consts, int32_t n,
+                                                       const ely_adamw_consts* __restrict__ consts,
+                                                       const int32_t* __restrict__ map, int32_t shift, int32_t n,
                                                        int64_t total_tiles, const float* __restrict__ coef_ptr) {
-    adamw_body<BF16G, ORDER, WD, CLIP, FOLD>(AdamTableRef{desc, consts}, n, total_tiles, coef_ptr);
+    adamw_body<BF16G, ORDER, WD, CLIP, FOLD>(AdamTableRef{desc, consts, map, shift}, n, total_tiles, coef_ptr);
 }
 
 template <bool BF16G, int ORDER, bool WD, bool CLIP, bool FOLD>
@@ -732,7 +700,8 @@ __global__ __launch_bounds__(kAdamBlock) void adamw_args_kernel(const AdamArgTab
     adamw_body<BF16G, ORDER, WD, CLIP, FOLD>(tab, n, total_tiles, coef_ptr);
 }
 
-typedef void (*AdamKernel)(const AdamDesc*, const ely_adamw_consts*, int32_t, int64_t, const float*);
+typedef void (*AdamKernel)(const AdamDesc*, const ely_adamw_consts*, const int32_t*, int32_t, int32_t, int64_t,
+                           const float*);
 typedef void (*AdamArgsKernel)(const AdamArgTable, int32_t, int64_t, const float*);
 
 template <bool BF16G, int ORDER, bool WD, bool CLIP, bool FOLD>
@@ -752,8 +721,10 @@ static K pick_adam(bool wd, bool clip) {
     return A ? (K)AdamKernels<BF16G, ORDER, false, false, FOLD>::args : (K)AdamKernels<BF16G, ORDER, false, false, FOLD>::table;
 }
 
+constexpr int kMapChunks = ELY_ADAM_MAP_CHUNKS;
 static size_t adam_table_bytes(int32_t n) {
-    return align_up((size_t)n * sizeof(AdamDesc), 256) + align_up((size_t)n * sizeof(ely_adamw_consts), 256);
+    return align_up((size_t)n * sizeof(AdamDesc), 256) + align_up((size_t)n * sizeof(ely_adamw_consts), 256) +
+           (size_t)kMapChunks * sizeof(int32_t);
 }
 
 static void check_list(const ely_tensor* t, int32_t n, const char* what) {
@@ -1001,19 +972,38 @@ static void adamw_impl(const ely_tensor* params, const ely_tensor* accs, const e
     AdamDesc* dtable = reinterpret_cast<AdamDesc*>(ws);
     const size_t consts_off = align_up((size_t)n * sizeof(AdamDesc), 256);
     ely_adamw_consts* dconsts = reinterpret_cast<ely_adamw_consts*>(ws + consts_off);
-#if ELY_ADAM_ONE_UPLOAD
-    // descriptors and constants go up in one copy, laid out as in the workspace
-    std::vector<char> staged(consts_off + cs.size() * sizeof(ely_adamw_consts), 0);
-    memcpy(staged.data(), table.data(), table.size() * sizeof(AdamDesc));
-    memcpy(staged.data() + consts_off, cs.data(), cs.size() * sizeof(ely_adamw_consts));
-    upload(dtable, staged.data(), staged.size(), s);
-#else
+    // One-shot grids (one block per tile) look each block's first tensor up
+    // in a chunk map: the tensor holding the first tile of every 2^shift
+    // consecutive tiles, at most kMapChunks entries, placed after the
+    // constants and uploaded with them (C1: 1.5 % off the launch against a
+    // binary search of the descriptors per block).  A capped grid's blocks
+    // search the descriptors once each.
+    int32_t shift = 0;
+    const size_t map_off = align_up(cs.size() * sizeof(ely_adamw_consts), 256);
+    std::vector<char> staged(map_off);
+    memcpy(staged.data(), cs.data(), cs.size() * sizeof(ely_adamw_consts));
+    const bool mapped = blocks == tiles;
+    if (mapped) {
+        while (((tiles - 1) >> shift) >= kMapChunks) ++shift;
+        const int64_t chunks = ((tiles - 1) >> shift) + 1;
+        staged.resize(map_off + (size_t)chunks * sizeof(int32_t));
+        int32_t* map = reinterpret_cast<int32_t*>(staged.data() + map_off);
+        int32_t ti = 0;
+        for (int64_t ch = 0; ch < chunks; ++ch) {
+            while (ti + 1 < (int32_t)table.size() && table[ti + 1].tile_begin <= (ch << shift)) ++ti;
+            map[ch] = ti;
+        }
+    } else {
+        staged.resize(cs.size() * sizeof(ely_adamw_consts));
+    }
+    // two copies, not one: a single merged copy made the staged host-moment
+    // step slower (its small table copies queue behind the moment copies)
     upload(dtable, table.data(), table.size() * sizeof(AdamDesc), s);
-    upload(dconsts, cs.data(), cs.size() * sizeof(ely_adamw_consts), s);
-#endif
+    upload(dconsts, staged.data(), staged.size(), s);
+    const int32_t* dmap = mapped ? reinterpret_cast<const int32_t*>(ws + consts_off + map_off) : nullptr;
     const AdamKernel k = pick_adam_kernel<AdamKernel>(accs != nullptr, gdt == ELY_BF16, order, wd, clip);
     hipLaunchKernelGGL(k, dim3((unsigned)blocks), dim3(kAdamBlock), 0, s, (const AdamDesc*)dtable,
-                       (const ely_adamw_consts*)dconsts, (int32_t)table.size(), tiles, coef_dev);
+                       (const ely_adamw_consts*)dconsts, dmap, shift, (int32_t)table.size(), tiles, coef_dev);
     check_launch("adamw_kernel");
 }
 

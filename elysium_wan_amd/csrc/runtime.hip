@@ -10,7 +10,7 @@
 #include "ely_host.hpp"
 
 #ifndef ELY_UPLOAD_SLOTS
-#define ELY_UPLOAD_SLOTS 8  // pinned upload ring slots per device (two per AdamW launch)
+#define ELY_UPLOAD_SLOTS 8  // pinned upload ring slots per device (two per table AdamW launch)
 #endif
 
 namespace ely {
@@ -65,6 +65,7 @@ int64_t mt_blocks(int per_cu) {
 // interleave with the bulk moment copies.
 namespace {
 struct Slot {
+    std::mutex mu;  // held while the slot is waited on and refilled
     void* host = nullptr;
     size_t cap = 0;
     hipEvent_t done = nullptr;
@@ -75,7 +76,7 @@ struct Ring {
     Slot slots[kSlots];
     int next = 0;
 };
-std::mutex g_ring_mu;
+std::mutex g_ring_mu;  // guards the map of rings and each ring's next slot, never held while waiting
 std::map<int, Ring> g_rings;
 }  // namespace
 
@@ -83,10 +84,17 @@ void upload(void* dst, const void* src, size_t bytes, hipStream_t stream) {
     if (bytes == 0) return;
     int dev = 0;
     check_hip(hipGetDevice(&dev), "hipGetDevice");
-    std::lock_guard<std::mutex> lk(g_ring_mu);
-    Ring& ring = g_rings[dev];
-    Slot& s = ring.slots[ring.next];
-    ring.next = (ring.next + 1) % Ring::kSlots;
+    Slot* slot;
+    {
+        std::lock_guard<std::mutex> lk(g_ring_mu);
+        Ring& ring = g_rings[dev];
+        slot = &ring.slots[ring.next];
+        ring.next = (ring.next + 1) % Ring::kSlots;
+    }
+    // Another thread whose ring wrapped onto the same slot waits here, not
+    // on the ring: uploads to other slots go on meanwhile.
+    Slot& s = *slot;
+    std::lock_guard<std::mutex> lk(s.mu);
     if (s.pending) {
         check_hip(hipEventSynchronize(s.done), "hipEventSynchronize(upload slot)");
         s.pending = false;

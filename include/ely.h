@@ -295,20 +295,6 @@ int ely_fp8_nibbles_encode(const void* t, int32_t t_dtype, int64_t n, uint8_t* h
  * codes. */
 int ely_fp8_nibbles_decode(const uint8_t* hi, const uint8_t* lo, int64_t n, float* out, void* stream);
 
-/* ---------------------------------------------------------- measurement */
-
-/* No counterpart in the reference: streaming probes with the fused AdamW's
- * five streams (p, m, v fp32; g and the working copy bf16; n elements each)
- * and no arithmetic, so that the update's rate can be held against what the
- * memory system gives the same traffic in the same placement.  which 0:
- * read p, g, m, v (14 B/elem; `sink` is a device float that is never
- * written in practice); 1: write p, m, v, copy (14 B/elem; overwrites
- * them); 2: both (28 B/elem, the update's traffic; p, m, v rotate their
- * values and copy := g).  n a multiple of 4; fp32 streams 16-byte
- * aligned, bf16 ones 8-byte aligned; `blocks` blocks of 256 threads. */
-int ely_probe_streams(int32_t which, void* p, void* g, void* m, void* v, void* copy, int64_t n,
-                      int32_t blocks, void* sink, void* stream);
-
 /* ------------------------------------------------------------ self-test */
 
 /* Device self-check of the gfx950 fp8 conversion instruction against the

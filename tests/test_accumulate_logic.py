@@ -2,8 +2,9 @@
 count lanes (the one part dtype the fold adds on the host, as
 runtime/pieces.py:206-214 does): prefix-ordered folding of out-of-order
 parts, quarantine holding its index until release or reject, the deferred
-last part and its merge, and the reference's duplicate and incompleteness
-refusals (runtime/accumulate.py:15-137)."""
+last part and its merge, the reference's duplicate and incompleteness
+refusals (runtime/accumulate.py:15-137), and the attributes the reference's
+stage reads (runtime/stage.py:175-177)."""
 
 from __future__ import annotations
 
@@ -40,9 +41,9 @@ def test_fold_part_holds_only_the_tensor_whose_prefix_is_missing():
     acc = OrderedAccumulator(range(2))
     acc.fold_part(1, 0, 2, _lane(5))
     acc.fold_part(0, 1, 2, _lane(7))
-    assert acc.next == [0, 1] and (1, 0) in acc.parts
+    assert list(acc.next) == [0, 1] and (1, 0) in acc.parts and len(acc.parts) == 1
     acc.fold_part(0, 0, 2, _lane(1))
-    assert acc.next == [2, 1]
+    assert list(acc.next) == [2, 1] and (1, 0) not in acc.parts
     acc.end_part(0)
     with pytest.raises(AssertionError, match="incomplete"):
         acc.result()
@@ -75,28 +76,39 @@ def test_deferred_last_part_and_its_merge(m):
         OrderedAccumulator([0]).step_inputs()
 
 
-def test_count_fold_sums_in_order_and_refuses_as_the_reference():
-    """runtime/accumulate.py:250-318 on the host: int64 (E,) vectors per
-    (microbatch, layer), summed exactly; the reference's refusals."""
-    from elysium_wan_amd.accumulate import CountFold
+def test_stage_reads_order_next_and_parts_as_the_reference_does():
+    """runtime/stage.py:175-177 asks, per tensor, whether microbatch mb's part
+    is neither held nor already folded: `(mb, i) not in a.parts and
+    a.next[i] <= k`; `a.next` is None before any part."""
+    from elysium_wan_amd.accumulate import OrderedAccumulator
 
-    cf = CountFold(step=7, n_mb=2, layers=[3], experts={3: 4}, total={3: 6})
-    cf.add(1, 3, torch.tensor([1, 2, 3, 0]), peer=1)
-    assert not cf.complete() and cf.missing() == [(0, 3)]
-    with pytest.raises(RuntimeError, match=r"MOE-COUNT \(step 7, mb 0, layer 3, peer -\): count vector missing at the owner \(1 missing\)"):
-        cf.result()
-    cf.add(0, 3, torch.tensor([0, 0, 6, 0]), peer=0)
-    assert torch.equal(cf.result()[3], torch.tensor([1, 2, 9, 0]))
-    bad = [
-        ((2, 3, torch.zeros(4, dtype=torch.int64)), "microbatch outside"),
-        ((0, 9, torch.zeros(4, dtype=torch.int64)), "no selection bias"),
-        ((0, 3, torch.zeros(4, dtype=torch.int64)), "given twice"),
-    ]
-    for args, msg in bad:
-        with pytest.raises(RuntimeError, match=msg):
-            cf.add(*args, peer=2)
-    fresh = CountFold(step=1, n_mb=1, layers=[0], experts={0: 2}, total={0: 3})
-    for vec, msg in ((torch.zeros(2), "not an int64"), (torch.zeros(3, dtype=torch.int64), "shape"),
-                     (torch.tensor([-1, 4]), "negative"), (torch.tensor([1, 1]), "sum to 2, want T_mb\\*k = 3")):
-        with pytest.raises(RuntimeError, match=msg):
-            fresh.add(0, 0, vec, peer=0)
+    acc = OrderedAccumulator([5, 3, 9])
+    assert acc.next is None and len(acc.parts) == 0 and acc.pos == 0
+    acc.fold_part(3, 0, 2, _lane(1))  # held: mb 5 is missing
+    k = acc.order.index(3)
+    missing = [i for i in range(2) if (3, i) not in acc.parts and acc.next[i] <= k]
+    assert missing == [1]
+    acc.fold_part(5, 0, 2, _lane(2))
+    acc.fold_part(5, 1, 2, _lane(3))
+    acc.end_part(5)
+    assert list(acc.next) == [2, 1] and acc.closed == {5} and acc.added == 1
+    acc.add(9, [_lane(4), _lane(5)], verified=False)
+    assert acc.quarantine == {9} and (9, 0) in acc.parts
+    acc.fold_part(3, 1, 2, _lane(6))
+    acc.end_part(3)
+    assert list(acc.next) == [2, 2] and not acc.complete()
+    acc.release(9)
+    assert acc.complete() and [int(t[0]) for t in acc.result()] == [7, 14]
+
+
+def test_microbatch_outside_the_order_is_held_and_never_folded():
+    from elysium_wan_amd.accumulate import OrderedAccumulator
+
+    acc = OrderedAccumulator([0])
+    acc.add(7, [_lane(1)])
+    assert (7, 0) in acc.parts and acc.pos == 0 and not acc.complete()
+    acc.add(0, [_lane(2)])
+    # the reference counts every closed microbatch: two closed for an order of one
+    assert not acc.complete()
+    with pytest.raises(AssertionError, match="incomplete: 2/1 microbatches in, 1 tensors held"):
+        acc.result()

@@ -84,6 +84,36 @@ def test_incomplete_fold_names_what_it_waits_for():
         fold.add_embed(0, torch.randn(3, 4, device="cuda"))
 
 
+def test_a_head_gradient_unlike_the_first_is_refused_before_any_launch():
+    """The row kernels size every row from the fold's table: a later Head
+    gradient of another width, dtype or device is refused at add_head, as
+    the reference's own shape and dtype errors stop it, and nothing of it
+    reaches the GPU; the fold then finishes as if it never came."""
+    from elysium_wan_amd.accumulate import TiedRowFold
+
+    fold = TiedRowFold(8, range(2))
+    h0 = torch.randn(8, 4, device="cuda")
+    fold.add_head(1, h0, torch.tensor([2]))  # held: microbatch 0 comes later
+    for bad in (torch.randn(8, 5, device="cuda"), torch.randn(8, 4, device="cuda").to(torch.bfloat16),
+                torch.randn(8, 4, dtype=torch.float64, device="cuda")):
+        with pytest.raises((RuntimeError, TypeError)):
+            fold.add_head(0, bad, torch.tensor([1]))
+    with pytest.raises(RuntimeError, match="not in the fold order"):
+        fold.add_head(7, h0, torch.tensor([1]))
+    h1 = torch.randn(8, 4, device="cuda")
+    fold.add_head(0, h1, torch.tensor([1]))
+    e0, e1 = torch.randn(1, 4, device="cuda"), torch.randn(1, 4, device="cuda")
+    fold.add_embed(0, e0)
+    fold.add_embed(1, e1)
+    assert fold.complete()
+    # the stock fold: g_i = h_i + E_i (E_i zero outside T_i), acc = g_0 + g_1
+    E0, E1 = torch.zeros_like(h1), torch.zeros_like(h0)
+    E0[1], E1[2] = e0[0], e1[0]
+    stock = (h1 + E0) + (h0 + E1)
+    torch.cuda.synchronize()
+    assert torch.equal(fold.result().view(torch.int32), stock.view(torch.int32))
+
+
 @settings(max_examples=25, deadline=None, derandomize=True, suppress_health_check=[HealthCheck.too_slow])
 @given(
     m=st.integers(1, 5),
