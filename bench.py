@@ -367,6 +367,44 @@ def bench_codec(device, stream, rows, cols, copies, iters=20, per_tensor=False, 
             "roundtrip_ms": r_ms,
             "roundtrip_GBs": n * ROUNDTRIP_BYTES_PER_ELEM / r_ms / 1e6,
         }
+        if per_tensor:
+            # the one-pass form given the exponent (fp8.quantize(...,
+            # per_tensor=True, k_hint=k)): a right hint (x read once) and a
+            # wrong one (the fixup pass at the true exponent), and the round
+            # trip with a right hint; the codes equal the split path's
+            hws = _lib.workspace(device, L.ely_fp8_hint_workspace_bytes(n))
+            hit = torch.zeros(1, dtype=torch.int32, device=device)
+            k_true = [int(kk.item()) for kk in ks]
+            qh = [torch.empty_like(qq) for qq in qs]
+
+            def qhint(i, f=f, off=0):
+                j = i % copies
+                _lib.check(L.ely_fp8_quantize_hint(xs[j].data_ptr(), _lib.BF16, n, f, k_true[j] + off, qh[j].data_ptr(), ks[j].data_ptr(),
+                                                   None, hit.data_ptr(), hws.data_ptr(), hws.numel(), sptr), "qh")
+
+            def rthint(i, f=f):
+                j = i % copies
+                _lib.check(L.ely_fp8_quantize_hint(xs[j].data_ptr(), _lib.BF16, n, f, k_true[j], None, ks[j].data_ptr(),
+                                                   outs[j].data_ptr(), hit.data_ptr(), hws.data_ptr(), hws.numel(), sptr), "rth")
+
+            h_ms = time_events(qhint, iters, stream)
+            hit_after = int(hit.item())
+            m_ms = time_events(lambda i: qhint(i, off=1), iters, stream)
+            miss_after = int(hit.item())
+            rh_ms = time_events(rthint, iters, stream)
+            qhint(0)
+            torch.cuda.synchronize()
+            out[fmt]["hint"] = {
+                "quantize_hit_ms": h_ms,
+                "quantize_hit_GBs": n * CODEC_BYTES_PER_ELEM / h_ms / 1e6,
+                "quantize_miss_ms": m_ms,
+                "quantize_miss_GBs": n * CODEC_BYTES_PER_ELEM / m_ms / 1e6,
+                "roundtrip_hit_ms": rh_ms,
+                "roundtrip_hit_GBs": n * ROUNDTRIP_BYTES_PER_ELEM / rh_ms / 1e6,
+                "hit_flags": [hit_after, miss_after],
+                "codes_equal_split_path": bool(torch.equal(qh[0], qs[0])),
+            }
+            del qh
         if back_to_back:
             # the same launches queued back to back (one event pair around all)
             out[fmt]["back_to_back_GBs"] = {

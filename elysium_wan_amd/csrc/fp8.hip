@@ -518,19 +518,12 @@ __global__ __launch_bounds__(kRowBlock) void rowmax_reduce_kernel(const uint32_t
     }
 }
 
+// Segment `seg` of row `row` converted at the row's scale rs (the split
+// path's convert launch and the hint path's fixup).
 template <int FMT, bool BF16>
-__global__ __launch_bounds__(kQBlock) void quant_split_kernel(const void* __restrict__ x, int64_t rows, int64_t cols,
-                                                              int64_t segs, int vec,
-                                                              const uint32_t* __restrict__ rowmax,
-                                                              uint8_t* __restrict__ q, int32_t* __restrict__ k,
-                                                              void* __restrict__ out) {
+__device__ __forceinline__ void quant_segment(const void* x, int64_t row, int64_t cols, int64_t seg, int vec,
+                                              const RowScale& rs, uint8_t* q, void* out, int lane) {
     constexpr int EPV = Seg<BF16>::EPV, VPL = Seg<BF16>::VPL, ESZ = BF16 ? 2 : 4;
-    const int lane = threadIdx.x & (kWave - 1);
-    const int64_t gw = (int64_t)blockIdx.x * kWavesPerBlock + wave_uniform(threadIdx.x / kWave);
-    const int64_t row = gw / segs, seg = gw % segs;
-    if (row >= rows) return;
-    const RowScale rs = row_scale<FMT>(to_f32_bits<BF16>(rowmax[row]), BF16, BF16);
-    if (seg == 0 && lane == 0 && k) k[row] = rs.k;
     const int64_t e0 = seg * kSegElems, e1 = min(e0 + kSegElems, cols);
     const int64_t base = row * cols;
     if (vec && rs.fast) {
@@ -562,6 +555,118 @@ __global__ __launch_bounds__(kQBlock) void quant_split_kernel(const void* __rest
     } else {
         quant_slow<FMT, BF16>(x, base, e0, e1, rs, q, out, lane);
     }
+}
+
+template <int FMT, bool BF16>
+__global__ __launch_bounds__(kQBlock) void quant_split_kernel(const void* __restrict__ x, int64_t rows, int64_t cols,
+                                                              int64_t segs, int vec,
+                                                              const uint32_t* __restrict__ rowmax,
+                                                              uint8_t* __restrict__ q, int32_t* __restrict__ k,
+                                                              void* __restrict__ out) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t gw = (int64_t)blockIdx.x * kWavesPerBlock + wave_uniform(threadIdx.x / kWave);
+    const int64_t row = gw / segs, seg = gw % segs;
+    if (row >= rows) return;
+    const RowScale rs = row_scale<FMT>(to_f32_bits<BF16>(rowmax[row]), BF16, BF16);
+    if (seg == 0 && lane == 0 && k) k[row] = rs.k;
+    quant_segment<FMT, BF16>(x, row, cols, seg, vec, rs, q, out, lane);
+}
+
+// ------------------------------------------------- per-tensor, with a hint
+//
+// Per-tensor scaling needs the whole tensor's |x|max before the first code,
+// so the split path reads x twice.  Given the exponent a caller expects (the
+// previous step's, say), one pass does both: wave w reads segment w once,
+// writes its |x|max to partial[w] and its codes at the hinted scale.  A
+// small launch folds the partials to kHintBlocks maxima, and a capped fixup
+// launch, whose every wave folds those to the tensor's k, writes k (and
+// whether it equals the hint) and exits when it does; on a miss its waves
+// convert every segment again at the true scale.  The codes depend on k
+// alone, so a hit's codes are the split path's, byte for byte.
+constexpr int kHintBlocks = 256;         // maxima the reduce launch leaves (4 per lane of a fixup wave)
+#ifndef ELY_HINT_FIXUP_WPC
+// fixup grid cap, waves per compute unit.  C4 per-tensor (1.07 GB of bf16):
+// a hit 6.25-6.32 TB/s with 8 or 32, 6.1 with 128; a miss 2.5 TB/s with 8,
+// 3.1 with 32 or 128
+#define ELY_HINT_FIXUP_WPC 32
+#endif
+constexpr int kHintFixupWavesPerCU = ELY_HINT_FIXUP_WPC;
+
+template <int FMT, bool BF16>
+__global__ __launch_bounds__(kQBlock) void quant_hint_kernel(const void* __restrict__ x, int64_t n, int64_t segs,
+                                                             RowScale hs, uint8_t* __restrict__ q,
+                                                             void* __restrict__ out, uint32_t* __restrict__ partial) {
+    constexpr int EPV = Seg<BF16>::EPV, VPL = Seg<BF16>::VPL, ESZ = BF16 ? 2 : 4;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t seg = (int64_t)blockIdx.x * kWavesPerBlock + wave_uniform(threadIdx.x / kWave);
+    if (seg >= segs) return;
+    const int64_t e0 = seg * kSegElems;
+    const int64_t nv = (min(e0 + kSegElems, n) - e0) / EPV;
+    const uint4* xr = reinterpret_cast<const uint4*>(static_cast<const char*>(x) + e0 * ESZ);
+    uint4 buf[VPL];
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+        const int64_t vi = lane + (int64_t)kWave * j;
+        buf[j] = ld_vec(xr + (vi < nv ? vi : nv - 1));
+    }
+    uint32_t amax = 0;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+        const int64_t vi = lane + (int64_t)kWave * j;
+        if (vi >= nv) continue;
+        amax = vec_absmax<BF16>(buf[j], amax);
+        uint32_t words[2];
+        const int64_t e = e0 + vi * EPV;
+        quant_vec_fast<FMT, BF16>(buf[j], hs, words, out ? static_cast<char*>(out) + e * ESZ : nullptr);
+        if (q) {
+            if (BF16) st_vec2(q + e, make_uint2(words[0], words[1]));
+            else st_u32(q + e, words[0]);
+        }
+    }
+    amax = wave_max_u32(amax);
+    if (lane == 0) partial[seg] = amax;
+}
+
+// partial[0, segs) -> out[b] for b < kHintBlocks (block b folds a contiguous
+// share; integer max, so the order does not matter).
+__global__ __launch_bounds__(kRowBlock) void hint_reduce_kernel(const uint32_t* __restrict__ partial, int64_t segs,
+                                                              uint32_t* __restrict__ out) {
+    __shared__ uint32_t red[kRowWaves];
+    const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
+    const int64_t per = (segs + kHintBlocks - 1) / kHintBlocks;
+    const int64_t i0 = (int64_t)blockIdx.x * per, i1 = min(i0 + per, segs);
+    uint32_t m = 0;
+    for (int64_t i = i0 + threadIdx.x; i < i1; i += kRowBlock) m = max(m, partial[i]);
+    m = wave_max_u32(m);
+    if (lane == 0) red[w] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t t = red[0];
+        for (int j = 1; j < kRowWaves; ++j) t = max(t, red[j]);
+        out[blockIdx.x] = t;
+    }
+}
+
+template <int FMT, bool BF16>
+__global__ __launch_bounds__(kQBlock) void quant_hint_fixup_kernel(const void* __restrict__ x, int64_t n, int64_t segs,
+                                                                   int vec, int32_t k_hint,
+                                                                   const uint32_t* __restrict__ block_max,
+                                                                   uint8_t* __restrict__ q, int32_t* __restrict__ k,
+                                                                   void* __restrict__ out, int32_t* __restrict__ hit) {
+    static_assert(kHintBlocks == 4 * kWave, "a fixup lane folds four block maxima");
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t gw = (int64_t)blockIdx.x * kWavesPerBlock + wave_uniform(threadIdx.x / kWave);
+    const int64_t waves = (int64_t)gridDim.x * kWavesPerBlock;
+    uint32_t m = max(max(block_max[lane], block_max[lane + kWave]), max(block_max[lane + 2 * kWave], block_max[lane + 3 * kWave]));
+    m = wave_max_u32(m);
+    const RowScale rs = row_scale<FMT>(to_f32_bits<BF16>(m), BF16, BF16);
+    const bool same = rs.fast && rs.k == k_hint;
+    if (gw == 0 && lane == 0) {
+        k[0] = rs.k;
+        if (hit) hit[0] = same ? 1 : 0;
+    }
+    if (same) return;
+    for (int64_t seg = gw; seg < segs; seg += waves) quant_segment<FMT, BF16>(x, 0, n, seg, vec, rs, q, out, lane);
 }
 
 // -------------------------------------------------------------- dequantize
@@ -1175,6 +1280,52 @@ static void quantize_impl(const void* x, int64_t rows, int64_t cols, uint8_t* q,
     check_launch("quant_split_kernel");
 }
 
+// Workspace of the hint path over n elements: one maximum per segment, the
+// reduce launch's kHintBlocks maxima; at least the split path's, which a
+// call falls back to when the one-pass form does not apply.
+static size_t hint_ws_bytes(int64_t n) {
+    const int64_t segs = std::max<int64_t>((n + kSegElems - 1) / kSegElems, 1);
+    return std::max(align_up((size_t)segs * 4, 256) + align_up((size_t)kHintBlocks * 4, 256), split_ws_bytes(1));
+}
+
+template <int FMT, bool BF16>
+static void quantize_hint_impl(const void* x, int64_t n, int32_t k_hint, uint8_t* q, int32_t* k, void* out,
+                               int32_t* hit, void* workspace, int64_t ws_bytes, hipStream_t s) {
+    if (!workspace || ws_bytes < (int64_t)hint_ws_bytes(n))
+        fail(ELY_EWORKSPACE, "ely_fp8_quantize_hint: workspace of " + std::to_string(ws_bytes) + " bytes, need " +
+                                 std::to_string(hint_ws_bytes(n)) + " (ely_fp8_hint_workspace_bytes)");
+    const int64_t epv = BF16 ? 8 : 4;
+    const bool vec = n > 0 && n % epv == 0 && aligned16(x) && (!out || aligned16(out)) &&
+                     (!q || reinterpret_cast<uintptr_t>(q) % (uintptr_t)epv == 0);
+    if (!vec || k_hint < -kFastK || k_hint > kFastK) {
+        // no one-pass form for this tensor or hint: the split path, a miss
+        quantize_impl<FMT, BF16>(x, 1, n, q, k, out, workspace, ws_bytes, s);
+        if (hit) {
+            hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(64), 0, s, reinterpret_cast<uint32_t*>(hit), (int64_t)1, 0u);
+            check_launch("fill_u32_kernel");
+        }
+        return;
+    }
+    const int64_t segs = (n + kSegElems - 1) / kSegElems;
+    uint32_t* partial = static_cast<uint32_t*>(workspace);
+    uint32_t* block_max = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + align_up((size_t)segs * 4, 256));
+    RowScale hs;
+    hs.k = k_hint;
+    hs.fast = true;
+    hs.s_down = __builtin_bit_cast(float, (uint32_t)(127 - k_hint) << 23);
+    hs.s_up = __builtin_bit_cast(float, (uint32_t)(127 + k_hint) << 23);
+    hipLaunchKernelGGL((quant_hint_kernel<FMT, BF16>), dim3(blocks_for_waves(segs)), dim3(kQBlock), 0, s, x, n, segs, hs,
+                       q, out, partial);
+    check_launch("quant_hint_kernel");
+    hipLaunchKernelGGL(hint_reduce_kernel, dim3(kHintBlocks), dim3(kRowBlock), 0, s, (const uint32_t*)partial, segs,
+                       block_max);
+    check_launch("hint_reduce_kernel");
+    const int64_t waves = std::min<int64_t>(segs, (int64_t)device_info().cus * kHintFixupWavesPerCU);
+    hipLaunchKernelGGL((quant_hint_fixup_kernel<FMT, BF16>), dim3(blocks_for_waves(waves)), dim3(kQBlock), 0, s, x, n,
+                       segs, 1, k_hint, (const uint32_t*)block_max, q, k, out, hit);
+    check_launch("quant_hint_fixup_kernel");
+}
+
 template <int FMT, bool BF16OUT>
 static void dequantize_impl(const uint8_t* q, const int32_t* k, int64_t rows, int64_t cols, void* out,
                             hipStream_t s) {
@@ -1399,6 +1550,30 @@ int ely_fp8_quantize_noalloc(const void* x, int32_t x_dtype, int64_t rows, int64
         } else {
             if (x_dtype == ELY_BF16) quantize_impl<kE5M2, true>(x, rows, cols, q, k, nullptr, ws, wsb, s);
             else quantize_impl<kE5M2, false>(x, rows, cols, q, k, nullptr, ws, wsb, s);
+        }
+    });
+}
+
+int64_t ely_fp8_hint_workspace_bytes(int64_t n) {
+    if (n < 0) return -1;
+    return (int64_t)hint_ws_bytes(n);
+}
+
+int ely_fp8_quantize_hint(const void* x, int32_t x_dtype, int64_t n, int32_t fmt, int32_t k_hint, uint8_t* q,
+                          int32_t* k, void* out, int32_t* hit_dev, void* workspace, int64_t ws_bytes, void* stream) {
+    return guarded([&] {
+        check_fmt(fmt);
+        check_dtype(x_dtype, "x_dtype");
+        check_shape(1, n);
+        if (!k) fail(ELY_EINVAL, "ely_fp8_quantize_hint: null k");
+        if (n > 0 && (!x || (!q && !out))) fail(ELY_EINVAL, "ely_fp8_quantize_hint: null x, or neither q nor out");
+        hipStream_t s = static_cast<hipStream_t>(stream);
+        if (fmt == ELY_E4M3) {
+            if (x_dtype == ELY_BF16) quantize_hint_impl<kE4M3, true>(x, n, k_hint, q, k, out, hit_dev, workspace, ws_bytes, s);
+            else quantize_hint_impl<kE4M3, false>(x, n, k_hint, q, k, out, hit_dev, workspace, ws_bytes, s);
+        } else {
+            if (x_dtype == ELY_BF16) quantize_hint_impl<kE5M2, true>(x, n, k_hint, q, k, out, hit_dev, workspace, ws_bytes, s);
+            else quantize_hint_impl<kE5M2, false>(x, n, k_hint, q, k, out, hit_dev, workspace, ws_bytes, s);
         }
     });
 }

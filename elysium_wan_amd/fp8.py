@@ -70,10 +70,50 @@ def scale_exp(x: torch.Tensor, fmt: str = "e4m3", per_tensor: bool = False) -> t
     return k
 
 
-def quantize(x: torch.Tensor, fmt: str = "e4m3", per_tensor: bool = False):
+def _hint(k_hint, per_tensor: bool, what: str) -> int | None:
+    if k_hint is None:
+        return None
+    if not per_tensor:
+        raise ValueError(f"{what}: k_hint applies to per-tensor scaling (per_tensor=True)")
+    k_hint = int(k_hint)
+    if not -(2**31) <= k_hint < 2**31:
+        raise ValueError(f"{what}: k_hint {k_hint} is not an int32")
+    return k_hint
+
+
+def _per_tensor_hint(x: torch.Tensor, f: int, k_hint: int, q, out, what: str) -> torch.Tensor:
+    """The one-pass per-tensor path (ely_fp8_quantize_hint): fills q and/or
+    out, returns k (one element, on x's device)."""
+    _lib.require_gpu(x, what)
+    x = x.detach().contiguous()
+    k = torch.empty(1, dtype=torch.int32, device=x.device)
+    L = _lib.load()
+    ws = _lib.workspace(x.device, L.ely_fp8_hint_workspace_bytes(x.numel()))
+    _lib.check(
+        L.ely_fp8_quantize_hint(x.data_ptr(), _lib.dtype_code(x), x.numel(), f, k_hint, None if q is None else q.data_ptr(),
+                                k.data_ptr(), None if out is None else out.data_ptr(), None, ws.data_ptr(), ws.numel(),
+                                _lib.stream_ptr(x.device)),
+        what,
+    )
+    return k
+
+
+def quantize(x: torch.Tensor, fmt: str = "e4m3", per_tensor: bool = False, k_hint: int | None = None):
     """x -> (fp8 tensor shaped like x, int32 k shaped like x with the last dim
-    1).  Exact given k (model/fp8.py:45-49)."""
+    1).  Exact given k (model/fp8.py:45-49).
+
+    k_hint (per-tensor only; an addition to the reference's signature): the
+    exponent the caller expects, e.g. the previous step's.  The results are
+    the same whatever the hint; when it is right, x is read once instead of
+    twice."""
     f = _fmt(fmt)
+    hint = _hint(k_hint, per_tensor, "quantize")
+    if hint is not None:
+        if x.dim() == 0:
+            raise ValueError("quantize: a 0-d tensor has no rows")
+        q = torch.empty(x.shape, dtype=FORMATS[fmt][0], device=x.device)
+        k = _per_tensor_hint(x, f, hint, q, None, "quantize")
+        return q, k.reshape((1,) * x.dim())
     if per_tensor:
         q, k = quantize(x.reshape(1, -1), fmt)
         return q.reshape(x.shape), k.reshape((1,) * x.dim())
@@ -124,10 +164,17 @@ def dequantize(q: torch.Tensor, k: torch.Tensor, dtype: torch.dtype = torch.floa
     return out
 
 
-def roundtrip(x: torch.Tensor, fmt: str = "e4m3", per_tensor: bool = False) -> torch.Tensor:
+def roundtrip(x: torch.Tensor, fmt: str = "e4m3", per_tensor: bool = False, k_hint: int | None = None) -> torch.Tensor:
     """The declared recipe at a boundary: quantize then dequantize, in x's
-    dtype (model/fp8.py:56-63), fused into one pass."""
+    dtype (model/fp8.py:56-63), fused into one pass.  k_hint as quantize's."""
     f = _fmt(fmt)
+    hint = _hint(k_hint, per_tensor, "roundtrip")
+    if hint is not None:
+        if x.dim() == 0:
+            raise ValueError("roundtrip: a 0-d tensor has no rows")
+        out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+        _per_tensor_hint(x, f, hint, None, out, "roundtrip")
+        return out
     if per_tensor:
         return roundtrip(x.reshape(1, -1), fmt).reshape(x.shape)
     x, rows, cols = _rows(x, "roundtrip")

@@ -1,0 +1,154 @@
+"""Per-tensor fp8 quantize with an exponent hint (fp8.quantize(...,
+per_tensor=True, k_hint=...), ely_fp8_quantize_hint): whatever the hint, the
+bytes and the exponent are model/fp8.py:28-49's for one row of every
+element, checked against the oracle, against the split path and against
+torch's own ops on the GPU at config C4's full size; the device flag says
+whether the one pass stood (hint right) or the fixup pass ran (hint wrong,
+out of range, or a tensor with no one-pass form)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import activation, bits, say
+
+pytestmark = pytest.mark.gpu
+
+
+def _oracle_in(x: torch.Tensor) -> np.ndarray:
+    return bits(x) if x.dtype == torch.bfloat16 else bits(x).astype(np.float32)
+
+
+def _hint_call(x: torch.Tensor, fmt: str, k_hint: int, want_q=True, want_out=False):
+    """ely_fp8_quantize_hint through the C ABI: (q, k, out, hit)."""
+    from elysium_wan_amd import _lib, fp8
+
+    L = _lib.load()
+    x = x.contiguous()
+    n = x.numel()
+    q = torch.full((n,), 0xA5, dtype=torch.uint8, device=x.device) if want_q else None
+    out = torch.full((n,), float("nan"), dtype=x.dtype, device=x.device) if want_out else None
+    k = torch.full((1,), -777, dtype=torch.int32, device=x.device)
+    hit = torch.full((1,), -1, dtype=torch.int32, device=x.device)
+    ws = torch.empty(L.ely_fp8_hint_workspace_bytes(n), dtype=torch.uint8, device=x.device)
+    _lib.check(L.ely_fp8_quantize_hint(x.data_ptr(), _lib.dtype_code(x), n, _lib.FMT[fmt], k_hint,
+                                       None if q is None else q.data_ptr(), k.data_ptr(),
+                                       None if out is None else out.data_ptr(), hit.data_ptr(), ws.data_ptr(), ws.numel(),
+                                       _lib.stream_ptr(x.device)), "quantize_hint")
+    torch.cuda.synchronize()
+    assert fp8.FORMATS[fmt]
+    return q, int(k.item()), out, int(hit.item())
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("n", [8, 2048, 2056, 65536 + 8, 3 * 2048 * 257])
+def test_hit_and_miss_equal_the_oracle(oracle, fmt, dtype, n):
+    """Hints equal to the exponent (one pass), one and five off (fixup), and
+    out of the one-pass range: the same bytes and exponent as the oracle's
+    per-tensor quantize, and the flag telling which pass stood."""
+    x = activation((n,), seed=300 + n % 97, dtype=dtype)
+    oq, ok = oracle.quantize(_oracle_in(x.reshape(1, -1)), fmt)
+    k_true = int(ok.reshape(-1)[0])
+    for hint in (k_true, k_true + 1, k_true - 1, k_true + 5, 200, -200):
+        say("fp8 hint", fmt, dtype, n, "hint", hint, "k", k_true)
+        q, k, _, hit = _hint_call(x, fmt, hint)
+        assert k == k_true
+        assert np.array_equal(bits(q), oq.reshape(-1)), f"fp8 bytes, hint {hint}"
+        assert hit == (1 if hint == k_true else 0)
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+def test_round_trip_with_a_hint_equals_the_round_trip(fmt):
+    from elysium_wan_amd import fp8
+
+    x = activation((16, 4096), seed=41)
+    want = fp8.roundtrip(x, fmt, per_tensor=True)
+    k = int(fp8.scale_exp(x, fmt, per_tensor=True).reshape(-1)[0])
+    for hint in (k, k - 2):
+        say("fp8 hint round trip", fmt, hint)
+        got = fp8.roundtrip(x, fmt, per_tensor=True, k_hint=hint)
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+        q, kk, out, hit = _hint_call(x, fmt, hint, want_q=False, want_out=True)
+        assert kk == k and hit == (1 if hint == k else 0)
+        assert torch.equal(out.view(torch.int16), want.reshape(-1).view(torch.int16))
+
+
+def test_no_one_pass_form_falls_back_exactly(oracle):
+    """n not a whole number of 16-byte vectors, an unaligned view, Inf and NaN
+    (|x|max not finite: the exact-arithmetic path), an all-zero tensor and an
+    empty one: the split path's results, and the flag 0."""
+    from elysium_wan_amd import fp8
+
+    base = activation((4096 + 24,), seed=43)
+    cases = {
+        "ragged": activation((4099,), seed=44),
+        "unaligned": base[3:3 + 4096],
+        "inf": torch.cat([activation((4095,), seed=45), torch.tensor([float("inf")], dtype=torch.bfloat16, device="cuda")]),
+        "nan": torch.cat([torch.tensor([float("nan")], dtype=torch.bfloat16, device="cuda"), activation((4095,), seed=46)]),
+        "zeros": torch.zeros(4096, dtype=torch.bfloat16, device="cuda"),
+    }
+    for name, x in cases.items():
+        for fmt in ("e4m3", "e5m2"):
+            say("fp8 hint fallback", name, fmt)
+            oq, ok = oracle.quantize(_oracle_in(x.reshape(1, -1)), fmt)
+            k_true = int(ok.reshape(-1)[0])
+            for hint in (k_true, 0, 3):
+                q, k = fp8.quantize(x, fmt, per_tensor=True, k_hint=hint)
+                assert int(k.reshape(-1)[0]) == k_true
+                assert np.array_equal(bits(q).reshape(-1), oq.reshape(-1)), (name, fmt, hint)
+    for name in ("ragged", "unaligned"):
+        _, _, _, hit = _hint_call(cases[name], "e4m3", 0)
+        assert hit == 0
+    q, k = fp8.quantize(torch.empty(0, dtype=torch.bfloat16, device="cuda"), "e4m3", per_tensor=True, k_hint=4)
+    assert q.numel() == 0 and int(k.reshape(-1)[0]) == 0
+
+
+def test_hint_argument_checks():
+    from elysium_wan_amd import fp8
+
+    x = activation((64,), seed=47)
+    with pytest.raises(ValueError, match="per-tensor"):
+        fp8.quantize(x, "e4m3", k_hint=0)
+    with pytest.raises(ValueError, match="int32"):
+        fp8.quantize(x, "e4m3", per_tensor=True, k_hint=2**40)
+
+
+def _c4_activation(seed: int) -> torch.Tensor:
+    """Config C4's activation [16, 4096, 8192] bf16: Student-t (df = 3) with
+    0.01% of the elements set to +-1e4."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    shape = (16, 4096, 8192)
+    z = torch.empty(shape, device="cuda").normal_(generator=g)
+    c = torch.zeros(shape, device="cuda")
+    for _ in range(3):
+        c.add_(torch.empty(shape, device="cuda").normal_(generator=g).square_())
+    z.div_(c.div_(3.0).sqrt_())
+    del c
+    n = z.numel()
+    idx = torch.randint(0, n, (n // 10000,), generator=g, device="cuda")
+    sign = torch.randint(0, 2, idx.shape, generator=g, device="cuda").float() * 2 - 1
+    z.view(-1)[idx] = 1e4 * sign
+    return z.to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+def test_c4_per_tensor_with_a_hint_equals_torch_on_the_gpu(fmt):
+    """Config C4's activation at full size, per-tensor, hint right and hint
+    wrong: bytes and exponent equal torch's own ops on the GPU running
+    model/fp8.py:28-49's arithmetic."""
+    from elysium_wan_amd import fp8
+
+    x = _c4_activation(63 if fmt == "e4m3" else 64)
+    dt, ebias = fp8.FORMATS[fmt]
+    amax = x.abs().amax()
+    kt = int(torch.frexp(amax).exponent) - ebias
+    qt = (x * torch.exp2(torch.tensor(-kt, dtype=torch.bfloat16, device="cuda"))).to(dt).view(torch.uint8)
+    for hint in (kt, kt + 1):
+        say("fp8 C4 per-tensor hint", fmt, hint, "k", kt)
+        q, k = fp8.quantize(x, fmt, per_tensor=True, k_hint=hint)
+        assert int(k.reshape(-1)[0]) == kt
+        assert torch.equal(q.view(torch.uint8), qt)
+        del q
