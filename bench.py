@@ -727,9 +727,31 @@ def bench_host_moments(device, steps=3):
             opt.step(grads=grads)  # synchronizes at its end, as the reference's does
         dt = (time.perf_counter() - t0) / steps
         out[name] = {"step_s": dt, "params_per_s": n_elem / dt, "pcie_GBs": n_elem * 16 / dt / 1e9}
+        if pipeline:
+            # one more staged step with HIP events around every chunk copy on
+            # its own stream (the step's time above is taken without them)
+            opt.copy_timing = []
+            opt.step(grads=grads)
+            out[name]["copies"] = _copy_event_summary(opt.copy_timing)
+            opt.copy_timing = None
         del opt
         torch.cuda.empty_cache()
     del params, grads
+    return out
+
+
+def _copy_event_summary(events) -> dict:
+    """Per direction: count, median / min / max duration (ms) and the median
+    rate of the staged step's chunk copies, from their HIP event pairs."""
+    out = {}
+    for what in ("h2d", "d2h"):
+        ms = sorted(e0.elapsed_time(e1) for w, e0, e1 in events if w == what)
+        if not ms:
+            continue
+        med = ms[len(ms) // 2]
+        out[what] = {"count": len(ms), "median_ms": med, "min_ms": ms[0], "max_ms": ms[-1],
+                     "slower_than_3ms": sum(1 for x in ms if x > 3.0),
+                     "median_GBs": (1 << 24) * 4 / med / 1e6}
     return out
 
 
@@ -1116,65 +1138,6 @@ def c4_summary(trace_dir: str, bench_out: str | None) -> None:
     print("\n".join(lines))
 
 
-def copy_summary(trace_dir: str) -> None:
-    """Copy and kernel durations of a rocprofv3 --kernel-trace
-    --memory-copy-trace run of `bench.py --leg host_moments`: the staged
-    host-moment step's bulk copies (chunks of 2^24 fp32 moments, 67 MB each)
-    in each direction, whether the slow ones overlapped a copy the other way,
-    and the fused update's launches.  Writes
-    profiles/host_moments_c1_copy_trace.md."""
-    import csv
-    import glob
-    import statistics
-
-    copies, kernels = [], []
-    for path in glob.glob(os.path.join(trace_dir, "**", "*memory_copy_trace.csv"), recursive=True):
-        with open(path) as f:
-            copies += [(r["Direction"], int(r["Start_Timestamp"]), int(r["End_Timestamp"])) for r in csv.DictReader(f)]
-    for path in glob.glob(os.path.join(trace_dir, "**", "*kernel_trace.csv"), recursive=True):
-        with open(path) as f:
-            kernels += [(r["Kernel_Name"], int(r["Start_Timestamp"]), int(r["End_Timestamp"])) for r in csv.DictReader(f)]
-    chunk_mb = (1 << 24) * 4 / 1e6
-    big = sorted((c for c in copies if c[2] - c[1] > 200_000), key=lambda c: c[1])  # the moment chunks, not the tables
-    lines = [
-        "# Copy durations, C1's staged host-moment step",
-        "",
-        "Commands (on one MI355X, from the repository root):",
-        "",
-        "    rocprofv3 --kernel-trace --memory-copy-trace --stats -T -d <dir> -o hm --output-format csv -- python3 bench.py --leg host_moments",
-        "    python bench.py --copy-summary <dir>",
-        "",
-        "Workload: C1's shard (192 tensors, 1,258,823,680 fp32 params, bf16 grads,",
-        "bf16 working copy, clip 1.0) with adamw-host's moments in pinned host",
-        "memory: four in-place steps (the kernel reads and writes the moments",
-        "through the GPU's mapping), then four staged steps (each 2^24-element",
-        f"chunk of m and v copied in, updated, copied out: {chunk_mb:.1f} MB per copy, 75",
-        "chunks per step, 3 staging slots).  Copies under 0.2 ms (the launch tables)",
-        "are left out.",
-        "",
-        "| copies | count | median (ms) | min (ms) | max (ms) | slower than 3 ms | of those, alone on the link | median rate |",
-        "|---|---|---|---|---|---|---|---|",
-    ]
-    for label, key in (("host to device", "HOST_TO_DEVICE"), ("device to host", "DEVICE_TO_HOST")):
-        mine = [c for c in big if c[0].endswith(key)]
-        other = [c for c in big if not c[0].endswith(key)]
-        if not mine:
-            continue
-        ds = [(c[2] - c[1]) / 1e6 for c in mine]
-        slow = [c for c in mine if c[2] - c[1] > 3_000_000]
-        alone = [c for c in slow if not any(min(c[2], o[2]) > max(c[1], o[1]) for o in other)]
-        med = statistics.median(ds)
-        lines.append(f"| {label} | {len(ds)} | {med:.2f} | {min(ds):.2f} | {max(ds):.2f} | {len(slow)} | {len(alone)} | "
-                     f"{chunk_mb / med:.0f} GB/s |")
-    adam = [(e - b) / 1e6 for n, b, e in kernels if n.startswith("adamw_kernel")]
-    if adam:
-        lines += ["", f"adamw_kernel launches: {len(adam)}, median {statistics.median(adam):.3f} ms "
-                  f"(a staged launch updates one chunk; an in-place launch the whole shard over PCIe)."]
-    with open(os.path.join(HERE, "profiles", "host_moments_c1_copy_trace.md"), "w") as f:
-        f.write("\n".join(lines) + "\n")
-    print("\n".join(lines))
-
-
 def _row(label, ds):
     return f"| {label} | {len(ds)} | {sum(ds) / len(ds):,.0f} | {min(ds):,} | {max(ds):,} |"
 
@@ -1512,7 +1475,6 @@ def main():
     ap.add_argument("--leg", action="append", choices=LEG_NAMES,
                     help="run only these extra legs (repeatable), no headline, and print their JSON (for profiling one leg)")
     ap.add_argument("--c4-summary", metavar="DIR", help="summarize a rocprofv3 --kernel-trace run of --no-optimizer --codec c4 into profiles/")
-    ap.add_argument("--copy-summary", metavar="DIR", help="summarize a rocprofv3 --memory-copy-trace run of --leg host_moments into profiles/")
     ap.add_argument("--cpu-sample", type=int, default=256 * 1024 * 1024)
     ap.add_argument("--profile-pass", action="store_true", help="launch each measured kernel a few times, untimed, for rocprofv3 --pmc runs")
     ap.add_argument("--traffic-summary", nargs="+", metavar="DIR",
@@ -1529,9 +1491,6 @@ def main():
         return
     if args.trace_summary:
         trace_summary(*args.trace_summary, args.bench_json)
-        return
-    if args.copy_summary:
-        copy_summary(args.copy_summary)
         return
     if args.c4_summary:
         c4_summary(args.c4_summary, (args.bench_json or [None])[0])

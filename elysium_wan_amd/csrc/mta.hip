@@ -86,6 +86,9 @@ namespace ely {
 // left free also take a concurrent forward's work.
 #define ELY_ADAM_MAPPED_BPC 1
 #endif
+#ifndef ELY_NORM_UNROLL_F32_SMALL
+#define ELY_NORM_UNROLL_F32_SMALL 1  // the same for the small tile of a list under ELY_NORM_SMALL_LIMIT elements
+#endif
 #ifndef ELY_NORM_TILE
 #define ELY_NORM_TILE 16384      // grad-norm elements per tile (one wave's share; fixes the summation order)
 #endif
@@ -225,7 +228,7 @@ __device__ __forceinline__ float raw8_sumsq(const Raw8<BF16, FOLD>& r) {
 template <bool BF16, bool FOLD, int64_t TILE, bool NT>
 __device__ __forceinline__ double tile_sumsq_vec(const NormDesc& d, int64_t e0, int lane) {
     constexpr int G = (int)(TILE / (kWave * 8));
-    constexpr int U = BF16 ? kNormUnroll : ELY_NORM_UNROLL_F32;
+    constexpr int U = BF16 ? kNormUnroll : (TILE == kNormSmallTile ? ELY_NORM_UNROLL_F32_SMALL : ELY_NORM_UNROLL_F32);
     static_assert(G % U == 0, "unroll divides the groups of a tile");
     double acc = 0.0;
     for (int j0 = 0; j0 < G; j0 += U) {
@@ -877,8 +880,10 @@ static ClipArgsKernel pick_clip_args(int dt) {
 // argument again; same stream, so the coefficient is in place when this runs).
 static void clip_scale(const NormLaunch& nl, const float* coef_dev, void* stream) {
     if (nl.tiles == 0) return;
-    const int64_t waves = std::min<int64_t>({nl.tiles, mt_blocks(ELY_CLIP_BPC) * (kBlock / kWave), 0xFFFFFFFFLL / kWave});
-    const int64_t blocks = (waves + kBlock / kWave - 1) / (kBlock / kWave);
+    // one wave per tile, in whole blocks; the blocks capped so that the
+    // dispatch's work-items stay within 2^32 - 1 (the waves stride past that)
+    const int64_t waves = std::min<int64_t>(nl.tiles, mt_blocks(ELY_CLIP_BPC) * (kBlock / kWave));
+    const int64_t blocks = std::min<int64_t>((waves + kBlock / kWave - 1) / (kBlock / kWave), 0xFFFFFFFFLL / kBlock);
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (nl.dtable) {
         const ClipKernel k = nl.tile == kNormTile ? pick_clip<kNormTile>(nl.dt) : pick_clip<kNormSmallTile>(nl.dt);

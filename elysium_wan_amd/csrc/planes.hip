@@ -462,7 +462,9 @@ int ely_fp8_nibbles_encode(const void* t, int32_t t_dtype, int64_t n, uint8_t* h
         if (!t || !hi || !lo || !bad_dev) fail(ELY_EINVAL, "ely_fp8_nibbles_encode: null pointer");
         hipStream_t s = static_cast<hipStream_t>(stream);
         const int vec = aligned16(t) && (reinterpret_cast<uintptr_t>(hi) % 4 == 0) && (reinterpret_cast<uintptr_t>(lo) % 4 == 0);
-        const unsigned g = grid_for(std::max<int64_t>(n / 8 / kNUnroll, 1), ELY_NIBBLES_BPC, kNBlock);
+        // one lane per kNUnroll 16-byte vectors of the input: 8 bf16 or 4 fp32 elements each
+        const int64_t epl = t_dtype == ELY_BF16 ? 8 : 4;
+        const unsigned g = grid_for(std::max<int64_t>(n / epl / kNUnroll, 1), ELY_NIBBLES_BPC, kNBlock);
         if (t_dtype == ELY_BF16)
             hipLaunchKernelGGL(nibbles_encode_kernel<true>, dim3(g), dim3(kNBlock), 0, s, t, n, vec, hi, lo, bad_dev);
         else

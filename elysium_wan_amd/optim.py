@@ -266,6 +266,10 @@ class FusedAdamW:
         self.chunk, self.pipeline, self.slots = int(chunk), pipeline, int(slots)
         self.resident: set = set()  # host mode: indices whose moments were promoted to the GPU
         self._staging = None  # host mode: per-step streaming buffers, streams and events
+        # host mode, staged copies: a list to receive ("h2d" | "d2h", start,
+        # end) timing-event pairs around every chunk copy, on the copy's own
+        # stream (for measurement; None records nothing)
+        self.copy_timing = None
         self._mapped = None  # host mode: the GPU's addresses of the pinned moment buffers
         self.order = order
         self.recipe = "adamw-host" if order == "host" else "adamw"
@@ -675,8 +679,8 @@ class FusedAdamW:
             if staged and st["used"][slot]:
                 up.wait_event(st["ev_back"][slot])
             with torch.cuda.stream(up):
-                md.copy_(mh[a:b], non_blocking=True)
-                vd.copy_(vh[a:b], non_blocking=True)
+                self._timed_copy(md, mh[a:b], "h2d", up)
+                self._timed_copy(vd, vh[a:b], "h2d", up)
                 for gdt in (torch.bfloat16, torch.float32):
                     sel = [(j, s0, e0) for j, s0, e0 in members if gs[j].dtype == gdt]
                     if not sel:
@@ -696,8 +700,8 @@ class FusedAdamW:
             if staged:
                 down.wait_event(st["ev_done"][slot])
             with torch.cuda.stream(down):
-                mh[a:b].copy_(md, non_blocking=True)
-                vh[a:b].copy_(vd, non_blocking=True)
+                self._timed_copy(mh[a:b], md, "d2h", down)
+                self._timed_copy(vh[a:b], vd, "d2h", down)
                 if staged:
                     st["ev_back"][slot].record(down)
             st["used"][slot] = staged
@@ -705,6 +709,19 @@ class FusedAdamW:
             caller.wait_stream(up)
             caller.wait_stream(down)
             st["used"] = [False] * len(st["bufs"])
+
+    def _timed_copy(self, dst, src, what: str, stream) -> None:
+        """dst.copy_(src) on the current stream, between timing events when
+        copy_timing is a list."""
+        tm = self.copy_timing
+        if tm is None:
+            dst.copy_(src, non_blocking=True)
+            return
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        dst.copy_(src, non_blocking=True)
+        e1.record(stream)
+        tm.append((what, e0, e1))
 
     def _staging_buffers(self, dev, need: int) -> dict:
         """`slots` pairs of fp32 device buffers of `chunk` elements, the copy

@@ -261,8 +261,8 @@ def test_torch_order_oracle_is_adamw(oracle, foreach):
     addcdiv likewise), so exp_avg is bit-identical, exp_avg_sq within 4 ulp,
     and the parameters within the reference's own tolerance for 'it is
     AdamW' (test_host_adamw.py:70-77).  The GPU kernel itself is held to
-    torch's GPU AdamW within 1 ulp on parameters and both moments
-    (tests/test_gpu_adamw.py)."""
+    torch's GPU AdamW bit for bit (0 ulp) on parameters and both moments
+    (tests/test_gpu_adamw.py); the north star's contract for it is 1 ulp."""
     from gpu_util import ulp_distance
 
     rng = np.random.default_rng(3)
