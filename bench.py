@@ -886,7 +886,22 @@ def profile_pass(device):
         _lib.check(L.ely_fp8_quantize(xa.data_ptr(), _lib.BF16, rows, cols, _lib.E4M3, q.data_ptr(), k.data_ptr(), ws.data_ptr(), ws.numel(), sptr), "q")
         _lib.check(L.ely_fp8_dequantize(q.data_ptr(), k.data_ptr(), rows, cols, _lib.E4M3, out.data_ptr(), _lib.BF16, sptr), "dq")
     torch.cuda.synchronize()
+    del xa, q, k, out
     log("profile pass: codec done")
+    # per-tensor quantize of a C4-sized activation with a right exponent hint
+    # (one pass: quant_hint_kernel), after one split-path call that finds k
+    n4 = 16 * 4096 * 8192
+    x4 = torch.randn(n4, device=device).to(torch.bfloat16)
+    q4 = torch.empty(n4, dtype=torch.uint8, device=device)
+    k4 = torch.empty(1, dtype=torch.int32, device=device)
+    ws = _lib.workspace(device, max(L.ely_fp8_workspace_bytes(1, n4, _lib.BF16), L.ely_fp8_hint_workspace_bytes(n4)))
+    _lib.check(L.ely_fp8_quantize(x4.data_ptr(), _lib.BF16, 1, n4, _lib.E4M3, q4.data_ptr(), k4.data_ptr(), ws.data_ptr(), ws.numel(), sptr), "q")
+    hint = int(k4.item())
+    for _ in range(3):
+        _lib.check(L.ely_fp8_quantize_hint(x4.data_ptr(), _lib.BF16, n4, _lib.E4M3, hint, q4.data_ptr(), k4.data_ptr(), None, None,
+                                           ws.data_ptr(), ws.numel(), sptr), "qh")
+    torch.cuda.synchronize()
+    log("profile pass: per-tensor hint done")
 
 
 # Kernels the traffic summary reports: name fragment -> (algorithmic bytes per
@@ -899,6 +914,8 @@ def _traffic_kernels():
         "norm_partials_kernel": (n * NORM_BYTES_PER_ELEM, "grad-norm partials, C1 bf16 grads, 2 B/elem"),
         "quant_rows_kernel": (act * CODEC_BYTES_PER_ELEM, "fp8 e4m3 quantize, C1 activation, 3 B/elem"),
         "dequant_flat_kernel": (act * CODEC_BYTES_PER_ELEM, "fp8 e4m3 dequantize -> bf16, C1 activation, 3 B/elem"),
+        "quant_hint_kernel": (16 * 4096 * 8192 * CODEC_BYTES_PER_ELEM,
+                              "fp8 e4m3 per-tensor quantize with a right hint, C4 activation, 3 B/elem"),
     }
 
 
@@ -950,7 +967,7 @@ def traffic_summary(fetch_dir: str, write_dir: str, command: str, sizes_dir: str
     cw = _pick(write, "cast_bf16_kernel") * 1024.0 / (CAL_ELEMS * 2)
     out = {"fetch_factor": cf, "write_factor": cw, "command": command, "kernels": {}}
     lines = [
-        "# HBM traffic per launch (rocprofv3 --pmc), C1 workload",
+        "# HBM traffic per launch (rocprofv3 --pmc), C1 workload and C4's per-tensor hint path",
         "",
         f"Command: `{command}`",
         "",
@@ -1054,6 +1071,7 @@ def c4_summary(trace_dir: str, bench_out: str | None) -> None:
     row-max kernels plus quant_split_kernel, added up.  Writes
     profiles/codec_c4_kernel_trace.md."""
     disp = _dispatches(trace_dir)
+    hint_calls = _hint_calls(disp)
     quant = ("quant_block_row_kernel", "quant_rows_kernel", "quant_split_kernel")
     pre = ("rowmax_partial_kernel", "rowmax_reduce_kernel")
     calls = {}  # (scaling, op) -> [total ns per call]
@@ -1122,6 +1140,22 @@ def c4_summary(trace_dir: str, bench_out: str | None) -> None:
         lines += ["", "Per-tensor calls by kernel (average µs):", "", "| operation | kernel | calls | average (µs) |", "|---|---|---|---|"]
         for (op, k), ds in sorted(parts.items()):
             lines.append(f"| {op} | {k} | {len(ds)} | {sum(ds) / len(ds) / 1e3:,.1f} |")
+    if hint_calls:
+        lines += ["", "Per-tensor calls with an exponent hint (`ely_fp8_quantize_hint`: the one-pass",
+                  "quant_hint_kernel, hint_reduce_kernel folding its per-segment maxima, and",
+                  "quant_hint_fixup_kernel, which exits on a hit and converts every segment again",
+                  "on a miss), average µs per call over both inputs and formats:", "",
+                  "| call | calls | quant_hint_kernel | hint_reduce_kernel | quant_hint_fixup_kernel | total | algorithmic rate | fraction of 8 TB/s |",
+                  "|---|---|---|---|---|---|---|---|"]
+        for label, nbytes in (("quantize, right hint", 3), ("quantize, hint off by one", 3), ("round trip, right hint", 4)):
+            cs = [c for lab, c in hint_calls if lab == label]
+            if not cs:
+                continue
+            avg = [sum(c[i] for c in cs) / len(cs) for i in range(3)]
+            tot = sum(avg)
+            rate = n * nbytes / tot / 1e3
+            lines.append(f"| {label} | {len(cs)} | {avg[0] / 1e3:,.1f} | {avg[1] / 1e3:,.1f} | {avg[2] / 1e3:,.1f} | {tot / 1e3:,.1f} | "
+                         f"{rate:.2f} TB/s | {rate / 8:.2f} |")
     b = None
     if bench_out:
         with open(bench_out) as f:
@@ -1136,6 +1170,30 @@ def c4_summary(trace_dir: str, bench_out: str | None) -> None:
     with open(os.path.join(HERE, "profiles", "codec_c4_kernel_trace.md"), "w") as f:
         f.write("\n".join(lines) + "\n")
     print("\n".join(lines))
+
+
+def _hint_calls(disp) -> list:
+    """The hint path's calls in a C4 codec trace as (label, [ns of its three
+    kernels]).  bench_codec's per-tensor order, per input and format: 11
+    quantize calls with the right hint (one untimed), 11 with the hint one
+    off, 11 round trips with the right hint, then one more right-hint
+    quantize (34 calls)."""
+    names = ("quant_hint_kernel", "hint_reduce_kernel", "quant_hint_fixup_kernel")
+    triples, cur = [], []
+    for name, ns in disp:
+        if name not in names:
+            continue
+        cur.append(ns)
+        if name == names[2]:
+            if len(cur) == 3:
+                triples.append(cur)
+            cur = []
+    out = []
+    for i, t in enumerate(triples):
+        j = i % 34
+        label = "quantize, right hint" if j < 11 or j == 33 else ("quantize, hint off by one" if j < 22 else "round trip, right hint")
+        out.append((label, t))
+    return out
 
 
 def _row(label, ds):
