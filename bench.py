@@ -379,12 +379,12 @@ def bench_codec(device, stream, rows, cols, copies, iters=20, per_tensor=False, 
 
             def qhint(i, f=f, off=0):
                 j = i % copies
-                _lib.check(L.ely_fp8_quantize_hint(xs[j].data_ptr(), _lib.BF16, n, f, k_true[j] + off, qh[j].data_ptr(), ks[j].data_ptr(),
-                                                   None, hit.data_ptr(), hws.data_ptr(), hws.numel(), sptr), "qh")
+                _lib.check(L.ely_fp8_quantize_hint(xs[j].data_ptr(), _lib.BF16, n, f, k_true[j] + off, None, qh[j].data_ptr(),
+                                                   ks[j].data_ptr(), None, hit.data_ptr(), hws.data_ptr(), hws.numel(), sptr), "qh")
 
             def rthint(i, f=f):
                 j = i % copies
-                _lib.check(L.ely_fp8_quantize_hint(xs[j].data_ptr(), _lib.BF16, n, f, k_true[j], None, ks[j].data_ptr(),
+                _lib.check(L.ely_fp8_quantize_hint(xs[j].data_ptr(), _lib.BF16, n, f, k_true[j], None, None, ks[j].data_ptr(),
                                                    outs[j].data_ptr(), hit.data_ptr(), hws.data_ptr(), hws.numel(), sptr), "rth")
 
             h_ms = time_events(qhint, iters, stream)
@@ -898,8 +898,8 @@ def profile_pass(device):
     _lib.check(L.ely_fp8_quantize(x4.data_ptr(), _lib.BF16, 1, n4, _lib.E4M3, q4.data_ptr(), k4.data_ptr(), ws.data_ptr(), ws.numel(), sptr), "q")
     hint = int(k4.item())
     for _ in range(3):
-        _lib.check(L.ely_fp8_quantize_hint(x4.data_ptr(), _lib.BF16, n4, _lib.E4M3, hint, q4.data_ptr(), k4.data_ptr(), None, None,
-                                           ws.data_ptr(), ws.numel(), sptr), "qh")
+        _lib.check(L.ely_fp8_quantize_hint(x4.data_ptr(), _lib.BF16, n4, _lib.E4M3, hint, None, q4.data_ptr(), k4.data_ptr(), None,
+                                           None, ws.data_ptr(), ws.numel(), sptr), "qh")
     torch.cuda.synchronize()
     log("profile pass: per-tensor hint done")
 

@@ -112,7 +112,7 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
         L.ely_fp8_quantize_noalloc.argtypes = [P, I32, I64, I64, I32, P, P, P]
         L.ely_fp8_hint_workspace_bytes.restype = I64
         L.ely_fp8_hint_workspace_bytes.argtypes = [I64]
-        L.ely_fp8_quantize_hint.argtypes = [P, I32, I64, I32, I32, P, P, P, P, P, I64, P]
+        L.ely_fp8_quantize_hint.argtypes = [P, I32, I64, I32, I32, P, P, P, P, P, P, I64, P]
         L.ely_fp8_dequantize.argtypes = [P, P, I64, I64, I32, P, I32, P]
         L.ely_fp8_roundtrip.argtypes = [P, I32, I64, I64, I32, P, P, P, P, I64, P]
         L.ely_fp8_recover_workspace_bytes.restype = I64

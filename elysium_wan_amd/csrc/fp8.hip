@@ -592,14 +592,28 @@ constexpr int kHintBlocks = 256;         // maxima the reduce launch leaves (4 p
 #endif
 constexpr int kHintFixupWavesPerCU = ELY_HINT_FIXUP_WPC;
 
+// The hint: k_hint, or *k_hint_dev when that is given (read here, before
+// the fixup launch writes k, which may be the same word).  Wave 0 keeps the
+// hint it read in hint_copy for the fixup.  A hint outside the instruction
+// path's range converts nothing here: the call is then a miss.
 template <int FMT, bool BF16>
 __global__ __launch_bounds__(kQBlock) void quant_hint_kernel(const void* __restrict__ x, int64_t n, int64_t segs,
-                                                             RowScale hs, uint8_t* __restrict__ q,
-                                                             void* __restrict__ out, uint32_t* __restrict__ partial) {
+                                                             int32_t k_hint, const int32_t* k_hint_dev,
+                                                             uint8_t* __restrict__ q, void* __restrict__ out,
+                                                             uint32_t* __restrict__ partial,
+                                                             int32_t* __restrict__ hint_copy) {
     constexpr int EPV = Seg<BF16>::EPV, VPL = Seg<BF16>::VPL, ESZ = BF16 ? 2 : 4;
     const int lane = threadIdx.x & (kWave - 1);
     const int64_t seg = (int64_t)blockIdx.x * kWavesPerBlock + wave_uniform(threadIdx.x / kWave);
     if (seg >= segs) return;
+    const int32_t hint = k_hint_dev ? __builtin_amdgcn_readfirstlane(*k_hint_dev) : k_hint;
+    if (seg == 0 && lane == 0) hint_copy[0] = hint;
+    const bool convert = hint >= -kFastK && hint <= kFastK;
+    RowScale hs;
+    hs.k = hint;
+    hs.fast = true;
+    hs.s_down = __uint_as_float((uint32_t)(127 - hint) << 23);
+    hs.s_up = __uint_as_float((uint32_t)(127 + hint) << 23);
     const int64_t e0 = seg * kSegElems;
     const int64_t nv = (min(e0 + kSegElems, n) - e0) / EPV;
     const uint4* xr = reinterpret_cast<const uint4*>(static_cast<const char*>(x) + e0 * ESZ);
@@ -615,6 +629,7 @@ __global__ __launch_bounds__(kQBlock) void quant_hint_kernel(const void* __restr
         const int64_t vi = lane + (int64_t)kWave * j;
         if (vi >= nv) continue;
         amax = vec_absmax<BF16>(buf[j], amax);
+        if (!convert) continue;
         uint32_t words[2];
         const int64_t e = e0 + vi * EPV;
         quant_vec_fast<FMT, BF16>(buf[j], hs, words, out ? static_cast<char*>(out) + e * ESZ : nullptr);
@@ -649,7 +664,7 @@ __global__ __launch_bounds__(kRowBlock) void hint_reduce_kernel(const uint32_t* 
 
 template <int FMT, bool BF16>
 __global__ __launch_bounds__(kQBlock) void quant_hint_fixup_kernel(const void* __restrict__ x, int64_t n, int64_t segs,
-                                                                   int vec, int32_t k_hint,
+                                                                   int vec, const int32_t* __restrict__ hint_copy,
                                                                    const uint32_t* __restrict__ block_max,
                                                                    uint8_t* __restrict__ q, int32_t* __restrict__ k,
                                                                    void* __restrict__ out, int32_t* __restrict__ hit) {
@@ -660,7 +675,8 @@ __global__ __launch_bounds__(kQBlock) void quant_hint_fixup_kernel(const void* _
     uint32_t m = max(max(block_max[lane], block_max[lane + kWave]), max(block_max[lane + 2 * kWave], block_max[lane + 3 * kWave]));
     m = wave_max_u32(m);
     const RowScale rs = row_scale<FMT>(to_f32_bits<BF16>(m), BF16, BF16);
-    const bool same = rs.fast && rs.k == k_hint;
+    const int32_t k_hint = hint_copy[0];
+    const bool same = rs.fast && rs.k == k_hint && k_hint >= -kFastK && k_hint <= kFastK;
     if (gw == 0 && lane == 0) {
         k[0] = rs.k;
         if (hit) hit[0] = same ? 1 : 0;
@@ -1281,23 +1297,24 @@ static void quantize_impl(const void* x, int64_t rows, int64_t cols, uint8_t* q,
 }
 
 // Workspace of the hint path over n elements: one maximum per segment, the
-// reduce launch's kHintBlocks maxima; at least the split path's, which a
-// call falls back to when the one-pass form does not apply.
+// reduce launch's kHintBlocks maxima, the hint as read; at least the split
+// path's, which a call falls back to when the one-pass form does not apply.
 static size_t hint_ws_bytes(int64_t n) {
     const int64_t segs = std::max<int64_t>((n + kSegElems - 1) / kSegElems, 1);
-    return std::max(align_up((size_t)segs * 4, 256) + align_up((size_t)kHintBlocks * 4, 256), split_ws_bytes(1));
+    return std::max(align_up((size_t)segs * 4, 256) + align_up((size_t)kHintBlocks * 4, 256) + 256, split_ws_bytes(1));
 }
 
 template <int FMT, bool BF16>
-static void quantize_hint_impl(const void* x, int64_t n, int32_t k_hint, uint8_t* q, int32_t* k, void* out,
-                               int32_t* hit, void* workspace, int64_t ws_bytes, hipStream_t s) {
+static void quantize_hint_impl(const void* x, int64_t n, int32_t k_hint, const int32_t* k_hint_dev, uint8_t* q,
+                               int32_t* k, void* out, int32_t* hit, void* workspace, int64_t ws_bytes,
+                               hipStream_t s) {
     if (!workspace || ws_bytes < (int64_t)hint_ws_bytes(n))
         fail(ELY_EWORKSPACE, "ely_fp8_quantize_hint: workspace of " + std::to_string(ws_bytes) + " bytes, need " +
                                  std::to_string(hint_ws_bytes(n)) + " (ely_fp8_hint_workspace_bytes)");
     const int64_t epv = BF16 ? 8 : 4;
     const bool vec = n > 0 && n % epv == 0 && aligned16(x) && (!out || aligned16(out)) &&
                      (!q || reinterpret_cast<uintptr_t>(q) % (uintptr_t)epv == 0);
-    if (!vec || k_hint < -kFastK || k_hint > kFastK) {
+    if (!vec || (!k_hint_dev && (k_hint < -kFastK || k_hint > kFastK))) {
         // no one-pass form for this tensor or hint: the split path, a miss
         quantize_impl<FMT, BF16>(x, 1, n, q, k, out, workspace, ws_bytes, s);
         if (hit) {
@@ -1309,20 +1326,16 @@ static void quantize_hint_impl(const void* x, int64_t n, int32_t k_hint, uint8_t
     const int64_t segs = (n + kSegElems - 1) / kSegElems;
     uint32_t* partial = static_cast<uint32_t*>(workspace);
     uint32_t* block_max = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + align_up((size_t)segs * 4, 256));
-    RowScale hs;
-    hs.k = k_hint;
-    hs.fast = true;
-    hs.s_down = __builtin_bit_cast(float, (uint32_t)(127 - k_hint) << 23);
-    hs.s_up = __builtin_bit_cast(float, (uint32_t)(127 + k_hint) << 23);
-    hipLaunchKernelGGL((quant_hint_kernel<FMT, BF16>), dim3(blocks_for_waves(segs)), dim3(kQBlock), 0, s, x, n, segs, hs,
-                       q, out, partial);
+    int32_t* hint_copy = reinterpret_cast<int32_t*>(reinterpret_cast<char*>(block_max) + align_up((size_t)kHintBlocks * 4, 256));
+    hipLaunchKernelGGL((quant_hint_kernel<FMT, BF16>), dim3(blocks_for_waves(segs)), dim3(kQBlock), 0, s, x, n, segs,
+                       k_hint, k_hint_dev, q, out, partial, hint_copy);
     check_launch("quant_hint_kernel");
     hipLaunchKernelGGL(hint_reduce_kernel, dim3(kHintBlocks), dim3(kRowBlock), 0, s, (const uint32_t*)partial, segs,
                        block_max);
     check_launch("hint_reduce_kernel");
     const int64_t waves = std::min<int64_t>(segs, (int64_t)device_info().cus * kHintFixupWavesPerCU);
     hipLaunchKernelGGL((quant_hint_fixup_kernel<FMT, BF16>), dim3(blocks_for_waves(waves)), dim3(kQBlock), 0, s, x, n,
-                       segs, 1, k_hint, (const uint32_t*)block_max, q, k, out, hit);
+                       segs, 1, (const int32_t*)hint_copy, (const uint32_t*)block_max, q, k, out, hit);
     check_launch("quant_hint_fixup_kernel");
 }
 
@@ -1559,8 +1572,9 @@ int64_t ely_fp8_hint_workspace_bytes(int64_t n) {
     return (int64_t)hint_ws_bytes(n);
 }
 
-int ely_fp8_quantize_hint(const void* x, int32_t x_dtype, int64_t n, int32_t fmt, int32_t k_hint, uint8_t* q,
-                          int32_t* k, void* out, int32_t* hit_dev, void* workspace, int64_t ws_bytes, void* stream) {
+int ely_fp8_quantize_hint(const void* x, int32_t x_dtype, int64_t n, int32_t fmt, int32_t k_hint,
+                          const int32_t* k_hint_dev, uint8_t* q, int32_t* k, void* out, int32_t* hit_dev,
+                          void* workspace, int64_t ws_bytes, void* stream) {
     return guarded([&] {
         check_fmt(fmt);
         check_dtype(x_dtype, "x_dtype");
@@ -1569,11 +1583,11 @@ int ely_fp8_quantize_hint(const void* x, int32_t x_dtype, int64_t n, int32_t fmt
         if (n > 0 && (!x || (!q && !out))) fail(ELY_EINVAL, "ely_fp8_quantize_hint: null x, or neither q nor out");
         hipStream_t s = static_cast<hipStream_t>(stream);
         if (fmt == ELY_E4M3) {
-            if (x_dtype == ELY_BF16) quantize_hint_impl<kE4M3, true>(x, n, k_hint, q, k, out, hit_dev, workspace, ws_bytes, s);
-            else quantize_hint_impl<kE4M3, false>(x, n, k_hint, q, k, out, hit_dev, workspace, ws_bytes, s);
+            if (x_dtype == ELY_BF16) quantize_hint_impl<kE4M3, true>(x, n, k_hint, k_hint_dev, q, k, out, hit_dev, workspace, ws_bytes, s);
+            else quantize_hint_impl<kE4M3, false>(x, n, k_hint, k_hint_dev, q, k, out, hit_dev, workspace, ws_bytes, s);
         } else {
-            if (x_dtype == ELY_BF16) quantize_hint_impl<kE5M2, true>(x, n, k_hint, q, k, out, hit_dev, workspace, ws_bytes, s);
-            else quantize_hint_impl<kE5M2, false>(x, n, k_hint, q, k, out, hit_dev, workspace, ws_bytes, s);
+            if (x_dtype == ELY_BF16) quantize_hint_impl<kE5M2, true>(x, n, k_hint, k_hint_dev, q, k, out, hit_dev, workspace, ws_bytes, s);
+            else quantize_hint_impl<kE5M2, false>(x, n, k_hint, k_hint_dev, q, k, out, hit_dev, workspace, ws_bytes, s);
         }
     });
 }

@@ -45,9 +45,6 @@ namespace ely {
 // 6.05, 2,048 6.39, 4,096 6.45, 8,192 6.65)
 #define ELY_ADAM_TILE 256
 #endif
-#ifndef ELY_ADAM_SCHED
-#define ELY_ADAM_SCHED 1         // 0: contiguous tile range per block, 1: interleaved rounds (a capped grid)
-#endif
 #ifndef ELY_NORM_SCHED
 #define ELY_NORM_SCHED 0         // same choice for the grad-norm waves
 #endif
@@ -652,23 +649,6 @@ __device__ __forceinline__ void adamw_body(const Tab& tab, int32_t n, int64_t to
     const int64_t G = gridDim.x;
     const int64_t b = blockIdx.x;
     const float coef = CLIP ? *coef_ptr : 1.0f;
-#if ELY_ADAM_SCHED == 0
-    // contiguous tile range per block
-    const int64_t t0 = b * total_tiles / G, t1 = (b + 1) * total_tiles / G;
-    if (t0 >= t1) return;
-    int64_t tile = t0;
-    for (int ti = tab.start(n, t0); ti < n && tile < t1; ++ti) {
-        const AdamDesc d = tab.d[ti];
-        const int64_t ntiles = (d.numel + kAdamTile - 1) / kAdamTile;
-        const int64_t tend = min(t1, (int64_t)d.tile_begin + ntiles);
-        if (tend <= tile) continue;
-        const int64_t e0 = (tile - d.tile_begin) * kAdamTile;
-        const int64_t e1 = min((tend - d.tile_begin) * kAdamTile, d.numel);
-        const ely_adamw_consts c = tab.consts(ti);
-        adam_range<BF16G, ORDER, WD, CLIP, FOLD>(d, c, coef, e0, e1);
-        tile = tend;
-    }
-#else
     // interleaved: in round r block b takes tile r*G + b, so at any moment the
     // whole grid streams one contiguous window of the shard
     if (b >= total_tiles) return;
@@ -681,7 +661,6 @@ __device__ __forceinline__ void adamw_body(const Tab& tab, int32_t n, int64_t to
         const ely_adamw_consts c = tab.consts(ti);
         adam_range<BF16G, ORDER, WD, CLIP, FOLD>(d, c, coef, e0, e1);
     }
-#endif
 }
 
 // The table kernel takes its tables as __restrict__ pointers: the compiler

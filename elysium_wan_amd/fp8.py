@@ -70,27 +70,39 @@ def scale_exp(x: torch.Tensor, fmt: str = "e4m3", per_tensor: bool = False) -> t
     return k
 
 
-def _hint(k_hint, per_tensor: bool, what: str) -> int | None:
+def _hint(k_hint, per_tensor: bool, what: str):
+    """None, an int32, or a one-element int32 tensor (read on the GPU)."""
     if k_hint is None:
         return None
     if not per_tensor:
         raise ValueError(f"{what}: k_hint applies to per-tensor scaling (per_tensor=True)")
+    if isinstance(k_hint, torch.Tensor):
+        if k_hint.dtype != torch.int32 or k_hint.numel() != 1:
+            raise ValueError(f"{what}: a k_hint tensor holds one int32 (an exponent quantize returned), got {k_hint.dtype} x {k_hint.numel()}")
+        return k_hint
     k_hint = int(k_hint)
     if not -(2**31) <= k_hint < 2**31:
         raise ValueError(f"{what}: k_hint {k_hint} is not an int32")
     return k_hint
 
 
-def _per_tensor_hint(x: torch.Tensor, f: int, k_hint: int, q, out, what: str) -> torch.Tensor:
+def _per_tensor_hint(x: torch.Tensor, f: int, k_hint, q, out, what: str) -> torch.Tensor:
     """The one-pass per-tensor path (ely_fp8_quantize_hint): fills q and/or
-    out, returns k (one element, on x's device)."""
+    out, returns k (one element, on x's device).  A tensor hint is read on
+    the GPU, so the call does not wait for it."""
     _lib.require_gpu(x, what)
     x = x.detach().contiguous()
+    dev_hint = None
+    if isinstance(k_hint, torch.Tensor):
+        if k_hint.device != x.device:
+            raise ValueError(f"{what}: the k_hint tensor is on {k_hint.device}, x on {x.device}")
+        dev_hint, k_hint = k_hint.contiguous(), 0
     k = torch.empty(1, dtype=torch.int32, device=x.device)
     L = _lib.load()
     ws = _lib.workspace(x.device, L.ely_fp8_hint_workspace_bytes(x.numel()))
     _lib.check(
-        L.ely_fp8_quantize_hint(x.data_ptr(), _lib.dtype_code(x), x.numel(), f, k_hint, None if q is None else q.data_ptr(),
+        L.ely_fp8_quantize_hint(x.data_ptr(), _lib.dtype_code(x), x.numel(), f, k_hint,
+                                None if dev_hint is None else dev_hint.data_ptr(), None if q is None else q.data_ptr(),
                                 k.data_ptr(), None if out is None else out.data_ptr(), None, ws.data_ptr(), ws.numel(),
                                 _lib.stream_ptr(x.device)),
         what,
@@ -98,14 +110,15 @@ def _per_tensor_hint(x: torch.Tensor, f: int, k_hint: int, q, out, what: str) ->
     return k
 
 
-def quantize(x: torch.Tensor, fmt: str = "e4m3", per_tensor: bool = False, k_hint: int | None = None):
+def quantize(x: torch.Tensor, fmt: str = "e4m3", per_tensor: bool = False, k_hint: int | torch.Tensor | None = None):
     """x -> (fp8 tensor shaped like x, int32 k shaped like x with the last dim
     1).  Exact given k (model/fp8.py:45-49).
 
     k_hint (per-tensor only; an addition to the reference's signature): the
-    exponent the caller expects, e.g. the previous step's.  The results are
-    the same whatever the hint; when it is right, x is read once instead of
-    twice."""
+    exponent the caller expects, e.g. the previous step's, as an int or as
+    the one-element int32 tensor an earlier call returned (read on the GPU,
+    no host wait).  The results are the same whatever the hint; when it is
+    right, x is read once instead of twice."""
     f = _fmt(fmt)
     hint = _hint(k_hint, per_tensor, "quantize")
     if hint is not None:
@@ -164,7 +177,7 @@ def dequantize(q: torch.Tensor, k: torch.Tensor, dtype: torch.dtype = torch.floa
     return out
 
 
-def roundtrip(x: torch.Tensor, fmt: str = "e4m3", per_tensor: bool = False, k_hint: int | None = None) -> torch.Tensor:
+def roundtrip(x: torch.Tensor, fmt: str = "e4m3", per_tensor: bool = False, k_hint: int | torch.Tensor | None = None) -> torch.Tensor:
     """The declared recipe at a boundary: quantize then dequantize, in x's
     dtype (model/fp8.py:56-63), fused into one pass.  k_hint as quantize's."""
     f = _fmt(fmt)

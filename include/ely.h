@@ -159,21 +159,25 @@ int ely_fp8_quantize_noalloc(const void* x, int32_t x_dtype, int64_t rows, int64
                              uint8_t* q, int32_t* k, void* stream);
 
 /* Per-tensor fp8.quantize / fp8.roundtrip (model/fp8.py:28-63 with rows = 1)
- * given a guess k_hint of the exponent; an addition to the reference's
- * interface (fp8.quantize(x, fmt, per_tensor=True, k_hint=...)).  The
- * results are exactly ely_fp8_quantize's / ely_fp8_roundtrip's over one row
- * of n elements: k[0] is the tensor's exponent whatever the hint, and the
- * codes depend on k alone.  When k[0] equals the hint, x is read once
- * (3 B/element for bf16 -> fp8) instead of twice; otherwise the call makes
- * a second pass at the true exponent.  *hit_dev (optional, device int32)
- * is 1 when the one pass stood, 0 otherwise (and 0 when the tensor or hint
- * admits no one-pass form: unaligned x, n not a whole number of 16-byte
- * vectors, or |k_hint| > 110).  q: n bytes, or NULL with out given (the
- * round trip without the codes); out: n elements in x's dtype or NULL.
- * Workspace: ely_fp8_hint_workspace_bytes(n). */
+ * given a guess of the exponent; an addition to the reference's interface
+ * (fp8.quantize(x, fmt, per_tensor=True, k_hint=...)).  The results are
+ * exactly ely_fp8_quantize's / ely_fp8_roundtrip's over one row of n
+ * elements: k[0] is the tensor's exponent whatever the hint, and the codes
+ * depend on k alone.  When k[0] equals the hint, x is read once (3 B/element
+ * for bf16 -> fp8) instead of twice; otherwise the call makes a second pass
+ * at the true exponent.  The hint is k_hint, or, when k_hint_dev is not
+ * NULL, the device int32 *k_hint_dev, read on the GPU (no host wait); it
+ * may be the same word as k, e.g. the last step's exponent updated in
+ * place.  *hit_dev (optional, device int32) is 1 when the one pass stood,
+ * 0 otherwise (and 0 when the tensor or hint admits no one-pass form:
+ * unaligned x, n not a whole number of 16-byte vectors, or a hint outside
+ * [-110, 110]).  q: n bytes, or NULL with out given (the round trip without
+ * the codes); out: n elements in x's dtype or NULL.  Workspace:
+ * ely_fp8_hint_workspace_bytes(n). */
 int64_t ely_fp8_hint_workspace_bytes(int64_t n);
-int ely_fp8_quantize_hint(const void* x, int32_t x_dtype, int64_t n, int32_t fmt, int32_t k_hint, uint8_t* q,
-                          int32_t* k, void* out, int32_t* hit_dev, void* workspace, int64_t ws_bytes, void* stream);
+int ely_fp8_quantize_hint(const void* x, int32_t x_dtype, int64_t n, int32_t fmt, int32_t k_hint,
+                          const int32_t* k_hint_dev, uint8_t* q, int32_t* k, void* out, int32_t* hit_dev,
+                          void* workspace, int64_t ws_bytes, void* stream);
 
 /* fp8.dequantize (model/fp8.py:52-53): out = float(q) * 2^k in out_dtype
  * (ELY_F32 is the reference's default; ELY_BF16 is roundtrip's dtype). */

@@ -21,8 +21,9 @@ def _oracle_in(x: torch.Tensor) -> np.ndarray:
     return bits(x) if x.dtype == torch.bfloat16 else bits(x).astype(np.float32)
 
 
-def _hint_call(x: torch.Tensor, fmt: str, k_hint: int, want_q=True, want_out=False):
-    """ely_fp8_quantize_hint through the C ABI: (q, k, out, hit)."""
+def _hint_call(x: torch.Tensor, fmt: str, k_hint: int, want_q=True, want_out=False, device_hint=False, alias=False):
+    """ely_fp8_quantize_hint through the C ABI: (q, k, out, hit).  device_hint:
+    the hint from device memory; alias: that word is also the k output."""
     from elysium_wan_amd import _lib, fp8
 
     L = _lib.load()
@@ -31,10 +32,14 @@ def _hint_call(x: torch.Tensor, fmt: str, k_hint: int, want_q=True, want_out=Fal
     q = torch.full((n,), 0xA5, dtype=torch.uint8, device=x.device) if want_q else None
     out = torch.full((n,), float("nan"), dtype=x.dtype, device=x.device) if want_out else None
     k = torch.full((1,), -777, dtype=torch.int32, device=x.device)
+    hdev = None
+    if device_hint:
+        hdev = k if alias else torch.empty(1, dtype=torch.int32, device=x.device)
+        hdev.fill_(k_hint)
     hit = torch.full((1,), -1, dtype=torch.int32, device=x.device)
     ws = torch.empty(L.ely_fp8_hint_workspace_bytes(n), dtype=torch.uint8, device=x.device)
-    _lib.check(L.ely_fp8_quantize_hint(x.data_ptr(), _lib.dtype_code(x), n, _lib.FMT[fmt], k_hint,
-                                       None if q is None else q.data_ptr(), k.data_ptr(),
+    _lib.check(L.ely_fp8_quantize_hint(x.data_ptr(), _lib.dtype_code(x), n, _lib.FMT[fmt], 12345 if device_hint else k_hint,
+                                       None if hdev is None else hdev.data_ptr(), None if q is None else q.data_ptr(), k.data_ptr(),
                                        None if out is None else out.data_ptr(), hit.data_ptr(), ws.data_ptr(), ws.numel(),
                                        _lib.stream_ptr(x.device)), "quantize_hint")
     torch.cuda.synchronize()
@@ -58,6 +63,40 @@ def test_hit_and_miss_equal_the_oracle(oracle, fmt, dtype, n):
         assert k == k_true
         assert np.array_equal(bits(q), oq.reshape(-1)), f"fp8 bytes, hint {hint}"
         assert hit == (1 if hint == k_true else 0)
+
+
+@pytest.mark.parametrize("alias", [False, True])
+def test_device_hint_read_on_the_gpu(oracle, alias):
+    """The hint from device memory (the int argument is then ignored: a wrong
+    one is passed), also when that word is the k output itself (the last
+    step's exponent updated in place): right, off and out-of-range hints
+    give the oracle's bytes and k, and the flag says which pass stood."""
+    x = activation((3 * 2048 * 33,), seed=331)
+    for fmt in ("e4m3", "e5m2"):
+        oq, ok = oracle.quantize(_oracle_in(x.reshape(1, -1)), fmt)
+        k_true = int(ok.reshape(-1)[0])
+        for hint in (k_true, k_true + 1, k_true - 3, 150):
+            say("fp8 device hint", fmt, "alias" if alias else "separate", hint, "k", k_true)
+            q, k, _, hit = _hint_call(x, fmt, hint, device_hint=True, alias=alias)
+            assert k == k_true
+            assert np.array_equal(bits(q), oq.reshape(-1))
+            assert hit == (1 if hint == k_true else 0)
+
+
+def test_steps_with_the_last_exponent_as_the_hint():
+    """A boundary quantized every step with the previous step's k tensor as
+    the hint (fp8.quantize(..., k_hint=k_prev)): every step equals the
+    hint-free per-tensor quantize, whether the scale held or moved."""
+    from elysium_wan_amd import fp8
+
+    k_prev = None
+    for step, scale in enumerate((1.0, 1.3, 1.3, 5.0, 0.2, 0.2)):
+        x = (activation((8, 4096), seed=500 + step) * scale).to(torch.bfloat16)
+        say("fp8 hint steps", step, scale)
+        q, k = fp8.quantize(x, "e4m3", per_tensor=True, k_hint=k_prev)
+        qw, kw = fp8.quantize(x, "e4m3", per_tensor=True)
+        assert torch.equal(q.view(torch.uint8), qw.view(torch.uint8)) and torch.equal(k, kw)
+        k_prev = k.reshape(1) if k_prev is None or step % 2 else k.reshape(1).clone()
 
 
 @pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
@@ -114,6 +153,10 @@ def test_hint_argument_checks():
         fp8.quantize(x, "e4m3", k_hint=0)
     with pytest.raises(ValueError, match="int32"):
         fp8.quantize(x, "e4m3", per_tensor=True, k_hint=2**40)
+    with pytest.raises(ValueError, match="one int32"):
+        fp8.quantize(x, "e4m3", per_tensor=True, k_hint=torch.zeros(2, dtype=torch.int32, device="cuda"))
+    with pytest.raises(ValueError, match="one int32"):
+        fp8.quantize(x, "e4m3", per_tensor=True, k_hint=torch.zeros(1, dtype=torch.int64, device="cuda"))
 
 
 def _c4_activation(seed: int) -> torch.Tensor:
