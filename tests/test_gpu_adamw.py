@@ -392,6 +392,56 @@ def test_step_on_a_side_thread_and_stream():
         assert torch.equal(x.view(torch.int16), y.view(torch.int16))
 
 
+def test_two_threads_share_the_upload_ring():
+    """Two threads, each on its own stream with its own 60-tensor optimizer
+    (past the 48 tensors whose tables ride in the kernel arguments, so every
+    norm and update uploads its tables through the library's pinned ring of
+    8 slots, which both threads wrap many times): each ends bit for bit where
+    the same steps run alone end."""
+    import threading
+
+    from elysium_wan_amd import optim
+
+    gen = torch.Generator().manual_seed(37)
+    shapes = [(1000 + 37 * i,) for i in range(60)]
+    init = [torch.randn(s, generator=gen) for s in shapes]
+    grads = [[(torch.randn(s, generator=gen) * 1e-2).to(torch.bfloat16).cuda() for s in shapes] for _ in range(2)]
+
+    def make():
+        ps = [t.clone().cuda().requires_grad_(True) for t in init]
+        return ps, optim.FusedAdamW(ps, lr=1e-3, betas=(0.9, 0.95), order="host", max_norm=1.0, working_copy=True)
+
+    alone = [make(), make()]
+    for j, (_, opt) in enumerate(alone):
+        for _ in range(25):
+            opt.step(grads=grads[j])
+    torch.cuda.synchronize()
+    together = [make(), make()]
+    errors = []
+
+    def run(j):
+        try:
+            with torch.cuda.stream(torch.cuda.Stream()):
+                for _ in range(25):
+                    together[j][1].step(grads=grads[j])
+                torch.cuda.current_stream().synchronize()
+        except Exception as e:  # surfaced below
+            errors.append(e)
+
+    say("two threads share the upload ring")
+    threads = [threading.Thread(target=run, args=(j,)) for j in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+    torch.cuda.synchronize()
+    for (pa, oa), (pb, ob) in zip(alone, together):
+        for x, y in zip(pa, pb):
+            assert torch.equal(x.detach().view(torch.int32), y.detach().view(torch.int32))
+        assert torch.equal(oa.grad_norm().view(torch.int32), ob.grad_norm().view(torch.int32))
+
+
 def test_frozen_parameters_get_no_moments():
     """A frozen tensor (a LoRA base, runtime/optim.py:97-99) is never
     stepped through p.grad and takes no moment memory; one stepped anyway
