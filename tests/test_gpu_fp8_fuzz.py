@@ -87,3 +87,46 @@ def test_codec_matches_the_oracle(oracle, rows, cols, bf16, fmt, per_tensor, spe
             fp8.recover_exp(r, fmt)
     else:
         assert np.array_equal(fp8.recover_exp(r, fmt).cpu().numpy().reshape(-1), rk)
+
+
+@FUZZ
+@given(
+    n=st.sampled_from([8, 24, 2048, 2056, 4096 + 8, 3 * 2048 + 16, 65536, 65536 + 24, 200008]),
+    bf16=st.booleans(),
+    fmt=st.sampled_from(["e4m3", "e5m2"]),
+    specials=st.sampled_from([0.0, 0.0, 1e-4, 0.05]),
+    offset=st.sampled_from([0, 0, 0, 1, -1, 2, -7, 300]),
+    as_tensor=st.booleans(),
+    seed=st.integers(0, 2**16),
+)
+def test_per_tensor_hint_matches_the_oracle(oracle, n, bf16, fmt, specials, offset, as_tensor, seed):
+    """fp8.quantize / roundtrip(per_tensor=True, k_hint=...) with the hint
+    right, a few off or far out of range, as an int or a device tensor, over
+    exponents across the range with NaN, Inf, zeros and subnormals sprinkled
+    in: codes, k and the round trip equal the oracle's per-tensor results."""
+    from elysium_wan_amd import fp8
+
+    rng = np.random.default_rng(seed)
+    e = int(rng.integers(-135, 125))
+    x = (rng.standard_normal(n) * np.exp2(float(e))).astype(np.float32)
+    if specials:
+        pick = rng.random(n) < specials
+        pool = np.array([np.nan, np.inf, -np.inf, 0.0, -0.0, 1e-40, -3e-39, 1e-45], dtype=np.float32)
+        x[pick] = pool[rng.integers(0, pool.size, size=int(pick.sum()))]
+    if bf16:
+        host = oracle.f32_to_bf16_bits(x).reshape(x.shape)
+        xt = torch.from_numpy(host.view(np.int16).copy()).view(torch.bfloat16).cuda()
+    else:
+        host = x
+        xt = torch.from_numpy(x.copy()).cuda()
+    oq, ok = oracle.quantize(host.reshape(1, -1), fmt)
+    hint = int(ok.reshape(-1)[0]) + offset
+    h = torch.tensor([hint], dtype=torch.int32, device="cuda") if as_tensor else hint
+    say("fp8 hint fuzz", n, "bf16" if bf16 else "f32", fmt, specials, "hint", hint, "k", int(ok.reshape(-1)[0]),
+        "tensor" if as_tensor else "int", seed)
+    q, k = fp8.quantize(xt, fmt, per_tensor=True, k_hint=h)
+    assert _codes_equal(bits(q).reshape(-1), oq.reshape(-1), fmt)
+    assert int(k.reshape(-1)[0]) == int(ok.reshape(-1)[0])
+    od = oracle.dequantize(oq, ok, fmt, "bf16" if bf16 else "f32").reshape(-1)
+    r = fp8.roundtrip(xt, fmt, per_tensor=True, k_hint=h)
+    assert _vals_equal(bits(r).reshape(-1), od)
