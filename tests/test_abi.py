@@ -347,3 +347,27 @@ def test_plane_compression_keeps_the_serial_bytes_and_survives_a_fork():
     p.join(timeout=60)
     assert p.exitcode == 0
     assert got == serial
+
+
+def test_argument_errors_of_the_hint_entry_point(lib):
+    """ely_fp8_quantize_hint refuses bad arguments and a short workspace with
+    status codes before the HIP runtime is touched; its workspace query is
+    host arithmetic, never below the split path's (its fallback)."""
+    from elysium_wan_amd import _lib
+
+    fake = 1 << 20  # never dereferenced
+    q = lib.ely_fp8_quantize_hint
+    assert q(fake, _lib.BF16, 64, 9, 0, None, fake, fake, None, None, fake, 1 << 20, None) == _lib.EINVAL
+    assert b"fp8 format" in lib.ely_last_error()
+    assert q(fake, 7, 64, _lib.E4M3, 0, None, fake, fake, None, None, fake, 1 << 20, None) == _lib.EINVAL
+    assert q(fake, _lib.BF16, -8, _lib.E4M3, 0, None, fake, fake, None, None, fake, 1 << 20, None) == _lib.EINVAL
+    assert q(fake, _lib.BF16, 64, _lib.E4M3, 0, None, fake, None, None, None, fake, 1 << 20, None) == _lib.EINVAL
+    assert b"null k" in lib.ely_last_error()
+    assert q(fake, _lib.BF16, 64, _lib.E4M3, 0, None, None, fake, None, None, fake, 1 << 20, None) == _lib.EINVAL
+    assert b"neither q nor out" in lib.ely_last_error()
+    assert q(fake, _lib.BF16, 1 << 24, _lib.E4M3, 3, None, fake, fake, None, None, fake, 256, None) == _lib.EWORKSPACE
+    assert b"ely_fp8_hint_workspace_bytes" in lib.ely_last_error()
+    ws = lib.ely_fp8_hint_workspace_bytes
+    assert ws(-1) == -1
+    assert ws(0) >= lib.ely_fp8_workspace_bytes(1, 0, _lib.BF16)
+    assert ws(1 << 29) >= (1 << 29) // 2048 * 4 and ws(1 << 29) >= ws(1 << 20)
