@@ -175,7 +175,7 @@ class OrderedAccumulator:
         self._advance(i)
 
     def end_part(self, mb) -> None:
-        """Every tensor of microbatch mb was handed to fold_part."""
+        """Closes microbatch mb once all of its tensors went through fold_part."""
         if self._flags(mb)[1]:
             raise AssertionError(f"duplicate contribution for mb {mb}")
         self._size(0 if self.acc is None else len(self.acc))
