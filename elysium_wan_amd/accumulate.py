@@ -301,7 +301,9 @@ class TiedRowFold:
     add_head(mb, h, rows): h the (n_rows, d) gradient of the Head's use (fp32
     or bf16, on the GPU; every microbatch's of one shape, dtype and device),
     rows T_mb (ascending unique ids, int64).  add_embed(mb, e_rows):
-    e_mb[T_mb] in ascending id.  Either may come first, for any microbatch.
+    e_mb[T_mb] in ascending id.  Either may come first, for any microbatch
+    of the order; an id outside the order is refused with a RuntimeError
+    (the reference would hold it forever without folding it).
 
     Bookkeeping: each microbatch of the order has a position with a state
     (no Head gradient taken / rows held / done) and slots for what has
