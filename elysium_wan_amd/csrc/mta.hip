@@ -12,7 +12,8 @@
 // full of short-lived waves streaming one small window of the shard (C1:
 // 5.94 ms against 6.64 for the persistent grid of one 256-thread block per
 // CU looping over 4,096-element tiles, and 7.5-8.7 ms for persistent grids
-// of these small tiles).  Norm: wave
+// of these small tiles; 5.81-5.87 ms since with buffer instructions and a
+// tile -> tensor chunk map).  Norm: wave
 // w takes the contiguous tile range [w*T/W, (w+1)*T/W), its last tiles
 // (ELY_NORM_CACHED_MB in all) with plain loads, the rest nontemporal.  A
 // table of tensor descriptors is staged into the caller's workspace per
