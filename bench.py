@@ -48,6 +48,7 @@ ADAM_BYTES_PER_ELEM = 28  # bf16 grads, bf16 copy out
 NORM_BYTES_PER_ELEM = 2
 CODEC_BYTES_PER_ELEM = 3  # bf16 in / fp8 out (quantize); fp8 in / bf16 out (dequantize)
 ROUNDTRIP_BYTES_PER_ELEM = 4  # bf16 in, bf16 out (fp8.roundtrip, nothing else written)
+C1_CODEC_COPIES, C1_CODEC_ITERS = 8, 20  # C1 codec leg: rotating inputs, launches per timed group
 CAL_ELEMS = 1 << 28  # calibration cast of the --pmc passes
 
 
@@ -1060,6 +1061,21 @@ def _runs(disp, names):
     return [r for r in runs if r[0] is not None]
 
 
+def _c1_codec_labels(fmts: int = 2) -> list:
+    """(kind, mode) of every quant_rows_kernel / dequant_flat_kernel launch of
+    `bench.py --no-optimizer --codec c1`, in launch order: per format,
+    bench_codec's warm-up quantizes, then time_events of quantize,
+    dequantize and the round trip, then time_back_to_back of the three; each
+    timed group opens with one untimed launch."""
+    labels = []
+    for _ in range(fmts):
+        labels += [("quantize", "warm")] * C1_CODEC_COPIES
+        for mode in ("single", "b2b"):
+            for kind in ("quantize", "dequantize", "roundtrip"):
+                labels += [(kind, "untimed")] + [(kind, mode)] * C1_CODEC_ITERS
+    return labels
+
+
 def c4_summary(trace_dir: str, bench_out: str | None) -> None:
     """Kernel durations of a rocprofv3 --kernel-trace run of `bench.py
     --no-optimizer --codec c4`: per scaling (per-row, per-tensor) and
@@ -1262,18 +1278,16 @@ def trace_summary(step_dir: str, codec_dir: str, bench_json: list | None) -> Non
         f.write("\n".join(lines) + "\n")
     print("\n".join(lines))
 
-    runs = _runs(_dispatches(codec_dir), ("quant_rows_kernel", "dequant_flat_kernel"))
-    kinds = {"quantize": [], "dequantize": [], "roundtrip": []}
-    rt_left = 0  # quant_rows_kernel launches still due as round trips
-    for name, ds in runs:
-        if name == "dequant_flat_kernel":
-            kinds["dequantize"] += ds
-            rt_left = len(ds)  # the round trips follow, as many as the dequantizes
-        else:
-            kinds["roundtrip"] += ds[:rt_left]
-            kinds["quantize"] += ds[rt_left:]
-            rt_left = max(0, rt_left - len(ds))
+    labels = _c1_codec_labels()
+    disp = [(name, ns) for name, ns in _dispatches(codec_dir) if name in ("quant_rows_kernel", "dequant_flat_kernel")]
+    want = ["dequant_flat_kernel" if lab[0] == "dequantize" else "quant_rows_kernel" for lab in labels]
+    if [name for name, _ in disp][: len(labels)] != want:
+        raise SystemExit("the codec trace does not follow bench_codec's launch order")
+    by = {}
+    for (kind, mode), (_, ns) in zip(labels, disp):
+        by.setdefault((kind, mode), []).append(ns)
     na = 8 * 2048 * D_MODEL
+    per = {"quantize": 3, "dequantize": 3, "roundtrip": 4}
     lines = [
         "# Kernel durations, fp8 codec on C1's activation",
         "",
@@ -1287,24 +1301,34 @@ def trace_summary(step_dir: str, codec_dir: str, bench_json: list | None) -> Non
         "row), e4m3 and e5m2, rotating through 8 copies so that no launch reads from",
         f"the 256 MB MALL.  Algorithmic traffic per launch: {na:,} x 3 B = {na * 3 / 1e6:.1f} MB",
         f"for quantize and dequantize, x 4 B = {na * 4 / 1e6:.1f} MB for the fused round trip.",
-        "quant_rows_kernel serves quantize and the round trip; the launches are",
-        "split by bench.py's order (per format: quantize, dequantize, then as many",
-        "round trips as dequantizes).",
+        "quant_rows_kernel serves quantize and the round trip; each launch is",
+        f"labelled by bench_codec's fixed order (per format: {C1_CODEC_COPIES} warm-up quantizes, then",
+        f"quantize, dequantize and round trip timed one launch between two HIP events,",
+        f"then the same three queued back to back; each timed group is {C1_CODEC_ITERS} launches",
+        "after one untimed launch that follows a device synchronize).",
         "",
-        "| launches | calls | average (ns) | min (ns) | max (ns) | kernel-time rate |",
-        "|---|---|---|---|---|---|",
+        "| launches | timed single launches | average (ns) | min (ns) | max (ns) | kernel-time rate | back-to-back launches | average (ns) | rate | every launch, warm-up and untimed included | average (ns) | rate |",
+        "|---|---|---|---|---|---|---|---|---|---|---|---|",
     ]
-    per = {"quantize": 3, "dequantize": 3, "roundtrip": 4}
-    for kind, ds in kinds.items():
-        if ds:
-            avg = sum(ds) / len(ds)
-            lines.append(_row(kind, ds)[:-2] + f" | {na * per[kind] / avg / 1e3:.2f} TB/s |")
+    for kind in ("quantize", "dequantize", "roundtrip"):
+        ev, bb = by.get((kind, "single"), []), by.get((kind, "b2b"), [])
+        every = ev + bb + by.get((kind, "untimed"), []) + (by.get(("quantize", "warm"), []) if kind == "quantize" else [])
+        if not ev or not bb:
+            continue
+        rate = lambda ds: na * per[kind] / (sum(ds) / len(ds)) / 1e3  # noqa: E731
+        lines.append(f"| {kind} | {len(ev)} | {sum(ev) / len(ev):,.0f} | {min(ev):,} | {max(ev):,} | {rate(ev):.2f} TB/s | "
+                     f"{len(bb)} | {sum(bb) / len(bb):,.0f} | {rate(bb):.2f} TB/s | {len(every)} | "
+                     f"{sum(every) / len(every):,.0f} | {rate(every):.2f} TB/s |")
     if bc and bc.get("fp8_codec"):
         c = bc["fp8_codec"]["c1_per_row"]["e4m3"]
-        lines += ["", "bench.py's HIP-event averages in the traced process (one launch between two events, so each also",
+        lines += ["", "bench.py's HIP-event averages in the traced process, e4m3 (one launch between two events, so each also",
                   f"holds the launch's dispatch latency): quantize {c['quantize_ms'] * 1e3:.1f} us ({c['quantize_GBs'] / 1e3:.2f} TB/s),",
                   f"dequantize {c['dequantize_ms'] * 1e3:.1f} us ({c['dequantize_GBs'] / 1e3:.2f} TB/s), round trip "
                   f"{c['roundtrip_ms'] * 1e3:.1f} us ({c['roundtrip_GBs'] / 1e3:.2f} TB/s)."]
+        b2b = c.get("back_to_back_GBs")
+        if b2b:
+            lines += [f"Back to back between one event pair: quantize {b2b['quantize'] / 1e3:.2f}, dequantize "
+                      f"{b2b['dequantize'] / 1e3:.2f}, round trip {b2b['roundtrip'] / 1e3:.2f} TB/s."]
     with open(os.path.join(HERE, "profiles", "codec_c1_kernel_trace.md"), "w") as f:
         f.write("\n".join(lines) + "\n")
     print("\n".join(lines))
@@ -1574,7 +1598,7 @@ def main():
         if args.no_optimizer:
             log("codec-only run")
             if args.codec in ("c1", "all"):
-                print(json.dumps({"c1": bench_codec(device, stream, 8 * 2048, D_MODEL, 8, iters=10)}), flush=True)
+                print(json.dumps({"c1": bench_codec(device, stream, 8 * 2048, D_MODEL, C1_CODEC_COPIES, iters=C1_CODEC_ITERS, back_to_back=True)}), flush=True)
             if args.codec in ("c4", "all"):
                 print(json.dumps({"c4": bench_c4(device, stream)}), flush=True)
             return
@@ -1585,7 +1609,7 @@ def main():
             log("codec leg")
             codec = {}
             if args.codec in ("c1", "all"):
-                codec["c1_per_row"] = bench_codec(device, stream, 8 * 2048, D_MODEL, 8, back_to_back=True)
+                codec["c1_per_row"] = bench_codec(device, stream, 8 * 2048, D_MODEL, C1_CODEC_COPIES, iters=C1_CODEC_ITERS, back_to_back=True)
                 torch.cuda.empty_cache()
             if args.codec in ("c4", "all"):
                 codec["c4"] = bench_c4(device, stream)

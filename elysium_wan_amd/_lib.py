@@ -59,6 +59,7 @@ EXPORTS = (
     "ely_fp8_nibbles_encode",
     "ely_fp8_nibbles_decode",
     "ely_selftest_fp8_cvt",
+    "ely_selftest_fp8_scaled",
     "ely_selftest_sqrt",
 )
 
@@ -134,6 +135,7 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
         L.ely_fp8_nibbles_encode.argtypes = [P, I32, I64, P, P, P, P]
         L.ely_fp8_nibbles_decode.argtypes = [P, P, I64, P, P]
         L.ely_selftest_fp8_cvt.argtypes = [ctypes.c_uint32, ctypes.c_uint64, I32, P, P]
+        L.ely_selftest_fp8_scaled.argtypes = [I32, P, P]
         L.ely_selftest_sqrt.argtypes = [ctypes.c_uint32, ctypes.c_uint64, P, P]
         _lib = L
     return _lib

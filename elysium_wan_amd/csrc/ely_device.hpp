@@ -122,6 +122,46 @@ __device__ __forceinline__ void cvt_pk_f32(uint32_t w, float& a, float& b) {
     b = r.y;
 }
 
+typedef short ely_s16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 ely_bf16x2 __attribute__((ext_vector_type(2)));
+
+// Two bf16 (the low and high half of `w`) -> two fp8 codes, each x / scale
+// rounded to the format in one step (v_cvt_scalef32_pk_fp8_bf16 /
+// v_cvt_scalef32_pk_bf8_bf16), into the low (HI=false) or high half of
+// `old`.  With scale = 2^k this is the code of x * 2^-k for every bf16 x and
+// |k| <= 110 with |x| 2^-k below 2^ebias, the pairs the quantize instruction
+// path meets (ely_selftest_fp8_scaled checks all of them).
+template <int FMT, bool HI>
+__device__ __forceinline__ uint32_t cvt_scaled_pk_fp8_bf16(uint32_t w, float scale, uint32_t old) {
+    const ely_bf16x2 x = __builtin_bit_cast(ely_bf16x2, w);
+    const ely_s16x2 o = __builtin_bit_cast(ely_s16x2, old);
+    ely_s16x2 r;
+    if (FMT == kE4M3) r = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(o, x, scale, HI);
+    else r = __builtin_amdgcn_cvt_scalef32_pk_bf8_bf16(o, x, scale, HI);
+    return __builtin_bit_cast(uint32_t, r);
+}
+
+// Two fp8 codes (low or high 16 bits of `w`) -> two bf16 (one word), each
+// code's value times `scale` (v_cvt_scalef32_pk_bf16_fp8 / _bf8).  With
+// scale = 2^k, |k| <= 110, the exact product for every code but the NaN
+// codes, whose result is a NaN with other bits than torch's 0x7FC0: callers
+// keep NaN codes off this path (ely_selftest_fp8_scaled checks the rest).
+template <int FMT, bool HI>
+__device__ __forceinline__ uint32_t cvt_scaled_pk_bf16(uint32_t w, float scale) {
+    ely_bf16x2 r;
+    if (FMT == kE4M3) r = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, scale, HI);
+    else r = __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(w, scale, HI);
+    return __builtin_bit_cast(uint32_t, r);
+}
+
+// Whether any of the four codes of `w` is a NaN code (e4m3: |c| = 0x7F;
+// e5m2: |c| in 0x7D..0x7F): adding 1 (3) to every 7-bit magnitude carries
+// into bit 7 exactly for those, and never into the next byte.
+template <int FMT>
+__device__ __forceinline__ uint32_t nan_code_bits(uint32_t w) {
+    return ((w & 0x7F7F7F7Fu) + (FMT == kE4M3 ? 0x01010101u : 0x03030303u)) & 0x80808080u;
+}
+
 // 2^n rounded once to fp32 (Inf at n >= 128, 0 below 2^-149 with the tie at
 // 2^-150 going to 0) and, for bf16 tensors, once more to bf16: torch.exp2 of
 // an integer-valued tensor of that dtype (fp8.py:41-42).

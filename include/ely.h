@@ -329,6 +329,16 @@ int ely_fp8_nibbles_decode(const uint8_t* hi, const uint8_t* lo, int64_t n, floa
 int ely_selftest_fp8_cvt(uint32_t start, uint64_t count, int32_t fmt,
                          unsigned long long* mismatches_dev, void* stream);
 
+/* Device self-check of the gfx950 scaled conversions the bf16 kernels use
+ * (v_cvt_scalef32_pk_{fp8,bf8}_bf16 to quantize, v_cvt_scalef32_pk_bf16_
+ * {fp8,bf8} to decode, at scale 2^k) against the library's restatement of
+ * torch's arithmetic, over every bf16 pattern and every |k| <= 110.
+ * mismatches_dev: two uint64 counters the caller zeroes: [0] quantized
+ * (pattern, k) pairs of the instruction path's domain (finite, |x| 2^-k
+ * below 2^ebias) whose code differs, in either half of the input word or of
+ * the output; [1] (code, k) pairs, NaN codes aside, whose bf16 differs. */
+int ely_selftest_fp8_scaled(int32_t fmt, unsigned long long* mismatches_dev, void* stream);
+
 /* Device self-check that the kernels' fp32 sqrt (used by the AdamW update)
  * equals the fp64 sqrt rounded once to fp32 (runtime/optim.py:288-291) on
  * the non-negative fp32 patterns of [start, start + count) (sign bit

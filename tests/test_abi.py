@@ -79,6 +79,8 @@ def test_argument_errors_are_status_codes(lib):
     assert lib.ely_cast_bf16(None, None, -3, None) == _lib.EINVAL
     assert lib.ely_fold_add(None, None, 5, 4, None) == _lib.EINVAL
     assert lib.ely_selftest_fp8_cvt(0, 1 << 33, 0, None, None) == _lib.EINVAL
+    assert lib.ely_selftest_fp8_scaled(0, None, None) == _lib.EINVAL
+    assert lib.ely_selftest_fp8_scaled(7, None, None) == _lib.EINVAL
     assert lib.ely_host_device_pointer(None, ctypes.byref(ctypes.c_void_p())) == _lib.EINVAL
 
 

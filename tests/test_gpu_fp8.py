@@ -203,6 +203,32 @@ def test_scale_exp_is_the_quantize_exponent():
     assert torch.equal(fp8.scale_exp(x, "e4m3"), k)
 
 
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+@pytest.mark.parametrize("cols", [16, 1008, 1024, 1040, 2560, 3072, 8192 + 16])
+def test_dequantize_every_code_with_a_distinct_exponent_per_row(oracle, fmt, cols):
+    """Codes cycling through all 256 bytes (NaN and Inf codes included) and an
+    exponent per row drawn from [-140, 140] (both of the kernel's paths, and
+    results that overflow or go subnormal), neighbours always different: a
+    value taken with its neighbour row's exponent, where a wave's 1,024 codes
+    cross a row boundary, changes the bytes.  bf16 and fp32 out, vs the oracle."""
+    from elysium_wan_amd import fp8
+
+    rows = max(3, (3 * 4096 + cols - 1) // cols)
+    rng = np.random.default_rng(cols)
+    codes = ((np.arange(rows * cols, dtype=np.int64) * 37 + rng.integers(0, 256)) % 256).astype(np.uint8)
+    kk = rng.integers(-140, 141, rows).astype(np.int32)
+    for r in range(1, rows):
+        if kk[r] == kk[r - 1]:
+            kk[r] += 1
+    q = torch.from_numpy(codes.reshape(rows, cols)).cuda().view(fp8.FORMATS[fmt][0])
+    k = torch.from_numpy(kk.reshape(rows, 1)).cuda()
+    for out_dt, name in ((torch.float32, "f32"), (torch.bfloat16, "bf16")):
+        say("fp8 dequantize distinct exponents", fmt, cols, name)
+        d = bits(fp8.dequantize(q, k, out_dt)).reshape(-1)
+        od = oracle.dequantize(codes.reshape(rows, cols), kk, fmt, name).reshape(-1)
+        assert f32_equal(d, od) if name == "f32" else np.array_equal(d, od)
+
+
 def test_empty_inputs():
     from elysium_wan_amd import fp8
 
