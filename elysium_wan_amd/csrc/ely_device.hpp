@@ -10,7 +10,9 @@
 //     an integer restatement of that rule; the hot loops use the gfx950
 //     conversion instruction (v_cvt_pk_fp8_f32 / v_cvt_pk_bf8_f32) on the
 //     domain ely_selftest_fp8_cvt proves it equal on (finite values at or below
-//     the format's largest finite value), and the restatement elsewhere.
+//     the format's largest finite value), for bf16 data the scaled
+//     conversions (v_cvt_scalef32_pk_*) on the pairs ely_selftest_fp8_scaled
+//     proves them equal on, and the restatement elsewhere.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -228,9 +230,10 @@ struct HostConsts {
 // The sqrt is the correctly rounded fp32 sqrt, which equals the reference's
 // fp64 sqrt rounded once to fp32 (53 >= 2*24 + 2 bits, so the double rounding
 // is innocuous); the division is IEEE.
-__device__ __forceinline__ void adamw_host_elem(float& p, float g, float& m, float& v,
-                                                const HostConsts& c, bool wd) {
-    if (wd) p = p * c.decay;
+// The moments' half and the parameter's half are separate calls, so that a
+// kernel can store m and v before the sqrt and the division; p's decay
+// touches p alone, so where it runs does not change a bit.
+__device__ __forceinline__ void adamw_host_moments(float g, float& m, float& v, const HostConsts& c) {
     m = m * c.b1;
     float t = g * c.one_b1;
     m = m + t;
@@ -238,6 +241,10 @@ __device__ __forceinline__ void adamw_host_elem(float& p, float g, float& m, flo
     float s = g * g;
     s = s * c.one_b2;
     v = v + s;
+}
+
+__device__ __forceinline__ void adamw_host_param(float& p, float m, float v, const HostConsts& c, bool wd) {
+    if (wd) p = p * c.decay;
     float d = __builtin_sqrtf(v);
     d = d * c.inv_bc2_sqrt;
     d = d + c.eps;
@@ -246,15 +253,19 @@ __device__ __forceinline__ void adamw_host_elem(float& p, float g, float& m, flo
     p = p - u;
 }
 
+__device__ __forceinline__ void adamw_host_elem(float& p, float g, float& m, float& v,
+                                                const HostConsts& c, bool wd) {
+    adamw_host_moments(g, m, v, c);
+    adamw_host_param(p, m, v, c, wd);
+}
+
 struct TorchConsts {
     float decay, w1, b2, one_b2, bc2_sqrt, eps, neg_step, unused;
 };
 
 // torch.optim.AdamW's foreach op order (TORCH/optim/adam.py:688-800):
 // lerp (ATen Lerp.h), addcmul/addcdiv as a + s * (b op c), as fmas.
-__device__ __forceinline__ void adamw_torch_elem(float& p, float g, float& m, float& v,
-                                                 const TorchConsts& c, bool wd) {
-    if (wd) p = p * c.decay;
+__device__ __forceinline__ void adamw_torch_moments(float g, float& m, float& v, const TorchConsts& c) {
     if (__builtin_fabsf(c.w1) < 0.5f) {
         m = __builtin_fmaf(c.w1, g - m, m);
     } else {
@@ -262,10 +273,20 @@ __device__ __forceinline__ void adamw_torch_elem(float& p, float g, float& m, fl
     }
     v = v * c.b2;
     v = __builtin_fmaf(c.one_b2, g * g, v);
+}
+
+__device__ __forceinline__ void adamw_torch_param(float& p, float m, float v, const TorchConsts& c, bool wd) {
+    if (wd) p = p * c.decay;
     float d = __builtin_sqrtf(v);
     d = d / c.bc2_sqrt;
     d = d + c.eps;
     p = __builtin_fmaf(c.neg_step, m / d, p);
+}
+
+__device__ __forceinline__ void adamw_torch_elem(float& p, float g, float& m, float& v,
+                                                 const TorchConsts& c, bool wd) {
+    adamw_torch_moments(g, m, v, c);
+    adamw_torch_param(p, m, v, c, wd);
 }
 
 }  // namespace ely
