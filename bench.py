@@ -49,6 +49,7 @@ NORM_BYTES_PER_ELEM = 2
 CODEC_BYTES_PER_ELEM = 3  # bf16 in / fp8 out (quantize); fp8 in / bf16 out (dequantize)
 ROUNDTRIP_BYTES_PER_ELEM = 4  # bf16 in, bf16 out (fp8.roundtrip, nothing else written)
 C1_CODEC_COPIES, C1_CODEC_ITERS = 8, 20  # C1 codec leg: rotating inputs, launches per timed group
+C4_CODEC_ITERS = 10  # C4 codec leg: launches per timed group
 CAL_ELEMS = 1 << 28  # calibration cast of the --pmc passes
 
 
@@ -431,7 +432,7 @@ def bench_codec(device, stream, rows, cols, copies, iters=20, per_tensor=False, 
     return out
 
 
-def bench_c4(device, stream, iters=10):
+def bench_c4(device, stream, iters=C4_CODEC_ITERS):
     """Config C4's sweep: {activation, gradient} x {e4m3, e5m2} x {per-row
     (8,192 wide), per-tensor}, encode -> decode, with timings, relative
     error, exponent range and digests of the exact fp8 bytes and scales."""
@@ -890,7 +891,8 @@ def profile_pass(device):
     del xa, q, k, out
     log("profile pass: codec done")
     # per-tensor quantize of a C4-sized activation with a right exponent hint
-    # (one pass: quant_hint_kernel), after one split-path call that finds k
+    # (one pass: quant_hint_kernel), after one call without a hint that finds
+    # k (the sampled guess, whose hint pass on this N(0, 1) input is right too)
     n4 = 16 * 4096 * 8192
     x4 = torch.randn(n4, device=device).to(torch.bfloat16)
     q4 = torch.empty(n4, dtype=torch.uint8, device=device)
@@ -1076,52 +1078,87 @@ def _c1_codec_labels(fmts: int = 2) -> list:
     return labels
 
 
+def _codec_calls(disp) -> list:
+    """Group a codec trace's dispatches into calls: (kind, [(kernel, ns)])
+    with kind "row" (one quant_rows / quant_block_row kernel: a per-row
+    quantize or round trip), "deq" (a dequantize), "guess" (a per-tensor
+    quantize or round trip without a hint: guess_amax, sample_max, then the
+    hint path's three kernels), "split" (the split path's row maxima and
+    quant_split_kernel) or "hint" (ely_fp8_quantize_hint's three kernels).
+    Other kernels (torch's) are skipped."""
+    calls, cur, kind = [], [], None
+    ends = {"guess": "quant_hint_fixup_kernel", "hint": "quant_hint_fixup_kernel", "split": "quant_split_kernel"}
+    for name, ns in disp:
+        if kind is not None:
+            cur.append((name, ns))
+            if name == ends[kind]:
+                calls.append((kind, cur))
+                cur, kind = [], None
+            continue
+        if name in ("quant_rows_kernel", "quant_block_row_kernel"):
+            calls.append(("row", [(name, ns)]))
+        elif name.startswith("dequant_"):
+            calls.append(("deq", [(name, ns)]))
+        elif name == "guess_amax_kernel":
+            cur, kind = [(name, ns)], "guess"
+        elif name == "rowmax_partial_kernel":
+            cur, kind = [(name, ns)], "split"
+        elif name == "quant_hint_kernel":
+            cur, kind = [(name, ns)], "hint"
+    return calls
+
+
+def _c4_labels() -> list:
+    """(scaling, op, mode) of every codec call of `bench.py --no-optimizer
+    --codec c4`, in launch order: per input (activation, gradient), scaling
+    (per-row, per-tensor) and format, bench_codec's two warm-up quantizes,
+    then quantize, dequantize and round trip timed one call between two
+    HIP events (each group after one untimed call), the per-tensor hint
+    calls (11 right, 11 one off, 11 round trips with the right hint, one
+    more right), then the stats pass's quantize and dequantize."""
+    labels = []
+    for _ in ("activation", "gradient"):
+        for sc in ("per-row", "per-tensor"):
+            for _f in ("e4m3", "e5m2"):
+                labels += [(sc, "quantize", "warm")] * 2
+                for op in ("quantize", "dequantize", "round trip"):
+                    labels += [(sc, op, "untimed")] + [(sc, op, "timed")] * C4_CODEC_ITERS
+                if sc == "per-tensor":
+                    labels += [(sc, "hint right", "untimed")] + [(sc, "hint right", "timed")] * C4_CODEC_ITERS
+                    labels += [(sc, "hint off", "untimed")] + [(sc, "hint off", "timed")] * C4_CODEC_ITERS
+                    labels += [(sc, "hint round trip", "untimed")] + [(sc, "hint round trip", "timed")] * C4_CODEC_ITERS
+                    labels += [(sc, "hint right", "extra")]
+                labels += [(sc, "quantize", "stats"), (sc, "dequantize", "stats")]
+    return labels
+
+
 def c4_summary(trace_dir: str, bench_out: str | None) -> None:
     """Kernel durations of a rocprofv3 --kernel-trace run of `bench.py
-    --no-optimizer --codec c4`: per scaling (per-row, per-tensor) and
-    operation, summed over both inputs and formats.  A call is told apart by
-    bench_codec's launch order: per format, quantize launches, dequantize
-    launches, then as many round trips as dequantizes (quantize and round
-    trip are one kernel), then the stats pass's one quantize and one
-    dequantize; a per-tensor quantize or round trip is its two
-    row-max kernels plus quant_split_kernel, added up.  Writes
+    --no-optimizer --codec c4`, the calls labelled by bench_codec's launch
+    order (_c4_labels), averaged over both inputs and formats over the
+    timed calls.  A per-tensor call is its kernels added up.  Writes
     profiles/codec_c4_kernel_trace.md."""
-    disp = _dispatches(trace_dir)
-    hint_calls = _hint_calls(disp)
-    quant = ("quant_block_row_kernel", "quant_rows_kernel", "quant_split_kernel")
-    pre = ("rowmax_partial_kernel", "rowmax_reduce_kernel")
-    calls = {}  # (scaling, op) -> [total ns per call]
-    parts = {}  # kernel -> [ns] of the per-tensor quantize / round trip
-    pending = 0  # ns of row-max kernels waiting for their quant_split_kernel
-    pend_parts = []
-    rt_left = 0
-    deq_run = 0
-    scaling = None
-    for name, ns in disp:
-        if name in pre:
-            pending += ns
-            pend_parts.append((name, ns))
+    calls = _codec_calls(_dispatches(trace_dir))
+    labels = _c4_labels()
+    if len(calls) < len(labels):
+        raise SystemExit(f"the C4 trace holds {len(calls)} codec calls, bench_codec makes {len(labels)}")
+    want = {"dequantize": ("deq",), "quantize": ("row", "guess", "split"), "round trip": ("row", "guess", "split"),
+            "hint right": ("hint", "split"), "hint off": ("hint", "split"), "hint round trip": ("hint", "split")}
+    timed = {}  # (scaling, op) -> [total ns per call]
+    parts = {}  # (scaling, op, kernel) -> [ns]
+    kinds = {}  # (scaling, op) -> call kinds seen
+    for (sc, op, mode), (kind, ks) in zip(labels, calls):
+        if kind not in want[op]:
+            raise SystemExit(f"codec call {kind} where bench_codec's order has {sc} {op}")
+        if mode != "timed":
             continue
-        if name.startswith("dequant"):
-            deq_run += 1
-            calls.setdefault((scaling or "per-row", "dequantize"), []).append(ns)
-            continue
-        if name in quant:
-            if deq_run:
-                # a timed run of dequantizes is followed by as many round trips;
-                # the stats pass's lone dequantize by none
-                rt_left, deq_run = (deq_run if deq_run > 1 else 0), 0
-            scaling = "per-tensor" if name == "quant_split_kernel" else "per-row"
-            op = "round trip" if rt_left > 0 else "quantize"
-            rt_left = max(0, rt_left - 1)
-            calls.setdefault((scaling, op), []).append(ns + pending)
-            if scaling == "per-tensor":
-                for k, v in pend_parts + [(name, ns)]:
-                    parts.setdefault((op, k), []).append(v)
-            pending, pend_parts = 0, []
+        timed.setdefault((sc, op), []).append(sum(ns for _, ns in ks))
+        kinds.setdefault((sc, op), set()).add(kind)
+        if sc == "per-tensor":
+            for k, ns in ks:
+                parts.setdefault((op, k), []).append(ns)
     n = 16 * 4096 * 8192
-    per = {"quantize": 3, "dequantize": 3, "round trip": 4}
-    actual = {("per-tensor", "quantize"): 5, ("per-tensor", "round trip"): 6}
+    per = {"quantize": 3, "dequantize": 3, "round trip": 4, "hint right": 3, "hint off": 3, "hint round trip": 4}
     lines = [
         "# Kernel durations, fp8 codec on C4's tensors",
         "",
@@ -1134,44 +1171,40 @@ def c4_summary(trace_dir: str, bench_out: str | None) -> None:
         "1.07 GB each; Student-t(3) with 0.01 % +-1e4 outliers, and N(0, 1e-5)), e4m3 and",
         "e5m2, per-row (8,192-wide rows) and per-tensor scaling, two copies of each",
         "input rotating.  Algorithmic bytes per element: 3 for quantize and",
-        "dequantize, 4 for the fused round trip; per-tensor quantize reads x twice",
-        "(its |x|max, then the codes), 5 B/element of actual traffic (6 for the",
-        "round trip).  Times summed over both inputs and formats; a per-tensor",
-        "call is its three kernels added up.",
+        "dequantize, 4 for the fused round trip.  Each call is labelled by",
+        "bench_codec's launch order; the figures are its timed calls (one call",
+        f"between two HIP events, {C4_CODEC_ITERS} per group), averaged over both inputs",
+        "and formats, a call's kernels added up.",
         "",
-        "| scaling | operation | calls | average (µs) | algorithmic rate | fraction of 8 TB/s | actual-traffic rate |",
-        "|---|---|---|---|---|---|---|",
+        "A per-tensor quantize or round trip with no hint guesses the exponent",
+        "from the |x|max of every 61st 2,048-element segment (guess_amax_kernel,",
+        "sample_max_kernel) and runs the hint path at the guess: quant_hint_kernel",
+        "converts at the guess while it reduces each segment's |x|max,",
+        "hint_reduce_kernel folds those, and quant_hint_fixup_kernel exits when",
+        "the tensor's exponent equals the guess, or converts every segment again",
+        "(a second read of x) when it does not.",
+        "",
+        "| scaling | operation | calls | average (µs) | algorithmic rate | fraction of 8 TB/s |",
+        "|---|---|---|---|---|---|",
     ]
+    names = {"hint right": "quantize, right hint (`k_hint`)", "hint off": "quantize, hint off by one",
+             "hint round trip": "round trip, right hint"}
     for sc in ("per-row", "per-tensor"):
-        for op in ("quantize", "dequantize", "round trip"):
-            ds = calls.get((sc, op))
+        for op in ("quantize", "dequantize", "round trip", "hint right", "hint off", "hint round trip"):
+            ds = timed.get((sc, op))
             if not ds:
                 continue
             avg = sum(ds) / len(ds)
             rate = n * per[op] / avg / 1e3
-            act = actual.get((sc, op))
-            lines.append(f"| {sc} | {op} | {len(ds)} | {avg / 1e3:,.1f} | {rate:.2f} TB/s | {rate / 8:.2f} | "
-                         + (f"{n * act / avg / 1e3:.2f} TB/s |" if act else "— |"))
+            lines.append(f"| {sc} | {names.get(op, op)} | {len(ds)} | {avg / 1e3:,.1f} | {rate:.2f} TB/s | {rate / 8:.2f} |")
     if parts:
-        lines += ["", "Per-tensor calls by kernel (average µs):", "", "| operation | kernel | calls | average (µs) |", "|---|---|---|---|"]
-        for (op, k), ds in sorted(parts.items()):
-            lines.append(f"| {op} | {k} | {len(ds)} | {sum(ds) / len(ds) / 1e3:,.1f} |")
-    if hint_calls:
-        lines += ["", "Per-tensor calls with an exponent hint (`ely_fp8_quantize_hint`: the one-pass",
-                  "quant_hint_kernel, hint_reduce_kernel folding its per-segment maxima, and",
-                  "quant_hint_fixup_kernel, which exits on a hit and converts every segment again",
-                  "on a miss), average µs per call over both inputs and formats:", "",
-                  "| call | calls | quant_hint_kernel | hint_reduce_kernel | quant_hint_fixup_kernel | total | algorithmic rate | fraction of 8 TB/s |",
-                  "|---|---|---|---|---|---|---|---|"]
-        for label, nbytes in (("quantize, right hint", 3), ("quantize, hint off by one", 3), ("round trip, right hint", 4)):
-            cs = [c for lab, c in hint_calls if lab == label]
-            if not cs:
-                continue
-            avg = [sum(c[i] for c in cs) / len(cs) for i in range(3)]
-            tot = sum(avg)
-            rate = n * nbytes / tot / 1e3
-            lines.append(f"| {label} | {len(cs)} | {avg[0] / 1e3:,.1f} | {avg[1] / 1e3:,.1f} | {avg[2] / 1e3:,.1f} | {tot / 1e3:,.1f} | "
-                         f"{rate:.2f} TB/s | {rate / 8:.2f} |")
+        lines += ["", "Per-tensor calls by kernel (average µs over the timed calls):", "",
+                  "| operation | kernel | calls | average (µs) |", "|---|---|---|---|"]
+        order = ("quantize", "round trip", "hint right", "hint off", "hint round trip")
+        for op in order:
+            for (o, k), ds in parts.items():
+                if o == op:
+                    lines.append(f"| {names.get(op, op)} | {k} | {len(ds)} | {sum(ds) / len(ds) / 1e3:,.1f} |")
     b = None
     if bench_out:
         with open(bench_out) as f:
@@ -1186,30 +1219,6 @@ def c4_summary(trace_dir: str, bench_out: str | None) -> None:
     with open(os.path.join(HERE, "profiles", "codec_c4_kernel_trace.md"), "w") as f:
         f.write("\n".join(lines) + "\n")
     print("\n".join(lines))
-
-
-def _hint_calls(disp) -> list:
-    """The hint path's calls in a C4 codec trace as (label, [ns of its three
-    kernels]).  bench_codec's per-tensor order, per input and format: 11
-    quantize calls with the right hint (one untimed), 11 with the hint one
-    off, 11 round trips with the right hint, then one more right-hint
-    quantize (34 calls)."""
-    names = ("quant_hint_kernel", "hint_reduce_kernel", "quant_hint_fixup_kernel")
-    triples, cur = [], []
-    for name, ns in disp:
-        if name not in names:
-            continue
-        cur.append(ns)
-        if name == names[2]:
-            if len(cur) == 3:
-                triples.append(cur)
-            cur = []
-    out = []
-    for i, t in enumerate(triples):
-        j = i % 34
-        label = "quantize, right hint" if j < 11 or j == 33 else ("quantize, hint off by one" if j < 22 else "round trip, right hint")
-        out.append((label, t))
-    return out
 
 
 def _row(label, ds):

@@ -609,22 +609,35 @@ constexpr int kHintBlocks = 256;         // maxima the reduce launch leaves (4 p
 #define ELY_HINT_FIXUP_WPC 32
 #endif
 constexpr int kHintFixupWavesPerCU = ELY_HINT_FIXUP_WPC;
+#ifndef ELY_GUESS_MIN_MB
+#define ELY_GUESS_MIN_MB 32  // per-tensor rows of at least this many MiB of x take the sampled guess
+#endif
+#ifndef ELY_GUESS_STRIDE
+#define ELY_GUESS_STRIDE 61  // the guess samples every this-many-th segment (a prime)
+#endif
+constexpr int64_t kGuessStride = ELY_GUESS_STRIDE;
 
 // The hint: k_hint, or *k_hint_dev when that is given (read here, before
-// the fixup launch writes k, which may be the same word).  Wave 0 keeps the
-// hint it read in hint_copy for the fixup.  A hint outside the instruction
-// path's range converts nothing here: the call is then a miss.
+// the fixup launch writes k, which may be the same word); with hint_is_amax,
+// *k_hint_dev holds fp32 |x|max bits (a sample's, guess_amax_kernel) and
+// the hint is their exponent.  Wave 0 keeps the hint it read in hint_copy
+// for the fixup.  A hint outside the instruction path's range converts
+// nothing here: the call is then a miss.
 template <int FMT, bool BF16>
 __global__ __launch_bounds__(kQBlock) void quant_hint_kernel(const void* __restrict__ x, int64_t n, int64_t segs,
                                                              int32_t k_hint, const int32_t* k_hint_dev,
-                                                             uint8_t* __restrict__ q, void* __restrict__ out,
-                                                             uint32_t* __restrict__ partial,
+                                                             int32_t hint_is_amax, uint8_t* __restrict__ q,
+                                                             void* __restrict__ out, uint32_t* __restrict__ partial,
                                                              int32_t* __restrict__ hint_copy) {
     constexpr int EPV = Seg<BF16>::EPV, VPL = Seg<BF16>::VPL, ESZ = BF16 ? 2 : 4;
     const int lane = threadIdx.x & (kWave - 1);
     const int64_t seg = (int64_t)blockIdx.x * kWavesPerBlock + wave_uniform(threadIdx.x / kWave);
     if (seg >= segs) return;
-    const int32_t hint = k_hint_dev ? __builtin_amdgcn_readfirstlane(*k_hint_dev) : k_hint;
+    int32_t hint = k_hint;
+    if (k_hint_dev) {
+        hint = __builtin_amdgcn_readfirstlane(*k_hint_dev);
+        if (hint_is_amax) hint = scale_exp_from_amax<FMT>((uint32_t)hint);
+    }
     if (seg == 0 && lane == 0) hint_copy[0] = hint;
     const bool convert = hint >= -kFastK && hint <= kFastK;
     RowScale hs;
@@ -658,6 +671,53 @@ __global__ __launch_bounds__(kQBlock) void quant_hint_kernel(const void* __restr
     }
     amax = wave_max_u32(amax);
     if (lane == 0) partial[seg] = amax;
+}
+
+// A per-tensor row's exponent guessed from a sample: wave w reads segment
+// w * stride (stride a prime, so that the sample does not fall in step with
+// a row length or an outlier channel) and writes its |x|max, as fp32 bits,
+// to partial[w].  The vector form only (n a whole number of 16-byte
+// vectors, aligned x).
+template <bool BF16>
+__global__ __launch_bounds__(kQBlock) void guess_amax_kernel(const void* __restrict__ x, int64_t n, int64_t stride,
+                                                             int64_t samples, uint32_t* __restrict__ partial) {
+    constexpr int EPV = Seg<BF16>::EPV, VPL = Seg<BF16>::VPL, ESZ = BF16 ? 2 : 4;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t w = (int64_t)blockIdx.x * kWavesPerBlock + wave_uniform(threadIdx.x / kWave);
+    if (w >= samples) return;
+    const int64_t e0 = w * stride * kSegElems;
+    const int64_t nv = (min(e0 + kSegElems, n) - e0) / EPV;
+    const uint4* xr = reinterpret_cast<const uint4*>(static_cast<const char*>(x) + e0 * ESZ);
+    uint4 buf[VPL];
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+        const int64_t vi = lane + (int64_t)kWave * j;
+        buf[j] = ld_vec(xr + (vi < nv ? vi : nv - 1));
+    }
+    uint32_t m = 0;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j)
+        if (lane + (int64_t)kWave * j < nv) m = vec_absmax<BF16>(buf[j], m);
+    m = wave_max_u32(m);
+    if (lane == 0) partial[w] = to_f32_bits<BF16>(m);
+}
+
+// out[0] = max of partial[0, count): one block (an integer max, order-free;
+// one word per sample, so no same-address atomics serialize the guess).
+__global__ __launch_bounds__(kRowBlock) void sample_max_kernel(const uint32_t* __restrict__ partial, int64_t count,
+                                                              uint32_t* __restrict__ out) {
+    __shared__ uint32_t red[kRowWaves];
+    const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
+    uint32_t m = 0;
+    for (int64_t i = threadIdx.x; i < count; i += kRowBlock) m = max(m, partial[i]);
+    m = wave_max_u32(m);
+    if (lane == 0) red[w] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t r = red[0];
+        for (int j = 1; j < kRowWaves; ++j) r = max(r, red[j]);
+        out[0] = r;
+    }
 }
 
 // partial[0, segs) -> out[b] for b < kHintBlocks (block b folds a contiguous
@@ -1335,9 +1395,14 @@ static void split_rowmax(const void* x, int64_t rows, int64_t cols, int vec, voi
     }
 }
 
+static size_t guess_ws_bytes(int64_t n);
+template <int FMT, bool BF16>
+static void quantize_guess_impl(const void* x, int64_t n, uint8_t* q, int32_t* k, void* out, void* workspace,
+                                int64_t ws_bytes, hipStream_t s);
+
 template <int FMT, bool BF16>
 static void quantize_impl(const void* x, int64_t rows, int64_t cols, uint8_t* q, int32_t* k, void* out,
-                          void* workspace, int64_t ws_bytes, hipStream_t s) {
+                          void* workspace, int64_t ws_bytes, hipStream_t s, bool allow_guess = true) {
     if (rows == 0) return;
     if (cols == 0) {
         // an empty row has |x|max 0, so k = 0 (fp8.py:38)
@@ -1366,6 +1431,9 @@ static void quantize_impl(const void* x, int64_t rows, int64_t cols, uint8_t* q,
     const int64_t epv = BF16 ? 8 : 4;
     const int vec = (cols % epv == 0) && aligned16(x) && (!out || aligned16(out)) &&
                     (!q || reinterpret_cast<uintptr_t>(q) % (uintptr_t)epv == 0);
+    if (allow_guess && rows == 1 && (q || out) && vec && cols >= ((int64_t)ELY_GUESS_MIN_MB << 20) / (BF16 ? 2 : 4) &&
+        workspace && ws_bytes >= (int64_t)guess_ws_bytes(cols))
+        return quantize_guess_impl<FMT, BF16>(x, cols, q, k, out, workspace, ws_bytes, s);
     if (!workspace || ws_bytes < (int64_t)split_ws_bytes(rows))
         fail(ELY_EWORKSPACE, "fp8 quantize: this shape needs " + std::to_string(split_ws_bytes(rows)) +
                                  " workspace bytes (ely_fp8_workspace_bytes)");
@@ -1390,7 +1458,7 @@ static size_t hint_ws_bytes(int64_t n) {
 template <int FMT, bool BF16>
 static void quantize_hint_impl(const void* x, int64_t n, int32_t k_hint, const int32_t* k_hint_dev, uint8_t* q,
                                int32_t* k, void* out, int32_t* hit, void* workspace, int64_t ws_bytes,
-                               hipStream_t s) {
+                               hipStream_t s, bool hint_is_amax = false) {
     if (!workspace || ws_bytes < (int64_t)hint_ws_bytes(n))
         fail(ELY_EWORKSPACE, "ely_fp8_quantize_hint: workspace of " + std::to_string(ws_bytes) + " bytes, need " +
                                  std::to_string(hint_ws_bytes(n)) + " (ely_fp8_hint_workspace_bytes)");
@@ -1399,7 +1467,7 @@ static void quantize_hint_impl(const void* x, int64_t n, int32_t k_hint, const i
                      (!q || reinterpret_cast<uintptr_t>(q) % (uintptr_t)epv == 0);
     if (!vec || (!k_hint_dev && (k_hint < -kFastK || k_hint > kFastK))) {
         // no one-pass form for this tensor or hint: the split path, a miss
-        quantize_impl<FMT, BF16>(x, 1, n, q, k, out, workspace, ws_bytes, s);
+        quantize_impl<FMT, BF16>(x, 1, n, q, k, out, workspace, ws_bytes, s, false);
         if (hit) {
             hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(64), 0, s, reinterpret_cast<uint32_t*>(hit), (int64_t)1, 0u);
             check_launch("fill_u32_kernel");
@@ -1411,7 +1479,7 @@ static void quantize_hint_impl(const void* x, int64_t n, int32_t k_hint, const i
     uint32_t* block_max = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + align_up((size_t)segs * 4, 256));
     int32_t* hint_copy = reinterpret_cast<int32_t*>(reinterpret_cast<char*>(block_max) + align_up((size_t)kHintBlocks * 4, 256));
     hipLaunchKernelGGL((quant_hint_kernel<FMT, BF16>), dim3(blocks_for_waves(segs)), dim3(kQBlock), 0, s, x, n, segs,
-                       k_hint, k_hint_dev, q, out, partial, hint_copy);
+                       k_hint, k_hint_dev, hint_is_amax ? 1 : 0, q, out, partial, hint_copy);
     check_launch("quant_hint_kernel");
     hipLaunchKernelGGL(hint_reduce_kernel, dim3(kHintBlocks), dim3(kRowBlock), 0, s, (const uint32_t*)partial, segs,
                        block_max);
@@ -1420,6 +1488,35 @@ static void quantize_hint_impl(const void* x, int64_t n, int32_t k_hint, const i
     hipLaunchKernelGGL((quant_hint_fixup_kernel<FMT, BF16>), dim3(blocks_for_waves(waves)), dim3(kQBlock), 0, s, x, n,
                        segs, 1, (const int32_t*)hint_copy, (const uint32_t*)block_max, q, k, out, hit);
     check_launch("quant_hint_fixup_kernel");
+}
+
+// Per-tensor rows of at least ELY_GUESS_MIN_MB MiB (the vector form, a
+// workspace of guess_ws_bytes): the exponent is guessed from every
+// kGuessStride-th segment's |x|max, and the row goes through the hint path
+// at that guess: one read of x when the sample holds the row's maximum
+// binade, the hint path's fixup (a second read and write) when it does not.
+// Either way the codes and k are the split path's, byte for byte.
+// C4 per-tensor, alternating fresh processes: see the measured figures.
+static size_t guess_ws_bytes(int64_t n) { return hint_ws_bytes(n) + 256; }
+
+template <int FMT, bool BF16>
+static void quantize_guess_impl(const void* x, int64_t n, uint8_t* q, int32_t* k, void* out, void* workspace,
+                                int64_t ws_bytes, hipStream_t s) {
+    // after the hint path's layout: the sampled |x|max, and k's word when
+    // the caller asked for no k (a round trip); the samples' maxima go where
+    // the hint path's per-segment maxima go later (samples <= segments)
+    uint32_t* amax = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + hint_ws_bytes(n));
+    int32_t* kword = k ? k : reinterpret_cast<int32_t*>(amax + 1);
+    uint32_t* partial = static_cast<uint32_t*>(workspace);
+    const int64_t segs = (n + kSegElems - 1) / kSegElems;
+    const int64_t samples = (segs + kGuessStride - 1) / kGuessStride;
+    hipLaunchKernelGGL((guess_amax_kernel<BF16>), dim3(blocks_for_waves(samples)), dim3(kQBlock), 0, s, x, n,
+                       (int64_t)kGuessStride, samples, partial);
+    check_launch("guess_amax_kernel");
+    hipLaunchKernelGGL(sample_max_kernel, dim3(1), dim3(kRowBlock), 0, s, (const uint32_t*)partial, samples, amax);
+    check_launch("sample_max_kernel");
+    quantize_hint_impl<FMT, BF16>(x, n, 0, reinterpret_cast<const int32_t*>(amax), q, kword, out, nullptr, workspace,
+                                  ws_bytes, s, true);
 }
 
 template <int FMT, bool BF16OUT>
@@ -1590,9 +1687,10 @@ using namespace ely;
 extern "C" {
 
 int64_t ely_fp8_workspace_bytes(int64_t rows, int64_t cols, int32_t x_dtype) {
-    (void)cols;
-    (void)x_dtype;
-    if (rows < 0) return -1;
+    if (rows < 0 || cols < 0) return -1;
+    // a long per-tensor row also has room for the sampled-guess path
+    if (rows == 1 && cols >= ((int64_t)ELY_GUESS_MIN_MB << 20) / (x_dtype == ELY_F32 ? 4 : 2))
+        return (int64_t)std::max(split_ws_bytes(1), guess_ws_bytes(cols));
     return (int64_t)split_ws_bytes(rows);
 }
 
@@ -1641,11 +1739,11 @@ int ely_fp8_quantize_noalloc(const void* x, int32_t x_dtype, int64_t rows, int64
         hipStream_t s = static_cast<hipStream_t>(stream);
         const int64_t wsb = split ? (int64_t)kNoallocScratchBytes : 0;
         if (fmt == ELY_E4M3) {
-            if (x_dtype == ELY_BF16) quantize_impl<kE4M3, true>(x, rows, cols, q, k, nullptr, ws, wsb, s);
-            else quantize_impl<kE4M3, false>(x, rows, cols, q, k, nullptr, ws, wsb, s);
+            if (x_dtype == ELY_BF16) quantize_impl<kE4M3, true>(x, rows, cols, q, k, nullptr, ws, wsb, s, false);
+            else quantize_impl<kE4M3, false>(x, rows, cols, q, k, nullptr, ws, wsb, s, false);
         } else {
-            if (x_dtype == ELY_BF16) quantize_impl<kE5M2, true>(x, rows, cols, q, k, nullptr, ws, wsb, s);
-            else quantize_impl<kE5M2, false>(x, rows, cols, q, k, nullptr, ws, wsb, s);
+            if (x_dtype == ELY_BF16) quantize_impl<kE5M2, true>(x, rows, cols, q, k, nullptr, ws, wsb, s, false);
+            else quantize_impl<kE5M2, false>(x, rows, cols, q, k, nullptr, ws, wsb, s, false);
         }
     });
 }

@@ -135,6 +135,10 @@ int ely_adamw_fold_step(const ely_tensor* params, const ely_tensor* accs, const 
 
 /* ---------------------------------------------------------------- (c) */
 
+/* Workspace bytes of ely_fp8_quantize / ely_fp8_roundtrip over [rows, cols]
+ * of x_dtype: the split path's row maxima and partial maxima; for one row of
+ * at least 32 MiB, also room for the sampled guess below (about cols / 512
+ * bytes).  -1 for negative sizes. */
 int64_t ely_fp8_workspace_bytes(int64_t rows, int64_t cols, int32_t x_dtype);
 
 /* fp8.quantize (model/fp8.py:28-49): per row of `cols` elements,
@@ -142,7 +146,14 @@ int64_t ely_fp8_workspace_bytes(int64_t rows, int64_t cols, int32_t x_dtype);
  * e4m3, 15 for e5m2) and q = fp8(x * 2^-k) with the multiply in x's dtype
  * and torch's round-to-nearest-even conversion.  Per-tensor scaling is
  * rows = 1.  x: [rows, cols] bf16 or fp32; q: [rows, cols] bytes, or NULL to
- * compute k alone (fp8.scale_exp); k: [rows] int32. */
+ * compute k alone (fp8.scale_exp); k: [rows] int32.
+ * A row that fits no register path is read twice (its |x|max, then its
+ * codes), except one row of at least 32 MiB (16-byte aligned, whole
+ * vectors) given the larger workspace: its exponent is guessed from every
+ * 61st 2,048-element segment and the codes are made at the guess in the
+ * same pass that finds |x|max (as ely_fp8_quantize_hint does), a second
+ * pass following only when the guess was wrong.  The bytes are the same
+ * either way. */
 int ely_fp8_quantize(const void* x, int32_t x_dtype, int64_t rows, int64_t cols, int32_t fmt,
                      uint8_t* q, int32_t* k, void* workspace, int64_t ws_bytes, void* stream);
 

@@ -135,7 +135,14 @@ def test_workspace_queries_are_host_arithmetic(lib):
     assert lib.ely_adamw_workspace_bytes(192) >= 192 * (64 + 32)
     assert lib.ely_fp8_workspace_bytes(16384, 2560, _lib.BF16) >= 16384 * 4
     # row maxima plus at most 2,048 partial maxima, whatever the row length
-    assert lib.ely_fp8_workspace_bytes(1, 1 << 40, _lib.BF16) >= 2048 * 4
+    assert lib.ely_fp8_workspace_bytes(2, 1 << 40, _lib.BF16) >= 2048 * 4
+    assert lib.ely_fp8_workspace_bytes(2, 1 << 40, _lib.BF16) == lib.ely_fp8_workspace_bytes(2, 64, _lib.BF16)
+    # a per-tensor row of at least 32 MiB also has room for the sampled-guess
+    # path (the hint path's workspace and two words); below that, the split path's
+    for dt, n in ((_lib.BF16, 1 << 24), (_lib.F32, 1 << 23)):
+        assert lib.ely_fp8_workspace_bytes(1, n, dt) >= lib.ely_fp8_hint_workspace_bytes(n) + 8
+        assert lib.ely_fp8_workspace_bytes(1, n - 8, dt) == lib.ely_fp8_workspace_bytes(1, 64, dt)
+    assert lib.ely_fp8_workspace_bytes(1, -1, _lib.BF16) == -1
     assert lib.ely_fp8_recover_workspace_bytes(100) >= lib.ely_fp8_workspace_bytes(100, 0, _lib.BF16) + 400
 
 

@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 import torch
 
-from gpu_util import activation, bits, say
+from gpu_util import activation, bits, f32_equal, say
 
 pytestmark = pytest.mark.gpu
 
@@ -157,6 +157,72 @@ def test_hint_argument_checks():
         fp8.quantize(x, "e4m3", per_tensor=True, k_hint=torch.zeros(2, dtype=torch.int32, device="cuda"))
     with pytest.raises(ValueError, match="one int32"):
         fp8.quantize(x, "e4m3", per_tensor=True, k_hint=torch.zeros(1, dtype=torch.int64, device="cuda"))
+
+
+GUESS_STRIDE, SEG_ELEMS = 61, 2048  # the sampled guess reads segments 0, 61, 122, ... of 2,048 elements
+
+
+def _guess_call(x: torch.Tensor, fmt: str, ws_bytes=None, roundtrip=False):
+    """ely_fp8_quantize (or ely_fp8_roundtrip with no q and no k) of x as one
+    row, with a workspace of ws_bytes (default: what ely_fp8_workspace_bytes
+    asks): (q, k, out, workspace)."""
+    from elysium_wan_amd import _lib
+
+    L = _lib.load()
+    n = x.numel()
+    dt = _lib.dtype_code(x)
+    need = L.ely_fp8_workspace_bytes(1, n, dt)
+    ws = torch.zeros(need if ws_bytes is None else ws_bytes, dtype=torch.uint8, device=x.device)
+    sp = _lib.stream_ptr(x.device)
+    if roundtrip:
+        out = torch.full_like(x, float("nan"))
+        _lib.check(L.ely_fp8_roundtrip(x.data_ptr(), dt, 1, n, _lib.FMT[fmt], out.data_ptr(), None, None, ws.data_ptr(), ws.numel(), sp), "roundtrip")
+        torch.cuda.synchronize()
+        return None, None, out, ws
+    q = torch.full((n,), 0xA5, dtype=torch.uint8, device=x.device)
+    k = torch.full((1,), -777, dtype=torch.int32, device=x.device)
+    _lib.check(L.ely_fp8_quantize(x.data_ptr(), dt, 1, n, _lib.FMT[fmt], q.data_ptr(), k.data_ptr(), ws.data_ptr(), ws.numel(), sp), "quantize")
+    torch.cuda.synchronize()
+    return q, int(k.item()), None, ws
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("where", ["sampled", "unsampled"])
+def test_sampled_guess_equals_the_oracle_and_the_split_path(oracle, fmt, dtype, where):
+    """A per-tensor row of 32 MiB takes the sampled guess: the exponent of
+    the |x|max of every 61st 2,048-element segment, then the hint path.  A
+    -8192 outlier in a sampled segment makes the guess right (one pass); in an
+    unsampled one, wrong (the fixup pass).  Either way the bytes and k are
+    the oracle's and the split path's (the same call given too small a
+    workspace for the guess), and the word the guess left in the workspace
+    is the sample's |x|max, so the sampling itself is checked."""
+    from elysium_wan_amd import _lib
+
+    L = _lib.load()
+    n = (32 << 20) // (2 if dtype == torch.bfloat16 else 4)
+    x = activation((n,), seed=700 + n % 89, dtype=dtype)
+    seg = GUESS_STRIDE * 7 if where == "sampled" else GUESS_STRIDE * 7 + 3
+    x[seg * SEG_ELEMS + 5] = -8192.0
+    say("fp8 sampled guess", fmt, dtype, where)
+    oq, ok = oracle.quantize(_oracle_in(x.reshape(1, -1)), fmt)
+    q, k, _, ws = _guess_call(x, fmt)
+    assert k == int(ok.reshape(-1)[0])
+    assert np.array_equal(bits(q), oq.reshape(-1))
+    off = L.ely_fp8_hint_workspace_bytes(n)
+    sample = x.float().reshape(-1, SEG_ELEMS)[::GUESS_STRIDE].abs().max()
+    assert int(ws[off:off + 4].view(torch.int32).item()) == int(sample.reshape(1).view(torch.int32).item())
+    assert (float(sample) == 8192.0) == (where == "sampled")
+    # the split path: a workspace too small for the guess
+    q2, k2, _, _ = _guess_call(x, fmt, ws_bytes=L.ely_fp8_workspace_bytes(2, n, _lib.dtype_code(x)))
+    assert k2 == k and torch.equal(q2, q)
+    # the round trip, with neither q nor k asked for
+    _, _, out, _ = _guess_call(x, fmt, roundtrip=True)
+    ort = oracle.roundtrip(_oracle_in(x.reshape(1, -1)), fmt).reshape(-1)
+    if dtype == torch.bfloat16:
+        assert np.array_equal(bits(out), ort)
+    else:
+        assert f32_equal(bits(out), ort)
 
 
 def _c4_activation(seed: int) -> torch.Tensor:
