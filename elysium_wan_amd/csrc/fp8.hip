@@ -704,18 +704,20 @@ __global__ __launch_bounds__(kQBlock) void guess_amax_kernel(const void* __restr
 
 // out[0] = max of partial[0, count): one block (an integer max, order-free;
 // one word per sample, so no same-address atomics serialize the guess).
-__global__ __launch_bounds__(kRowBlock) void sample_max_kernel(const uint32_t* __restrict__ partial, int64_t count,
-                                                              uint32_t* __restrict__ out) {
-    __shared__ uint32_t red[kRowWaves];
+constexpr int kSampleMaxBlock = 1024;
+__global__ __launch_bounds__(kSampleMaxBlock) void sample_max_kernel(const uint32_t* __restrict__ partial,
+                                                                    int64_t count, uint32_t* __restrict__ out) {
+    __shared__ uint32_t red[kSampleMaxBlock / kWave];
     const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
     uint32_t m = 0;
-    for (int64_t i = threadIdx.x; i < count; i += kRowBlock) m = max(m, partial[i]);
+#pragma unroll 4
+    for (int64_t i = threadIdx.x; i < count; i += kSampleMaxBlock) m = max(m, partial[i]);
     m = wave_max_u32(m);
     if (lane == 0) red[w] = m;
     __syncthreads();
     if (threadIdx.x == 0) {
         uint32_t r = red[0];
-        for (int j = 1; j < kRowWaves; ++j) r = max(r, red[j]);
+        for (int j = 1; j < kSampleMaxBlock / kWave; ++j) r = max(r, red[j]);
         out[0] = r;
     }
 }
@@ -1513,7 +1515,7 @@ static void quantize_guess_impl(const void* x, int64_t n, uint8_t* q, int32_t* k
     hipLaunchKernelGGL((guess_amax_kernel<BF16>), dim3(blocks_for_waves(samples)), dim3(kQBlock), 0, s, x, n,
                        (int64_t)kGuessStride, samples, partial);
     check_launch("guess_amax_kernel");
-    hipLaunchKernelGGL(sample_max_kernel, dim3(1), dim3(kRowBlock), 0, s, (const uint32_t*)partial, samples, amax);
+    hipLaunchKernelGGL(sample_max_kernel, dim3(1), dim3(kSampleMaxBlock), 0, s, (const uint32_t*)partial, samples, amax);
     check_launch("sample_max_kernel");
     quantize_hint_impl<FMT, BF16>(x, n, 0, reinterpret_cast<const int32_t*>(amax), q, kword, out, nullptr, workspace,
                                   ws_bytes, s, true);
