@@ -610,7 +610,13 @@ constexpr int kHintBlocks = 256;         // maxima the reduce launch leaves (4 p
 #endif
 constexpr int kHintFixupWavesPerCU = ELY_HINT_FIXUP_WPC;
 #ifndef ELY_GUESS_MIN_MB
-#define ELY_GUESS_MIN_MB 32  // per-tensor rows of at least this many MiB of x take the sampled guess
+// per-tensor rows of at least this many MiB of x take the sampled guess.
+// Back to back on N(0, 1) bf16 (a right guess), per call: 8 MiB 16.4-18.1 us
+// against 12.6-16.5 on the split path, 32 MiB 21.4-21.9 against 17.7-18.8,
+// 64 MiB 29.3-29.9 against 28.8-29.5, 128 MiB 45 against 54, 512 MiB 139
+// against 201: the guess's four small launches cost what its saved read wins
+// back near 64 MiB
+#define ELY_GUESS_MIN_MB 64
 #endif
 #ifndef ELY_GUESS_STRIDE
 #define ELY_GUESS_STRIDE 61  // the guess samples every this-many-th segment (a prime)

@@ -119,7 +119,7 @@ def quantize(x: torch.Tensor, fmt: str = "e4m3", per_tensor: bool = False, k_hin
     the one-element int32 tensor an earlier call returned (read on the GPU,
     no host wait).  The results are the same whatever the hint; when it is
     right, x is read once instead of twice.  Without one, a per-tensor x of
-    32 MiB or more guesses its exponent from a sample of x (every 61st
+    64 MiB or more guesses its exponent from a sample of x (every 61st
     2,048-element segment) and is read once when the guess holds."""
     f = _fmt(fmt)
     hint = _hint(k_hint, per_tensor, "quantize")

@@ -137,7 +137,7 @@ int ely_adamw_fold_step(const ely_tensor* params, const ely_tensor* accs, const 
 
 /* Workspace bytes of ely_fp8_quantize / ely_fp8_roundtrip over [rows, cols]
  * of x_dtype: the split path's row maxima and partial maxima; for one row of
- * at least 32 MiB, also room for the sampled guess below (about cols / 512
+ * at least 64 MiB, also room for the sampled guess below (about cols / 512
  * bytes).  -1 for negative sizes. */
 int64_t ely_fp8_workspace_bytes(int64_t rows, int64_t cols, int32_t x_dtype);
 
@@ -148,7 +148,7 @@ int64_t ely_fp8_workspace_bytes(int64_t rows, int64_t cols, int32_t x_dtype);
  * rows = 1.  x: [rows, cols] bf16 or fp32; q: [rows, cols] bytes, or NULL to
  * compute k alone (fp8.scale_exp); k: [rows] int32.
  * A row that fits no register path is read twice (its |x|max, then its
- * codes), except one row of at least 32 MiB (16-byte aligned, whole
+ * codes), except one row of at least 64 MiB (16-byte aligned, whole
  * vectors) given the larger workspace: its exponent is guessed from every
  * 61st 2,048-element segment and the codes are made at the guess in the
  * same pass that finds |x|max (as ely_fp8_quantize_hint does), a second

@@ -137,9 +137,9 @@ def test_workspace_queries_are_host_arithmetic(lib):
     # row maxima plus at most 2,048 partial maxima, whatever the row length
     assert lib.ely_fp8_workspace_bytes(2, 1 << 40, _lib.BF16) >= 2048 * 4
     assert lib.ely_fp8_workspace_bytes(2, 1 << 40, _lib.BF16) == lib.ely_fp8_workspace_bytes(2, 64, _lib.BF16)
-    # a per-tensor row of at least 32 MiB also has room for the sampled-guess
+    # a per-tensor row of at least 64 MiB also has room for the sampled-guess
     # path (the hint path's workspace and two words); below that, the split path's
-    for dt, n in ((_lib.BF16, 1 << 24), (_lib.F32, 1 << 23)):
+    for dt, n in ((_lib.BF16, 1 << 25), (_lib.F32, 1 << 24)):
         assert lib.ely_fp8_workspace_bytes(1, n, dt) >= lib.ely_fp8_hint_workspace_bytes(n) + 8
         assert lib.ely_fp8_workspace_bytes(1, n - 8, dt) == lib.ely_fp8_workspace_bytes(1, 64, dt)
     assert lib.ely_fp8_workspace_bytes(1, -1, _lib.BF16) == -1

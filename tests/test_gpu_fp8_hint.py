@@ -190,7 +190,7 @@ def _guess_call(x: torch.Tensor, fmt: str, ws_bytes=None, roundtrip=False):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("where", ["sampled", "unsampled"])
 def test_sampled_guess_equals_the_oracle_and_the_split_path(oracle, fmt, dtype, where):
-    """A per-tensor row of 32 MiB takes the sampled guess: the exponent of
+    """A per-tensor row of 64 MiB takes the sampled guess: the exponent of
     the |x|max of every 61st 2,048-element segment, then the hint path.  A
     -8192 outlier in a sampled segment makes the guess right (one pass); in an
     unsampled one, wrong (the fixup pass).  Either way the bytes and k are
@@ -200,7 +200,7 @@ def test_sampled_guess_equals_the_oracle_and_the_split_path(oracle, fmt, dtype, 
     from elysium_wan_amd import _lib
 
     L = _lib.load()
-    n = (32 << 20) // (2 if dtype == torch.bfloat16 else 4)
+    n = (64 << 20) // (2 if dtype == torch.bfloat16 else 4)
     x = activation((n,), seed=700 + n % 89, dtype=dtype)
     seg = GUESS_STRIDE * 7 if where == "sampled" else GUESS_STRIDE * 7 + 3
     x[seg * SEG_ELEMS + 5] = -8192.0
