@@ -188,12 +188,14 @@ def _guess_call(x: torch.Tensor, fmt: str, ws_bytes=None, roundtrip=False):
 
 @pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("where", ["sampled", "unsampled"])
+@pytest.mark.parametrize("where", ["sampled", "unsampled", "nan sampled", "inf unsampled"])
 def test_sampled_guess_equals_the_oracle_and_the_split_path(oracle, fmt, dtype, where):
     """A per-tensor row of 64 MiB takes the sampled guess: the exponent of
     the |x|max of every 61st 2,048-element segment, then the hint path.  A
     -8192 outlier in a sampled segment makes the guess right (one pass); in an
-    unsampled one, wrong (the fixup pass).  Either way the bytes and k are
+    unsampled one, wrong (the fixup pass); a NaN in the sample, or an Inf
+    outside it, leaves the row off the instruction path, so the fixup
+    converts it element by element.  Either way the bytes and k are
     the oracle's and the split path's (the same call given too small a
     workspace for the guess), and the word the guess left in the workspace
     is the sample's |x|max, so the sampling itself is checked."""
@@ -202,17 +204,20 @@ def test_sampled_guess_equals_the_oracle_and_the_split_path(oracle, fmt, dtype, 
     L = _lib.load()
     n = (64 << 20) // (2 if dtype == torch.bfloat16 else 4)
     x = activation((n,), seed=700 + n % 89, dtype=dtype)
-    seg = GUESS_STRIDE * 7 if where == "sampled" else GUESS_STRIDE * 7 + 3
-    x[seg * SEG_ELEMS + 5] = -8192.0
+    seg = GUESS_STRIDE * 7 if where in ("sampled", "nan sampled") else GUESS_STRIDE * 7 + 3
+    x[seg * SEG_ELEMS + 5] = {"sampled": -8192.0, "unsampled": -8192.0, "nan sampled": float("nan"), "inf unsampled": float("inf")}[where]
     say("fp8 sampled guess", fmt, dtype, where)
     oq, ok = oracle.quantize(_oracle_in(x.reshape(1, -1)), fmt)
     q, k, _, ws = _guess_call(x, fmt)
     assert k == int(ok.reshape(-1)[0])
     assert np.array_equal(bits(q), oq.reshape(-1))
     off = L.ely_fp8_hint_workspace_bytes(n)
-    sample = x.float().reshape(-1, SEG_ELEMS)[::GUESS_STRIDE].abs().max()
-    assert int(ws[off:off + 4].view(torch.int32).item()) == int(sample.reshape(1).view(torch.int32).item())
-    assert (float(sample) == 8192.0) == (where == "sampled")
+    if where in ("sampled", "unsampled"):
+        sample = x.float().reshape(-1, SEG_ELEMS)[::GUESS_STRIDE].abs().max()
+        assert int(ws[off:off + 4].view(torch.int32).item()) == int(sample.reshape(1).view(torch.int32).item())
+        assert (float(sample) == 8192.0) == (where == "sampled")
+    elif where == "nan sampled":
+        assert torch.isnan(ws[off:off + 4].view(torch.float32)).item()
     # the split path: a workspace too small for the guess
     q2, k2, _, _ = _guess_call(x, fmt, ws_bytes=L.ely_fp8_workspace_bytes(2, n, _lib.dtype_code(x)))
     assert k2 == k and torch.equal(q2, q)
