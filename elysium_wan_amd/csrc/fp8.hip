@@ -1503,8 +1503,9 @@ static void quantize_hint_impl(const void* x, int64_t n, int32_t k_hint, const i
 // kGuessStride-th segment's |x|max, and the row goes through the hint path
 // at that guess: one read of x when the sample holds the row's maximum
 // binade, the hint path's fixup (a second read and write) when it does not.
-// Either way the codes and k are the split path's, byte for byte.
-// C4 per-tensor, alternating fresh processes: see the measured figures.
+// Either way the codes and k are the split path's, byte for byte.  C4
+// per-tensor (both inputs guess right), kernel time per call: quantize
+// 272 us against 404 on the split path, round trip 357 against 488.
 static size_t guess_ws_bytes(int64_t n) { return hint_ws_bytes(n) + 256; }
 
 template <int FMT, bool BF16>
